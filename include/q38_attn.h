@@ -1,0 +1,229 @@
+/*
+ * q38_attn.h -- C ABI of the MI355X (gfx950) attention path of the
+ * Qwen3.8-27B hybrid: full-attention GQA decode/prefill over a paged KV cache
+ * and the Gated-DeltaNet recurrence.
+ *
+ * Reference: StepfenShawn/qwen3.8_27b_in_rust.  The path there is two private
+ * functions of the model layer, full_core (src/model/ops.rs:813-940) and
+ * linear_core (src/model/ops.rs:648-742), called per token from
+ * full_attention / linear_attention (ops.rs:942, :744) and, token by token,
+ * from the prefill loops (ops.rs:1153-1172, :1084-1099).  Their state lives
+ * in Q38Model (src/model/mod.rs:155-158): key_cache / value_cache
+ * [17][ctx][1024], conv_state [48][10240*3], delta_state [48][48*128*128].
+ *
+ * Conventions (mirroring the reference's Result<_, i32> with Err(-1)):
+ *  - every function returns 0 on success and -1 on failure; q38_last_error()
+ *    then gives the reason (thread-local, valid until the next failing call);
+ *  - pointers named d_* are device pointers; all other pointers are host
+ *    memory that is read during the call and never retained;
+ *  - work is stream-ordered on the context's stream; results are visible to
+ *    the host after q38_sync() or q38_download();
+ *  - a context and everything created from it is used from one host thread
+ *    at a time (the reference has one caller thread; its parallelism is
+ *    internal, as here);
+ *  - shapes are the model's compile-time constants (src/model/mod.rs:13-24):
+ *    attention 24 query heads, 4 kv heads, head_dim 256 (query head h reads
+ *    kv head h/6); DeltaNet 16 q/k heads, 48 value heads, head_dim 128 (value
+ *    head vh reads q/k head vh%16).
+ */
+#ifndef Q38_ATTN_H
+#define Q38_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct q38_ctx q38_ctx;
+typedef struct q38_kv q38_kv;
+
+/* ------------------------------------------------------------ errors, context */
+
+/* Text of the last failure on this thread ("" if none). */
+const char *q38_last_error(void);
+
+/* Number of HIP devices visible to this process (0 without a GPU). */
+int q38_device_count(int *count);
+
+/* Open device `device`, create the context's stream and load the gfx950 code
+ * objects from module_dir (NULL: the directory holding this library).
+ * Replaces the host-side setup the reference does in Q38Model::bind
+ * (ops.rs:1450-1501) for the path's buffers. */
+int q38_ctx_create(q38_ctx **out, int device, const char *module_dir);
+int q38_ctx_destroy(q38_ctx *ctx);
+/* The hipStream_t all work of this context is ordered on. */
+void *q38_ctx_stream(q38_ctx *ctx);
+int q38_sync(q38_ctx *ctx);
+/* Compute units, peak engine clock (kHz), LDS bytes per workgroup, and the
+ * device name (name_len bytes, NUL-terminated). */
+int q38_device_info(q38_ctx *ctx, int *cu_count, int *clock_khz, int *lds_bytes, char *name,
+                    size_t name_len);
+
+/* Device buffers for callers that have no allocator of their own. */
+int q38_alloc(q38_ctx *ctx, size_t bytes, void **d_ptr);
+int q38_free(q38_ctx *ctx, void *d_ptr);
+int q38_upload(q38_ctx *ctx, void *d_dst, const void *src, size_t bytes);
+int q38_download(q38_ctx *ctx, void *dst, const void *d_src, size_t bytes);
+int q38_zero(q38_ctx *ctx, void *d_dst, size_t bytes);
+
+/* Events on the context's stream, for timing. */
+int q38_event_create(q38_ctx *ctx, void **event);
+int q38_event_record(q38_ctx *ctx, void *event);
+int q38_event_elapsed_ms(void *start, void *stop, float *ms);
+int q38_event_destroy(void *event);
+
+/* Time every launch of one kernel of this library (by its symbol name, e.g.
+ * "q38_attn_decode_split") with a pair of events on the context's stream,
+ * for up to max_launches launches; stop returns the summed kernel time. */
+int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launches);
+int q38_kernel_timer_stop(q38_ctx *ctx, float *total_ms, int *launches);
+
+/* Seeded N(mean, sigma^2) f32 fill on the device: element i equals what the
+ * host generator (SplitMix64 + Box-Muller, qwen3.8_27b_in_rust_amd/synth.py)
+ * gives for the same seed.  For benchmark inputs of many gigabytes. */
+int q38_fill_normal(q38_ctx *ctx, float *d_out, size_t n, uint64_t seed, float sigma, float mean);
+
+/* ------------------------------------------------------------- paged KV cache */
+
+/*
+ * Device-resident paged replacement of Q38Model.key_cache / value_cache
+ * (src/model/mod.rs:157-158, sized at ops.rs:1464).  n_slots full-attention
+ * layer slots (the reference has 17: layers 3, 7, ..., 63 and the MTP layer
+ * 64, slot = layer/4, ops.rs:858).  Each slot holds max_pages pages of 16
+ * tokens; a page is [4 kv heads][16 tokens][256] f32 for K and the same for
+ * V (128 KiB per page and slot).  Sequences map logical pages to physical
+ * pages through a page table of max_tokens_per_seq/16 entries; one page id
+ * serves the same positions in every slot.
+ */
+int q38_kv_create(q38_ctx *ctx, int n_slots, int max_pages, int max_seqs, int max_tokens_per_seq,
+                  q38_kv **out);
+int q38_kv_destroy(q38_kv *kv);
+/* Pages not held by any sequence. */
+int q38_kv_free_pages(q38_kv *kv, int *n_free);
+
+/* A new empty sequence (capacity 0). */
+int q38_seq_create(q38_kv *kv, int *seq);
+/* Release the sequence and its pages. */
+int q38_seq_free(q38_kv *kv, int seq);
+/* Back to position 0 with no pages (Q38ModelOps::reset, ops.rs:1691-1699:
+ * positions are rewritten before they are read again, so no page is
+ * cleared). */
+int q38_seq_reset(q38_kv *kv, int seq);
+/* Positional rollback: keep positions < n_tokens, release whole pages past
+ * them (the reference rolls the KV cache back by position only,
+ * restore_target_state ops.rs:1642-1647). */
+int q38_seq_truncate(q38_kv *kv, int seq, int n_tokens);
+/* Make positions < n_tokens addressable, taking pages from the pool. */
+int q38_seq_reserve(q38_kv *kv, int seq, int n_tokens);
+/* Map the sequence's logical pages 0..n_pages-1 to the given physical pages
+ * (taken out of the pool; they must be free).  For callers that place pages
+ * themselves, e.g. a randomly permuted page table. */
+int q38_seq_set_pages(q38_kv *kv, int seq, int n_pages, const int32_t *page_ids);
+/* Positions currently addressable (a multiple of 16). */
+int q38_seq_capacity(q38_kv *kv, int seq, int *n_tokens);
+
+/* Store token rows [n_tokens][1024] (4 kv heads x 256) of K and V at
+ * positions pos0.. of the sequence in layer `layer`'s slot (the append of
+ * ops.rs:858-866, for many tokens).  Reserves pages as needed. */
+int q38_kv_write(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, const float *d_k,
+                 const float *d_v);
+/* Gather positions pos0..pos0+n_tokens-1 back into rows [n_tokens][1024]. */
+int q38_kv_read(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float *d_k, float *d_v);
+
+/* --------------------------------------------------------- full attention */
+
+/*
+ * Attention core of full_core (ops.rs:858-938) for n_seq sequences, one
+ * decode token each, in layer `layer` (a full-attention layer: (layer+1)%4 ==
+ * 0, or 64).  For sequence b: if d_k_new is not NULL its row b
+ * ([1024] = 4 kv heads x 256, post-norm and post-RoPE) and d_v_new's row b
+ * are first stored at positions[b] (ops.rs:858-866); then every query head
+ * attends over positions 0..positions[b] (ops.rs:879-913) and, if d_gate is
+ * not NULL, is multiplied by sigmoid(gate) (ops.rs:914-917).
+ * d_q, d_gate, d_out: [n_seq][24][256] (q post-norm, post-RoPE).
+ * Sequence ids must be distinct.  Fails (-1) when positions[b] + 1 exceeds
+ * the sequence's context limit (the check of ops.rs:860-864 and :1702).
+ */
+int q38_attn_decode(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
+                    const int32_t *positions, const float *d_q, const float *d_k_new,
+                    const float *d_v_new, const float *d_gate, float *d_out);
+
+/*
+ * full_core whole (ops.rs:813-940), n_seq sequences, one token each:
+ * d_q_and_gate [n_seq][24][512] (per head: 256 q then 256 gate, the layout
+ * of ops.rs:832-837), d_key / d_value [n_seq][1024] raw projections,
+ * d_q_norm / d_k_norm [256].  q and k get RMSNorm (eps 1e-6) and RoPE at
+ * positions[b]; the new k/v are appended; d_out [n_seq][24][256] receives
+ * the gated attention output.
+ */
+int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
+                  const int32_t *positions, const float *d_q_norm, const float *d_k_norm,
+                  const float *d_q_and_gate, const float *d_key, const float *d_value,
+                  float *d_out);
+
+/* The q/k RMSNorm + RoPE prologue of full_core alone (ops.rs:832-856) for
+ * n_tokens tokens at positions pos0, pos0+1, ...: writes d_q_out, d_gate_out
+ * [n_tokens][24][256] and d_k_out [n_tokens][1024]. */
+int q38_attn_pre(q38_ctx *ctx, int n_tokens, int pos0, const float *d_q_norm, const float *d_k_norm,
+                 const float *d_q_and_gate, const float *d_key, float *d_q_out, float *d_gate_out,
+                 float *d_k_out);
+
+/*
+ * Prefill of one sequence (batch_full_attention, ops.rs:1153-1172, which runs
+ * full_core for tokens base_pos .. base_pos+n_tokens-1 in order): stores the
+ * n_tokens rows of d_k / d_v ([n][1024], post-norm, post-RoPE) at base_pos..,
+ * then token t attends causally over positions 0..base_pos+t.
+ * d_q, d_gate (nullable), d_out: [n_tokens][24][256].
+ */
+int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens, const float *d_q,
+                     const float *d_k, const float *d_v, const float *d_gate, float *d_out);
+
+/* ----------------------------------------------------------- Gated DeltaNet */
+
+/*
+ * Recurrence core of linear_core (ops.rs:689-733) for n_seq independent
+ * states, one token each.  Sequence s: state d_state + s*state_stride floats,
+ * [48][128][128] (row c of value head vh is S[vh][c][0..128]); d_q, d_k
+ * [n_seq][16][128] (L2-normalised); d_v, d_out [n_seq][48][128]; d_beta
+ * [n_seq][48] (post-sigmoid); d_g [n_seq][48] the log-decay (the
+ * reference's alpha after ops.rs:686; the state is scaled by exp(g)).
+ */
+int q38_gdn_step(q38_ctx *ctx, int n_seq, float *d_state, int64_t state_stride, const float *d_q,
+                 const float *d_k, const float *d_v, const float *d_beta, const float *d_g,
+                 float *d_out);
+
+/*
+ * The same recurrence over n_tokens consecutive tokens of one state
+ * (batch_linear_attention's token loop, ops.rs:1088-1099): d_q, d_k
+ * [n_tokens][16][128], d_v and d_out [n_tokens][48][128], d_beta, d_g
+ * [n_tokens][48].  The state ends as after n_tokens calls of q38_gdn_step.
+ */
+int q38_gdn_prefill(q38_ctx *ctx, float *d_state, int n_tokens, const float *d_q, const float *d_k,
+                    const float *d_v, const float *d_beta, const float *d_g, float *d_out);
+
+/* Per-layer DeltaNet weights of linear_core (bound at ops.rs:62-100). */
+typedef struct {
+    const float *d_conv_w; /* ssm_conv1d [10240][4] */
+    const float *d_dt;     /* ssm_dt.bias [48] */
+    const float *d_a;      /* ssm_a [48] */
+    const float *d_norm;   /* ssm_norm [128] */
+} q38_linear_weights;
+
+/*
+ * linear_core whole (ops.rs:648-742) for n_tokens consecutive tokens of each
+ * of n_seq sequences (n_tokens > 1 is batch_linear_attention's loop,
+ * ops.rs:1084-1099, with n_seq 1).  Sequence s: d_conv_state + s*30720
+ * ([10240][3]), d_delta_state + s*786432 ([48][128][128]).  Per token
+ * (index s*n_tokens + t): d_qkv [10240] raw projection, d_z [6144], d_beta,
+ * d_alpha [48] raw; d_out [6144] receives rmsnorm(o) * silu(z).
+ */
+int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weights *w,
+                    float *d_conv_state, float *d_delta_state, const float *d_qkv,
+                    const float *d_z, const float *d_beta, const float *d_alpha, float *d_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

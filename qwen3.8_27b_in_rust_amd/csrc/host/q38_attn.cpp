@@ -1,0 +1,907 @@
+/*
+ * Host side of the MI355X attention path: the C ABI of include/q38_attn.h.
+ *
+ * Kernels live in gfx950 code objects (one .hsaco per source file) loaded
+ * with hipModuleLoad and launched with hipModuleLaunchKernel; their argument
+ * blocks (q38_kargs.h) travel by value in the kernarg segment, so a decode
+ * step needs no host-to-device copy besides page-table updates.
+ *
+ * Validation happens here, before any launch, and turns every bad input
+ * into -1 with a message (the reference's Err(-1), e.g. the KV bounds check
+ * of src/model/ops.rs:858-864): no kernel ever sees an index it was not
+ * sized for.
+ */
+#define __HIP_PLATFORM_AMD__ 1
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+/* From hip/hip_ext.h (whose templates need the HIP compiler): a module launch
+ * whose start/stop events are stamped by the kernel dispatch itself. */
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void **kernelParams, void **extra,
+                                               hipEvent_t startEvent, hipEvent_t stopEvent,
+                                               uint32_t flags);
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../../include/q38_attn.h"
+#include "../q38_kargs.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return -1;
+}
+
+#define Q38_HIP(call)                                                                   \
+    do {                                                                                \
+        hipError_t e_ = (call);                                                         \
+        if (e_ != hipSuccess) return fail("%s: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                                          __FILE__, __LINE__);                          \
+    } while (0)
+
+std::string library_dir() {
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void *>(&library_dir), &info) == 0 || info.dli_fname == nullptr)
+        return ".";
+    std::string path(info.dli_fname);
+    size_t slash = path.find_last_of('/');
+    return slash == std::string::npos ? std::string(".") : path.substr(0, slash);
+}
+
+/* Full-attention layers: every fourth block and the MTP block 64
+ * (ops.rs:38-41); their slot is layer/4 (ops.rs:858). */
+bool is_full_attention(int layer) { return layer >= 0 && ((layer + 1) % 4 == 0 || layer == 64); }
+
+}  // namespace
+
+struct q38_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipModule_t mod_decode = nullptr;
+    hipModule_t mod_gdn = nullptr;
+    hipFunction_t f_decode_split = nullptr;
+    hipFunction_t f_decode_merge = nullptr;
+    hipFunction_t f_kv_copy = nullptr;
+    hipFunction_t f_attn_pre = nullptr;
+    hipFunction_t f_gdn_recurrent = nullptr;
+    hipFunction_t f_gdn_pre = nullptr;
+    hipModule_t mod_synth = nullptr;
+    hipFunction_t f_fill_normal = nullptr;
+    /* per-kernel event timer (q38_kernel_timer_*) */
+    hipFunction_t timed = nullptr;
+    std::vector<hipEvent_t> timer_events;
+    int timer_used = 0;
+    int cu_count = 0;
+    int clock_khz = 0;
+    int lds_bytes = 0;
+    char name[256] = {0};
+    /* grow-only device workspace (split-K partials, pre-kernel outputs) */
+    void *work = nullptr;
+    size_t work_bytes = 0;
+    float rope_theta_scale = 0.0f;
+
+    int ensure_work(size_t bytes) {
+        if (bytes <= work_bytes) return 0;
+        if (work != nullptr) {
+            Q38_HIP(hipStreamSynchronize(stream));
+            Q38_HIP(hipFree(work));
+            work = nullptr;
+            work_bytes = 0;
+        }
+        size_t want = std::max(bytes, (size_t)1 << 20);
+        Q38_HIP(hipMalloc(&work, want));
+        work_bytes = want;
+        return 0;
+    }
+
+    int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned block, void *args) {
+        void *params[] = {args};
+        const bool timing = f == timed && timer_used + 2 <= (int)timer_events.size();
+        if (timing) {
+            /* start/stop timestamps taken by the dispatch itself */
+            Q38_HIP(hipExtModuleLaunchKernel(f, gx * block, gy, gz, block, 1, 1, 0, stream, params, nullptr,
+                                             timer_events[timer_used], timer_events[timer_used + 1], 0));
+            timer_used += 2;
+            return 0;
+        }
+        Q38_HIP(hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, 0, stream, params, nullptr));
+        return 0;
+    }
+};
+
+struct q38_kv {
+    q38_ctx *ctx = nullptr;
+    int n_slots = 0;
+    int max_pages = 0;
+    int max_seqs = 0;
+    int pt_stride = 0; /* pages per sequence at most */
+    float *kpool = nullptr;
+    float *vpool = nullptr;
+    int32_t *d_page_table = nullptr;
+    std::vector<int32_t> page_table; /* host mirror [max_seqs][pt_stride] */
+    std::vector<int32_t> free_pages; /* stack */
+    std::vector<char> seq_live;
+    std::vector<int32_t> seq_pages; /* pages held per sequence */
+    /* pinned staging for page-table uploads, used as a ring */
+    int32_t *staging = nullptr;
+    size_t staging_len = 0;
+    size_t staging_head = 0;
+
+    size_t slot_floats() const { return (size_t)max_pages * Q38_PAGE_FLOATS; }
+    float *kslot(int slot) const { return kpool + (size_t)slot * slot_floats(); }
+    float *vslot(int slot) const { return vpool + (size_t)slot * slot_floats(); }
+
+    int check_seq(int seq) const {
+        if (seq < 0 || seq >= max_seqs || !seq_live[seq]) return fail("sequence %d does not exist", seq);
+        return 0;
+    }
+
+    /* Copy page-table entries [first, first+count) of `seq` to the device,
+     * stream-ordered, through the pinned ring. */
+    int upload_entries(int seq, int first, int count) {
+        if (count <= 0) return 0;
+        if ((size_t)count > staging_len) return fail("page-table update larger than staging");
+        if (staging_head + count > staging_len) {
+            Q38_HIP(hipStreamSynchronize(ctx->stream));
+            staging_head = 0;
+        }
+        int32_t *src = staging + staging_head;
+        memcpy(src, &page_table[(size_t)seq * pt_stride + first], sizeof(int32_t) * count);
+        staging_head += count;
+        Q38_HIP(hipMemcpyAsync(d_page_table + (size_t)seq * pt_stride + first, src,
+                               sizeof(int32_t) * count, hipMemcpyHostToDevice, ctx->stream));
+        return 0;
+    }
+
+    int reserve(int seq, int n_tokens) {
+        if (n_tokens < 0) return fail("negative token count");
+        const int need = (n_tokens + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS;
+        if (need > pt_stride)
+            return fail("sequence %d: %d tokens exceed the per-sequence limit of %d", seq, n_tokens,
+                        pt_stride * Q38_PAGE_TOKENS);
+        const int have = seq_pages[seq];
+        if (need <= have) return 0;
+        if ((size_t)(need - have) > free_pages.size())
+            return fail("KV pool exhausted: need %d pages, %zu free", need - have, free_pages.size());
+        for (int p = have; p < need; ++p) {
+            page_table[(size_t)seq * pt_stride + p] = free_pages.back();
+            free_pages.pop_back();
+        }
+        seq_pages[seq] = need;
+        return upload_entries(seq, have, need - have);
+    }
+
+    void release_from(int seq, int keep_pages) {
+        for (int p = seq_pages[seq] - 1; p >= keep_pages; --p) {
+            free_pages.push_back(page_table[(size_t)seq * pt_stride + p]);
+            page_table[(size_t)seq * pt_stride + p] = -1;
+        }
+        seq_pages[seq] = std::min(seq_pages[seq], keep_pages);
+    }
+
+    int slot_of(int layer, int *slot) const {
+        if (!is_full_attention(layer)) return fail("layer %d is not a full-attention layer", layer);
+        if (layer / 4 >= n_slots) return fail("layer %d needs slot %d, cache has %d", layer, layer / 4, n_slots);
+        *slot = layer / 4;
+        return 0;
+    }
+};
+
+/* ======================================================================= */
+
+extern "C" {
+
+const char *q38_last_error(void) { return g_last_error.c_str(); }
+
+int q38_device_count(int *count) {
+    if (count == nullptr) return fail("count is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return 0;
+}
+
+int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
+    if (out == nullptr) return fail("out is NULL");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail("no HIP device available");
+    if (device < 0 || device >= n) return fail("device %d out of range (%d devices)", device, n);
+    std::unique_ptr<q38_ctx> ctx(new q38_ctx);
+    ctx->device = device;
+    Q38_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    Q38_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail("device %d is %s; this library is built for gfx950 only", device, prop.gcnArchName);
+    ctx->cu_count = prop.multiProcessorCount;
+    ctx->clock_khz = prop.clockRate;
+    ctx->lds_bytes = (int)prop.sharedMemPerBlock;
+    snprintf(ctx->name, sizeof(ctx->name), "%.200s (%.40s)", prop.name, prop.gcnArchName);
+    Q38_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+
+    const std::string dir = module_dir != nullptr ? std::string(module_dir) : library_dir();
+    const std::string p_decode = dir + "/attn_decode.hsaco";
+    const std::string p_gdn = dir + "/gdn.hsaco";
+    Q38_HIP(hipModuleLoad(&ctx->mod_decode, p_decode.c_str()));
+    Q38_HIP(hipModuleLoad(&ctx->mod_gdn, p_gdn.c_str()));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split, ctx->mod_decode, "q38_attn_decode_split"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "q38_attn_decode_merge"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_kv_copy, ctx->mod_decode, "q38_kv_copy"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_attn_pre, ctx->mod_decode, "q38_attn_pre"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_recurrent, ctx->mod_gdn, "q38_gdn_recurrent"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_pre, ctx->mod_gdn, "q38_gdn_pre"));
+    const std::string p_synth = dir + "/synth.hsaco";
+    Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
+    /* ops.rs:596: 1e7^(-2/64) in f32, computed once with the host's powf */
+    ctx->rope_theta_scale = powf(10000000.0f, -2.0f / 64.0f);
+    *out = ctx.release();
+    return 0;
+}
+
+int q38_ctx_destroy(q38_ctx *ctx) {
+    if (ctx == nullptr) return 0;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->work) (void)hipFree(ctx->work);
+    if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
+    if (ctx->mod_gdn) (void)hipModuleUnload(ctx->mod_gdn);
+    if (ctx->mod_synth) (void)hipModuleUnload(ctx->mod_synth);
+    for (hipEvent_t e : ctx->timer_events) (void)hipEventDestroy(e);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return 0;
+}
+
+void *q38_ctx_stream(q38_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int q38_sync(q38_ctx *ctx) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    Q38_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int q38_device_info(q38_ctx *ctx, int *cu_count, int *clock_khz, int *lds_bytes, char *name,
+                    size_t name_len) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    if (cu_count) *cu_count = ctx->cu_count;
+    if (clock_khz) *clock_khz = ctx->clock_khz;
+    if (lds_bytes) *lds_bytes = ctx->lds_bytes;
+    if (name && name_len) snprintf(name, name_len, "%s", ctx->name);
+    return 0;
+}
+
+int q38_alloc(q38_ctx *ctx, size_t bytes, void **d_ptr) {
+    if (ctx == nullptr || d_ptr == nullptr) return fail("NULL argument");
+    *d_ptr = nullptr;
+    Q38_HIP(hipMalloc(d_ptr, bytes ? bytes : 4));
+    return 0;
+}
+
+int q38_free(q38_ctx *ctx, void *d_ptr) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    if (d_ptr == nullptr) return 0;
+    Q38_HIP(hipStreamSynchronize(ctx->stream));
+    Q38_HIP(hipFree(d_ptr));
+    return 0;
+}
+
+int q38_upload(q38_ctx *ctx, void *d_dst, const void *src, size_t bytes) {
+    if (ctx == nullptr || d_dst == nullptr || src == nullptr) return fail("NULL argument");
+    Q38_HIP(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    Q38_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int q38_download(q38_ctx *ctx, void *dst, const void *d_src, size_t bytes) {
+    if (ctx == nullptr || dst == nullptr || d_src == nullptr) return fail("NULL argument");
+    Q38_HIP(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    Q38_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int q38_zero(q38_ctx *ctx, void *d_dst, size_t bytes) {
+    if (ctx == nullptr || d_dst == nullptr) return fail("NULL argument");
+    Q38_HIP(hipMemsetAsync(d_dst, 0, bytes, ctx->stream));
+    return 0;
+}
+
+int q38_event_create(q38_ctx *ctx, void **event) {
+    if (ctx == nullptr || event == nullptr) return fail("NULL argument");
+    hipEvent_t e;
+    Q38_HIP(hipEventCreate(&e));
+    *event = (void *)e;
+    return 0;
+}
+
+int q38_event_record(q38_ctx *ctx, void *event) {
+    if (ctx == nullptr || event == nullptr) return fail("NULL argument");
+    Q38_HIP(hipEventRecord((hipEvent_t)event, ctx->stream));
+    return 0;
+}
+
+int q38_event_elapsed_ms(void *start, void *stop, float *ms) {
+    if (start == nullptr || stop == nullptr || ms == nullptr) return fail("NULL argument");
+    Q38_HIP(hipEventSynchronize((hipEvent_t)stop));
+    Q38_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return 0;
+}
+
+int q38_event_destroy(void *event) {
+    if (event == nullptr) return 0;
+    Q38_HIP(hipEventDestroy((hipEvent_t)event));
+    return 0;
+}
+
+int q38_fill_normal(q38_ctx *ctx, float *d_out, size_t n, uint64_t seed, float sigma, float mean) {
+    if (ctx == nullptr || d_out == nullptr) return fail("NULL argument");
+    if (n == 0) return 0;
+    struct {
+        float *out;
+        uint64_t n;
+        uint64_t seed;
+        float sigma;
+        float mean;
+    } a = {d_out, (uint64_t)n, seed, sigma, mean};
+    const uint64_t pairs = ((uint64_t)n + 1) / 2;
+    const uint64_t blocks = (pairs + 255) / 256;
+    if (blocks > 0x7FFFFFFFull) return fail("fill of %zu elements is too large", n);
+    return ctx->launch(ctx->f_fill_normal, (unsigned)blocks, 1, 1, 256, &a);
+}
+
+int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launches) {
+    if (ctx == nullptr || kernel_name == nullptr) return fail("NULL argument");
+    if (max_launches < 1) return fail("max_launches must be positive");
+    hipFunction_t f = nullptr;
+    const std::string name(kernel_name);
+    if (name == "q38_attn_decode_split") f = ctx->f_decode_split;
+    else if (name == "q38_attn_decode_merge") f = ctx->f_decode_merge;
+    else if (name == "q38_kv_copy") f = ctx->f_kv_copy;
+    else if (name == "q38_attn_pre") f = ctx->f_attn_pre;
+    else if (name == "q38_gdn_recurrent") f = ctx->f_gdn_recurrent;
+    else if (name == "q38_gdn_pre") f = ctx->f_gdn_pre;
+    else return fail("unknown kernel %s", kernel_name);
+    while ((int)ctx->timer_events.size() < 2 * max_launches) {
+        hipEvent_t e;
+        Q38_HIP(hipEventCreate(&e));
+        ctx->timer_events.push_back(e);
+    }
+    ctx->timed = f;
+    ctx->timer_used = 0;
+    return 0;
+}
+
+int q38_kernel_timer_stop(q38_ctx *ctx, float *total_ms, int *launches) {
+    if (ctx == nullptr || total_ms == nullptr || launches == nullptr) return fail("NULL argument");
+    ctx->timed = nullptr;
+    Q38_HIP(hipStreamSynchronize(ctx->stream));
+    double total = 0.0;
+    for (int i = 0; i + 1 < ctx->timer_used; i += 2) {
+        float ms = 0.0f;
+        Q38_HIP(hipEventElapsedTime(&ms, ctx->timer_events[i], ctx->timer_events[i + 1]));
+        total += ms;
+    }
+    *total_ms = (float)total;
+    *launches = ctx->timer_used / 2;
+    ctx->timer_used = 0;
+    return 0;
+}
+
+/* ------------------------------------------------------------------ KV cache */
+
+int q38_kv_create(q38_ctx *ctx, int n_slots, int max_pages, int max_seqs, int max_tokens_per_seq,
+                  q38_kv **out) {
+    if (ctx == nullptr || out == nullptr) return fail("NULL argument");
+    *out = nullptr;
+    if (n_slots < 1 || n_slots > 17) return fail("n_slots %d outside 1..17", n_slots);
+    if (max_pages < 1 || max_seqs < 1 || max_tokens_per_seq < 1)
+        return fail("max_pages, max_seqs and max_tokens_per_seq must be positive");
+    std::unique_ptr<q38_kv> kv(new q38_kv);
+    kv->ctx = ctx;
+    kv->n_slots = n_slots;
+    kv->max_pages = max_pages;
+    kv->max_seqs = max_seqs;
+    kv->pt_stride = (max_tokens_per_seq + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS;
+    const size_t pool_bytes = (size_t)n_slots * max_pages * Q38_PAGE_FLOATS * sizeof(float);
+    Q38_HIP(hipSetDevice(ctx->device));
+    Q38_HIP(hipMalloc(&kv->kpool, pool_bytes));
+    if (hipMalloc(&kv->vpool, pool_bytes) != hipSuccess) {
+        (void)hipFree(kv->kpool);
+        return fail("cannot allocate %zu bytes for the V pool", pool_bytes);
+    }
+    /* zeroed once so that no page ever holds non-finite garbage */
+    Q38_HIP(hipMemsetAsync(kv->kpool, 0, pool_bytes, ctx->stream));
+    Q38_HIP(hipMemsetAsync(kv->vpool, 0, pool_bytes, ctx->stream));
+    const size_t pt_entries = (size_t)max_seqs * kv->pt_stride;
+    Q38_HIP(hipMalloc(&kv->d_page_table, pt_entries * sizeof(int32_t)));
+    Q38_HIP(hipMemsetAsync(kv->d_page_table, 0xFF, pt_entries * sizeof(int32_t), ctx->stream));
+    kv->page_table.assign(pt_entries, -1);
+    kv->free_pages.resize(max_pages);
+    for (int p = 0; p < max_pages; ++p) kv->free_pages[p] = max_pages - 1 - p; /* pop gives 0,1,2.. */
+    kv->seq_live.assign(max_seqs, 0);
+    kv->seq_pages.assign(max_seqs, 0);
+    kv->staging_len = std::max<size_t>(1 << 16, (size_t)kv->pt_stride * 4);
+    Q38_HIP(hipHostMalloc((void **)&kv->staging, kv->staging_len * sizeof(int32_t), hipHostMallocDefault));
+    Q38_HIP(hipStreamSynchronize(ctx->stream));
+    *out = kv.release();
+    return 0;
+}
+
+int q38_kv_destroy(q38_kv *kv) {
+    if (kv == nullptr) return 0;
+    (void)hipStreamSynchronize(kv->ctx->stream);
+    (void)hipFree(kv->kpool);
+    (void)hipFree(kv->vpool);
+    (void)hipFree(kv->d_page_table);
+    (void)hipHostFree(kv->staging);
+    delete kv;
+    return 0;
+}
+
+int q38_kv_free_pages(q38_kv *kv, int *n_free) {
+    if (kv == nullptr || n_free == nullptr) return fail("NULL argument");
+    *n_free = (int)kv->free_pages.size();
+    return 0;
+}
+
+int q38_seq_create(q38_kv *kv, int *seq) {
+    if (kv == nullptr || seq == nullptr) return fail("NULL argument");
+    for (int s = 0; s < kv->max_seqs; ++s) {
+        if (!kv->seq_live[s]) {
+            kv->seq_live[s] = 1;
+            kv->seq_pages[s] = 0;
+            *seq = s;
+            return 0;
+        }
+    }
+    return fail("all %d sequence slots are in use", kv->max_seqs);
+}
+
+int q38_seq_free(q38_kv *kv, int seq) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (kv->check_seq(seq)) return -1;
+    kv->release_from(seq, 0);
+    kv->seq_live[seq] = 0;
+    return 0;
+}
+
+int q38_seq_reset(q38_kv *kv, int seq) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (kv->check_seq(seq)) return -1;
+    kv->release_from(seq, 0);
+    return 0;
+}
+
+int q38_seq_truncate(q38_kv *kv, int seq, int n_tokens) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (kv->check_seq(seq)) return -1;
+    if (n_tokens < 0) return fail("negative token count");
+    kv->release_from(seq, (n_tokens + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS);
+    return 0;
+}
+
+int q38_seq_reserve(q38_kv *kv, int seq, int n_tokens) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (kv->check_seq(seq)) return -1;
+    return kv->reserve(seq, n_tokens);
+}
+
+int q38_seq_set_pages(q38_kv *kv, int seq, int n_pages, const int32_t *page_ids) {
+    if (kv == nullptr || (page_ids == nullptr && n_pages > 0)) return fail("NULL argument");
+    if (kv->check_seq(seq)) return -1;
+    if (n_pages < 0 || n_pages > kv->pt_stride)
+        return fail("n_pages %d outside 0..%d", n_pages, kv->pt_stride);
+    kv->release_from(seq, 0);
+    std::vector<char> is_free(kv->max_pages, 0);
+    for (int32_t p : kv->free_pages) is_free[p] = 1;
+    for (int i = 0; i < n_pages; ++i) {
+        const int32_t p = page_ids[i];
+        if (p < 0 || p >= kv->max_pages) return fail("page id %d outside the pool of %d", p, kv->max_pages);
+        if (!is_free[p]) return fail("page %d is not free (held, or listed twice)", p);
+        is_free[p] = 0;
+    }
+    std::vector<int32_t> rest;
+    rest.reserve(kv->free_pages.size());
+    for (int32_t p : kv->free_pages)
+        if (is_free[p]) rest.push_back(p);
+    kv->free_pages.swap(rest);
+    for (int i = 0; i < n_pages; ++i) kv->page_table[(size_t)seq * kv->pt_stride + i] = page_ids[i];
+    kv->seq_pages[seq] = n_pages;
+    return kv->upload_entries(seq, 0, n_pages);
+}
+
+int q38_seq_capacity(q38_kv *kv, int seq, int *n_tokens) {
+    if (kv == nullptr || n_tokens == nullptr) return fail("NULL argument");
+    if (kv->check_seq(seq)) return -1;
+    *n_tokens = kv->seq_pages[seq] * Q38_PAGE_TOKENS;
+    return 0;
+}
+
+static int kv_copy(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float *d_k, float *d_v,
+                   int to_pages) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (d_k == nullptr || d_v == nullptr) return fail("NULL row buffer");
+    if (kv->check_seq(seq)) return -1;
+    int slot = 0;
+    if (kv->slot_of(layer, &slot)) return -1;
+    if (pos0 < 0 || n_tokens < 0) return fail("negative position or count");
+    if (n_tokens == 0) return 0;
+    if (to_pages) {
+        if (kv->reserve(seq, pos0 + n_tokens)) return -1;
+    } else if (pos0 + n_tokens > kv->seq_pages[seq] * Q38_PAGE_TOKENS) {
+        return fail("positions %d..%d are not reserved", pos0, pos0 + n_tokens - 1);
+    }
+    q38_kv_copy_args a;
+    memset(&a, 0, sizeof(a));
+    a.kpool = kv->kslot(slot);
+    a.vpool = kv->vslot(slot);
+    a.page_table = kv->d_page_table;
+    a.k_rows = d_k;
+    a.v_rows = d_v;
+    a.pt_stride = kv->pt_stride;
+    a.seq = seq;
+    a.pos0 = pos0;
+    a.n_tokens = n_tokens;
+    a.to_pages = to_pages;
+    return kv->ctx->launch(kv->ctx->f_kv_copy, n_tokens, 2, 1, 256, &a);
+}
+
+int q38_kv_write(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, const float *d_k,
+                 const float *d_v) {
+    return kv_copy(kv, layer, seq, pos0, n_tokens, const_cast<float *>(d_k), const_cast<float *>(d_v), 1);
+}
+
+int q38_kv_read(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float *d_k, float *d_v) {
+    return kv_copy(kv, layer, seq, pos0, n_tokens, d_k, d_v, 0);
+}
+
+/* ------------------------------------------------------------ attention decode */
+
+namespace {
+
+/* Context split per workgroup.  Enough splits to give every CU about two
+ * workgroups of 4 waves, no fewer than 64 tokens (one page per wave) and no
+ * more than 1024; Q38_SPLIT_TOKENS overrides (rounded to a multiple of 64). */
+constexpr int kMaxSplitsPerSeq = 4096; /* LDS weights of the merge kernel */
+
+int choose_split_tokens(const q38_ctx *ctx, long total_tokens, long max_tokens) {
+    long split = 64;
+    const char *env = getenv("Q38_SPLIT_TOKENS");
+    if (env != nullptr && atoi(env) >= 64) {
+        split = (atoi(env) + 63) / 64 * 64;
+    } else {
+        const long target_wgs = 2L * std::max(ctx->cu_count, 1);
+        const long per = (total_tokens * Q38_ATTN_KV_HEADS + target_wgs - 1) / target_wgs;
+        while (split < per && split < 1024) split *= 2;
+    }
+    /* no sequence may need more splits than the merge kernel holds */
+    while ((max_tokens + split - 1) / split > kMaxSplitsPerSeq) split *= 2;
+    return (int)split;
+}
+
+int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                 const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate,
+                 float *d_out) {
+    q38_ctx *ctx = kv->ctx;
+    long total_tokens = 0, max_tokens = 0;
+    for (int b = 0; b < n_seq; ++b) {
+        total_tokens += positions[b] + 1;
+        max_tokens = std::max<long>(max_tokens, positions[b] + 1);
+    }
+    const int split_tokens = choose_split_tokens(ctx, total_tokens, max_tokens);
+
+    q38_decode_args a;
+    memset(&a, 0, sizeof(a));
+    a.kpool = kv->kslot(slot);
+    a.vpool = kv->vslot(slot);
+    a.page_table = kv->d_page_table;
+    a.q = d_q;
+    a.k_new = d_k_new;
+    a.v_new = d_v_new;
+    a.gate = d_gate;
+    a.out = d_out;
+    a.pt_stride = kv->pt_stride;
+    a.n_seq = n_seq;
+    a.split_tokens = split_tokens;
+    int total = 0;
+    bool any_multi = false;
+    for (int b = 0; b < n_seq; ++b) {
+        a.seq[b] = seq_ids[b];
+        a.pos[b] = positions[b];
+        a.split_base[b] = total;
+        const int ns = (positions[b] + split_tokens) / split_tokens; /* ceil((pos+1)/split) */
+        any_multi |= ns > 1;
+        total += ns;
+    }
+    a.split_base[n_seq] = total;
+    a.total_splits = total;
+
+    const size_t part_o_floats = (size_t)total * Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
+    const size_t part_ml_floats = (size_t)total * Q38_ATTN_HEADS * 2;
+    if (any_multi) {
+        if (ctx->ensure_work((part_o_floats + part_ml_floats) * sizeof(float))) return -1;
+        a.part_o = static_cast<float *>(ctx->work);
+        a.part_ml = a.part_o + part_o_floats;
+    }
+    if (ctx->launch(ctx->f_decode_split, total, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
+    if (any_multi) {
+        q38_merge_args m;
+        memset(&m, 0, sizeof(m));
+        m.part_o = a.part_o;
+        m.part_ml = a.part_ml;
+        m.gate = d_gate;
+        m.out = d_out;
+        m.n_seq = n_seq;
+        memcpy(m.split_base, a.split_base, sizeof(m.split_base));
+        if (ctx->launch(ctx->f_decode_merge, n_seq, Q38_ATTN_HEADS, 4, 256, &m)) return -1;
+    }
+    return 0;
+}
+
+int validate_decode(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                    bool appends, int *slot) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (kv->slot_of(layer, slot)) return -1;
+    if (n_seq < 0) return fail("negative n_seq");
+    if (n_seq > 0 && (seq_ids == nullptr || positions == nullptr)) return fail("NULL seq_ids/positions");
+    for (int b = 0; b < n_seq; ++b) {
+        if (kv->check_seq(seq_ids[b])) return -1;
+        if (positions[b] < 0) return fail("negative position %d", positions[b]);
+        if (positions[b] + 1 > kv->pt_stride * Q38_PAGE_TOKENS)
+            return fail("position %d is past the context limit %d", positions[b],
+                        kv->pt_stride * Q38_PAGE_TOKENS);
+        for (int c = 0; c < b; ++c)
+            if (seq_ids[c] == seq_ids[b] && appends) return fail("sequence %d appears twice", seq_ids[b]);
+    }
+    for (int b = 0; b < n_seq; ++b) {
+        const int s = seq_ids[b];
+        if (appends) {
+            if (kv->reserve(s, positions[b] + 1)) return -1;
+        } else if (positions[b] + 1 > kv->seq_pages[s] * Q38_PAGE_TOKENS) {
+            return fail("sequence %d: position %d is not reserved", s, positions[b]);
+        }
+    }
+    return 0;
+}
+
+}  // namespace
+
+int q38_attn_decode(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
+                    const int32_t *positions, const float *d_q, const float *d_k_new,
+                    const float *d_v_new, const float *d_gate, float *d_out) {
+    int slot = 0;
+    if ((d_k_new == nullptr) != (d_v_new == nullptr)) return fail("d_k_new and d_v_new go together");
+    if (validate_decode(kv, layer, n_seq, seq_ids, positions, d_k_new != nullptr, &slot)) return -1;
+    if (n_seq == 0) return 0;
+    if (d_q == nullptr || d_out == nullptr) return fail("NULL q/out");
+    for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
+        const int n = std::min(Q38_MAX_BATCH, n_seq - b0);
+        const size_t qoff = (size_t)b0 * Q38_ATTN_Q_DIM;
+        const size_t kvoff = (size_t)b0 * Q38_ATTN_KV_DIM;
+        if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, d_q + qoff,
+                         d_k_new ? d_k_new + kvoff : nullptr, d_v_new ? d_v_new + kvoff : nullptr,
+                         d_gate ? d_gate + qoff : nullptr, d_out + qoff))
+            return -1;
+    }
+    return 0;
+}
+
+int q38_attn_pre(q38_ctx *ctx, int n_tokens, int pos0, const float *d_q_norm, const float *d_k_norm,
+                 const float *d_q_and_gate, const float *d_key, float *d_q_out, float *d_gate_out,
+                 float *d_k_out) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    if (n_tokens < 0 || pos0 < 0) return fail("negative count or position");
+    if (n_tokens == 0) return 0;
+    if (!d_q_norm || !d_k_norm || !d_q_and_gate || !d_key || !d_q_out || !d_gate_out || !d_k_out)
+        return fail("NULL argument");
+    q38_attn_pre_args a;
+    memset(&a, 0, sizeof(a));
+    a.q_and_gate = d_q_and_gate;
+    a.key = d_key;
+    a.q_norm = d_q_norm;
+    a.k_norm = d_k_norm;
+    a.q_out = d_q_out;
+    a.gate_out = d_gate_out;
+    a.k_out = d_k_out;
+    a.pos0 = pos0;
+    a.n_tokens = n_tokens;
+    a.theta_scale = ctx->rope_theta_scale;
+    return ctx->launch(ctx->f_attn_pre, n_tokens, Q38_ATTN_HEADS + Q38_ATTN_KV_HEADS, 1, 64, &a);
+}
+
+int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
+                  const int32_t *positions, const float *d_q_norm, const float *d_k_norm,
+                  const float *d_q_and_gate, const float *d_key, const float *d_value,
+                  float *d_out) {
+    int slot = 0;
+    if (validate_decode(kv, layer, n_seq, seq_ids, positions, true, &slot)) return -1;
+    if (n_seq == 0) return 0;
+    if (!d_q_norm || !d_k_norm || !d_q_and_gate || !d_key || !d_value || !d_out) return fail("NULL argument");
+    q38_ctx *ctx = kv->ctx;
+    for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
+        const int n = std::min(Q38_MAX_BATCH, n_seq - b0);
+        /* workspace: q [n][6144] | gate [n][6144] | k [n][1024], after the
+         * region decode_chunk uses for its partials */
+        const size_t pre_floats = (size_t)n * (2 * Q38_ATTN_Q_DIM + Q38_ATTN_KV_DIM);
+        long total_tokens = 0, max_tokens = 0;
+        for (int b = 0; b < n; ++b) {
+            total_tokens += positions[b0 + b] + 1;
+            max_tokens = std::max<long>(max_tokens, positions[b0 + b] + 1);
+        }
+        const int split = choose_split_tokens(ctx, total_tokens, max_tokens);
+        size_t splits = 0;
+        for (int b = 0; b < n; ++b) splits += (positions[b0 + b] + split) / split;
+        const size_t part_floats = splits * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2);
+        if (ctx->ensure_work((part_floats + pre_floats) * sizeof(float))) return -1;
+        float *qo = static_cast<float *>(ctx->work) + part_floats;
+        float *go = qo + (size_t)n * Q38_ATTN_Q_DIM;
+        float *ko = go + (size_t)n * Q38_ATTN_Q_DIM;
+        /* positions differ per sequence: one pre launch per sequence keeps
+         * the kernel's position = pos0 + token contract */
+        for (int b = 0; b < n; ++b) {
+            if (q38_attn_pre(ctx, 1, positions[b0 + b], d_q_norm, d_k_norm,
+                             d_q_and_gate + (size_t)(b0 + b) * Q38_ATTN_QG_DIM,
+                             d_key + (size_t)(b0 + b) * Q38_ATTN_KV_DIM, qo + (size_t)b * Q38_ATTN_Q_DIM,
+                             go + (size_t)b * Q38_ATTN_Q_DIM, ko + (size_t)b * Q38_ATTN_KV_DIM))
+                return -1;
+        }
+        if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, qo, ko,
+                         d_value + (size_t)b0 * Q38_ATTN_KV_DIM, go,
+                         d_out + (size_t)b0 * Q38_ATTN_Q_DIM))
+            return -1;
+    }
+    return 0;
+}
+
+int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens, const float *d_q,
+                     const float *d_k, const float *d_v, const float *d_gate, float *d_out) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (n_tokens < 0 || base_pos < 0) return fail("negative count or position");
+    if (n_tokens == 0) return 0;
+    if (!d_q || !d_k || !d_v || !d_out) return fail("NULL argument");
+    if (q38_kv_write(kv, layer, seq, base_pos, n_tokens, d_k, d_v)) return -1;
+    int slot = 0;
+    if (kv->slot_of(layer, &slot)) return -1;
+    /* causal rows through the decode kernel, 64 query tokens per launch */
+    std::vector<int32_t> seqs(Q38_MAX_BATCH, seq), pos(Q38_MAX_BATCH);
+    for (int t0 = 0; t0 < n_tokens; t0 += Q38_MAX_BATCH) {
+        const int n = std::min(Q38_MAX_BATCH, n_tokens - t0);
+        for (int i = 0; i < n; ++i) pos[i] = base_pos + t0 + i;
+        const size_t off = (size_t)t0 * Q38_ATTN_Q_DIM;
+        if (decode_chunk(kv, slot, n, seqs.data(), pos.data(), d_q + off, nullptr, nullptr,
+                         d_gate ? d_gate + off : nullptr, d_out + off))
+            return -1;
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- DeltaNet */
+
+static int gdn_launch(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, int64_t state_stride,
+                      const float *d_q, const float *d_k, const float *d_v, const float *d_beta,
+                      const float *d_g, float *d_out, int q_stride, int v_stride, const float *d_z,
+                      const float *d_norm) {
+    q38_gdn_args a;
+    memset(&a, 0, sizeof(a));
+    a.state = d_state;
+    a.q = d_q;
+    a.k = d_k;
+    a.v = d_v;
+    a.beta = d_beta;
+    a.g = d_g;
+    a.out = d_out;
+    a.z = d_z;
+    a.norm_w = d_norm;
+    a.state_stride = state_stride;
+    a.q_stride = q_stride;
+    a.v_stride = v_stride;
+    a.n_tokens = n_tokens;
+    a.n_seq = n_seq;
+    return ctx->launch(ctx->f_gdn_recurrent, Q38_LIN_V_HEADS, n_seq, 1, 512, &a);
+}
+
+int q38_gdn_step(q38_ctx *ctx, int n_seq, float *d_state, int64_t state_stride, const float *d_q,
+                 const float *d_k, const float *d_v, const float *d_beta, const float *d_g,
+                 float *d_out) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    if (n_seq < 0) return fail("negative n_seq");
+    if (n_seq == 0) return 0;
+    if (!d_state || !d_q || !d_k || !d_v || !d_beta || !d_g || !d_out) return fail("NULL argument");
+    if (n_seq > 65535) return fail("n_seq %d above 65535", n_seq);
+    if (n_seq > 1 && state_stride < (int64_t)Q38_LIN_STATE_FLOATS)
+        return fail("state_stride %lld overlaps states", (long long)state_stride);
+    return gdn_launch(ctx, n_seq, 1, d_state, state_stride, d_q, d_k, d_v, d_beta, d_g, d_out,
+                      Q38_LIN_QK_DIM, Q38_LIN_V_DIM, nullptr, nullptr);
+}
+
+int q38_gdn_prefill(q38_ctx *ctx, float *d_state, int n_tokens, const float *d_q, const float *d_k,
+                    const float *d_v, const float *d_beta, const float *d_g, float *d_out) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    if (n_tokens < 0) return fail("negative n_tokens");
+    if (n_tokens == 0) return 0;
+    if (!d_state || !d_q || !d_k || !d_v || !d_beta || !d_g || !d_out) return fail("NULL argument");
+    return gdn_launch(ctx, 1, n_tokens, d_state, Q38_LIN_STATE_FLOATS, d_q, d_k, d_v, d_beta, d_g,
+                      d_out, Q38_LIN_QK_DIM, Q38_LIN_V_DIM, nullptr, nullptr);
+}
+
+int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weights *w,
+                    float *d_conv_state, float *d_delta_state, const float *d_qkv,
+                    const float *d_z, const float *d_beta, const float *d_alpha, float *d_out) {
+    if (ctx == nullptr || w == nullptr) return fail("NULL argument");
+    if (n_seq < 0 || n_tokens < 0) return fail("negative count");
+    if (n_seq == 0 || n_tokens == 0) return 0;
+    if (!w->d_conv_w || !w->d_dt || !w->d_a || !w->d_norm || !d_conv_state || !d_delta_state ||
+        !d_qkv || !d_z || !d_beta || !d_alpha || !d_out)
+        return fail("NULL argument");
+    if (n_seq > 65535) return fail("n_seq %d above 65535", n_seq);
+    const int n_chunks = (n_tokens + 63) / 64;
+    const size_t toks = (size_t)n_seq * n_tokens;
+    /* workspace: qkv after conv/SiLU/L2 | beta | g | conv state out */
+    const size_t conv_floats = (size_t)n_seq * Q38_LIN_QKV_DIM * 3;
+    const size_t need = toks * (Q38_LIN_QKV_DIM + 2 * Q38_LIN_V_HEADS) + (n_chunks > 1 ? conv_floats : 0);
+    if (ctx->ensure_work(need * sizeof(float))) return -1;
+    float *x = static_cast<float *>(ctx->work);
+    float *beta = x + toks * Q38_LIN_QKV_DIM;
+    float *g = beta + toks * Q38_LIN_V_HEADS;
+    float *conv_out = n_chunks > 1 ? g + toks * Q38_LIN_V_HEADS : d_conv_state;
+
+    q38_gdn_pre_args p;
+    memset(&p, 0, sizeof(p));
+    p.qkv_raw = d_qkv;
+    p.conv_w = w->d_conv_w;
+    p.conv_state_in = d_conv_state;
+    p.conv_state_out = conv_out;
+    p.qkv_out = x;
+    p.beta_raw = d_beta;
+    p.alpha_raw = d_alpha;
+    p.dt = w->d_dt;
+    p.a = w->d_a;
+    p.beta_out = beta;
+    p.g_out = g;
+    p.n_tokens = n_tokens;
+    p.n_seq = n_seq;
+    if (ctx->launch(ctx->f_gdn_pre, 81, n_chunks, n_seq, 128, &p)) return -1;
+    if (n_chunks > 1)
+        Q38_HIP(hipMemcpyAsync(d_conv_state, conv_out, conv_floats * sizeof(float),
+                               hipMemcpyDeviceToDevice, ctx->stream));
+    q38_gdn_args a;
+    memset(&a, 0, sizeof(a));
+    a.state = d_delta_state;
+    a.q = x;
+    a.k = x + Q38_LIN_QK_DIM;
+    a.v = x + 2 * Q38_LIN_QK_DIM;
+    a.beta = beta;
+    a.g = g;
+    a.out = d_out;
+    a.z = d_z;
+    a.norm_w = w->d_norm;
+    a.state_stride = Q38_LIN_STATE_FLOATS;
+    a.q_stride = Q38_LIN_QKV_DIM;
+    a.v_stride = Q38_LIN_QKV_DIM;
+    a.n_tokens = n_tokens;
+    a.n_seq = n_seq;
+    return ctx->launch(ctx->f_gdn_recurrent, Q38_LIN_V_HEADS, n_seq, 1, 512, &a);
+}
+
+}  /* extern "C" */

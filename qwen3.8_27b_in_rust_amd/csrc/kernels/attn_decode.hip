@@ -1,0 +1,429 @@
+/*
+ * Full-attention GQA decode over the paged KV cache (gfx950, wave64).
+ *
+ * Reference semantics: full_core, src/model/ops.rs:813-940 -- for every query
+ * head h (kv head j = h/6): scores q.k_p * 1/16 over positions 0..pos,
+ * softmax, probability-weighted sum of value rows, times sigmoid(gate).
+ *
+ * Design:
+ *  - grid (split, kv head): one workgroup streams one kv head's K and V rows
+ *    of one context split ONCE and serves all 6 query heads of the group from
+ *    registers (the reference re-reads each row once per query head);
+ *  - a half-wave (32 lanes) owns one token row: lane i holds dims 4i..4i+3 and
+ *    128+4i..128+4i+3, loaded as 128-bit vectors, so one row is two fully
+ *    coalesced 512-byte segments; the 256-long dot is 8 FMAs per lane plus a
+ *    DPP row reduction and one v_permlane16_swap;
+ *  - online softmax in base 2 (q is pre-scaled by log2(e)/16) with the running
+ *    max/sum per head; the split's 8 half-waves merge through LDS;
+ *  - a single split finishes the heads itself (output gate included);
+ *    several splits leave unnormalised partials for q38_attn_decode_merge.
+ */
+#include "q38_device.h"
+
+/* 1/sqrt(256) (ops.rs:869) times log2(e). */
+#define Q38_SCORE_LOG2 0.09016844005556021f
+
+namespace {
+
+struct DecodeState {
+    float m[Q38_ATTN_GROUP];
+    float l[Q38_ATTN_GROUP];
+    f32x4 o0[Q38_ATTN_GROUP];
+    f32x4 o1[Q38_ATTN_GROUP];
+};
+
+/* Where one half-wave reads its 4 rows of the half-page that holds the
+ * sequence's last position: the page rows, the new token's row for position
+ * `pos`, or -- past the end -- a row known to hold finite data (weight 0). */
+struct TailRows {
+    const float *k[4];
+    const float *v[4];
+    bool valid[4];
+};
+
+struct Rows {
+    f32x4 x0[4], x1[4];
+};
+
+/* Full half-page at element offset `base` of the pools: rows 2s+grp. */
+Q38_DEV void load_rows(Rows &r, const float *pool, size_t base, int lane_off) {
+    const float *p = pool + base + lane_off;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        r.x0[s] = q38_ld4_stream(p + 2 * s * Q38_ATTN_HEAD_DIM);
+        r.x1[s] = q38_ld4_stream(p + 2 * s * Q38_ATTN_HEAD_DIM + 128);
+    }
+}
+
+Q38_DEV size_t half_page_base(const int32_t *pt, int j, int tb) {
+    const int phys = pt[tb >> 4];
+    return ((size_t)phys * Q38_ATTN_KV_HEADS + j) * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM +
+           (size_t)(tb & 15) * Q38_ATTN_HEAD_DIM;
+}
+
+/* Scores of 4 rows for the 6 heads, online-softmax update, weighted V sum. */
+Q38_DEV void decode_rows(DecodeState &st, const f32x4 (&q0)[Q38_ATTN_GROUP],
+                         const f32x4 (&q1)[Q38_ATTN_GROUP], const Rows &K, const Rows &V,
+                         const bool (&valid)[4]) {
+    float sc[4][Q38_ATTN_GROUP];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+            float x = q38_dot4(q0[hh], K.x0[s], 0.0f);
+            x = q38_dot4(q1[hh], K.x1[s], x);
+            sc[s][hh] = valid[s] ? q38_sum32(x) : -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+        const float mx = fmaxf(fmaxf(sc[0][hh], sc[1][hh]), fmaxf(sc[2][hh], sc[3][hh]));
+        if (mx > st.m[hh]) {
+            const float f = q38_exp2(st.m[hh] - mx); /* 0 while m is -inf */
+            st.l[hh] *= f;
+            st.o0[hh] *= f;
+            st.o1[hh] *= f;
+            st.m[hh] = mx;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float p = valid[s] ? q38_exp2(sc[s][hh] - st.m[hh]) : 0.0f;
+            st.l[hh] += p;
+            st.o0[hh] = q38_fma4(p, V.x0[s], st.o0[hh]);
+            st.o1[hh] = q38_fma4(p, V.x1[s], st.o1[hh]);
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_decode_args a) {
+    __shared__ float red_o[4][Q38_ATTN_GROUP][Q38_ATTN_HEAD_DIM];
+    __shared__ float red_m[4][Q38_ATTN_GROUP];
+    __shared__ float red_l[4][Q38_ATTN_GROUP];
+
+    const int g = blockIdx.x;
+    const int j = blockIdx.y;
+    int b = 0;
+    while (b + 1 < a.n_seq && a.split_base[b + 1] <= g) ++b;
+    const int seq = a.seq[b];
+    const int pos = a.pos[b];
+    const int split = g - a.split_base[b];
+    const int nsplit = a.split_base[b + 1] - a.split_base[b];
+    const int t_begin = split * a.split_tokens;
+    const int t_end = min(pos + 1, t_begin + a.split_tokens);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int grp = lane >> 5;
+    const int li = lane & 31;
+    const int d0 = 4 * li;
+    const int d1 = 128 + 4 * li;
+
+    const int32_t *pt = a.page_table + (size_t)seq * a.pt_stride;
+    const float *k_new_row = nullptr;
+    const float *v_new_row = nullptr;
+    if (a.k_new != nullptr) {
+        k_new_row = a.k_new + (size_t)b * Q38_ATTN_KV_DIM + j * Q38_ATTN_HEAD_DIM;
+        v_new_row = a.v_new + (size_t)b * Q38_ATTN_KV_DIM + j * Q38_ATTN_HEAD_DIM;
+        /* KV append (ops.rs:858-866): the split that holds `pos` stores the row. */
+        if (pos >= t_begin && pos < t_end && wave == 0) {
+            const int phys = pt[pos >> 4];
+            const size_t row = ((size_t)phys * Q38_ATTN_KV_HEADS + j) * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM +
+                               (size_t)(pos & 15) * Q38_ATTN_HEAD_DIM;
+            q38_st4(a.kpool + row + 4 * lane, q38_ld4(k_new_row + 4 * lane));
+            q38_st4(a.vpool + row + 4 * lane, q38_ld4(v_new_row + 4 * lane));
+        }
+    }
+
+    const int n_tok = t_end - t_begin;
+    const int n_hp = (n_tok + 7) / 8;
+    /* every half-page is full except, in the split that holds `pos` (always
+     * the sequence's last position), the last one: that one is handled after
+     * the loop with per-row redirection */
+    const bool has_tail = t_end == pos + 1;
+    const int n_regular = has_tail ? n_hp - 1 : n_hp;
+    const int lane_off = grp * Q38_ATTN_HEAD_DIM + d0;
+    const bool all_valid[4] = {true, true, true, true};
+
+    /* software pipeline: the K rows of the next half-page are in flight
+     * while the current one is scored, and its V rows while the current one
+     * is accumulated */
+    Rows K, V;
+    if (wave < n_regular) {
+        const size_t base = half_page_base(pt, j, t_begin + wave * 8);
+        load_rows(K, a.kpool, base, lane_off);
+        load_rows(V, a.vpool, base, lane_off);
+    }
+
+    f32x4 q0[Q38_ATTN_GROUP], q1[Q38_ATTN_GROUP];
+    const float *qb = a.q + ((size_t)b * Q38_ATTN_HEADS + j * Q38_ATTN_GROUP) * Q38_ATTN_HEAD_DIM;
+#pragma unroll
+    for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+        q0[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d0) * Q38_SCORE_LOG2;
+        q1[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d1) * Q38_SCORE_LOG2;
+    }
+
+    DecodeState st;
+#pragma unroll
+    for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+        st.m[hh] = -INFINITY;
+        st.l[hh] = 0.0f;
+        st.o0[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+        st.o1[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    for (int hp = wave; hp < n_regular; hp += 4) {
+        const bool has_next = hp + 4 < n_regular;
+        size_t nbase = 0;
+        Rows Kn;
+        if (has_next) {
+            nbase = half_page_base(pt, j, t_begin + (hp + 4) * 8);
+            load_rows(Kn, a.kpool, nbase, lane_off);
+        }
+        decode_rows(st, q0, q1, K, V, all_valid);
+        if (has_next) {
+            load_rows(V, a.vpool, nbase, lane_off);
+            K = Kn;
+        }
+    }
+
+    if (has_tail && wave == (n_hp - 1) % 4) {
+        const int tb = t_begin + (n_hp - 1) * 8;
+        const size_t base = half_page_base(pt, j, tb);
+        TailRows tr;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int r = 2 * s + grp;
+            const int t = tb + r;
+            tr.valid[s] = t < t_end;
+            tr.k[s] = a.kpool + base + r * Q38_ATTN_HEAD_DIM;
+            tr.v[s] = a.vpool + base + r * Q38_ATTN_HEAD_DIM;
+            if (k_new_row != nullptr && (t == pos || !tr.valid[s])) {
+                tr.k[s] = k_new_row;
+                tr.v[s] = v_new_row;
+            } else if (!tr.valid[s]) {
+                tr.k[s] = a.kpool + base;
+                tr.v[s] = a.vpool + base;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            K.x0[s] = q38_ld4_stream(tr.k[s] + d0);
+            K.x1[s] = q38_ld4_stream(tr.k[s] + d1);
+            V.x0[s] = q38_ld4_stream(tr.v[s] + d0);
+            V.x1[s] = q38_ld4_stream(tr.v[s] + d1);
+        }
+        decode_rows(st, q0, q1, K, V, tr.valid);
+    }
+
+    /* merge the wave's two half-waves (lane i with lane i^32, same dims) */
+#pragma unroll
+    for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+        const q38_halves mh = q38_both_halves(st.m[hh]);
+        const float M = fmaxf(mh.a, mh.b);
+        const float fa = mh.a == -INFINITY ? 0.0f : q38_exp2(mh.a - M);
+        const float fb = mh.b == -INFINITY ? 0.0f : q38_exp2(mh.b - M);
+        const q38_halves lh = q38_both_halves(st.l[hh]);
+        const float L = lh.a * fa + lh.b * fb;
+        f32x4 o0, o1;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const q38_halves x0 = q38_both_halves(st.o0[hh][c]);
+            const q38_halves x1 = q38_both_halves(st.o1[hh][c]);
+            o0[c] = x0.a * fa + x0.b * fb;
+            o1[c] = x1.a * fa + x1.b * fb;
+        }
+        if (grp == 0) {
+            q38_st4(&red_o[wave][hh][d0], o0);
+            q38_st4(&red_o[wave][hh][d1], o1);
+        }
+        if (lane == 0) {
+            red_m[wave][hh] = M;
+            red_l[wave][hh] = L;
+        }
+    }
+    __syncthreads();
+
+    const int d = tid; /* one output dim per thread */
+#pragma unroll
+    for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][hh]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float mw = red_m[w][hh];
+            const float f = mw == -INFINITY ? 0.0f : q38_exp2(mw - M);
+            L += red_l[w][hh] * f;
+            O += red_o[w][hh][d] * f;
+        }
+        const int h = j * Q38_ATTN_GROUP + hh;
+        if (nsplit == 1) {
+            float r = O / L;
+            if (a.gate != nullptr) r *= q38_sigmoid(a.gate[(size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d]);
+            a.out[(size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d] = r;
+        } else {
+            a.part_o[((size_t)g * Q38_ATTN_HEADS + h) * Q38_ATTN_HEAD_DIM + d] = O;
+            if (d == 0) {
+                a.part_ml[((size_t)g * Q38_ATTN_HEADS + h) * 2 + 0] = M;
+                a.part_ml[((size_t)g * Q38_ATTN_HEADS + h) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+/* Combine the splits of each (sequence, head): rescale every partial to the
+ * common max, sum, normalise, gate.  grid (n_seq, 24, 4): z picks 64 of the
+ * 256 dims, so 96 workgroups share a sequence's merge.  Every load is issued
+ * without waiting on another: the (m, l) pairs go to LDS in one pass, then
+ * thread (sl, dl) sums splits sl, sl+16, ... of dims 4dl..4dl+3 with the loop
+ * unrolled so its loads are in flight together.  At most Q38_MAX_SPLITS
+ * splits per sequence (the host sizes splits so). */
+#define Q38_MAX_SPLITS 4096
+extern "C" __global__ __launch_bounds__(256) void q38_attn_decode_merge(q38_merge_args a) {
+    __shared__ float w_lds[Q38_MAX_SPLITS];
+    __shared__ f32x4 red[16][16];
+    __shared__ float red_s[4][2];
+    const int b = blockIdx.x;
+    const int h = blockIdx.y;
+    const int dq = blockIdx.z;
+    const int base = a.split_base[b];
+    const int n = a.split_base[b + 1] - base;
+    if (n <= 1) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    float M = -INFINITY;
+    for (int s = tid; s < n; s += 256) {
+        const float m = a.part_ml[((size_t)(base + s) * Q38_ATTN_HEADS + h) * 2];
+        w_lds[s] = m;
+        M = fmaxf(M, m);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) red_s[wave][0] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red_s[0][0], red_s[1][0]), fmaxf(red_s[2][0], red_s[3][0]));
+    float L = 0.0f;
+    for (int s = tid; s < n; s += 256) {
+        const float w = q38_exp2(w_lds[s] - M);
+        w_lds[s] = w;
+        L += w * a.part_ml[((size_t)(base + s) * Q38_ATTN_HEADS + h) * 2 + 1];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
+    if (lane == 0) red_s[wave][1] = L;
+    __syncthreads();
+
+    const int dl = tid & 15;
+    const int sl = tid >> 4;
+    const int d = dq * 64 + 4 * dl;
+    const float *po = a.part_o + ((size_t)base * Q38_ATTN_HEADS + h) * Q38_ATTN_HEAD_DIM + d;
+    const size_t step = (size_t)Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int s = sl; s < n; s += 16) acc = q38_fma4(w_lds[s], q38_ld4(po + (size_t)s * step), acc);
+    red[sl][dl] = acc;
+    __syncthreads();
+    if (sl == 0) {
+        f32x4 o = red[0][dl];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) o += red[i][dl];
+        const float Lt = red_s[0][1] + red_s[1][1] + red_s[2][1] + red_s[3][1];
+        f32x4 r = o / Lt;
+        const size_t off = (size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d;
+        if (a.gate != nullptr) {
+            const f32x4 gt = q38_ld4(a.gate + off);
+            r.x *= q38_sigmoid(gt.x);
+            r.y *= q38_sigmoid(gt.y);
+            r.z *= q38_sigmoid(gt.z);
+            r.w *= q38_sigmoid(gt.w);
+        }
+        q38_st4(a.out + off, r);
+    }
+}
+
+/* Rows <-> pages.  grid (n_tokens, 2), 256 threads x float4 = one 1024-float row. */
+extern "C" __global__ __launch_bounds__(256) void q38_kv_copy(q38_kv_copy_args a) {
+    const int t = blockIdx.x;
+    const int which = blockIdx.y;
+    const int p = a.pos0 + t;
+    const int phys = a.page_table[(size_t)a.seq * a.pt_stride + (p >> 4)];
+    float *pool = which ? a.vpool : a.kpool;
+    float *rows = which ? a.v_rows : a.k_rows;
+    const int e = 4 * threadIdx.x;
+    const int head = e >> 8;
+    const int d = e & 255;
+    float *page_ptr = pool + ((size_t)phys * Q38_ATTN_KV_HEADS + head) * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM +
+                      (size_t)(p & 15) * Q38_ATTN_HEAD_DIM + d;
+    float *row_ptr = rows + (size_t)t * Q38_ATTN_KV_DIM + e;
+    if (a.to_pages)
+        q38_st4(page_ptr, q38_ld4(row_ptr));
+    else
+        q38_st4(row_ptr, q38_ld4(page_ptr));
+}
+
+/* q/gate split + q RMSNorm (ops.rs:832-843), k RMSNorm (ops.rs:844-850) and
+ * RoPE on lanes (p, p+32), p < 32 (ops.rs:595-610, applied :851-856).
+ * grid (n_tokens, 28), one wave per head, lane i holds dims 4i..4i+3. */
+extern "C" __global__ __launch_bounds__(64) void q38_attn_pre(q38_attn_pre_args a) {
+    const int t = blockIdx.x;
+    const int hd = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int position = a.positions_dev != nullptr ? a.positions_dev[t] : a.pos0 + t;
+    const bool is_q = hd < Q38_ATTN_HEADS;
+    const float *src;
+    const float *w;
+    float *dst;
+    if (is_q) {
+        src = a.q_and_gate + ((size_t)t * Q38_ATTN_HEADS + hd) * 2 * Q38_ATTN_HEAD_DIM;
+        w = a.q_norm;
+        dst = a.q_out + ((size_t)t * Q38_ATTN_HEADS + hd) * Q38_ATTN_HEAD_DIM;
+        q38_st4(a.gate_out + ((size_t)t * Q38_ATTN_HEADS + hd) * Q38_ATTN_HEAD_DIM + 4 * lane,
+                q38_ld4(src + Q38_ATTN_HEAD_DIM + 4 * lane));
+    } else {
+        const int kh = hd - Q38_ATTN_HEADS;
+        src = a.key + ((size_t)t * Q38_ATTN_KV_HEADS + kh) * Q38_ATTN_HEAD_DIM;
+        w = a.k_norm;
+        dst = a.k_out + ((size_t)t * Q38_ATTN_KV_HEADS + kh) * Q38_ATTN_HEAD_DIM;
+    }
+    f32x4 x = q38_ld4(src + 4 * lane);
+    /* rms_scale (ops.rs:476-483): every f32 square is exact in f64, so the
+     * f64 sum rounds to the same f32 mean in any order */
+    double ss = (double)x.x * (double)x.x + (double)x.y * (double)x.y + (double)x.z * (double)x.z +
+                (double)x.w * (double)x.w;
+    ss = q38_wave_sum_f64(ss);
+    const float mean = (float)(ss / (double)Q38_ATTN_HEAD_DIM);
+    const float scale = 1.0f / sqrtf(mean + 1e-6f);
+    const f32x4 wv = q38_ld4(w + 4 * lane);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[c] = x[c] * scale * wv[c];
+
+    /* RoPE: lanes 0..7 hold x0 = dims 0..31, lanes 8..15 hold x1 = dims 32..63 */
+    f32x4 partner;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) partner[c] = __shfl_xor(x[c], 8, 64);
+    if (lane < 16) {
+        const int p0 = 4 * (lane & 7);
+        float theta = (float)position;
+        for (int i = 0; i < p0; ++i) theta *= a.theta_scale;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float cosine = cosf(theta);
+            const float sine = sinf(theta);
+            if (lane < 8) {
+                const float x0 = x[c], x1 = partner[c];
+                x[c] = x0 * cosine - x1 * sine;
+            } else {
+                const float x0 = partner[c], x1 = x[c];
+                x[c] = x0 * sine + x1 * cosine;
+            }
+            theta *= a.theta_scale;
+        }
+    }
+    q38_st4(dst + 4 * lane, x);
+}

@@ -1,0 +1,36 @@
+/*
+ * Seeded N(mean, sigma^2) fill on the device, for benchmark inputs of many
+ * gigabytes.  Same stream as the host generator (synth.py): SplitMix64 word i
+ * of `seed`, the top 53 bits made a double in (0, 1], Box-Muller over word
+ * pairs (2j, 2j+1) in f64, rounded once to f32.
+ */
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+__device__ __forceinline__ double q38_unit(uint64_t seed, uint64_t idx) {
+    uint64_t z = seed + (idx + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z = z ^ (z >> 31);
+    return ((double)(z >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+}
+
+typedef struct {
+    float *out;
+    uint64_t n;
+    uint64_t seed;
+    float sigma;
+    float mean;
+} q38_fill_args;
+
+extern "C" __global__ __launch_bounds__(256) void q38_fill_normal(q38_fill_args a) {
+    const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x; /* pair index */
+    const uint64_t i0 = 2 * j;
+    if (i0 >= a.n) return;
+    const double u1 = q38_unit(a.seed, 2 * j);
+    const double u2 = q38_unit(a.seed, 2 * j + 1);
+    const double r = sqrt(-2.0 * log(u1));
+    const double t = (2.0 * 3.141592653589793) * u2;
+    a.out[i0] = (float)(r * cos(t) * (double)a.sigma + (double)a.mean);
+    if (i0 + 1 < a.n) a.out[i0 + 1] = (float)(r * sin(t) * (double)a.sigma + (double)a.mean);
+}

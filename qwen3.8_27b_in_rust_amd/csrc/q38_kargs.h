@@ -1,0 +1,141 @@
+/*
+ * Kernel argument blocks shared by the host launcher (g++) and the gfx950
+ * code objects (hipcc --genco).  Plain C structs of pointers and 32-bit
+ * integers so both compilers lay them out identically; each kernel takes its
+ * block by value (it travels in the kernarg segment, so per-call metadata
+ * such as sequence ids and positions needs no host-to-device copy).
+ *
+ * Shapes are the model's compile-time constants (reference
+ * src/model/mod.rs:13-24).
+ */
+#ifndef Q38_KARGS_H
+#define Q38_KARGS_H
+
+#include <stdint.h>
+
+#define Q38_ATTN_HEADS 24
+#define Q38_ATTN_KV_HEADS 4
+#define Q38_ATTN_GROUP 6 /* query heads per kv head: heads 6j..6j+5 read kv head j */
+#define Q38_ATTN_HEAD_DIM 256
+#define Q38_ATTN_Q_DIM 6144
+#define Q38_ATTN_QG_DIM 12288
+#define Q38_ATTN_KV_DIM 1024
+#define Q38_PAGE_TOKENS 16
+/* one page of one layer: [4 kv heads][16 tokens][256] floats, K and V pools apart */
+#define Q38_PAGE_FLOATS (Q38_ATTN_KV_HEADS * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM)
+
+#define Q38_LIN_QK_HEADS 16
+#define Q38_LIN_V_HEADS 48
+#define Q38_LIN_HEAD_DIM 128
+#define Q38_LIN_QK_DIM 2048
+#define Q38_LIN_V_DIM 6144
+#define Q38_LIN_QKV_DIM 10240
+#define Q38_LIN_STATE_FLOATS (Q38_LIN_V_HEADS * Q38_LIN_HEAD_DIM * Q38_LIN_HEAD_DIM)
+
+#define Q38_MAX_BATCH 64 /* sequences per decode launch */
+
+/* Split-K paged decode: grid (total_splits, 4 kv heads). */
+typedef struct {
+    float *kpool;              /* this layer's K pages: [max_pages][4][16][256] */
+    float *vpool;              /* this layer's V pages */
+    const int32_t *page_table; /* [max_seqs][pt_stride] physical page ids */
+    const float *q;            /* [n_seq][24][256], post-norm, post-RoPE */
+    const float *k_new;        /* [n_seq][1024] appended at pos[b] first, or NULL */
+    const float *v_new;        /* [n_seq][1024] or NULL */
+    const float *gate;         /* [n_seq][24][256] output gate logits, or NULL */
+    float *out;                /* [n_seq][24][256] */
+    float *part_o;             /* [total_splits][24][256] unnormalised partial outputs */
+    float *part_ml;            /* [total_splits][24][2]  (running max in log2 units, sum) */
+    int32_t pt_stride;
+    int32_t n_seq;
+    int32_t split_tokens; /* multiple of 64 */
+    int32_t total_splits;
+    int32_t seq[Q38_MAX_BATCH];
+    int32_t pos[Q38_MAX_BATCH]; /* attend over positions 0..pos inclusive */
+    int32_t split_base[Q38_MAX_BATCH + 1];
+} q38_decode_args;
+
+/* Copy token rows between [n][1024] arrays and a sequence's pages.
+ * grid (n_tokens, 2): y = 0 moves K, y = 1 moves V. */
+typedef struct {
+    float *kpool;
+    float *vpool;
+    const int32_t *page_table;
+    float *k_rows; /* [n][1024] */
+    float *v_rows;
+    int32_t pt_stride;
+    int32_t seq;
+    int32_t pos0;
+    int32_t n_tokens;
+    int32_t to_pages; /* 1: rows -> pages (append), 0: pages -> rows (gather) */
+    int32_t pad_;
+} q38_kv_copy_args;
+
+/* q/gate split, q and k RMSNorm, RoPE.  grid (n_tokens, 28): y < 24 is a
+ * query head, y >= 24 a kv head. */
+typedef struct {
+    const float *q_and_gate; /* [n][24][512] head-interleaved q | gate */
+    const float *key;        /* [n][4][256] raw */
+    const float *q_norm;     /* [256] */
+    const float *k_norm;     /* [256] */
+    float *q_out;            /* [n][24][256] */
+    float *gate_out;         /* [n][24][256] */
+    float *k_out;            /* [n][4][256] */
+    const int32_t *positions_dev; /* [n] or NULL: then position = pos0 + token */
+    int32_t pos0;
+    int32_t n_tokens;
+    float theta_scale; /* 1e7^(-2/64) in f32 */
+    int32_t pad_;
+} q38_attn_pre_args;
+
+/* Gated-DeltaNet recurrence over n_tokens consecutive tokens of each of
+ * n_seq independent states.  grid (48 value heads, n_seq), 512 threads;
+ * the head's 128x128 state stays in registers for all the tokens. */
+typedef struct {
+    float *state;      /* seq s at state + s*state_stride: [48][128][128] */
+    const float *q;    /* [(s*T + t)*q_stride + kh*128 ...] */
+    const float *k;
+    const float *v;    /* [(s*T + t)*v_stride + vh*128 ...] */
+    const float *beta; /* [(s*T + t)*48 + vh], post-sigmoid */
+    const float *g;    /* log-decay, same layout */
+    float *out;        /* [(s*T + t)*6144 + vh*128 + c] */
+    const float *z;        /* post: [(s*T + t)*6144 ...] gate of the gated RMSNorm, or NULL */
+    const float *norm_w;   /* post: [128] */
+    int64_t state_stride;
+    int32_t q_stride; /* floats between consecutive tokens' q (and k) */
+    int32_t v_stride;
+    int32_t n_tokens;
+    int32_t n_seq;
+} q38_gdn_args;
+
+/* conv1d(k=4) with state shift, SiLU, per-head L2 norm of q and k, and the
+ * beta / decay gates, for n_tokens consecutive tokens of n_seq sequences.
+ * grid (81, n_seq): x < 80 is a 128-channel group, x == 80 the gates. */
+typedef struct {
+    const float *qkv_raw;   /* [(s*T + t)*10240] */
+    const float *conv_w;    /* [10240][4] */
+    const float *conv_state_in;  /* seq s at + s*30720: [10240][3] */
+    float *conv_state_out;       /* may equal conv_state_in when T == 1 */
+    float *qkv_out;         /* [(s*T + t)*10240]: q | k | v after conv, SiLU, L2 */
+    const float *beta_raw;  /* [(s*T + t)*48] */
+    const float *alpha_raw;
+    const float *dt;        /* [48] */
+    const float *a;         /* [48] */
+    float *beta_out;        /* sigmoid(beta) */
+    float *g_out;           /* a * softplus(alpha + dt) */
+    int32_t n_tokens;
+    int32_t n_seq;
+} q38_gdn_pre_args;
+
+/* Merge of split-K partials.  grid (n_seq, 24). */
+typedef struct {
+    const float *part_o;
+    const float *part_ml;
+    const float *gate;
+    float *out;
+    int32_t n_seq;
+    int32_t pad_;
+    int32_t split_base[Q38_MAX_BATCH + 1];
+} q38_merge_args;
+
+#endif

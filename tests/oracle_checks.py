@@ -1,0 +1,292 @@
+"""Checks that pin the CPU restatement (oracle/) of the reference's attention
+path.  Each check returns None when it holds and a message when it fails, so
+the same list runs against the real restatement (tests/test_oracle.py) and
+against builds with a planted mistake (tests/test_oracle_mutants.py), each of
+which must be rejected by at least one check.
+
+Three kinds of evidence, none of which retypes the restatement's formulas:
+  - golden fixtures (tests/golden/attention_path.npz) written by an
+    independent float64 numpy formulation (tests/golden/make_fixtures.py);
+  - closed forms and invariants that the mathematics fixes (a single position
+    returns v; identical keys average v; beta = 0 is pure decay; the delta
+    rule stores v under k; RMSNorm/L2 norms; RoPE at position 0 is the
+    identity and preserves pair norms);
+  - the reference's own contract for its dispatch: serial and parallel runs
+    agree bit for bit (the pattern of src/kernel/tensor.rs:791-926).
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+FIXTURE = os.path.join(HERE, "golden", "attention_path.npz")
+
+
+def _fx():
+    return np.load(FIXTURE, allow_pickle=False)
+
+
+def _close(got, want, atol, rtol=0.0, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    bad = err > atol + rtol * np.abs(want)
+    if np.any(~np.isfinite(got)) or np.any(bad):
+        return f"{what}: max err {np.nanmax(err):.3e} (atol {atol}, rtol {rtol})"
+    return None
+
+
+# ------------------------------------------------------------------ fixtures
+def check_generator(ref, synth):
+    f = _fx()
+    seed = int(f["gen_seed"][0])
+    if not np.array_equal(synth.splitmix64(seed, 0, 8), f["gen_words"]):
+        return "SplitMix64 words differ from the fixture"
+    return _close(synth.normal(seed, 8), f["gen_normals"], 0.0, 1e-7, "Box-Muller normals")
+
+
+def check_attention_fixture(ref, synth):
+    f = _fx()
+    P = 256
+    q = synth.normal(0x51333801, 6144)
+    K = synth.normal(0x51333802, P * 1024).reshape(P, 1024)
+    V = synth.normal(0x51333803, P * 1024).reshape(P, 1024)
+    G = synth.normal(0x51333804, 6144)
+    return (_close(ref.attn_heads(q, K, V), f["attn256_nogate"], 2e-6, 0, "attention 256, no gate")
+            or _close(ref.attn_heads(q, K, V, gate=G), f["attn256_gate"], 2e-6, 0, "attention 256, gate"))
+
+
+def check_full_core_fixture(ref, synth):
+    f = _fx()
+    pos, ctx_len, layer = 37, 40, 7
+    qn = synth.normal(0x51333811, 256, sigma=0.2, mean=1.0)
+    kn = synth.normal(0x51333812, 256, sigma=0.2, mean=1.0)
+    qg = synth.normal(0x51333813, 12288)
+    key = synth.normal(0x51333814, 1024)
+    val = synth.normal(0x51333815, 1024)
+    kc = np.zeros(2 * ctx_len * 1024, np.float32)
+    vc = np.zeros(2 * ctx_len * 1024, np.float32)
+    kc[ctx_len * 1024: ctx_len * 1024 + pos * 1024] = synth.normal(0x51333816, pos * 1024)
+    vc[ctx_len * 1024: ctx_len * 1024 + pos * 1024] = synth.normal(0x51333817, pos * 1024)
+    out, k = ref.full_core(qn, kn, qg, key, val, kc, vc, ctx_len, pos, layer)
+    row = (ctx_len + pos) * 1024
+    if not np.array_equal(kc[row:row + 1024], k) or not np.array_equal(vc[row:row + 1024], val):
+        return "full_core did not append k/v at slot layer/4, row pos"
+    return (_close(k, f["full_core37_k"], 1e-5, 0, "full_core k after norm+RoPE")
+            or _close(out, f["full_core37"], 2e-6, 0, "full_core output"))
+
+
+def check_full_core_bounds(ref, synth):
+    """The cache-row bounds check of ops.rs:860-864 returns Err(-1)."""
+    kc = np.zeros(4 * 1024, np.float32)
+    try:
+        ref.full_core(np.ones(256, np.float32), np.ones(256, np.float32), np.ones(12288, np.float32),
+                      np.ones(1024, np.float32), np.ones(1024, np.float32), kc, kc.copy(), 4, 4, 3)
+    except ValueError:
+        return None
+    return "position == context_length was accepted"
+
+
+def check_rope_fixture(ref, synth):
+    f = _fx()
+    x = synth.normal(0x51333821, 512)
+    for p in (0, 1, 1000, 131071):
+        msg = _close(ref.rope(x, 2, p), f[f"rope_{p}"], 2e-6, 1e-6, f"rope at {p}")
+        if msg:
+            return msg
+    return None
+
+
+def check_softplus_fixture(ref, synth):
+    f = _fx()
+    got = [ref.scalar_fn("softplus", x) for x in f["softplus_in"]]
+    return _close(got, f["softplus"], 1e-6, 1e-6, "softplus")
+
+
+def check_rms_fixture(ref, synth):
+    f = _fx()
+    v = synth.normal(0x51333822, 256)
+    return _close([ref.rms_scale(v)], f["rms_scale_256"], 0, 1e-6, "rms_scale")
+
+
+def check_gdn_fixture(ref, synth):
+    f = _fx()
+    S = synth.normal(0x51333831, 48 * 128 * 128, sigma=0.02)
+    gen = synth.GdnStepInputs(0x51333832)
+    outs = []
+    for t in range(64):
+        outs.append(ref.gdn_heads(S, *gen.step(t), threads=4))
+    idx = f["gdn64_sample_idx"]
+    scale = np.max(np.abs(f["gdn64_state_sample"]))
+    return (_close(S[idx], f["gdn64_state_sample"], 1e-5 * scale, 0, "gdn state after 64 steps")
+            or _close((S.astype(np.float64).reshape(48, -1) ** 2).sum(1), f["gdn64_state_head_sumsq"], 0, 1e-4,
+                      "gdn per-head state energy")
+            or _close(outs[-1], f["gdn64_out_last"], 1e-5, 0, "gdn last output")
+            or _close(np.stack([o[:128] for o in outs]), f["gdn64_out_head0"], 1e-5, 0, "gdn head 0 outputs")
+            or _close(np.stack([o[17 * 128:18 * 128] for o in outs]), f["gdn64_out_head17"], 1e-5, 0,
+                      "gdn head 17 outputs"))
+
+
+def check_linear_core_fixture(ref, synth):
+    f = _fx()
+    conv_w = synth.normal(0x51333841, 10240 * 4, sigma=0.5)
+    dt = synth.normal(0x51333842, 48)
+    a = -np.abs(synth.normal(0x51333843, 48))
+    norm = synth.normal(0x51333844, 128, sigma=0.1, mean=1.0)
+    cs = synth.normal(0x51333845, 10240 * 3)
+    S = synth.normal(0x51333846, 48 * 128 * 128, sigma=0.02)
+    raw = []
+    for t in range(4):
+        qkv = synth.normal(0x51333850 + t, 10240)
+        raw.append(qkv)
+        o = ref.linear_core(conv_w, dt, a, norm, cs, S, qkv, synth.normal(0x51333860 + t, 6144),
+                            synth.normal(0x51333870 + t, 48), synth.normal(0x51333880 + t, 48))
+        msg = _close(o, f["linear4_out"][t], 2e-5, 1e-5, f"linear_core output, token {t}")
+        if msg:
+            return msg
+    # the conv state holds the last three raw inputs, channel-major (closed form)
+    want_cs = np.stack([raw[1], raw[2], raw[3]], axis=1).reshape(-1)
+    if not np.array_equal(cs, want_cs):
+        return "conv state is not the last three raw inputs"
+    scale = np.max(np.abs(f["linear4_state_sample"]))
+    return _close(S[f["gdn64_sample_idx"]], f["linear4_state_sample"], 1e-5 * scale, 0, "linear_core state")
+
+
+# -------------------------------------------------------------- closed forms
+def check_single_position(ref, synth):
+    """One position: softmax weight 1, so o == v exactly (ops.rs:905-913)."""
+    q = synth.normal(1, 6144)
+    K = synth.normal(2, 1024).reshape(1, 1024)
+    V = synth.normal(3, 1024).reshape(1, 1024)
+    o = ref.attn_heads(q, K, V)
+    want = np.repeat(V.reshape(4, 256), 6, axis=0)
+    return None if np.array_equal(o, want) else "single position does not return v"
+
+
+def check_identical_keys(ref, synth):
+    """Identical keys: uniform weights, o = mean of the value rows."""
+    P = 50
+    q = synth.normal(4, 6144)
+    K = np.tile(synth.normal(5, 1024), (P, 1))
+    V = synth.normal(6, P * 1024).reshape(P, 1024)
+    o = ref.attn_heads(q, K, V)
+    want = np.repeat(V.astype(np.float64).mean(0).reshape(4, 256), 6, axis=0)
+    return _close(o, want, 2e-6, 0, "identical keys")
+
+
+def check_gqa_grouping(ref, synth):
+    """Query heads 6j..6j+5 read kv head j: equal q rows give equal outputs,
+    and permuting kv head j's rows changes exactly heads 6j..6j+5."""
+    P = 40
+    q1 = synth.normal(7, 256)
+    q = np.tile(q1, 24)
+    K = synth.normal(8, P * 1024).reshape(P, 1024)
+    V = synth.normal(9, P * 1024).reshape(P, 1024)
+    o = ref.attn_heads(q, K, V)
+    for j in range(4):
+        if not all(np.array_equal(o[6 * j], o[6 * j + i]) for i in range(6)):
+            return f"heads of group {j} differ"
+    K2 = K.copy()
+    K2[:, 256:512] = K2[::-1, 256:512]  # change kv head 1 only
+    o2 = ref.attn_heads(q, K2, V)
+    changed = [h for h in range(24) if not np.array_equal(o[h], o2[h])]
+    return None if changed == list(range(6, 12)) else f"changing kv head 1 changed heads {changed}"
+
+
+def check_position_permutation(ref, synth):
+    P = 64
+    q = synth.normal(10, 6144)
+    K = synth.normal(11, P * 1024).reshape(P, 1024)
+    V = synth.normal(12, P * 1024).reshape(P, 1024)
+    perm = np.random.default_rng(3).permutation(P)
+    return _close(ref.attn_heads(q, K[perm], V[perm]), ref.attn_heads(q, K, V), 2e-6, 0, "position permutation")
+
+
+def check_rope_identities(ref, synth):
+    x = synth.normal(13, 24 * 256)
+    if not np.array_equal(ref.rope(x, 24, 0)[:64], x[:64]):
+        # theta_p = 0 for every pair at position 0: cos 1, sin 0
+        return "RoPE at position 0 is not the identity"
+    y = ref.rope(x, 24, 5000).reshape(24, 256)
+    xr = x.reshape(24, 256)
+    if not np.array_equal(y[:, 64:], xr[:, 64:]):
+        return "RoPE touched lanes 64..255"
+    n0 = np.hypot(xr[:, :32], xr[:, 32:64])
+    n1 = np.hypot(y[:, :32], y[:, 32:64])
+    return _close(n1, n0, 1e-5, 1e-6, "RoPE pair norms")
+
+
+def check_norms(ref, synth):
+    x = synth.normal(14, 256)
+    w = synth.normal(15, 256)
+    want = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * w
+    msg = _close(ref.rmsnorm(x, w), want, 1e-6, 1e-6, "rmsnorm closed form")
+    if msg:
+        return msg
+    y = ref.l2norm(x)
+    if abs(np.linalg.norm(y.astype(np.float64)) - 1.0) > 1e-6:
+        return "l2norm result is not unit length"
+    z = ref.l2norm(np.zeros(128, np.float32))
+    return None if np.all(z == 0) else "l2norm of zero is not zero (floor 1e-6 missing)"
+
+
+def check_gdn_beta_zero(ref, synth):
+    """beta = 0: S_t = exp(g) S_{t-1}, o = S_t q / sqrt(128)."""
+    S0 = synth.normal(16, 48 * 128 * 128, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(17).step(0)
+    S = S0.copy()
+    o = ref.gdn_heads(S, q, k, v, np.zeros_like(beta), g)
+    want_S = S0.reshape(48, 128, 128).astype(np.float64) * np.exp(g.astype(np.float64))[:, None, None]
+    qh = q.reshape(16, 128)[np.arange(48) % 16].astype(np.float64)
+    want_o = np.einsum("hcd,hd->hc", want_S, qh) / np.sqrt(128.0)
+    return (_close(S.reshape(48, 128, 128), want_S, 1e-8, 1e-6, "beta=0 state")
+            or _close(o.reshape(48, 128), want_o, 1e-6, 0, "beta=0 output"))
+
+
+def check_gdn_write(ref, synth):
+    """decay 1, beta 1, |k| = 1: after the step S k = v for every row."""
+    S = synth.normal(18, 48 * 128 * 128, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(19).step(0)
+    ref.gdn_heads(S, q, k, v, np.ones_like(beta), np.zeros_like(g))
+    kh = k.reshape(16, 128)[np.arange(48) % 16].astype(np.float64)
+    Sk = np.einsum("hcd,hd->hc", S.reshape(48, 128, 128).astype(np.float64), kh)
+    return _close(Sk, v.reshape(48, 128), 1e-5, 0, "delta-rule write S k = v")
+
+
+def check_gdn_zero_state(ref, synth):
+    """S_0 = 0: o = beta (k.q) v / sqrt(128)."""
+    S = np.zeros(48 * 128 * 128, np.float32)
+    q, k, v, beta, g = synth.GdnStepInputs(20).step(0)
+    o = ref.gdn_heads(S, q, k, v, beta, g)
+    kh = k.reshape(16, 128)[np.arange(48) % 16].astype(np.float64)
+    qh = q.reshape(16, 128)[np.arange(48) % 16].astype(np.float64)
+    want = beta.astype(np.float64)[:, None] * (kh * qh).sum(1)[:, None] * v.reshape(48, 128) / np.sqrt(128.0)
+    return _close(o.reshape(48, 128), want, 1e-6, 0, "zero initial state")
+
+
+def check_serial_equals_parallel(ref, synth):
+    P = 300
+    q = synth.normal(21, 6144)
+    K = synth.normal(22, P * 1024).reshape(P, 1024)
+    V = synth.normal(23, P * 1024).reshape(P, 1024)
+    if not np.array_equal(ref.attn_heads(q, K, V, threads=1), ref.attn_heads(q, K, V, threads=7)):
+        return "attention: serial and parallel differ"
+    S1 = synth.normal(24, 48 * 128 * 128, sigma=0.02)
+    S2 = S1.copy()
+    ins = synth.GdnStepInputs(25).step(0)
+    o1 = ref.gdn_heads(S1, *ins, threads=1)
+    o2 = ref.gdn_heads(S2, *ins, threads=5)
+    return None if np.array_equal(o1, o2) and np.array_equal(S1, S2) else "gdn: serial and parallel differ"
+
+
+def check_layer_maps(ref, synth):
+    full = [l for l in range(65) if ref.lib().q38r_is_full_attention(l)]
+    if full != [3 + 4 * i for i in range(16)] + [64]:
+        return f"full-attention layers {full}"
+    rec = [ref.lib().q38r_recurrent_index(l) for l in range(64) if l not in full]
+    return None if rec == list(range(48)) else "recurrent indices are not 0..47 in order"
+
+
+CHECKS = [v for k, v in sorted(globals().items()) if k.startswith("check_")]

@@ -1,0 +1,258 @@
+"""Full-attention decode and prefill on the GPU against the CPU restatement
+of full_core (src/model/ops.rs:813-940).  Tolerance: max-abs <= 1e-3."""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _decode_one(pkg, ctx, P, seed, gate=True, layer=3, split=None):
+    from q38amd import synth
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=(P + 15) // 16 + 4, max_seqs=2, max_tokens_per_seq=P + 64)
+    try:
+        seq = kv.seq_create()
+        K = synth.normal(seed + 1, P * 1024)
+        V = synth.normal(seed + 2, P * 1024)
+        Q = synth.normal(seed + 3, 6144)
+        G = synth.normal(seed + 4, 6144) if gate else None
+        d_k, d_v, d_q = ctx.array(K), ctx.array(V), ctx.array(Q)
+        d_g = ctx.array(G) if gate else None
+        d_o = ctx.empty((24, 256))
+        if P > 1:
+            kv.write(layer, seq, 0, P - 1, d_k, d_v)
+        old = os.environ.get("Q38_SPLIT_TOKENS")
+        if split:
+            os.environ["Q38_SPLIT_TOKENS"] = str(split)
+        try:
+            kv.attn_decode(layer, [seq], [P - 1], d_q, d_o, k_new=d_k.offset((P - 1) * 1024),
+                           v_new=d_v.offset((P - 1) * 1024), gate=d_g)
+        finally:
+            if split:
+                if old is None:
+                    del os.environ["Q38_SPLIT_TOKENS"]
+                else:
+                    os.environ["Q38_SPLIT_TOKENS"] = old
+        got = d_o.download()
+        # the append must have landed in the cache
+        d_kr, d_vr = ctx.empty((1, 1024)), ctx.empty((1, 1024))
+        kv.read(layer, seq, P - 1, 1, d_kr, d_vr)
+        assert np.array_equal(d_kr.download().reshape(-1), K[(P - 1) * 1024:])
+        assert np.array_equal(d_vr.download().reshape(-1), V[(P - 1) * 1024:])
+        for d in (d_k, d_v, d_q, d_o, d_kr, d_vr) + ((d_g,) if gate else ()):
+            d.free()
+        return got, Q, K.reshape(P, 1024), V.reshape(P, 1024), G
+    finally:
+        kv.close()
+
+
+@pytest.mark.parametrize("gate", [False, True])
+def test_decode_256_tokens(pkg, ctx, ref, gate):
+    """Config: 24 q / 4 kv heads, d 256, 256 cached tokens (position 255)."""
+    got, Q, K, V, G = _decode_one(pkg, ctx, 256, 0x51333800, gate=gate)
+    want = ref.attn_heads(Q, K, V, gate=G)
+    err = float(np.max(np.abs(got - want)))
+    print(f"256 tokens gate={gate}: max-abs {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("P", [1, 2, 15, 16, 17, 63, 64, 65, 200, 1000])
+def test_decode_ragged_lengths(pkg, ctx, ref, P):
+    """Edge lengths: one position (o = v exactly up to the gate), partial pages,
+    partial half-pages, lengths around the split size."""
+    got, Q, K, V, G = _decode_one(pkg, ctx, P, 7000 + P, gate=True)
+    want = ref.attn_heads(Q, K, V, gate=G)
+    assert float(np.max(np.abs(got - want))) <= TOL
+
+
+@pytest.mark.parametrize("split", [64, 128, 512, 1024])
+def test_decode_split_invariance(pkg, ctx, ref, split):
+    got, Q, K, V, G = _decode_one(pkg, ctx, 3000, 9100, gate=True, split=split)
+    want = ref.attn_heads(Q, K, V, gate=G)
+    assert float(np.max(np.abs(got - want))) <= TOL
+
+
+def test_decode_32k_metric_shape(pkg, ctx, ref):
+    """The benchmark shape: 32768 cached tokens."""
+    got, Q, K, V, G = _decode_one(pkg, ctx, 32768, 0x51333810, gate=False)
+    want = ref.attn_heads(Q, K, V, threads=8)
+    err = float(np.max(np.abs(got - want)))
+    print(f"32K: max-abs {err:.3e}")
+    assert err <= TOL
+
+
+def test_decode_batched_paged_permuted(pkg, ctx, ref):
+    """Config: 32 sequences, context ~U[1K, 32K], 16-token pages, page table a
+    random permutation of the pool, one decode token per sequence."""
+    from q38amd import synth
+    n = 32
+    rng = np.random.default_rng(0x51333802)
+    ctx_len = rng.integers(1024, 32768, size=n, endpoint=True)
+    pages_needed = [(int(c) + 15) // 16 for c in ctx_len]
+    pool = sum(pages_needed) + 8
+    kv = pkg.KVCache(ctx, n_slots=1, max_pages=pool, max_seqs=n, max_tokens_per_seq=32768 + 16)
+    perm = rng.permutation(pool)
+    seqs, off = [], 0
+    for i in range(n):
+        s = kv.seq_create()
+        kv.seq_set_pages(s, perm[off:off + pages_needed[i]].tolist())
+        off += pages_needed[i]
+        seqs.append(s)
+    layer = 3
+    Ks, Vs = [], []
+    d_k, d_v = ctx.empty((32768, 1024)), ctx.empty((32768, 1024))
+    for i in range(n):
+        P = int(ctx_len[i])
+        # seeded N(0,1) rows made on the device (same stream as synth.normal)
+        ctx.fill_normal(d_k, P * 1024, 0x5000 + 2 * i)
+        ctx.fill_normal(d_v, P * 1024, 0x5001 + 2 * i)
+        kv.write(layer, seqs[i], 0, P, d_k, d_v)
+        Ks.append(d_k.download(P))
+        Vs.append(d_v.download(P))
+    d_k.free()
+    d_v.free()
+    Q = synth.normal(0x6000, n * 6144)
+    G = synth.normal(0x6001, n * 6144)
+    d_q, d_g, d_o = ctx.array(Q), ctx.array(G), ctx.empty((n, 24, 256))
+    kv.attn_decode(layer, seqs, [int(c) - 1 for c in ctx_len], d_q, d_o, gate=d_g)
+    got = d_o.download()
+    worst = 0.0
+    for i in range(n):
+        want = ref.attn_heads(Q[i * 6144:(i + 1) * 6144], Ks[i], Vs[i], gate=G[i * 6144:(i + 1) * 6144],
+                              threads=8)
+        worst = max(worst, float(np.max(np.abs(got[i] - want))))
+    print(f"batched paged: max-abs {worst:.3e}")
+    kv.close()
+    assert worst <= TOL
+
+
+def test_full_core_matches_reference(pkg, ctx, ref):
+    """full_core whole: q/gate split, q and k RMSNorm, RoPE, append, attention,
+    gate, for consecutive tokens, including a position past 2^16 (RoPE angles
+    of the iterative f32 recurrence at large arguments)."""
+    from q38amd import synth
+    ctx_len = 70000
+    layer = 7
+    qn = synth.normal(1, 256, sigma=0.2, mean=1.0)
+    kn = synth.normal(2, 256, sigma=0.2, mean=1.0)
+    # the reference caches: only slot 1 (layer 7) is used; keep [2][ctx][1024]
+    kc = np.zeros(2 * ctx_len * 1024, np.float32)
+    vc = np.zeros(2 * ctx_len * 1024, np.float32)
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=ctx_len // 16 + 8, max_seqs=1, max_tokens_per_seq=ctx_len)
+    seq = kv.seq_create()
+    d_qn, d_kn = ctx.array(qn), ctx.array(kn)
+    # fill positions 0..65599 directly (same rows in both caches), then run
+    # full_core for positions 65600..65603
+    base = 65600
+    K0 = synth.normal(3, base * 1024)
+    V0 = synth.normal(4, base * 1024)
+    kc[ctx_len * 1024: ctx_len * 1024 + base * 1024] = K0
+    vc[ctx_len * 1024: ctx_len * 1024 + base * 1024] = V0
+    d_k0, d_v0 = ctx.array(K0), ctx.array(V0)
+    kv.write(layer, seq, 0, base, d_k0, d_v0)
+    d_k0.free()
+    d_v0.free()
+    worst = 0.0
+    for i in range(4):
+        pos = base + i
+        qg = synth.normal(100 + i, 12288)
+        key = synth.normal(200 + i, 1024)
+        val = synth.normal(300 + i, 1024)
+        d_o = ctx.empty((24, 256))
+        kv.full_core(layer, [seq], [pos], d_qn, d_kn, ctx.array(qg), ctx.array(key), ctx.array(val), d_o)
+        want, _ = ref.full_core(qn, kn, qg, key, val, kc, vc, ctx_len, pos, layer, threads=8)
+        worst = max(worst, float(np.max(np.abs(d_o.download() - want))))
+    kv.close()
+    print(f"full_core: max-abs {worst:.3e}")
+    assert worst <= TOL
+
+
+def test_attn_pre_matches_reference(pkg, ctx, ref):
+    """RMSNorm + RoPE prologue alone, bit for bit where the math is exact."""
+    from q38amd import synth
+    n = 8
+    qn = synth.normal(11, 256, sigma=0.2, mean=1.0)
+    kn = synth.normal(12, 256, sigma=0.2, mean=1.0)
+    qg = synth.normal(13, n * 12288)
+    key = synth.normal(14, n * 1024)
+    pos0 = 123457
+    d_q, d_g, d_k = ctx.empty((n, 6144)), ctx.empty((n, 6144)), ctx.empty((n, 1024))
+    ctx.attn_pre(n, pos0, ctx.array(qn), ctx.array(kn), ctx.array(qg), ctx.array(key), d_q, d_g, d_k)
+    gq, gg, gk = d_q.download(), d_g.download(), d_k.download()
+    for t in range(n):
+        src = qg[t * 12288:(t + 1) * 12288].reshape(24, 512)
+        q = np.stack([ref.rmsnorm(src[h, :256], qn) for h in range(24)]).reshape(-1)
+        q = ref.rope(q, 24, pos0 + t)
+        k = np.stack([ref.rmsnorm(key[t * 1024 + h * 256: t * 1024 + (h + 1) * 256], kn) for h in range(4)])
+        k = ref.rope(k.reshape(-1), 4, pos0 + t)
+        assert np.array_equal(gg[t].reshape(24, 256), src[:, 256:])
+        assert np.max(np.abs(gq[t] - q)) <= 1e-5
+        assert np.max(np.abs(gk[t] - k)) <= 1e-5
+
+
+def test_prefill_matches_reference_rows(pkg, ctx, ref):
+    """batch_full_attention (ops.rs:1153-1172) over a 1024-token prompt after
+    a 300-token prefix; sampled rows against the restatement."""
+    from q38amd import synth
+    base, T = 300, 1024
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=(base + T) // 16 + 8, max_seqs=1, max_tokens_per_seq=base + T)
+    seq = kv.seq_create()
+    layer = 11
+    K = synth.normal(41, (base + T) * 1024)
+    V = synth.normal(42, (base + T) * 1024)
+    Q = synth.normal(43, T * 6144)
+    G = synth.normal(44, T * 6144)
+    d_k, d_v = ctx.array(K), ctx.array(V)
+    kv.write(layer, seq, 0, base, d_k, d_v)
+    d_o = ctx.empty((T, 24, 256))
+    kv.attn_prefill(layer, seq, base, T, ctx.array(Q), d_k.offset(base * 1024), d_v.offset(base * 1024), d_o,
+                    gate=ctx.array(G))
+    got = d_o.download()
+    Kr, Vr = K.reshape(-1, 1024), V.reshape(-1, 1024)
+    rows = sorted(set([0, 1, 15, 16, 511, T - 1] + list(np.random.default_rng(5).integers(0, T, 10))))
+    worst = 0.0
+    for t in rows:
+        n_pos = base + t + 1
+        want = ref.attn_heads(Q[t * 6144:(t + 1) * 6144], Kr[:n_pos], Vr[:n_pos], gate=G[t * 6144:(t + 1) * 6144])
+        worst = max(worst, float(np.max(np.abs(got[t] - want))))
+    kv.close()
+    assert worst <= TOL
+
+
+def test_kv_pages_roundtrip_and_rollback(pkg, ctx, synth):
+    """Write/read through a permuted page table; truncate releases whole pages
+    past the kept positions; reset releases all."""
+    kv = pkg.KVCache(ctx, n_slots=2, max_pages=64, max_seqs=4, max_tokens_per_seq=512)
+    a = kv.seq_create()
+    kv.seq_set_pages(a, list(range(63, 43, -1)))  # 20 pages, reversed order
+    K = synth.normal(51, 300 * 1024)
+    V = synth.normal(52, 300 * 1024)
+    d_k, d_v = ctx.array(K), ctx.array(V)
+    kv.write(3, a, 0, 300, d_k, d_v)
+    r_k, r_v = ctx.empty((300, 1024)), ctx.empty((300, 1024))
+    kv.read(3, a, 0, 300, r_k, r_v)
+    assert np.array_equal(r_k.download().reshape(-1), K)
+    assert np.array_equal(r_v.download().reshape(-1), V)
+    assert kv.seq_capacity(a) == 320 and kv.free_pages() == 44
+    kv.seq_truncate(a, 100)  # keeps pages for positions < 100 (7 pages)
+    assert kv.seq_capacity(a) == 112 and kv.free_pages() == 57
+    kv.read(3, a, 0, 100, r_k, r_v)
+    assert np.array_equal(r_k.download().reshape(-1)[:100 * 1024], K[:100 * 1024])
+    kv.seq_reset(a)
+    assert kv.seq_capacity(a) == 0 and kv.free_pages() == 64
+    kv.close()
+
+
+def test_device_generator_matches_host(pkg, ctx, synth):
+    """The device fill reproduces the host generator (same SplitMix64 words,
+    same Box-Muller), so device-made inputs are the documented inputs."""
+    n = 100001
+    d = ctx.empty((n,))
+    ctx.fill_normal(d, n, 0x1234, sigma=0.5, mean=0.25)
+    got = d.download()
+    want = synth.normal(0x1234, n, sigma=0.5, mean=0.25)
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+    assert np.mean(ulps == 0) > 0.999 and int(ulps.max()) <= 1

@@ -1,0 +1,171 @@
+"""Gated-DeltaNet on the GPU against the CPU restatement of linear_core.
+
+Tolerances (stated by the task for this path): outputs max-abs <= 1e-3;
+state after 1024 steps relative <= 1e-4, measured as max|dS| / max|S_ref|
+and as ||dS||_F / ||S_ref||_F.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+STATE = 48 * 128 * 128
+
+
+def _rel(got, want):
+    d = got.astype(np.float64) - want
+    return (float(np.max(np.abs(d)) / np.max(np.abs(want))),
+            float(np.linalg.norm(d) / np.linalg.norm(want)))
+
+
+def test_gdn_step_matches_reference(ctx, ref, synth):
+    state0 = synth.normal(101, STATE, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(102).step(0)
+    d_state = ctx.array(state0)
+    d_out = ctx.empty((6144,))
+    ctx.gdn_step(1, d_state, *[ctx.array(x) for x in (q, k, v, beta, g)], d_out)
+    s_ref = state0.copy()
+    o_ref = ref.gdn_heads(s_ref, q, k, v, beta, g)
+    assert np.max(np.abs(d_out.download() - o_ref)) <= 1e-3
+    assert max(_rel(d_state.download(), s_ref)) <= 1e-4
+
+
+def test_gdn_1024_steps_state_drift(ctx, ref, synth):
+    """Config: 16 qk / 48 v heads, state ~N(0, 0.02^2), 1024 consecutive steps."""
+    T = 1024
+    state0 = synth.normal(0x51333801, STATE, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(0x51333802).steps(0, T)
+    d_state = ctx.array(state0)
+    dq, dk, dv, db, dg = (ctx.array(x) for x in (q, k, v, beta, g))
+    d_out = ctx.empty((T, 6144))
+    for t in range(T):
+        ctx.gdn_step(1, d_state, dq.offset(t * 2048), dk.offset(t * 2048), dv.offset(t * 6144),
+                     db.offset(t * 48), dg.offset(t * 48), d_out.offset(t * 6144))
+    got_out = d_out.download()
+    s_ref = state0.copy()
+    worst = 0.0
+    for t in range(T):
+        o = ref.gdn_heads(s_ref, q[t], k[t], v[t], beta[t], g[t], threads=8)
+        worst = max(worst, float(np.max(np.abs(got_out[t] - o))))
+    rel_max, rel_fro = _rel(d_state.download(), s_ref)
+    print(f"1024 steps: out max-abs {worst:.3e}, state rel max {rel_max:.3e}, rel fro {rel_fro:.3e}")
+    assert worst <= 1e-3
+    assert rel_max <= 1e-4 and rel_fro <= 1e-4
+
+
+def test_gdn_prefill_equals_steps(ctx, synth):
+    """One launch over T tokens keeps the state in registers; it must give the
+    same bits as T single-token launches (same arithmetic, same order)."""
+    T = 37
+    state0 = synth.normal(201, STATE, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(202).steps(0, T)
+    dq, dk, dv, db, dg = (ctx.array(x) for x in (q, k, v, beta, g))
+    d_a, d_b = ctx.array(state0), ctx.array(state0)
+    o_a, o_b = ctx.empty((T, 6144)), ctx.empty((T, 6144))
+    ctx.gdn_prefill(d_a, T, dq, dk, dv, db, dg, o_a)
+    for t in range(T):
+        ctx.gdn_step(1, d_b, dq.offset(t * 2048), dk.offset(t * 2048), dv.offset(t * 6144),
+                     db.offset(t * 48), dg.offset(t * 48), o_b.offset(t * 6144))
+    assert np.array_equal(d_a.download(), d_b.download())
+    assert np.array_equal(o_a.download(), o_b.download())
+
+
+def test_gdn_batched_states(ctx, synth):
+    """n_seq states in one launch equal one launch per state."""
+    n = 5
+    states = synth.normal(301, n * STATE, sigma=0.02)
+    ins = synth.GdnStepInputs(302, n_seq=n).step(0)
+    d_all = ctx.array(states)
+    d_out = ctx.empty((n, 6144))
+    dins = [ctx.array(x) for x in ins]
+    ctx.gdn_step(n, d_all, *dins, d_out)
+    got_s, got_o = d_all.download().reshape(n, STATE), d_out.download()
+    for s in range(n):
+        d_one = ctx.array(states[s * STATE:(s + 1) * STATE])
+        o_one = ctx.empty((6144,))
+        ctx.gdn_step(1, d_one, dins[0].offset(s * 2048), dins[1].offset(s * 2048), dins[2].offset(s * 6144),
+                     dins[3].offset(s * 48), dins[4].offset(s * 48), o_one)
+        assert np.array_equal(d_one.download(), got_s[s])
+        assert np.array_equal(o_one.download(), got_o[s])
+
+
+def test_gdn_beta_zero_is_pure_decay(ctx, synth):
+    """beta = 0: S_t = exp(g) S_{t-1} and o = S_t q / sqrt(128) (closed form)."""
+    state0 = synth.normal(401, STATE, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(402).step(0)
+    beta = np.zeros_like(beta)
+    d_state, d_out = ctx.array(state0), ctx.empty((6144,))
+    ctx.gdn_step(1, d_state, *[ctx.array(x) for x in (q, k, v, beta, g)], d_out)
+    S = state0.reshape(48, 128, 128).astype(np.float64) * np.exp(g.astype(np.float64))[:, None, None]
+    qh = q.reshape(16, 128)[np.arange(48) % 16].astype(np.float64)
+    o = np.einsum("hcd,hd->hc", S, qh) / np.sqrt(128.0)
+    assert np.max(np.abs(d_state.download().reshape(48, 128, 128) - S)) <= 1e-6
+    assert np.max(np.abs(d_out.download().reshape(48, 128) - o)) <= 1e-5
+
+
+def test_gdn_delta_rule_write(ctx, synth):
+    """decay 1, beta 1, |k| = 1: the updated state maps k to v exactly (S_new k = v)."""
+    state0 = synth.normal(501, STATE, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(502).step(0)
+    beta = np.ones_like(beta)
+    g = np.zeros_like(g)
+    d_state, d_out = ctx.array(state0), ctx.empty((6144,))
+    ctx.gdn_step(1, d_state, *[ctx.array(x) for x in (q, k, v, beta, g)], d_out)
+    S = d_state.download().reshape(48, 128, 128).astype(np.float64)
+    kh = k.reshape(16, 128)[np.arange(48) % 16].astype(np.float64)
+    Sk = np.einsum("hcd,hd->hc", S, kh)
+    assert np.max(np.abs(Sk - v.reshape(48, 128))) <= 1e-4
+
+
+def test_linear_core_decode_matches_reference(ctx, ref, synth):
+    """linear_core whole: conv1d + SiLU + L2 + gates + recurrence + gated RMSNorm, 6 tokens."""
+    conv_w = synth.normal(601, 10240 * 4, sigma=0.5)
+    dt = synth.normal(602, 48)
+    a = -np.abs(synth.normal(603, 48))
+    norm = synth.normal(604, 128, sigma=0.1, mean=1.0)
+    conv_state = synth.normal(605, 10240 * 3)
+    delta = synth.normal(606, STATE, sigma=0.02)
+    d_w = [ctx.array(x) for x in (conv_w, dt, a, norm)]
+    d_conv, d_delta = ctx.array(conv_state), ctx.array(delta)
+    c_ref, s_ref = conv_state.copy(), delta.copy()
+    for t in range(6):
+        qkv = synth.normal(700 + t, 10240)
+        z = synth.normal(800 + t, 6144)
+        b = synth.normal(900 + t, 48)
+        al = synth.normal(1000 + t, 48)
+        d_out = ctx.empty((6144,))
+        ctx.linear_core(1, 1, *d_w, d_conv, d_delta, ctx.array(qkv), ctx.array(z), ctx.array(b), ctx.array(al),
+                        d_out)
+        o_ref = ref.linear_core(conv_w, dt, a, norm, c_ref, s_ref, qkv, z, b, al)
+        assert np.max(np.abs(d_out.download() - o_ref)) <= 1e-3, t
+    assert np.max(np.abs(d_conv.download() - c_ref)) == 0.0
+    assert max(_rel(d_delta.download(), s_ref)) <= 1e-4
+
+
+@pytest.mark.parametrize("T", [5, 70, 200])
+def test_linear_core_prefill_matches_reference(ctx, ref, synth, T):
+    """batch_linear_attention's token loop (ops.rs:1088-1099) in one call."""
+    conv_w = synth.normal(611, 10240 * 4, sigma=0.5)
+    dt = synth.normal(612, 48)
+    a = -np.abs(synth.normal(613, 48))
+    norm = synth.normal(614, 128, sigma=0.1, mean=1.0)
+    conv_state = synth.normal(615, 10240 * 3)
+    delta = synth.normal(616, STATE, sigma=0.02)
+    qkv = synth.normal(617, T * 10240)
+    z = synth.normal(618, T * 6144)
+    b = synth.normal(619, T * 48)
+    al = synth.normal(620, T * 48)
+    d_conv, d_delta = ctx.array(conv_state), ctx.array(delta)
+    d_out = ctx.empty((T, 6144))
+    ctx.linear_core(1, T, *[ctx.array(x) for x in (conv_w, dt, a, norm)], d_conv, d_delta, ctx.array(qkv),
+                    ctx.array(z), ctx.array(b), ctx.array(al), d_out)
+    got = d_out.download()
+    c_ref, s_ref = conv_state.copy(), delta.copy()
+    worst = 0.0
+    for t in range(T):
+        o = ref.linear_core(conv_w, dt, a, norm, c_ref, s_ref, qkv[t * 10240:(t + 1) * 10240],
+                            z[t * 6144:(t + 1) * 6144], b[t * 48:(t + 1) * 48], al[t * 48:(t + 1) * 48], threads=8)
+        worst = max(worst, float(np.max(np.abs(got[t] - o))))
+    assert worst <= 1e-3
+    assert np.max(np.abs(d_conv.download() - c_ref)) == 0.0
+    assert max(_rel(d_delta.download(), s_ref)) <= 1e-4

@@ -1,0 +1,46 @@
+"""Each planted mistake in the restatement (q38_ref.c built with
+-DQ38R_MUTANT=k) must be rejected by at least one check, so a plausible slip
+in the checker cannot pass unnoticed (CPU only)."""
+import os
+import subprocess
+
+import pytest
+
+import oracle_checks as oc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+MUTANTS = {
+    1: "query head h reads kv head h % 4 instead of h / 6",
+    2: "value head vh reads q/k head vh / 3 instead of vh % 16",
+    3: "RoPE angle pos * s^p instead of the f32 recurrence",
+    4: "decay applied after the prediction",
+    5: "score scale 1 instead of 1/16",
+    6: "L2 norm without the 1e-6 floor",
+    7: "softplus without the identity above 20",
+    8: "RMSNorm without eps",
+    9: "conv1d taps reversed",
+    10: "output gate silu instead of sigmoid",
+    11: "delta sign flipped",
+    12: "DeltaNet readout without 1/sqrt(128)",
+}
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS), ids=[f"m{k}" for k in sorted(MUTANTS)])
+def test_mutant_is_rejected(mutant, ref, synth, tmp_path):
+    so = tmp_path / f"libq38ref_m{mutant}.so"
+    subprocess.run(["gcc", "-O2", "-mfma", "-ffp-contract=off", "-fPIC", "-shared", f"-DQ38R_MUTANT={mutant}",
+                    "-o", str(so), os.path.join(ROOT, "oracle", "q38_ref.c"), "-lm", "-lpthread"], check=True)
+    prev = ref.use_library(str(so))
+    try:
+        failures = []
+        for check in oc.CHECKS:
+            try:
+                msg = check(ref, synth)
+            except Exception as e:  # a crash of the check also rejects the mutant
+                msg = f"raised {e!r}"
+            if msg:
+                failures.append(f"{check.__name__}: {msg}")
+    finally:
+        ref.restore_library(prev)
+    assert failures, f"mutant {mutant} ({MUTANTS[mutant]}) passed every check"
+    print(f"mutant {mutant} ({MUTANTS[mutant]}) rejected by {len(failures)} checks, e.g. {failures[0]}")
