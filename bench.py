@@ -10,9 +10,10 @@ above the 256 MB last-level cache).
 
 Prints ONE JSON line.  `value` is decode steps per second over the timed
 region (inputs resident in HBM).  `roofline` is for the dominant kernel,
-q38_attn_decode_split: algorithmic bytes per launch (K + V of one kv head
-group each read once + q) over its mean duration, timed with events on its
-own stream around every launch in the timed region.  `cpu_baseline` times the
+q38_attn_decode_split (a decode step is this launch plus the small
+q38_attn_decode_merge that combines the split-K partials): algorithmic bytes
+per launch (K + V each read once + q) over its mean duration, from start/stop
+events stamped by each dispatch on the launch stream in the timed region.  `cpu_baseline` times the
 CPU restatement of the reference's attention on the same data.
 
 Also measured and reported under "extra": the Gated-DeltaNet decode step
@@ -81,7 +82,7 @@ def attention_decode(pkg, ctx, steps: int, warmup: int):
     ms_total = ctx.elapsed_ms(e0, e1)
     k_ms, k_n = ctx.kernel_timer_stop()
     ctx.sync()
-    # merge-kernel time, from a separate short timed loop (not part of value)
+    # merge-kernel time, from a separate short loop (not part of `value`)
     ctx.kernel_timer_start("q38_attn_decode_merge", 64)
     for i in range(64):
         step(i)
@@ -185,8 +186,8 @@ def main():
     k_ms = r["kernel_ms"]
     achieved = SPLIT_BYTES / (k_ms * 1e-3) / 1e9
     step_gbs = STEP_BYTES / (r["ms_per_step"] * 1e-3) / 1e9
-    log(f"step {r['ms_per_step'] * 1e3:.2f} us, split kernel {k_ms * 1e3:.2f} us "
-        f"({achieved:.0f} GB/s), merge {r['merge_ms'] * 1e3:.2f} us")
+    log(f"step {r['ms_per_step'] * 1e3:.2f} us, split kernel {k_ms * 1e3:.2f} us ({achieved:.0f} GB/s), "
+        f"merge {r['merge_ms'] * 1e3:.2f} us")
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "attn_decode_split_32k_traffic.json")

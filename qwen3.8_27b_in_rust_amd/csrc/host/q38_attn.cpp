@@ -583,7 +583,7 @@ namespace {
 /* Context split per workgroup.  Enough splits to give every CU about two
  * workgroups of 4 waves, no fewer than 64 tokens (one page per wave) and no
  * more than 1024; Q38_SPLIT_TOKENS overrides (rounded to a multiple of 64). */
-constexpr int kMaxSplitsPerSeq = 4096; /* LDS weights of the merge kernel */
+constexpr int kMaxSplitsPerSeq = Q38_MAX_SPLITS; /* LDS weights of the merge kernel */
 
 int choose_split_tokens(const q38_ctx *ctx, long total_tokens, long max_tokens) {
     long split = 64;

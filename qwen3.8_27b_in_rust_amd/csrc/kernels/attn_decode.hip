@@ -282,7 +282,6 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
  * thread (sl, dl) sums splits sl, sl+16, ... of dims 4dl..4dl+3 with the loop
  * unrolled so its loads are in flight together.  At most Q38_MAX_SPLITS
  * splits per sequence (the host sizes splits so). */
-#define Q38_MAX_SPLITS 4096
 extern "C" __global__ __launch_bounds__(256) void q38_attn_decode_merge(q38_merge_args a) {
     __shared__ float w_lds[Q38_MAX_SPLITS];
     __shared__ f32x4 red[16][16];

@@ -33,6 +33,7 @@
 #define Q38_LIN_STATE_FLOATS (Q38_LIN_V_HEADS * Q38_LIN_HEAD_DIM * Q38_LIN_HEAD_DIM)
 
 #define Q38_MAX_BATCH 64 /* sequences per decode launch */
+#define Q38_MAX_SPLITS 4096 /* splits of one sequence in one decode launch */
 
 /* Split-K paged decode: grid (total_splits, 4 kv heads). */
 typedef struct {
@@ -127,7 +128,7 @@ typedef struct {
     int32_t n_seq;
 } q38_gdn_pre_args;
 
-/* Merge of split-K partials.  grid (n_seq, 24). */
+/* Merge of split-K partials.  grid (n_seq, 24, 4). */
 typedef struct {
     const float *part_o;
     const float *part_ml;

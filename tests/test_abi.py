@@ -59,7 +59,7 @@ def test_kargs_layout_matches_device_expectations():
     import tempfile
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     hdr = os.path.join(root, "qwen3.8_27b_in_rust_amd", "csrc", "q38_kargs.h")
-    src = f'#include "{hdr}"\n#include <stdio.h>\nint main(){{printf("%zu %zu %zu\\n", sizeof(q38_decode_args), sizeof(q38_merge_args), sizeof(q38_gdn_args));return 0;}}\n'
+    src = f'#include "{hdr}"\n#include <stdio.h>\nint main(){{printf("%zu %zu %zu\\n", sizeof(q38_decode_args), sizeof(q38_gdn_pre_args), sizeof(q38_gdn_args));return 0;}}\n'
     with tempfile.TemporaryDirectory() as d:
         c = os.path.join(d, "p.c")
         open(c, "w").write(src)
