@@ -40,6 +40,7 @@ LAYERS = [3 + 4 * i for i in range(16)]
 KV_BYTES = CTX * 1024 * 4 * 2                 # K + V of one layer: 268,435,456
 SPLIT_BYTES = KV_BYTES + 24 * 256 * 4         # + q: bytes the split kernel must read
 STEP_BYTES = KV_BYTES + 2 * 24 * 256 * 4      # + q + o: the decode step's unique bytes
+COPY_BYTES = 512 << 20
 GDN_STATE_BYTES = 48 * 128 * 128 * 4
 GDN_STEP_BYTES = 2 * GDN_STATE_BYTES + 4 * (2 * 2048 + 6144 + 2 * 48 + 6144)  # state R+W + q,k,v,beta,g,o
 
@@ -160,6 +161,24 @@ def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float):
                       f"{el:.1f} s, {threads} threads available, heads split over min(threads, 24)"}, out
 
 
+def copy_calibration(ctx, steps: int) -> None:
+    """A plain copy of a known size: each launch reads and writes COPY_BYTES."""
+    n = COPY_BYTES // 4
+    src, dst = ctx.empty((n,)), ctx.empty((n,))
+    ctx.fill_normal(src, n, 0x51334100)
+    for _ in range(3):
+        ctx.copy(dst, src, COPY_BYTES)
+    ctx.sync()
+    ctx.kernel_timer_start("q38_copy_f32", steps)
+    for _ in range(steps):
+        ctx.copy(dst, src, COPY_BYTES)
+    k_ms, k_n = ctx.kernel_timer_stop()
+    us = k_ms * 1e3 / max(k_n, 1)
+    print(json.dumps({"mode": "copy-calibration", "kernel": "q38_copy_f32", "bytes_read": COPY_BYTES,
+                      "bytes_written": COPY_BYTES, "launches": k_n, "kernel_us": us,
+                      "gb_s": 2 * COPY_BYTES / (us * 1e-6) / 1e9}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +187,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the DeltaNet measurements")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="instead of the benchmark: time a plain 512 MiB device copy (q38_copy_f32), "
+                    "the reference figure that scales the HBM byte counters")
     ap.add_argument("--module-dir", default=None, help="load the code objects from this directory "
                     "(default: next to the library), to compare builds")
     args = ap.parse_args()
@@ -180,6 +202,10 @@ def main():
     pkg = entry.load_package()
     ctx = pkg.Context(0, module_dir=args.module_dir)
     info = ctx.info()
+    if args.copy_calibration:
+        copy_calibration(ctx, args.steps)
+        ctx.close()
+        return
     log(f"device {info}")
     log(f"attention decode 32K: warmup {args.warmup}, steps {args.steps}")
     r = attention_decode(pkg, ctx, args.steps, args.warmup)

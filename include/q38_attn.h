@@ -85,6 +85,12 @@ int q38_kernel_timer_stop(q38_ctx *ctx, float *total_ms, int *launches);
  * gives for the same seed.  For benchmark inputs of many gigabytes. */
 int q38_fill_normal(q38_ctx *ctx, float *d_out, size_t n, uint64_t seed, float sigma, float mean);
 
+/* Plain device-to-device copy by a kernel of this library (bytes a multiple
+ * of 16, pointers 16-byte aligned): reads and writes exactly `bytes` each,
+ * the calibration figure for hardware memory counters.  No counterpart in
+ * the reference (which has no device). */
+int q38_device_copy(q38_ctx *ctx, void *d_dst, const void *d_src, size_t bytes);
+
 /* ------------------------------------------------------------- paged KV cache */
 
 /*

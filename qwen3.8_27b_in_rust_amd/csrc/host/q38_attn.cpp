@@ -86,6 +86,7 @@ struct q38_ctx {
     hipFunction_t f_gdn_pre = nullptr;
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
+    hipFunction_t f_copy = nullptr;
     /* per-kernel event timer (q38_kernel_timer_*) */
     hipFunction_t timed = nullptr;
     std::vector<hipEvent_t> timer_events;
@@ -254,6 +255,7 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_copy, ctx->mod_synth, "q38_copy_f32"));
     /* ops.rs:596: 1e7^(-2/64) in f32, computed once with the host's powf */
     ctx->rope_theta_scale = powf(10000000.0f, -2.0f / 64.0f);
     *out = ctx.release();
@@ -370,6 +372,21 @@ int q38_fill_normal(q38_ctx *ctx, float *d_out, size_t n, uint64_t seed, float s
     return ctx->launch(ctx->f_fill_normal, (unsigned)blocks, 1, 1, 256, &a);
 }
 
+int q38_device_copy(q38_ctx *ctx, void *d_dst, const void *d_src, size_t bytes) {
+    if (ctx == nullptr || d_dst == nullptr || d_src == nullptr) return fail("NULL argument");
+    if (bytes == 0) return 0;
+    if (bytes % 16 != 0 || ((uintptr_t)d_dst | (uintptr_t)d_src) % 16 != 0)
+        return fail("q38_device_copy needs 16-byte aligned pointers and a multiple of 16 bytes");
+    struct {
+        const void *src;
+        void *dst;
+        uint64_t n4;
+    } a = {d_src, d_dst, (uint64_t)(bytes / 16)};
+    const uint64_t blocks = (a.n4 + 255) / 256;
+    if (blocks > 0x7FFFFFFFull) return fail("copy of %zu bytes is too large", bytes);
+    return ctx->launch(ctx->f_copy, (unsigned)blocks, 1, 1, 256, &a);
+}
+
 int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launches) {
     if (ctx == nullptr || kernel_name == nullptr) return fail("NULL argument");
     if (max_launches < 1) return fail("max_launches must be positive");
@@ -381,6 +398,7 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_attn_pre") f = ctx->f_attn_pre;
     else if (name == "q38_gdn_recurrent") f = ctx->f_gdn_recurrent;
     else if (name == "q38_gdn_pre") f = ctx->f_gdn_pre;
+    else if (name == "q38_copy_f32") f = ctx->f_copy;
     else return fail("unknown kernel %s", kernel_name);
     while ((int)ctx->timer_events.size() < 2 * max_launches) {
         hipEvent_t e;

@@ -34,3 +34,17 @@ extern "C" __global__ __launch_bounds__(256) void q38_fill_normal(q38_fill_args 
     a.out[i0] = (float)(r * cos(t) * (double)a.sigma + (double)a.mean);
     if (i0 + 1 < a.n) a.out[i0 + 1] = (float)(r * sin(t) * (double)a.sigma + (double)a.mean);
 }
+
+/* Plain device copy, n4 float4 elements, one per thread (grid sized by the
+ * host).  The reference figure for HBM counters: it reads and writes exactly
+ * 16*n4 bytes each. */
+typedef struct {
+    const float4 *src;
+    float4 *dst;
+    uint64_t n4;
+} q38_copy_args;
+
+extern "C" __global__ __launch_bounds__(256) void q38_copy_f32(q38_copy_args a) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < a.n4) a.dst[i] = a.src[i];
+}
