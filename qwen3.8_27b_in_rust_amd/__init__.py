@@ -169,6 +169,9 @@ class Context:
     """One device, one stream, the loaded code objects."""
 
     def __init__(self, device: int = 0, module_dir: str | None = None):
+        """module_dir: where the code objects are (default: $Q38_MODULE_DIR,
+        else next to the library)."""
+        module_dir = module_dir or os.environ.get("Q38_MODULE_DIR") or None
         h = c_void_p()
         md = module_dir.encode() if module_dir else None
         _check(lib().q38_ctx_create(ctypes.byref(h), device, md), "q38_ctx_create")

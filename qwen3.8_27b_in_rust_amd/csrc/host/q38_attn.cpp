@@ -92,6 +92,7 @@ struct q38_ctx {
     std::vector<hipEvent_t> timer_events;
     int timer_used = 0;
     int cu_count = 0;
+    int decode_block = 256; /* threads of a decode workgroup (the kernel's launch bound) */
     int clock_khz = 0;
     int lds_bytes = 0;
     char name[256] = {0};
@@ -252,6 +253,10 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_attn_pre, ctx->mod_decode, "q38_attn_pre"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_recurrent, ctx->mod_gdn, "q38_gdn_recurrent"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_pre, ctx->mod_gdn, "q38_gdn_pre"));
+    Q38_HIP(hipFuncGetAttribute(&ctx->decode_block, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
+                                ctx->f_decode_split));
+    if (ctx->decode_block < 256 || ctx->decode_block > 1024 || ctx->decode_block % 64 != 0)
+        return fail("decode kernel has an unexpected block size %d", ctx->decode_block);
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
@@ -598,24 +603,32 @@ int q38_kv_read(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float *d
 
 namespace {
 
-/* Context split per workgroup.  Enough splits to give every CU about two
- * workgroups of 4 waves, no fewer than 64 tokens (one page per wave) and no
- * more than 1024; Q38_SPLIT_TOKENS overrides (rounded to a multiple of 64). */
+/* Context tokens per decode workgroup: a multiple of 64, at least 64 and at
+ * most Q38_MAX_SPLIT_TOKENS, chosen to give one workgroup per CU (the split
+ * kernel streams fastest with one workgroup per CU: 46 us at 32768 tokens
+ * against 50 us with two); Q38_SPLIT_TOKENS overrides (rounded up to a
+ * multiple of 64). */
 constexpr int kMaxSplitsPerSeq = Q38_MAX_SPLITS; /* LDS weights of the merge kernel */
 
-int choose_split_tokens(const q38_ctx *ctx, long total_tokens, long max_tokens) {
+int choose_split_tokens(const q38_ctx *ctx, long total_tokens, long max_tokens, int *split_out) {
     long split = 64;
     const char *env = getenv("Q38_SPLIT_TOKENS");
     if (env != nullptr && atoi(env) >= 64) {
-        split = (atoi(env) + 63) / 64 * 64;
+        split = std::min<long>((atoi(env) + 63) / 64 * 64, Q38_MAX_SPLIT_TOKENS);
     } else {
-        const long target_wgs = 2L * std::max(ctx->cu_count, 1);
-        const long per = (total_tokens * Q38_ATTN_KV_HEADS + target_wgs - 1) / target_wgs;
-        while (split < per && split < 1024) split *= 2;
+        const long slots = std::max(ctx->cu_count, 1);
+        const long per = (total_tokens * Q38_ATTN_KV_HEADS + slots - 1) / slots;
+        split = std::min<long>(std::max<long>((per + 63) / 64 * 64, 64), Q38_MAX_SPLIT_TOKENS);
     }
-    /* no sequence may need more splits than the merge kernel holds */
-    while ((max_tokens + split - 1) / split > kMaxSplitsPerSeq) split *= 2;
-    return (int)split;
+    /* no sequence may need more splits than the merge kernel holds, and no
+     * split more pages than the kernel's page-id array */
+    while ((max_tokens + split - 1) / split > kMaxSplitsPerSeq && split < Q38_MAX_SPLIT_TOKENS)
+        split = std::min<long>(split * 2, Q38_MAX_SPLIT_TOKENS);
+    if ((max_tokens + split - 1) / split > kMaxSplitsPerSeq)
+        return fail("context of %ld tokens exceeds %d splits of %d tokens", max_tokens, kMaxSplitsPerSeq,
+                    Q38_MAX_SPLIT_TOKENS);
+    *split_out = (int)split;
+    return 0;
 }
 
 int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const int32_t *positions,
@@ -627,7 +640,8 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
         total_tokens += positions[b] + 1;
         max_tokens = std::max<long>(max_tokens, positions[b] + 1);
     }
-    const int split_tokens = choose_split_tokens(ctx, total_tokens, max_tokens);
+    int split_tokens = 0;
+    if (choose_split_tokens(ctx, total_tokens, max_tokens, &split_tokens)) return -1;
 
     q38_decode_args a;
     memset(&a, 0, sizeof(a));
@@ -662,7 +676,7 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
         a.part_o = static_cast<float *>(ctx->work);
         a.part_ml = a.part_o + part_o_floats;
     }
-    if (ctx->launch(ctx->f_decode_split, total, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
+    if (ctx->launch(ctx->f_decode_split, total, Q38_ATTN_KV_HEADS, 1, ctx->decode_block, &a)) return -1;
     if (any_multi) {
         q38_merge_args m;
         memset(&m, 0, sizeof(m));
@@ -767,7 +781,8 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
             total_tokens += positions[b0 + b] + 1;
             max_tokens = std::max<long>(max_tokens, positions[b0 + b] + 1);
         }
-        const int split = choose_split_tokens(ctx, total_tokens, max_tokens);
+        int split = 0;
+        if (choose_split_tokens(ctx, total_tokens, max_tokens, &split)) return -1;
         size_t splits = 0;
         for (int b = 0; b < n; ++b) splits += (positions[b0 + b] + split) / split;
         const size_t part_floats = splits * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2);

@@ -55,8 +55,10 @@ Q38_DEV void load_rows(Rows &r, const float *pool, size_t base, int lane_off) {
     }
 }
 
-Q38_DEV size_t half_page_base(const int32_t *pt, int j, int tb) {
-    const int phys = pt[tb >> 4];
+/* pages: the split's physical page ids in LDS (entry i holds the page of
+ * tokens t_begin + 16i ..); tb is relative to t_begin. */
+Q38_DEV size_t half_page_base(const int32_t *pages, int j, int tb) {
+    const int phys = pages[tb >> 4];
     return ((size_t)phys * Q38_ATTN_KV_HEADS + j) * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM +
            (size_t)(tb & 15) * Q38_ATTN_HEAD_DIM;
 }
@@ -97,10 +99,17 @@ Q38_DEV void decode_rows(DecodeState &st, const f32x4 (&q0)[Q38_ATTN_GROUP],
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_decode_args a) {
-    __shared__ float red_o[4][Q38_ATTN_GROUP][Q38_ATTN_HEAD_DIM];
-    __shared__ float red_m[4][Q38_ATTN_GROUP];
-    __shared__ float red_l[4][Q38_ATTN_GROUP];
+#ifndef Q38_DECODE_MIN_WGS
+#define Q38_DECODE_MIN_WGS 1 /* workgroups per CU the register budget is sized for */
+#endif
+
+extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split(
+    q38_decode_args a) {
+    constexpr int NW = Q38_DECODE_WAVES;
+    __shared__ float red_o[NW][Q38_ATTN_GROUP][Q38_ATTN_HEAD_DIM];
+    __shared__ float red_m[NW][Q38_ATTN_GROUP];
+    __shared__ float red_l[NW][Q38_ATTN_GROUP];
+    __shared__ int32_t pages[Q38_MAX_SPLIT_TOKENS / Q38_PAGE_TOKENS];
 
     const int g = blockIdx.x;
     const int j = blockIdx.y;
@@ -115,13 +124,18 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = lane >> 5;
     const int li = lane & 31;
     const int d0 = 4 * li;
     const int d1 = 128 + 4 * li;
 
+    /* the split's page ids, loaded once: the streaming loop below then has
+     * no global load whose address depends on another global load */
     const int32_t *pt = a.page_table + (size_t)seq * a.pt_stride;
+    const int n_split_pages = (t_end - t_begin + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS;
+    if (tid < n_split_pages) pages[tid] = pt[(t_begin >> 4) + tid];
+    __syncthreads();
     const float *k_new_row = nullptr;
     const float *v_new_row = nullptr;
     if (a.k_new != nullptr) {
@@ -129,7 +143,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
         v_new_row = a.v_new + (size_t)b * Q38_ATTN_KV_DIM + j * Q38_ATTN_HEAD_DIM;
         /* KV append (ops.rs:858-866): the split that holds `pos` stores the row. */
         if (pos >= t_begin && pos < t_end && wave == 0) {
-            const int phys = pt[pos >> 4];
+            const int phys = pages[(pos - t_begin) >> 4];
             const size_t row = ((size_t)phys * Q38_ATTN_KV_HEADS + j) * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM +
                                (size_t)(pos & 15) * Q38_ATTN_HEAD_DIM;
             q38_st4(a.kpool + row + 4 * lane, q38_ld4(k_new_row + 4 * lane));
@@ -152,7 +166,7 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
      * is accumulated */
     Rows K, V;
     if (wave < n_regular) {
-        const size_t base = half_page_base(pt, j, t_begin + wave * 8);
+        const size_t base = half_page_base(pages, j, wave * 8);
         load_rows(K, a.kpool, base, lane_off);
         load_rows(V, a.vpool, base, lane_off);
     }
@@ -174,12 +188,12 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
         st.o1[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int hp = wave; hp < n_regular; hp += 4) {
-        const bool has_next = hp + 4 < n_regular;
+    for (int hp = wave; hp < n_regular; hp += NW) {
+        const bool has_next = hp + NW < n_regular;
         size_t nbase = 0;
         Rows Kn;
         if (has_next) {
-            nbase = half_page_base(pt, j, t_begin + (hp + 4) * 8);
+            nbase = half_page_base(pages, j, (hp + NW) * 8);
             load_rows(Kn, a.kpool, nbase, lane_off);
         }
         decode_rows(st, q0, q1, K, V, all_valid);
@@ -189,9 +203,9 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
         }
     }
 
-    if (has_tail && wave == (n_hp - 1) % 4) {
+    if (has_tail && wave == (n_hp - 1) % NW) {
         const int tb = t_begin + (n_hp - 1) * 8;
-        const size_t base = half_page_base(pt, j, tb);
+        const size_t base = half_page_base(pages, j, tb - t_begin);
         TailRows tr;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -246,15 +260,16 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
     }
     __syncthreads();
 
+    if (tid >= Q38_ATTN_HEAD_DIM) return;
     const int d = tid; /* one output dim per thread */
 #pragma unroll
     for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w][hh]);
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, red_m[w][hh]);
         float L = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float mw = red_m[w][hh];
             const float f = mw == -INFINITY ? 0.0f : q38_exp2(mw - M);
             L += red_l[w][hh] * f;
@@ -277,15 +292,16 @@ extern "C" __global__ __launch_bounds__(256, 2) void q38_attn_decode_split(q38_d
 
 /* Combine the splits of each (sequence, head): rescale every partial to the
  * common max, sum, normalise, gate.  grid (n_seq, 24, 4): z picks 64 of the
- * 256 dims, so 96 workgroups share a sequence's merge.  Every load is issued
- * without waiting on another: the (m, l) pairs go to LDS in one pass, then
- * thread (sl, dl) sums splits sl, sl+16, ... of dims 4dl..4dl+3 with the loop
- * unrolled so its loads are in flight together.  At most Q38_MAX_SPLITS
- * splits per sequence (the host sizes splits so). */
+ * 256 dims, so 96 workgroups share a sequence's merge.  Thread (sl, dl)
+ * merges splits sl, sl + 16, ... of dims 4dl..4dl+3 online (running max,
+ * sum and output in registers); up to 8 splits' (m, l, o) are loaded at
+ * once, so a merge of up to 128 splits costs one memory round trip.  The 16
+ * per-thread results of each dim quad then meet in LDS. */
 extern "C" __global__ __launch_bounds__(256) void q38_attn_decode_merge(q38_merge_args a) {
-    __shared__ float w_lds[Q38_MAX_SPLITS];
-    __shared__ f32x4 red[16][16];
-    __shared__ float red_s[4][2];
+    constexpr int kBatch = 8;
+    __shared__ f32x4 red_o[16][16];
+    __shared__ float red_m[16][16];
+    __shared__ float red_l[16][16];
     const int b = blockIdx.x;
     const int h = blockIdx.y;
     const int dq = blockIdx.z;
@@ -293,47 +309,61 @@ extern "C" __global__ __launch_bounds__(256) void q38_attn_decode_merge(q38_merg
     const int n = a.split_base[b + 1] - base;
     if (n <= 1) return;
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-
-    float M = -INFINITY;
-    for (int s = tid; s < n; s += 256) {
-        const float m = a.part_ml[((size_t)(base + s) * Q38_ATTN_HEADS + h) * 2];
-        w_lds[s] = m;
-        M = fmaxf(M, m);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if (lane == 0) red_s[wave][0] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red_s[0][0], red_s[1][0]), fmaxf(red_s[2][0], red_s[3][0]));
-    float L = 0.0f;
-    for (int s = tid; s < n; s += 256) {
-        const float w = q38_exp2(w_lds[s] - M);
-        w_lds[s] = w;
-        L += w * a.part_ml[((size_t)(base + s) * Q38_ATTN_HEADS + h) * 2 + 1];
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
-    if (lane == 0) red_s[wave][1] = L;
-    __syncthreads();
-
     const int dl = tid & 15;
     const int sl = tid >> 4;
     const int d = dq * 64 + 4 * dl;
+    const size_t o_step = (size_t)Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
     const float *po = a.part_o + ((size_t)base * Q38_ATTN_HEADS + h) * Q38_ATTN_HEAD_DIM + d;
-    const size_t step = (size_t)Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int s = sl; s < n; s += 16) acc = q38_fma4(w_lds[s], q38_ld4(po + (size_t)s * step), acc);
-    red[sl][dl] = acc;
+    const float *pml = a.part_ml + ((size_t)base * Q38_ATTN_HEADS + h) * 2;
+
+    float M = -INFINITY, L = 0.0f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = sl; s0 < n; s0 += 16 * kBatch) {
+        float m[kBatch], l[kBatch];
+        f32x4 o[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int s = s0 + 16 * k;
+            const bool in = s < n;
+            const int sc = in ? s : s0; /* a split known to exist */
+            m[k] = in ? pml[(size_t)sc * Q38_ATTN_HEADS * 2] : -INFINITY;
+            l[k] = pml[(size_t)sc * Q38_ATTN_HEADS * 2 + 1];
+            o[k] = q38_ld4(po + (size_t)sc * o_step);
+        }
+        float mx = M;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) mx = fmaxf(mx, m[k]);
+        if (mx != -INFINITY) {
+            const float f = q38_exp2(M - mx); /* 0 while M is -inf */
+            L *= f;
+            O *= f;
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const float w = q38_exp2(m[k] - mx); /* 0 for absent or empty splits */
+                L = __builtin_fmaf(w, l[k], L);
+                O = q38_fma4(w, o[k], O);
+            }
+            M = mx;
+        }
+    }
+    red_o[sl][dl] = O;
+    red_m[sl][dl] = M;
+    red_l[sl][dl] = L;
     __syncthreads();
     if (sl == 0) {
-        f32x4 o = red[0][dl];
+        float Mt = -INFINITY;
 #pragma unroll
-        for (int i = 1; i < 16; ++i) o += red[i][dl];
-        const float Lt = red_s[0][1] + red_s[1][1] + red_s[2][1] + red_s[3][1];
-        f32x4 r = o / Lt;
+        for (int i = 0; i < 16; ++i) Mt = fmaxf(Mt, red_m[i][dl]);
+        float Lt = 0.0f;
+        f32x4 Ot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float mi = red_m[i][dl];
+            const float w = mi == -INFINITY ? 0.0f : q38_exp2(mi - Mt);
+            Lt = __builtin_fmaf(w, red_l[i][dl], Lt);
+            Ot = q38_fma4(w, red_o[i][dl], Ot);
+        }
+        f32x4 r = Ot / Lt;
         const size_t off = (size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d;
         if (a.gate != nullptr) {
             const f32x4 gt = q38_ld4(a.gate + off);
