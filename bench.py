@@ -123,7 +123,7 @@ def gdn_steps(pkg, ctx, n_seq: int, n_states: int, steps: int, warmup: int):
         step(i)
     ctx.sync()
     e0, e1 = ctx.event(), ctx.event()
-    ctx.kernel_timer_start("q38_gdn_recurrent", steps)
+    ctx.kernel_timer_start("q38_gdn_step_rows", steps)
     ctx.record(e0)
     for i in range(steps):
         step(warmup + i)
@@ -141,6 +141,44 @@ def gdn_steps(pkg, ctx, n_seq: int, n_states: int, steps: int, warmup: int):
         "kernel_frac_hbm": n_seq * GDN_STEP_BYTES / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "us_per_state_step": kern * 1e3 / n_seq,
     }
+
+
+PREFILL_T = 4096
+# causal attention flops of a 4096-token prompt: per (query t, head) (t+1)
+# keys x 256 dims x 2 (QK^T) + the same for PV
+PREFILL_FLOPS = 24 * 4 * 256 * (PREFILL_T * (PREFILL_T + 1) // 2)
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_attention(pkg, ctx, reps: int):
+    """Causal prefill attention of a 4096-token prompt (batch_full_attention,
+    ops.rs:1153-1172) on the bf16x3 MFMA kernel: kernel time per prompt."""
+    T = PREFILL_T
+    kv = pkg.KVCache(ctx, n_slots=1, max_pages=T // 16, max_seqs=1, max_tokens_per_seq=T)
+    seq = kv.seq_create()
+    k, v = ctx.empty((T, 1024)), ctx.empty((T, 1024))
+    q, g, o = ctx.empty((T, 24, 256)), ctx.empty((T, 24, 256)), ctx.empty((T, 24, 256))
+    for i, (buf, n) in enumerate(((k, T * 1024), (v, T * 1024), (q, T * 6144), (g, T * 6144))):
+        ctx.fill_normal(buf, n, 0x51334200 + i)
+    for _ in range(2):
+        kv.seq_reset(seq)
+        kv.attn_prefill(3, seq, 0, T, q, k, v, o, gate=g)
+    ctx.sync()
+    ctx.kernel_timer_start("q38_attn_prefill_mfma", reps)
+    for _ in range(reps):
+        kv.seq_reset(seq)
+        kv.attn_prefill(3, seq, 0, T, q, k, v, o, gate=g)
+    k_ms, k_n = ctx.kernel_timer_stop()
+    kv.close()
+    for b in (k, v, q, g, o):
+        b.free()
+    ms = k_ms / max(k_n, 1)
+    tflops = PREFILL_FLOPS / (ms * 1e-3) / 1e12
+    return {"tokens": T, "kernel_ms": ms, "algorithmic_gflop": PREFILL_FLOPS / 1e9, "tflop_s": tflops,
+            "frac_bf16_peak": tflops / BF16_PEAK_TFLOPS,
+            "mfma_tflop_s_executed": 3 * tflops,
+            "note": "bf16x3 (hi*hi + hi*lo + lo*hi) MFMA products with f32 accumulation; "
+                    "algorithmic flops count each product once"}
 
 
 def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float):
@@ -248,6 +286,9 @@ def main():
     r["kv"].close()
 
     if not args.no_extra:
+        log("prefill attention: 4096-token causal prompt")
+        extra["prefill_attention_4096"] = prefill_attention(pkg, ctx, 5)
+        log(f"prefill: {json.dumps(extra['prefill_attention_4096'])}")
         log("Gated-DeltaNet step: 1 state per launch over 192 states; 32 per launch over 192")
         extra["gdn_step_1"] = gdn_steps(pkg, ctx, 1, 192, 384, 32)
         extra["gdn_step_32"] = gdn_steps(pkg, ctx, 32, 192, 60, 6)

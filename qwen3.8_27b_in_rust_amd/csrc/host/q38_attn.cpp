@@ -78,12 +78,15 @@ struct q38_ctx {
     hipStream_t stream = nullptr;
     hipModule_t mod_decode = nullptr;
     hipModule_t mod_gdn = nullptr;
+    hipModule_t mod_prefill = nullptr;
+    hipFunction_t f_prefill = nullptr;
     hipFunction_t f_decode_split = nullptr;
     hipFunction_t f_decode_merge = nullptr;
     hipFunction_t f_kv_copy = nullptr;
     hipFunction_t f_attn_pre = nullptr;
     hipFunction_t f_gdn_recurrent = nullptr;
     hipFunction_t f_gdn_pre = nullptr;
+    hipFunction_t f_gdn_step_rows = nullptr;
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
     hipFunction_t f_copy = nullptr;
@@ -247,12 +250,16 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     const std::string p_gdn = dir + "/gdn.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_decode, p_decode.c_str()));
     Q38_HIP(hipModuleLoad(&ctx->mod_gdn, p_gdn.c_str()));
+    const std::string p_prefill = dir + "/attn_prefill.hsaco";
+    Q38_HIP(hipModuleLoad(&ctx->mod_prefill, p_prefill.c_str()));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_prefill, ctx->mod_prefill, "q38_attn_prefill_mfma"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split, ctx->mod_decode, "q38_attn_decode_split"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "q38_attn_decode_merge"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_copy, ctx->mod_decode, "q38_kv_copy"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_attn_pre, ctx->mod_decode, "q38_attn_pre"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_recurrent, ctx->mod_gdn, "q38_gdn_recurrent"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_pre, ctx->mod_gdn, "q38_gdn_pre"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_step_rows, ctx->mod_gdn, "q38_gdn_step_rows"));
     Q38_HIP(hipFuncGetAttribute(&ctx->decode_block, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
                                 ctx->f_decode_split));
     if (ctx->decode_block < 256 || ctx->decode_block > 1024 || ctx->decode_block % 64 != 0)
@@ -274,6 +281,7 @@ int q38_ctx_destroy(q38_ctx *ctx) {
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
     if (ctx->mod_gdn) (void)hipModuleUnload(ctx->mod_gdn);
+    if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
     if (ctx->mod_synth) (void)hipModuleUnload(ctx->mod_synth);
     for (hipEvent_t e : ctx->timer_events) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -403,7 +411,9 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_attn_pre") f = ctx->f_attn_pre;
     else if (name == "q38_gdn_recurrent") f = ctx->f_gdn_recurrent;
     else if (name == "q38_gdn_pre") f = ctx->f_gdn_pre;
+    else if (name == "q38_gdn_step_rows") f = ctx->f_gdn_step_rows;
     else if (name == "q38_copy_f32") f = ctx->f_copy;
+    else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else return fail("unknown kernel %s", kernel_name);
     while ((int)ctx->timer_events.size() < 2 * max_launches) {
         hipEvent_t e;
@@ -813,20 +823,24 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     if (n_tokens < 0 || base_pos < 0) return fail("negative count or position");
     if (n_tokens == 0) return 0;
     if (!d_q || !d_k || !d_v || !d_out) return fail("NULL argument");
+    /* append the prompt's rows (reserves pages; fails past the context limit) */
     if (q38_kv_write(kv, layer, seq, base_pos, n_tokens, d_k, d_v)) return -1;
     int slot = 0;
     if (kv->slot_of(layer, &slot)) return -1;
-    /* causal rows through the decode kernel, 64 query tokens per launch */
-    std::vector<int32_t> seqs(Q38_MAX_BATCH, seq), pos(Q38_MAX_BATCH);
-    for (int t0 = 0; t0 < n_tokens; t0 += Q38_MAX_BATCH) {
-        const int n = std::min(Q38_MAX_BATCH, n_tokens - t0);
-        for (int i = 0; i < n; ++i) pos[i] = base_pos + t0 + i;
-        const size_t off = (size_t)t0 * Q38_ATTN_Q_DIM;
-        if (decode_chunk(kv, slot, n, seqs.data(), pos.data(), d_q + off, nullptr, nullptr,
-                         d_gate ? d_gate + off : nullptr, d_out + off))
-            return -1;
-    }
-    return 0;
+    q38_ctx *ctx = kv->ctx;
+    constexpr int kQueryBlock = 16; /* query tokens per workgroup of the kernel */
+    q38_prefill_args a;
+    memset(&a, 0, sizeof(a));
+    a.kpool = kv->kslot(slot);
+    a.vpool = kv->vslot(slot);
+    a.page_table = kv->d_page_table + (size_t)seq * kv->pt_stride;
+    a.q = d_q;
+    a.gate = d_gate;
+    a.out = d_out;
+    a.base_pos = base_pos;
+    a.n_tokens = n_tokens;
+    a.n_qblocks = (n_tokens + kQueryBlock - 1) / kQueryBlock;
+    return ctx->launch(ctx->f_prefill, a.n_qblocks, Q38_ATTN_KV_HEADS, 1, 64 * Q38_ATTN_GROUP, &a);
 }
 
 /* ---------------------------------------------------------------- DeltaNet */
@@ -864,8 +878,22 @@ int q38_gdn_step(q38_ctx *ctx, int n_seq, float *d_state, int64_t state_stride, 
     if (n_seq > 65535) return fail("n_seq %d above 65535", n_seq);
     if (n_seq > 1 && state_stride < (int64_t)Q38_LIN_STATE_FLOATS)
         return fail("state_stride %lld overlaps states", (long long)state_stride);
-    return gdn_launch(ctx, n_seq, 1, d_state, state_stride, d_q, d_k, d_v, d_beta, d_g, d_out,
-                      Q38_LIN_QK_DIM, Q38_LIN_V_DIM, nullptr, nullptr);
+    /* one token: the row-parallel kernel (8 workgroups per value head) */
+    q38_gdn_args a;
+    memset(&a, 0, sizeof(a));
+    a.state = d_state;
+    a.q = d_q;
+    a.k = d_k;
+    a.v = d_v;
+    a.beta = d_beta;
+    a.g = d_g;
+    a.out = d_out;
+    a.state_stride = state_stride;
+    a.q_stride = Q38_LIN_QK_DIM;
+    a.v_stride = Q38_LIN_V_DIM;
+    a.n_tokens = 1;
+    a.n_seq = n_seq;
+    return ctx->launch(ctx->f_gdn_step_rows, Q38_LIN_V_HEADS * (Q38_LIN_HEAD_DIM / 16), n_seq, 1, 256, &a);
 }
 
 int q38_gdn_prefill(q38_ctx *ctx, float *d_state, int n_tokens, const float *d_q, const float *d_k,

@@ -204,3 +204,51 @@ extern "C" __global__ __launch_bounds__(128) void q38_gdn_pre(q38_gdn_pre_args a
         st_out[2] = win[2];
     }
 }
+
+/* One recurrent step (n_tokens == 1) spread over the whole chip: the 128
+ * rows of a value head are independent (ops.rs:707-713 touches row c only
+ * through k, q, v_c, beta and the decay), so a workgroup takes 16 rows of
+ * one head -- grid (48 heads x 8 row blocks, n_seq), 256 threads, 16 lanes
+ * per row, lane i holding columns 4i..4i+3 and 64+4i..64+4i+3.  Every load
+ * of a thread (its 8 state values, k, q, v_c, beta, g) is issued at once,
+ * so the step costs one memory round trip; the state is read and written
+ * exactly once.  Arithmetic per row is the same as q38_gdn_recurrent's. */
+extern "C" __global__ __launch_bounds__(256) void q38_gdn_step_rows(q38_gdn_args a) {
+    constexpr int kRowBlocks = Q38_LIN_HEAD_DIM / 16;
+    const int vh = blockIdx.x / kRowBlocks;
+    const int rb = blockIdx.x % kRowBlocks;
+    const size_t s = blockIdx.y;
+    const int kh = vh % Q38_LIN_QK_HEADS;
+    const int tid = threadIdx.x;
+    const int row = rb * 16 + (tid >> 4);
+    const int li = tid & 15;
+    const int d0 = 4 * li;
+    const int d1 = 64 + 4 * li;
+    const float query_scale = 1.0f / sqrtf((float)Q38_LIN_HEAD_DIM);
+
+    float *st = a.state + s * a.state_stride + ((size_t)vh * Q38_LIN_HEAD_DIM + row) * Q38_LIN_HEAD_DIM;
+    f32x4 S0 = q38_ld4_stream(st + d0);
+    f32x4 S1 = q38_ld4_stream(st + d1);
+    const float *kp = a.k + s * a.q_stride + kh * Q38_LIN_HEAD_DIM;
+    const float *qp = a.q + s * a.q_stride + kh * Q38_LIN_HEAD_DIM;
+    const f32x4 k0 = q38_ld4(kp + d0), k1 = q38_ld4(kp + d1);
+    const f32x4 q0 = q38_ld4(qp + d0), q1 = q38_ld4(qp + d1);
+    const float v = a.v[s * a.v_stride + vh * Q38_LIN_HEAD_DIM + row];
+    const float beta = a.beta[s * Q38_LIN_V_HEADS + vh];
+    const float decay = expf(a.g[s * Q38_LIN_V_HEADS + vh]);
+
+    S0 *= decay;
+    S1 *= decay;
+    float pred = q38_dot4(S0, k0, 0.0f);
+    pred = q38_dot4(S1, k1, pred);
+    pred = q38_sum16(pred);
+    const float delta = (v - pred) * beta;
+    S0 = q38_fma4(delta, k0, S0);
+    S1 = q38_fma4(delta, k1, S1);
+    float res = q38_dot4(S0, q0, 0.0f);
+    res = q38_dot4(S1, q1, res);
+    res = q38_sum16(res);
+    q38_st4_stream(st + d0, S0);
+    q38_st4_stream(st + d1, S1);
+    if (li == 0) a.out[s * Q38_LIN_V_DIM + vh * Q38_LIN_HEAD_DIM + row] = res * query_scale;
+}

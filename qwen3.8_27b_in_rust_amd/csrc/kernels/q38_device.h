@@ -70,6 +70,11 @@ Q38_DEV f32x4 q38_ld4_stream(const float *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
 }
 
+/* Streaming store of data no kernel of this launch reads again. */
+Q38_DEV void q38_st4_stream(float *p, f32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p));
+}
+
 Q38_DEV float q38_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 /* 1/(1+exp(-x)), ops.rs:501-503, with the accurate expf. */

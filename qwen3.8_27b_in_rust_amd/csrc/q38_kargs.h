@@ -130,6 +130,22 @@ typedef struct {
     int32_t n_seq;
 } q38_gdn_pre_args;
 
+/* Causal prefill attention of one sequence on bf16 MFMA.  grid (n_qblocks,
+ * 4 kv heads), 6 waves (one per query head of the group), 32 query tokens
+ * per workgroup. */
+typedef struct {
+    const float *kpool;        /* this layer's K pages: [max_pages][4][16][256] */
+    const float *vpool;
+    const int32_t *page_table; /* the sequence's row of the page table */
+    const float *q;            /* [n_tokens][24][256] for positions base_pos.. */
+    const float *gate;         /* [n_tokens][24][256] or NULL */
+    float *out;                /* [n_tokens][24][256] */
+    int32_t base_pos;
+    int32_t n_tokens;
+    int32_t n_qblocks;
+    int32_t pad_;
+} q38_prefill_args;
+
 /* Merge of split-K partials.  grid (n_seq, 24, 4). */
 typedef struct {
     const float *part_o;

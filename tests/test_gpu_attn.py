@@ -222,6 +222,60 @@ def test_prefill_matches_reference_rows(pkg, ctx, ref):
     assert worst <= TOL
 
 
+def _prefill_case(pkg, ctx, ref, base, T, seed, gate=True, permute=False, rows=None):
+    """Prefill of T tokens after a base-token prefix through q38_attn_prefill
+    (bf16x3 MFMA kernel); rows (default: all) against the restatement."""
+    from q38amd import synth
+    n_pages = (base + T + 15) // 16
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=n_pages + 8, max_seqs=1, max_tokens_per_seq=base + T)
+    try:
+        seq = kv.seq_create()
+        if permute:
+            pages = np.random.default_rng(seed).permutation(n_pages + 8)[:n_pages]
+            kv.seq_set_pages(seq, pages.tolist())
+        layer = 7
+        K = synth.normal(seed + 1, (base + T) * 1024)
+        V = synth.normal(seed + 2, (base + T) * 1024)
+        Q = synth.normal(seed + 3, T * 6144)
+        G = synth.normal(seed + 4, T * 6144) if gate else None
+        d_k, d_v = ctx.array(K), ctx.array(V)
+        if base:
+            kv.write(layer, seq, 0, base, d_k, d_v)
+        d_o = ctx.empty((T, 24, 256))
+        kv.attn_prefill(layer, seq, base, T, ctx.array(Q), d_k.offset(base * 1024), d_v.offset(base * 1024), d_o,
+                        gate=ctx.array(G) if gate else None)
+        got = d_o.download()
+        Kr, Vr = K.reshape(-1, 1024), V.reshape(-1, 1024)
+        worst = 0.0
+        for t in (range(T) if rows is None else rows):
+            n_pos = base + t + 1
+            want = ref.attn_heads(Q[t * 6144:(t + 1) * 6144], Kr[:n_pos], Vr[:n_pos],
+                                  gate=None if G is None else G[t * 6144:(t + 1) * 6144])
+            worst = max(worst, float(np.max(np.abs(got[t] - want))))
+        return worst
+    finally:
+        kv.close()
+
+
+@pytest.mark.parametrize("T", [1, 2, 15, 16, 17, 31, 33, 100])
+def test_prefill_short_prompts_all_rows(pkg, ctx, ref, T):
+    """Ragged prompt lengths from position 0 (partial query and key blocks)."""
+    assert _prefill_case(pkg, ctx, ref, 0, T, 900 + T) <= TOL
+
+
+def test_prefill_permuted_pages_no_gate(pkg, ctx, ref):
+    """Randomly permuted page table, prefix of 37 tokens, no output gate."""
+    assert _prefill_case(pkg, ctx, ref, 37, 150, 960, gate=False, permute=True) <= TOL
+
+
+def test_prefill_4096_prompt(pkg, ctx, ref):
+    """The chunked-prefill workload: a 4096-token causal prompt; sampled rows
+    cover every query block position and both ends."""
+    rows = sorted(set([0, 1, 15, 16, 17, 31, 32, 1000, 2047, 2048, 4000, 4094, 4095]
+                      + list(np.random.default_rng(7).integers(0, 4096, 12))))
+    assert _prefill_case(pkg, ctx, ref, 0, 4096, 980, rows=rows) <= TOL
+
+
 def test_kv_pages_roundtrip_and_rollback(pkg, ctx, synth):
     """Write/read through a permuted page table; truncate releases whole pages
     past the kept positions; reset releases all."""
