@@ -181,6 +181,123 @@ def prefill_attention(pkg, ctx, reps: int):
                     "algorithmic flops count each product once"}
 
 
+def batched_decode(pkg, ctx, steps: int, warmup: int):
+    """Batched paged decode: 32 sequences, context lengths ~U[1024, 32768]
+    (seeded), 16-token pages placed by a random permutation of the pool, one
+    decode token per sequence (append + attention + gate)."""
+    rng = np.random.default_rng(0x51334300)
+    n = 32
+    ctxs = rng.integers(1024, 32769, n)
+    pages = [(int(c) + 15) // 16 for c in ctxs]
+    pool = sum(pages) + 64
+    kv = pkg.KVCache(ctx, n_slots=1, max_pages=pool, max_seqs=n, max_tokens_per_seq=32768)
+    perm = rng.permutation(pool)
+    seqs, at = [], 0
+    rows_k, rows_v = ctx.empty((32768, 1024)), ctx.empty((32768, 1024))
+    for i in range(n):
+        s = kv.seq_create()
+        kv.seq_set_pages(s, perm[at:at + pages[i]].tolist())
+        at += pages[i]
+        c = int(ctxs[i])
+        ctx.fill_normal(rows_k, c * 1024, 0x51334310 + 2 * i)
+        ctx.fill_normal(rows_v, c * 1024, 0x51334311 + 2 * i)
+        kv.write(3, s, 0, c, rows_k, rows_v)
+        seqs.append(s)
+    q, g, o = ctx.empty((n, 6144)), ctx.empty((n, 6144)), ctx.empty((n, 6144))
+    kn, vn = ctx.empty((n, 1024)), ctx.empty((n, 1024))
+    for i, (b, m) in enumerate(((q, n * 6144), (g, n * 6144), (kn, n * 1024), (vn, n * 1024))):
+        ctx.fill_normal(b, m, 0x51334390 + i)
+    positions = [int(c) - 1 for c in ctxs]
+
+    def step():
+        kv.attn_decode(3, seqs, positions, q, o, k_new=kn, v_new=vn, gate=g)
+
+    for _ in range(warmup):
+        step()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.kernel_timer_start("q38_attn_decode_split", steps)
+    ctx.record(e0)
+    for _ in range(steps):
+        step()
+    ctx.record(e1)
+    ms = ctx.elapsed_ms(e0, e1) / steps
+    k_ms, k_n = ctx.kernel_timer_stop()
+    kv.close()
+    for b in (rows_k, rows_v, q, g, o, kn, vn):
+        b.free()
+    total = int(ctxs.sum())
+    alg = total * 8192 + n * 2 * 6144 * 4
+    kern = k_ms / max(k_n, 1)
+    return {"sequences": n, "total_context_tokens": total, "algorithmic_bytes": alg,
+            "step_ms": ms, "split_kernel_ms": kern,
+            "step_gb_s": alg / (ms * 1e-3) / 1e9, "step_frac_hbm": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "split_kernel_gb_s": alg / (kern * 1e-3) / 1e9,
+            "split_kernel_frac_hbm": alg / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def full_stack(pkg, ctx, tokens: int, warmup: int):
+    """One decode token through the attention path of all 64 layers of the
+    hybrid (layer % 4 == 3 full attention, the other 48 Gated DeltaNet),
+    batch 1, 131072 cached tokens: full_core (norms, RoPE, append, attention,
+    gate) and linear_core (conv, gates, recurrence, gated norm) per layer, in
+    layer order.  Projections are outside the path and not run."""
+    CTXF = 131072
+    pos = CTXF - 1
+    kv = pkg.KVCache(ctx, n_slots=16, max_pages=CTXF // 16, max_seqs=1, max_tokens_per_seq=CTXF)
+    seq = kv.seq_create()
+    rows_k, rows_v = ctx.empty((CTXF, 1024)), ctx.empty((CTXF, 1024))
+    full_layers = [l for l in range(64) if (l + 1) % 4 == 0]
+    lin_layers = [l for l in range(64) if (l + 1) % 4 != 0]
+    for i, layer in enumerate(full_layers):
+        ctx.fill_normal(rows_k, CTXF * 1024, 0x51334400 + 2 * i)
+        ctx.fill_normal(rows_v, CTXF * 1024, 0x51334401 + 2 * i)
+        kv.write(layer, seq, 0, pos, rows_k, rows_v)
+    rows_k.free()
+    rows_v.free()
+    per = 48 * 128 * 128
+    states = ctx.empty((48 * per,))
+    ctx.fill_normal(states, 48 * per, 0x51334480, sigma=0.02)
+    conv = ctx.empty((48 * 30720,))
+    ctx.fill_normal(conv, 48 * 30720, 0x51334481)
+    bufs = {}
+    for name, m in (("qn", 256), ("kn", 256), ("qg", 12288), ("key", 1024), ("val", 1024), ("conv_w", 40960),
+                    ("dt", 48), ("a", 48), ("norm", 128), ("qkv", 10240), ("z", 6144), ("beta", 48),
+                    ("alpha", 48), ("out_a", 6144), ("out_l", 6144)):
+        bufs[name] = ctx.empty((m,))
+        ctx.fill_normal(bufs[name], m, 0x51334490 + len(bufs))
+    b = bufs
+
+    def token():
+        li = 0
+        for layer in range(64):
+            if (layer + 1) % 4 == 0:
+                kv.full_core(layer, [seq], [pos], b["qn"], b["kn"], b["qg"], b["key"], b["val"], b["out_a"])
+            else:
+                ctx.linear_core(1, 1, b["conv_w"], b["dt"], b["a"], b["norm"], conv.offset(li * 30720),
+                                states.offset(li * per), b["qkv"], b["z"], b["beta"], b["alpha"], b["out_l"])
+                li += 1
+
+    for _ in range(warmup):
+        token()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(tokens):
+        token()
+    ctx.record(e1)
+    ms = ctx.elapsed_ms(e0, e1) / tokens
+    kv.close()
+    states.free()
+    conv.free()
+    for v in bufs.values():
+        v.free()
+    alg = 16 * CTXF * 8192 + 48 * 2 * per * 4
+    return {"layers": 64, "full_attention_layers": len(full_layers), "deltanet_layers": len(lin_layers),
+            "context": CTXF, "ms_per_token": ms, "tokens_per_s": 1e3 / ms, "algorithmic_bytes": alg,
+            "gb_s": alg / (ms * 1e-3) / 1e9, "frac_hbm": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
 def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float):
     """The CPU restatement of the reference's attention (ops.rs:868-938) on the
     32K workload, all cores of this host (heads split across threads as the
@@ -289,6 +406,12 @@ def main():
         log("prefill attention: 4096-token causal prompt")
         extra["prefill_attention_4096"] = prefill_attention(pkg, ctx, 5)
         log(f"prefill: {json.dumps(extra['prefill_attention_4096'])}")
+        log("batched paged decode: 32 sequences, context ~U[1K, 32K]")
+        extra["batched_decode_32"] = batched_decode(pkg, ctx, 20, 3)
+        log(f"batched: {json.dumps(extra['batched_decode_32'])}")
+        log("full stack: 64 layers (48 DeltaNet + 16 attention), 128K context, one token")
+        extra["full_stack_128k"] = full_stack(pkg, ctx, 10, 2)
+        log(f"full stack: {json.dumps(extra['full_stack_128k'])}")
         log("Gated-DeltaNet step: 1 state per launch over 192 states; 32 per launch over 192")
         extra["gdn_step_1"] = gdn_steps(pkg, ctx, 1, 192, 384, 32)
         extra["gdn_step_32"] = gdn_steps(pkg, ctx, 32, 192, 60, 6)

@@ -34,7 +34,7 @@
 
 #define Q38_MAX_BATCH 64 /* sequences per decode launch */
 #define Q38_MAX_SPLITS 4096 /* splits of one sequence in one decode launch */
-#define Q38_MAX_SPLIT_TOKENS 1024 /* context tokens one decode workgroup streams */
+#define Q38_MAX_SPLIT_TOKENS 4096 /* context tokens one decode workgroup streams */
 #define Q38_DECODE_WAVES 4 /* waves of a decode workgroup */
 
 /* Split-K paged decode: grid (total_splits, 4 kv heads). */

@@ -68,10 +68,18 @@ def test_decode_ragged_lengths(pkg, ctx, ref, P):
     assert float(np.max(np.abs(got - want))) <= TOL
 
 
-@pytest.mark.parametrize("split", [64, 128, 512, 1024])
+@pytest.mark.parametrize("split", [64, 128, 512, 1024, 2048, 4096])
 def test_decode_split_invariance(pkg, ctx, ref, split):
+    """Splits from one page per wave to the whole context in one workgroup."""
     got, Q, K, V, G = _decode_one(pkg, ctx, 3000, 9100, gate=True, split=split)
     want = ref.attn_heads(Q, K, V, gate=G)
+    assert float(np.max(np.abs(got - want))) <= TOL
+
+
+def test_decode_128k_context(pkg, ctx, ref):
+    """The full-stack context: 131072 cached tokens (2048-token splits)."""
+    got, Q, K, V, G = _decode_one(pkg, ctx, 131072, 0x51333820, gate=True)
+    want = ref.attn_heads(Q, K, V, gate=G, threads=16)
     assert float(np.max(np.abs(got - want))) <= TOL
 
 
