@@ -298,6 +298,41 @@ def full_stack(pkg, ctx, tokens: int, warmup: int):
             "gb_s": alg / (ms * 1e-3) / 1e9, "frac_hbm": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+# chunked Gated-DeltaNet flops per (value head, 64-token chunk): KK^T, QK^T,
+# W = T(bgK), U' = T(bV) (4 x 64*64*128*2), the triangular inverse (~64^3/3*2),
+# and the state products W S^T, Q S^T, U^T K (3 x 64*128*128*2) and Bm U
+GDN_CHUNK_FLOPS = 4 * 64 * 64 * 128 * 2 + (64 ** 3 // 3) * 2 + 3 * 64 * 128 * 128 * 2 + 64 * 64 * 128 * 2
+
+
+def gdn_prefill(pkg, ctx, reps: int):
+    """Chunked Gated-DeltaNet prefill of a 4096-token prompt (one layer, 48
+    value heads, 64-token chunks on bf16x3 MFMA): prep + scan time per prompt."""
+    from q38amd import synth
+    T = PREFILL_T
+    per = 48 * 128 * 128
+    state = ctx.empty((per,))
+    q, k, v, beta, g = synth.GdnStepInputs(0x51334a00).steps(0, T)
+    dq, dk, dv, db, dg = (ctx.array(x) for x in (q, k, v, beta, g))
+    out = ctx.empty((T, 6144))
+    ctx.fill_normal(state, per, 0x51334a01, sigma=0.02)
+    ctx.gdn_prefill(state, T, dq, dk, dv, db, dg, out)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(reps):
+        ctx.gdn_prefill(state, T, dq, dk, dv, db, dg, out)
+    ctx.record(e1)
+    ms = ctx.elapsed_ms(e0, e1) / reps
+    for b in (state, dq, dk, dv, db, dg, out):
+        b.free()
+    flops = GDN_CHUNK_FLOPS * 48 * (T // 64)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"tokens": T, "ms": ms, "algorithmic_gflop": flops / 1e9, "tflop_s": tflops,
+            "frac_bf16_peak": tflops / BF16_PEAK_TFLOPS,
+            "note": "prep (KK^T, QK^T, triangular inverse, W, U') and scan (state products) kernels, "
+                    "bf16x3 MFMA products"}
+
+
 def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float):
     """The CPU restatement of the reference's attention (ops.rs:868-938) on the
     32K workload, all cores of this host (heads split across threads as the
@@ -406,6 +441,9 @@ def main():
         log("prefill attention: 4096-token causal prompt")
         extra["prefill_attention_4096"] = prefill_attention(pkg, ctx, 5)
         log(f"prefill: {json.dumps(extra['prefill_attention_4096'])}")
+        log("chunked Gated-DeltaNet prefill: 4096 tokens")
+        extra["gdn_prefill_4096"] = gdn_prefill(pkg, ctx, 5)
+        log(f"gdn prefill: {json.dumps(extra['gdn_prefill_4096'])}")
         log("batched paged decode: 32 sequences, context ~U[1K, 32K]")
         extra["batched_decode_32"] = batched_decode(pkg, ctx, 20, 3)
         log(f"batched: {json.dumps(extra['batched_decode_32'])}")

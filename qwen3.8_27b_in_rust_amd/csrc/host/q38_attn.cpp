@@ -80,6 +80,10 @@ struct q38_ctx {
     hipModule_t mod_gdn = nullptr;
     hipModule_t mod_prefill = nullptr;
     hipFunction_t f_prefill = nullptr;
+    hipModule_t mod_gdn_chunk = nullptr;
+    hipFunction_t f_chunk_prep = nullptr;
+    hipFunction_t f_chunk_scan = nullptr;
+    hipFunction_t f_gdn_post = nullptr;
     hipFunction_t f_decode_split = nullptr;
     hipFunction_t f_decode_merge = nullptr;
     hipFunction_t f_kv_copy = nullptr;
@@ -250,6 +254,11 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     const std::string p_gdn = dir + "/gdn.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_decode, p_decode.c_str()));
     Q38_HIP(hipModuleLoad(&ctx->mod_gdn, p_gdn.c_str()));
+    const std::string p_chunk = dir + "/gdn_chunk.hsaco";
+    Q38_HIP(hipModuleLoad(&ctx->mod_gdn_chunk, p_chunk.c_str()));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_chunk_prep, ctx->mod_gdn_chunk, "q38_gdn_chunk_prep"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_chunk_scan, ctx->mod_gdn_chunk, "q38_gdn_chunk_scan"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_post, ctx->mod_gdn_chunk, "q38_gdn_post"));
     const std::string p_prefill = dir + "/attn_prefill.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_prefill, p_prefill.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_prefill, ctx->mod_prefill, "q38_attn_prefill_mfma"));
@@ -282,6 +291,7 @@ int q38_ctx_destroy(q38_ctx *ctx) {
     if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
     if (ctx->mod_gdn) (void)hipModuleUnload(ctx->mod_gdn);
     if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
+    if (ctx->mod_gdn_chunk) (void)hipModuleUnload(ctx->mod_gdn_chunk);
     if (ctx->mod_synth) (void)hipModuleUnload(ctx->mod_synth);
     for (hipEvent_t e : ctx->timer_events) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -414,6 +424,9 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gdn_step_rows") f = ctx->f_gdn_step_rows;
     else if (name == "q38_copy_f32") f = ctx->f_copy;
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
+    else if (name == "q38_gdn_chunk_prep") f = ctx->f_chunk_prep;
+    else if (name == "q38_gdn_chunk_scan") f = ctx->f_chunk_scan;
+    else if (name == "q38_gdn_post") f = ctx->f_gdn_post;
     else return fail("unknown kernel %s", kernel_name);
     while ((int)ctx->timer_events.size() < 2 * max_launches) {
         hipEvent_t e;
@@ -614,13 +627,13 @@ int q38_kv_read(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float *d
 namespace {
 
 /* Context tokens per decode workgroup: a multiple of 64, at least 64 and at
- * most Q38_MAX_SPLIT_TOKENS, chosen to give one workgroup per CU (the split
- * kernel streams fastest with one workgroup per CU: 46 us at 32768 tokens
- * against 50 us with two); Q38_SPLIT_TOKENS overrides (rounded up to a
- * multiple of 64). */
+ * most Q38_MAX_SPLIT_TOKENS, chosen to give one workgroup per CU for one
+ * sequence (the split kernel streams fastest so: 46 us at 32768 tokens
+ * against 50 us with two per CU); Q38_SPLIT_TOKENS overrides (rounded up to
+ * a multiple of 64). */
 constexpr int kMaxSplitsPerSeq = Q38_MAX_SPLITS; /* LDS weights of the merge kernel */
 
-int choose_split_tokens(const q38_ctx *ctx, long total_tokens, long max_tokens, int *split_out) {
+int choose_split_tokens(const q38_ctx *ctx, int n_seq, long total_tokens, long max_tokens, int *split_out) {
     long split = 64;
     const char *env = getenv("Q38_SPLIT_TOKENS");
     if (env != nullptr && atoi(env) >= 64) {
@@ -629,6 +642,11 @@ int choose_split_tokens(const q38_ctx *ctx, long total_tokens, long max_tokens, 
         const long slots = std::max(ctx->cu_count, 1);
         const long per = (total_tokens * Q38_ATTN_KV_HEADS + slots - 1) / slots;
         split = std::min<long>(std::max<long>((per + 63) / 64 * 64, 64), Q38_MAX_SPLIT_TOKENS);
+        /* sequences of different lengths make workgroups of different
+         * lengths; past one round of workgroups, 1024-token splits balance
+         * them best (32 sequences of 1K-32K tokens: 74% of HBM against 64%
+         * with 4096-token splits) */
+        if (n_seq > 1) split = std::min<long>(split, 1024);
     }
     /* no sequence may need more splits than the merge kernel holds, and no
      * split more pages than the kernel's page-id array */
@@ -651,7 +669,7 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
         max_tokens = std::max<long>(max_tokens, positions[b] + 1);
     }
     int split_tokens = 0;
-    if (choose_split_tokens(ctx, total_tokens, max_tokens, &split_tokens)) return -1;
+    if (choose_split_tokens(ctx, n_seq, total_tokens, max_tokens, &split_tokens)) return -1;
 
     q38_decode_args a;
     memset(&a, 0, sizeof(a));
@@ -792,7 +810,7 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
             max_tokens = std::max<long>(max_tokens, positions[b0 + b] + 1);
         }
         int split = 0;
-        if (choose_split_tokens(ctx, total_tokens, max_tokens, &split)) return -1;
+        if (choose_split_tokens(ctx, n, total_tokens, max_tokens, &split)) return -1;
         size_t splits = 0;
         for (int b = 0; b < n; ++b) splits += (positions[b0 + b] + split) / split;
         const size_t part_floats = splits * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2);
@@ -845,11 +863,20 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
 
 /* ---------------------------------------------------------------- DeltaNet */
 
-static int gdn_launch(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, int64_t state_stride,
-                      const float *d_q, const float *d_k, const float *d_v, const float *d_beta,
-                      const float *d_g, float *d_out, int q_stride, int v_stride, const float *d_z,
-                      const float *d_norm) {
-    q38_gdn_args a;
+/* Chunked recurrence over n_tokens > 1 tokens of n_seq states (the token
+ * loop of ops.rs:1088-1099 in 64-token chunks); work holds
+ * chunk_work_floats(n_seq, n_tokens) floats. */
+static size_t chunk_work_floats(int n_seq, int n_tokens) {
+    const size_t n_chunks = ((size_t)n_tokens + Q38_GDN_CHUNK - 1) / Q38_GDN_CHUNK;
+    return (size_t)n_seq * Q38_LIN_V_HEADS * n_chunks * Q38_GDN_CHUNK_FLOATS;
+}
+
+static int gdn_chunked(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, int64_t state_stride,
+                       const float *d_q, const float *d_k, const float *d_v, const float *d_beta,
+                       const float *d_g, float *d_out, int q_stride, int v_stride, float *work) {
+    const int n_chunks = (n_tokens + Q38_GDN_CHUNK - 1) / Q38_GDN_CHUNK;
+    if (n_chunks > 65535) return fail("%d tokens exceed the chunked prefill's 65535 chunks", n_tokens);
+    q38_gdn_chunk_args a;
     memset(&a, 0, sizeof(a));
     a.state = d_state;
     a.q = d_q;
@@ -858,14 +885,14 @@ static int gdn_launch(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, int
     a.beta = d_beta;
     a.g = d_g;
     a.out = d_out;
-    a.z = d_z;
-    a.norm_w = d_norm;
+    a.work = work;
     a.state_stride = state_stride;
     a.q_stride = q_stride;
     a.v_stride = v_stride;
     a.n_tokens = n_tokens;
-    a.n_seq = n_seq;
-    return ctx->launch(ctx->f_gdn_recurrent, Q38_LIN_V_HEADS, n_seq, 1, 512, &a);
+    a.n_chunks = n_chunks;
+    if (ctx->launch(ctx->f_chunk_prep, Q38_LIN_V_HEADS, n_chunks, n_seq, 256, &a)) return -1;
+    return ctx->launch(ctx->f_chunk_scan, Q38_LIN_V_HEADS * 4, n_seq, 1, 256, &a);
 }
 
 int q38_gdn_step(q38_ctx *ctx, int n_seq, float *d_state, int64_t state_stride, const float *d_q,
@@ -902,8 +929,11 @@ int q38_gdn_prefill(q38_ctx *ctx, float *d_state, int n_tokens, const float *d_q
     if (n_tokens < 0) return fail("negative n_tokens");
     if (n_tokens == 0) return 0;
     if (!d_state || !d_q || !d_k || !d_v || !d_beta || !d_g || !d_out) return fail("NULL argument");
-    return gdn_launch(ctx, 1, n_tokens, d_state, Q38_LIN_STATE_FLOATS, d_q, d_k, d_v, d_beta, d_g,
-                      d_out, Q38_LIN_QK_DIM, Q38_LIN_V_DIM, nullptr, nullptr);
+    if (n_tokens == 1)
+        return q38_gdn_step(ctx, 1, d_state, Q38_LIN_STATE_FLOATS, d_q, d_k, d_v, d_beta, d_g, d_out);
+    if (ctx->ensure_work(chunk_work_floats(1, n_tokens) * sizeof(float))) return -1;
+    return gdn_chunked(ctx, 1, n_tokens, d_state, Q38_LIN_STATE_FLOATS, d_q, d_k, d_v, d_beta, d_g, d_out,
+                       Q38_LIN_QK_DIM, Q38_LIN_V_DIM, static_cast<float *>(ctx->work));
 }
 
 int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weights *w,
@@ -918,14 +948,19 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
     if (n_seq > 65535) return fail("n_seq %d above 65535", n_seq);
     const int n_chunks = (n_tokens + 63) / 64;
     const size_t toks = (size_t)n_seq * n_tokens;
-    /* workspace: qkv after conv/SiLU/L2 | beta | g | conv state out */
+    /* workspace: qkv after conv/SiLU/L2 | beta | g | conv state out |
+     * (n_tokens > 1) recurrence output before the norm | chunk products */
     const size_t conv_floats = (size_t)n_seq * Q38_LIN_QKV_DIM * 3;
-    const size_t need = toks * (Q38_LIN_QKV_DIM + 2 * Q38_LIN_V_HEADS) + (n_chunks > 1 ? conv_floats : 0);
-    if (ctx->ensure_work(need * sizeof(float))) return -1;
+    const size_t base_floats = toks * (Q38_LIN_QKV_DIM + 2 * Q38_LIN_V_HEADS) + (n_chunks > 1 ? conv_floats : 0);
+    const size_t o_floats = n_tokens > 1 ? toks * Q38_LIN_V_DIM : 0;
+    const size_t chunk_floats = n_tokens > 1 ? chunk_work_floats(n_seq, n_tokens) : 0;
+    if (ctx->ensure_work((base_floats + o_floats + chunk_floats) * sizeof(float))) return -1;
     float *x = static_cast<float *>(ctx->work);
     float *beta = x + toks * Q38_LIN_QKV_DIM;
     float *g = beta + toks * Q38_LIN_V_HEADS;
     float *conv_out = n_chunks > 1 ? g + toks * Q38_LIN_V_HEADS : d_conv_state;
+    float *o_raw = x + base_floats;
+    float *chunk_work = o_raw + o_floats;
 
     q38_gdn_pre_args p;
     memset(&p, 0, sizeof(p));
@@ -946,6 +981,21 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
     if (n_chunks > 1)
         Q38_HIP(hipMemcpyAsync(d_conv_state, conv_out, conv_floats * sizeof(float),
                                hipMemcpyDeviceToDevice, ctx->stream));
+    if (n_tokens > 1) {
+        /* prompt: chunked recurrence, then the gated RMSNorm */
+        if (gdn_chunked(ctx, n_seq, n_tokens, d_delta_state, Q38_LIN_STATE_FLOATS, x, x + Q38_LIN_QK_DIM,
+                        x + 2 * Q38_LIN_QK_DIM, beta, g, o_raw, Q38_LIN_QKV_DIM, Q38_LIN_QKV_DIM, chunk_work))
+            return -1;
+        if (toks > 0x7FFFFFFFull) return fail("too many tokens");
+        q38_gdn_post_args pa;
+        memset(&pa, 0, sizeof(pa));
+        pa.o = o_raw;
+        pa.z = d_z;
+        pa.norm_w = w->d_norm;
+        pa.out = d_out;
+        return ctx->launch(ctx->f_gdn_post, (unsigned)toks, Q38_LIN_V_HEADS, 1, 64, &pa);
+    }
+    /* one token: the recurrence with the gated RMSNorm fused */
     q38_gdn_args a;
     memset(&a, 0, sizeof(a));
     a.state = d_delta_state;

@@ -106,3 +106,48 @@ Q38_DEV double q38_wave_sum_f64(double x) {
     for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
     return x;
 }
+
+/* ------------------------------------------------ bf16x3 matrix-core tiles */
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+/* x = hi + lo with hi = bf16(x), lo = bf16(x - hi): hi + lo is within
+ * ~2^-16 of x, so hi*hi + hi*lo + lo*hi carries f32-class products. */
+Q38_DEV void q38_split8(const float (&x)[8], bf16x8 &hi, bf16x8 &lo) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const __bf16 h = (__bf16)x[j];
+        hi[j] = h;
+        lo[j] = (__bf16)(x[j] - (float)h);
+    }
+}
+
+/*
+ * One 16x16 output tile on v_mfma_f32_16x16x32_bf16 with bf16x3 products:
+ * c += A B, A(m, k) = fa(m, k) (16 x KD), B(k, n) = fb(k, n) (KD x 16),
+ * KD a multiple of 32.  Lane l supplies A row l%16 and B column l%16 at
+ * k = k0 + 8(l/16) .. +7; the tile it returns holds rows 4(l/16) + i
+ * (i = 0..3) of column l%16.
+ */
+template <int KD, class FA, class FB>
+Q38_DEV f32x4 q38_mma16(f32x4 c, FA fa, FB fb) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    const int r = lane & 15;
+#pragma unroll
+    for (int k0 = 0; k0 < KD; k0 += 32) {
+        float av[8], bv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            av[j] = fa(r, k0 + 8 * g + j);
+            bv[j] = fb(k0 + 8 * g + j, r);
+        }
+        bf16x8 ah, al, bh, bl;
+        q38_split8(av, ah, al);
+        q38_split8(bv, bh, bl);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+    }
+    return c;
+}

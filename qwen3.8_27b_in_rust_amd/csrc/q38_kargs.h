@@ -111,6 +111,38 @@ typedef struct {
     int32_t n_seq;
 } q38_gdn_args;
 
+/* Chunked Gated-DeltaNet prefill (chunk Q38_GDN_CHUNK tokens).  The prep
+ * kernel (grid (48 value heads, n_chunks, n_seq)) writes, per head and chunk,
+ * Q38_GDN_CHUNK_FLOATS floats to `work`: W [64][128] | U' [64][128] |
+ * B [64][64] | G [64]; the scan kernel (grid (48 x 4 row slabs, n_seq))
+ * carries the state through the chunks. */
+#define Q38_GDN_CHUNK 64
+#define Q38_GDN_CHUNK_FLOATS (2 * 64 * 128 + 64 * 64 + 64)
+typedef struct {
+    float *state;      /* seq s at state + s*state_stride: [48][128][128] */
+    const float *q;    /* token (s*T + t): q + (s*T + t)*q_stride + kh*128 */
+    const float *k;
+    const float *v;    /* v + (s*T + t)*v_stride + vh*128 */
+    const float *beta; /* [(s*T + t)*48 + vh], post-sigmoid */
+    const float *g;    /* log-decay, same layout */
+    float *out;        /* [(s*T + t)*6144 + vh*128 + c], before the gated norm */
+    float *work;       /* [n_seq][48][n_chunks][Q38_GDN_CHUNK_FLOATS] */
+    int64_t state_stride;
+    int32_t q_stride;
+    int32_t v_stride;
+    int32_t n_tokens;
+    int32_t n_chunks;
+} q38_gdn_chunk_args;
+
+/* Gated RMSNorm of ops.rs:735-740 on [n][48][128] recurrence outputs:
+ * grid (n_tokens * n_seq, 48), 64 threads. */
+typedef struct {
+    const float *o;    /* [(s*T + t)*6144 + vh*128 + c] */
+    const float *z;    /* same layout */
+    const float *norm_w; /* [128] */
+    float *out;
+} q38_gdn_post_args;
+
 /* conv1d(k=4) with state shift, SiLU, per-head L2 norm of q and k, and the
  * beta / decay gates, for n_tokens consecutive tokens of n_seq sequences.
  * grid (81, n_seq): x < 80 is a 128-channel group, x == 80 the gates. */

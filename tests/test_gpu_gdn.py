@@ -53,21 +53,70 @@ def test_gdn_1024_steps_state_drift(ctx, ref, synth):
     assert rel_max <= 1e-4 and rel_fro <= 1e-4
 
 
-def test_gdn_prefill_equals_steps(ctx, synth):
-    """One launch over T tokens keeps the state in registers; it must give the
-    same bits as T single-token launches (same arithmetic, same order)."""
-    T = 37
-    state0 = synth.normal(201, STATE, sigma=0.02)
-    q, k, v, beta, g = synth.GdnStepInputs(202).steps(0, T)
-    dq, dk, dv, db, dg = (ctx.array(x) for x in (q, k, v, beta, g))
-    d_a, d_b = ctx.array(state0), ctx.array(state0)
-    o_a, o_b = ctx.empty((T, 6144)), ctx.empty((T, 6144))
-    ctx.gdn_prefill(d_a, T, dq, dk, dv, db, dg, o_a)
+def _chunked_vs_reference(ctx, ref, synth, T, seed, g_override=None, beta_override=None):
+    """q38_gdn_prefill over T tokens (64-token chunks on bf16x3 MFMA) against
+    T sequential steps of the restatement (ops.rs:1088-1099)."""
+    state0 = synth.normal(seed, STATE, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(seed + 1).steps(0, T)
+    if g_override is not None:
+        g = np.full_like(g, g_override)
+    if beta_override is not None:
+        beta = np.full_like(beta, beta_override)
+    d_state = ctx.array(state0)
+    d_out = ctx.empty((T, 6144))
+    ctx.gdn_prefill(d_state, T, *[ctx.array(x) for x in (q, k, v, beta, g)], d_out)
+    got_out, got_s = d_out.download(), d_state.download()
+    s_ref = state0.copy()
+    worst = 0.0
     for t in range(T):
-        ctx.gdn_step(1, d_b, dq.offset(t * 2048), dk.offset(t * 2048), dv.offset(t * 6144),
-                     db.offset(t * 48), dg.offset(t * 48), o_b.offset(t * 6144))
-    assert np.array_equal(d_a.download(), d_b.download())
-    assert np.array_equal(o_a.download(), o_b.download())
+        o = ref.gdn_heads(s_ref, q[t], k[t], v[t], beta[t], g[t], threads=16)
+        worst = max(worst, float(np.max(np.abs(got_out[t] - o))))
+    assert np.all(np.isfinite(got_s)) and np.all(np.isfinite(got_out))
+    return worst, _rel(got_s, s_ref)
+
+
+@pytest.mark.parametrize("T", [2, 37, 63, 64, 65, 129, 300])
+def test_gdn_chunked_prefill_matches_reference(ctx, ref, synth, T):
+    """Chunk boundaries: partial first chunk, exact chunks, one token past."""
+    worst, (rel_max, rel_fro) = _chunked_vs_reference(ctx, ref, synth, T, 0x51334600 + T)
+    assert worst <= 1e-3
+    assert rel_max <= 1e-4 and rel_fro <= 1e-4
+
+
+def test_gdn_chunked_prefill_4096(ctx, ref, synth):
+    """The chunked-prefill workload: 4096 tokens of the config-1 distributions
+    (state ~N(0, 0.02^2), L2-normalised q/k, beta = sigmoid(N), decay
+    exp(-softplus(N))); every output and the final state."""
+    worst, (rel_max, rel_fro) = _chunked_vs_reference(ctx, ref, synth, 4096, 0x51334700)
+    print(f"4096 chunked: out max-abs {worst:.3e}, state rel max {rel_max:.3e}, rel fro {rel_fro:.3e}")
+    assert worst <= 1e-3
+    assert rel_max <= 1e-4 and rel_fro <= 1e-4
+
+
+def test_gdn_chunked_strong_decay(ctx, ref, synth):
+    """log-decay -60 per token: exp(G) underflows inside a chunk; the chunked
+    form uses only exp of differences G_t - G_s <= 0, so nothing overflows."""
+    worst, (rel_max, rel_fro) = _chunked_vs_reference(ctx, ref, synth, 150, 0x51334800, g_override=-60.0)
+    assert worst <= 1e-3
+    assert rel_max <= 1e-4 and rel_fro <= 1e-4
+
+
+def test_gdn_chunked_beta_zero_closed_form(ctx, synth):
+    """beta = 0 over 100 tokens: S_T = exp(sum g) S_0 and o_t = exp(G_t) S_0 q_t / sqrt(128)."""
+    T = 100
+    state0 = synth.normal(0x51334900, STATE, sigma=0.02)
+    q, k, v, beta, g = synth.GdnStepInputs(0x51334901).steps(0, T)
+    beta = np.zeros_like(beta)
+    g = (g * 0.05).astype(np.float32)  # mild decays keep exp(G_T) well above 0
+    d_state, d_out = ctx.array(state0), ctx.empty((T, 6144))
+    ctx.gdn_prefill(d_state, T, *[ctx.array(x) for x in (q, k, v, beta, g)], d_out)
+    S0 = state0.reshape(48, 128, 128).astype(np.float64)
+    G = np.cumsum(g.astype(np.float64), axis=0)  # [T][48]
+    ST = S0 * np.exp(G[-1])[:, None, None]
+    assert np.max(np.abs(d_state.download().reshape(48, 128, 128) - ST)) <= 1e-4 * np.max(np.abs(ST))
+    qh = q.reshape(T, 16, 128)[:, np.arange(48) % 16].astype(np.float64)  # [T][48][128]
+    o = np.einsum("hcd,thd->thc", S0, qh) * np.exp(G)[:, :, None] / np.sqrt(128.0)
+    assert np.max(np.abs(d_out.download().reshape(T, 48, 128) - o)) <= 1e-5
 
 
 def test_gdn_batched_states(ctx, synth):
