@@ -80,6 +80,7 @@ struct q38_ctx {
     hipModule_t mod_gdn = nullptr;
     hipModule_t mod_prefill = nullptr;
     hipFunction_t f_prefill = nullptr;
+    hipFunction_t f_kv_split = nullptr;
     hipModule_t mod_gdn_chunk = nullptr;
     hipFunction_t f_chunk_prep = nullptr;
     hipFunction_t f_chunk_scan = nullptr;
@@ -262,6 +263,7 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     const std::string p_prefill = dir + "/attn_prefill.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_prefill, p_prefill.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_prefill, ctx->mod_prefill, "q38_attn_prefill_mfma"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_kv_split, ctx->mod_prefill, "q38_kv_split_mfma"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split, ctx->mod_decode, "q38_attn_decode_split"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "q38_attn_decode_merge"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_copy, ctx->mod_decode, "q38_kv_copy"));
@@ -424,6 +426,7 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gdn_step_rows") f = ctx->f_gdn_step_rows;
     else if (name == "q38_copy_f32") f = ctx->f_copy;
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
+    else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
     else if (name == "q38_gdn_chunk_prep") f = ctx->f_chunk_prep;
     else if (name == "q38_gdn_chunk_scan") f = ctx->f_chunk_scan;
     else if (name == "q38_gdn_post") f = ctx->f_gdn_post;
@@ -846,7 +849,7 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     int slot = 0;
     if (kv->slot_of(layer, &slot)) return -1;
     q38_ctx *ctx = kv->ctx;
-    constexpr int kQueryBlock = 16; /* query tokens per workgroup of the kernel */
+    constexpr int kQueryBlock = Q38_PREFILL_QUERIES; /* query tokens per workgroup of the kernel */
     q38_prefill_args a;
     memset(&a, 0, sizeof(a));
     a.kpool = kv->kslot(slot);
@@ -858,7 +861,14 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     a.base_pos = base_pos;
     a.n_tokens = n_tokens;
     a.n_qblocks = (n_tokens + kQueryBlock - 1) / kQueryBlock;
-    return ctx->launch(ctx->f_prefill, a.n_qblocks, Q38_ATTN_KV_HEADS, 1, 64 * Q38_ATTN_GROUP, &a);
+    a.n_kblocks = (base_pos + n_tokens - 1) / Q38_PREFILL_KEYS + 1;
+    /* the K/V of positions 0 .. base_pos+n_tokens-1 split once into bf16
+     * hi/lo block images (workspace), then the attention kernel */
+    if (ctx->ensure_work((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES)) return -1;
+    a.images = ctx->work;
+    if (ctx->launch(ctx->f_kv_split, a.n_kblocks, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
+    if ((size_t)a.n_qblocks * Q38_ATTN_KV_HEADS > 0x7FFFFFFFull) return fail("prompt too long");
+    return ctx->launch(ctx->f_prefill, a.n_qblocks * Q38_ATTN_KV_HEADS, 1, 1, 256, &a);
 }
 
 /* ---------------------------------------------------------------- DeltaNet */

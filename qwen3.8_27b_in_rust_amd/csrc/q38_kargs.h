@@ -162,9 +162,17 @@ typedef struct {
     int32_t n_seq;
 } q38_gdn_pre_args;
 
-/* Causal prefill attention of one sequence on bf16 MFMA.  grid (n_qblocks,
- * 4 kv heads), 6 waves (one per query head of the group), 32 query tokens
- * per workgroup. */
+/* Causal prefill attention of one sequence on bf16 MFMA.  grid
+ * (4 * n_qblocks), 4 waves, Q38_PREFILL_QUERIES query tokens of the 6
+ * query heads of one kv head per workgroup. */
+#define Q38_PREFILL_KEYS 32   /* keys per K/V block */
+#define Q38_PREFILL_QUERIES 32 /* query tokens per prefill workgroup */
+#define Q38_PREFILL_KROW 264  /* bf16 per K row in a block image (256 + 16 B pad) */
+#define Q38_PREFILL_VROW 40   /* bf16 per transposed V row (32 key slots + 16 B pad) */
+/* One K/V block of one kv head split into bf16 hi/lo, laid out exactly as
+ * the prefill kernel's LDS tile: K hi [32][264] | K lo | V^T hi [256][40] |
+ * V^T lo, 74,752 bytes. */
+#define Q38_PREFILL_IMAGE_BYTES (2 * Q38_PREFILL_KEYS * Q38_PREFILL_KROW * 2 + 2 * 256 * Q38_PREFILL_VROW * 2)
 typedef struct {
     const float *kpool;        /* this layer's K pages: [max_pages][4][16][256] */
     const float *vpool;
@@ -172,10 +180,11 @@ typedef struct {
     const float *q;            /* [n_tokens][24][256] for positions base_pos.. */
     const float *gate;         /* [n_tokens][24][256] or NULL */
     float *out;                /* [n_tokens][24][256] */
+    void *images;              /* [4 kv heads][n_kblocks] block images */
     int32_t base_pos;
     int32_t n_tokens;
     int32_t n_qblocks;
-    int32_t pad_;
+    int32_t n_kblocks;         /* blocks of keys 0 .. base_pos + n_tokens - 1 */
 } q38_prefill_args;
 
 /* Merge of split-K partials.  grid (n_seq, 24, 4). */
