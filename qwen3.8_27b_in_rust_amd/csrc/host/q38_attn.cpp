@@ -878,7 +878,7 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
  * chunk_work_floats(n_seq, n_tokens) floats. */
 static size_t chunk_work_floats(int n_seq, int n_tokens) {
     const size_t n_chunks = ((size_t)n_tokens + Q38_GDN_CHUNK - 1) / Q38_GDN_CHUNK;
-    return (size_t)n_seq * Q38_LIN_V_HEADS * n_chunks * Q38_GDN_CHUNK_FLOATS;
+    return (size_t)n_seq * Q38_LIN_V_HEADS * n_chunks * (Q38_GDN_RECORD_BYTES / sizeof(float));
 }
 
 static int gdn_chunked(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, int64_t state_stride,
@@ -901,7 +901,7 @@ static int gdn_chunked(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, in
     a.v_stride = v_stride;
     a.n_tokens = n_tokens;
     a.n_chunks = n_chunks;
-    if (ctx->launch(ctx->f_chunk_prep, Q38_LIN_V_HEADS, n_chunks, n_seq, 256, &a)) return -1;
+    if (ctx->launch(ctx->f_chunk_prep, Q38_LIN_V_HEADS, n_chunks, n_seq, 512, &a)) return -1;
     return ctx->launch(ctx->f_chunk_scan, Q38_LIN_V_HEADS * 4, n_seq, 1, 256, &a);
 }
 

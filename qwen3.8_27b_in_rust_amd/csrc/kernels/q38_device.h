@@ -107,6 +107,34 @@ Q38_DEV double q38_wave_sum_f64(double x) {
     return x;
 }
 
+/* s_waitcnt immediate (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+ * lgkmcnt 11:8) that waits until at most `vm` vector memory operations and
+ * `lgkm` LDS/scalar operations of this wave are outstanding. */
+constexpr int q38_waitcnt(int vm, int lgkm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (lgkm << 8); }
+
+/* Workgroup barrier once this wave's LDS operations and all but its VM
+ * youngest vector memory operations have completed.  Vector memory
+ * operations complete in issue order, so loads issued ahead as prefetch (the
+ * VM youngest) stay in flight across it; __syncthreads() would wait for
+ * them, as its fences count direct-to-LDS loads as outstanding LDS writes. */
+template <int VM>
+Q38_DEV void q38_barrier_vm() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(q38_waitcnt(VM, 0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+/* Store of one bf16 to LDS that the compiler does not see as a memory access,
+ * so its wait-count pass cannot order it after outstanding direct-to-LDS loads
+ * into other arrays (it may not tell them apart).  The caller makes it
+ * visible with a barrier that waits for lgkmcnt 0. */
+Q38_DEV void q38_lds_store_bf16(__bf16 *p, __bf16 x) {
+    const uint32_t addr = (uint32_t)(size_t)(__attribute__((address_space(3))) __bf16 *)p;
+    const uint32_t v = __builtin_bit_cast(uint16_t, x);
+    asm volatile("ds_write_b16 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
 /* ------------------------------------------------ bf16x3 matrix-core tiles */
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -145,6 +173,33 @@ Q38_DEV f32x4 q38_mma16(f32x4 c, FA fa, FB fb) {
         bf16x8 ah, al, bh, bl;
         q38_split8(av, ah, al);
         q38_split8(bv, bh, bl);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+    }
+    return c;
+}
+
+/*
+ * The same tile with both operands already split into bf16 hi/lo arrays
+ * (LDS): A row m at a_hi/a_lo + m*lda, and B given by its columns, B(k, n)
+ * = b[n*ldb + k], each contiguous in k.  One 16-byte read per fragment half.
+ * Row strides and the arrays must keep 16-byte alignment.
+ */
+template <int KD>
+Q38_DEV f32x4 q38_mma16_split(f32x4 c, const __bf16 *a_hi, const __bf16 *a_lo, int lda, const __bf16 *b_hi,
+                              const __bf16 *b_lo, int ldb) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    const int r = lane & 15;
+#pragma unroll
+    for (int k0 = 0; k0 < KD; k0 += 32) {
+        const int ao = r * lda + k0 + 8 * g;
+        const int bo = r * ldb + k0 + 8 * g;
+        const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(a_hi + ao);
+        const bf16x8 al = *reinterpret_cast<const bf16x8 *>(a_lo + ao);
+        const bf16x8 bh = *reinterpret_cast<const bf16x8 *>(b_hi + bo);
+        const bf16x8 bl = *reinterpret_cast<const bf16x8 *>(b_lo + bo);
         c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);

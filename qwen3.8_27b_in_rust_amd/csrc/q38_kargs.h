@@ -112,12 +112,22 @@ typedef struct {
 } q38_gdn_args;
 
 /* Chunked Gated-DeltaNet prefill (chunk Q38_GDN_CHUNK tokens).  The prep
- * kernel (grid (48 value heads, n_chunks, n_seq)) writes, per head and chunk,
- * Q38_GDN_CHUNK_FLOATS floats to `work`: W [64][128] | U' [64][128] |
- * B [64][64] | G [64]; the scan kernel (grid (48 x 4 row slabs, n_seq))
- * carries the state through the chunks. */
+ * kernel (grid (48 value heads, n_chunks, n_seq)) writes one record per head
+ * and chunk to `work`: a bf16 hi/lo image of the scan's operands laid out as
+ * the scan's LDS, in three parts the scan fetches separately, each a
+ * multiple of 4 KiB: W hi, W lo [64][136] + 2 KiB pad (36 KiB) | Q' hi, lo
+ * [64][136], Bm hi, lo [64][72] (52 KiB) | K'^T hi, lo [128][72] (36 KiB) --
+ * then U' f32 [64][128] and gamma_C; the
+ * scan kernel (grid (48 x 4 row slabs, n_seq)) carries the state through the
+ * chunks. */
 #define Q38_GDN_CHUNK 64
-#define Q38_GDN_CHUNK_FLOATS (2 * 64 * 128 + 64 * 64 + 64)
+#define Q38_GDN_WROW 136 /* bf16 per W / Q' image row: 128 + 16 B pad */
+#define Q38_GDN_BROW 72  /* bf16 per Bm / K'^T image row: 64 + 16 B pad */
+#define Q38_GDN_W_BYTES (36 * 1024)  /* W hi, lo + pad */
+#define Q38_GDN_QB_BYTES (52 * 1024) /* Q' hi, lo, Bm hi, lo */
+#define Q38_GDN_KT_BYTES (36 * 1024) /* K'^T hi, lo */
+#define Q38_GDN_IMAGE_BYTES (Q38_GDN_W_BYTES + Q38_GDN_QB_BYTES + Q38_GDN_KT_BYTES)
+#define Q38_GDN_RECORD_BYTES (Q38_GDN_IMAGE_BYTES + 64 * 128 * 4 + 256)
 typedef struct {
     float *state;      /* seq s at state + s*state_stride: [48][128][128] */
     const float *q;    /* token (s*T + t): q + (s*T + t)*q_stride + kh*128 */
@@ -126,7 +136,7 @@ typedef struct {
     const float *beta; /* [(s*T + t)*48 + vh], post-sigmoid */
     const float *g;    /* log-decay, same layout */
     float *out;        /* [(s*T + t)*6144 + vh*128 + c], before the gated norm */
-    float *work;       /* [n_seq][48][n_chunks][Q38_GDN_CHUNK_FLOATS] */
+    void *work;        /* [n_seq][48][n_chunks] records of Q38_GDN_RECORD_BYTES */
     int64_t state_stride;
     int32_t q_stride;
     int32_t v_stride;
