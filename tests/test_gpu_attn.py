@@ -76,6 +76,40 @@ def test_decode_split_invariance(pkg, ctx, ref, split):
     assert float(np.max(np.abs(got - want))) <= TOL
 
 
+def test_decode_merge_repeated(pkg, ctx, ref):
+    """The split-K partials and their merge over many launches in a row: 40
+    decodes over 1 to 47 splits, sharing the partial workspace, the output
+    poisoned with NaN before each launch and checked after it."""
+    from q38amd import synth
+    P = 3000
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=(P + 15) // 16 + 4, max_seqs=1, max_tokens_per_seq=P + 64)
+    old = os.environ.get("Q38_SPLIT_TOKENS")
+    try:
+        seq = kv.seq_create()
+        K = synth.normal(0x9200, P * 1024)
+        V = synth.normal(0x9201, P * 1024)
+        Q = synth.normal(0x9202, 6144)
+        G = synth.normal(0x9203, 6144)
+        d_k, d_v, d_q, d_g = ctx.array(K), ctx.array(V), ctx.array(Q), ctx.array(G)
+        kv.write(3, seq, 0, P, d_k, d_v)
+        want = ref.attn_heads(Q, K.reshape(P, 1024), V.reshape(P, 1024), gate=G)
+        d_o = ctx.empty((24, 256))
+        poison = np.full(6144, np.nan, np.float32)
+        for i in range(40):
+            split = [64, 128, 192, 384, 3008][i % 5]
+            os.environ["Q38_SPLIT_TOKENS"] = str(split)
+            d_o.upload(poison)
+            kv.attn_decode(3, [seq], [P - 1], d_q, d_o, gate=d_g)
+            err = float(np.max(np.abs(d_o.download() - want)))
+            assert err <= TOL, (i, split, err)
+    finally:
+        if old is None:
+            os.environ.pop("Q38_SPLIT_TOKENS", None)
+        else:
+            os.environ["Q38_SPLIT_TOKENS"] = old
+        kv.close()
+
+
 def test_decode_128k_context(pkg, ctx, ref):
     """The full-stack context: 131072 cached tokens (2048-token splits)."""
     got, Q, K, V, G = _decode_one(pkg, ctx, 131072, 0x51333820, gate=True)
