@@ -867,8 +867,9 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     if (ctx->ensure_work((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES)) return -1;
     a.images = ctx->work;
     if (ctx->launch(ctx->f_kv_split, a.n_kblocks, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
-    if ((size_t)a.n_qblocks * Q38_ATTN_KV_HEADS > 0x7FFFFFFFull) return fail("prompt too long");
-    return ctx->launch(ctx->f_prefill, a.n_qblocks * Q38_ATTN_KV_HEADS, 1, 1, 256, &a);
+    const size_t n_wg = (size_t)a.n_qblocks * Q38_ATTN_KV_HEADS * Q38_PREFILL_HEAD_PAIRS;
+    if (n_wg > 0x7FFFFFFFull) return fail("prompt too long");
+    return ctx->launch(ctx->f_prefill, (unsigned)n_wg, 1, 1, 256, &a);
 }
 
 /* ---------------------------------------------------------------- DeltaNet */

@@ -7,37 +7,39 @@
  * (ops.rs:914-917).  Scores are q.k / 16, softmax in f32.
  *
  * Precision: every f32 operand x is split into bf16 hi = bf16(x) and
- * lo = bf16(x - hi), and each product is hi*hi + hi*lo + lo*hi on
- * v_mfma_f32_16x16x32_bf16 with f32 accumulation: the represented value is
- * within ~2^-16 of x, far inside the 1e-3 output bound that plain bf16
- * (2^-8) would miss.
+ * lo = bf16(x - hi), and each product is hi*hi + hi*lo + lo*hi with f32
+ * accumulation: the represented value is within ~2^-16 of x, far inside
+ * the 1e-3 output bound that plain bf16 (2^-8) would miss.
  *
- * Layout (wave64, v_mfma_f32_16x16x32_bf16: A lane l = row l%16, k =
- * 8(l/16)..+7; B lane l = column l%16, same k; C lane l = rows 4(l/16)+i,
- * column l%16):
- *  - a workgroup serves 32 query tokens of all 6 query heads of kv head j
- *    from one copy of each K/V block: 12 (head, 16-query) tiles over 4 waves
- *    (one per SIMD, so 512 registers per lane hold 3 tiles' Q and O), and
- *    each K or V fragment read from LDS feeds 3 tiles x 3 MFMAs;
+ * Layout (wave64, v_mfma_f32_32x32x16_bf16: A lane l = row l%32, k =
+ * 8(l/32)..+7; B lane l = column l%32, same k; C lane l = column l%32,
+ * element 4J+i = row 8J + 4(l/32) + i):
+ *  - a workgroup serves 64 query tokens of 2 query heads of kv head j; each
+ *    wave owns 32 tokens x 1 head: its Q (bf16 hi/lo, 128 registers) and
+ *    its O (32 x 256 f32, 128 accumulation registers), no spills;
  *  - scores are computed transposed, S^T = K Q^T (A = K rows from LDS, B =
- *    Q^T from registers), so lane (g = l/16, c = l%16) holds query c's
- *    scores for keys 16kt + 4g + i -- exactly the P values it supplies as
- *    the A operand of O += P V when the key order inside the 32-key block
- *    is permuted to slot 8g + 4kt + i; V is stored transposed in LDS in that
+ *    Q^T from registers), so lane l holds query l%32's scores for keys
+ *    8J + 4(l/32) + i -- the P values it supplies as the A operand of
+ *    O += P V once the keys of a 32-key block are permuted to slot
+ *    16(J/2) + 8(l/32) + 4(J%2) + i; V is stored transposed in LDS in that
  *    slot order, so P never leaves registers;
  *  - q38_kv_split_mfma first splits the prompt's K/V (f32 pages) once into
  *    bf16 hi/lo block images laid out exactly as the LDS tile (V already
  *    transposed and slot-permuted); the attention kernel moves each 32-key
  *    image HBM -> LDS with direct-to-LDS loads one block ahead
  *    (double-buffered), one barrier per block, no conversion in its loop;
- *  - online softmax in base 2 per query row; the rows' max and sum cross the
- *    4 lane groups with permlane swaps.
+ *  - online softmax in base 2 per query, the two lane halves of a query
+ *    combined with v_permlane32_swap; a query's reference max moves only
+ *    when passed by more than 2^8, so rescaling O is rare; blocks wholly
+ *    after a wave's queries are skipped, and only diagonal blocks are
+ *    masked.
  */
 #include "q38_device.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 /* 1/sqrt(256) (ops.rs:869) times log2(e). */
 #define Q38_SCORE_LOG2 0.09016844005556021f
@@ -45,15 +47,25 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 namespace {
 
 constexpr int kQ = Q38_PREFILL_QUERIES;   /* query tokens per workgroup */
-constexpr int kWaves = 4;                 /* one per SIMD: 512 registers per lane */
-constexpr int kTiles = Q38_ATTN_GROUP * (kQ / 16) / kWaves; /* (head, 16-query) tiles per wave: 3 */
+constexpr int kQW = 32;                   /* query tokens per wave */
+constexpr int kWaves = 4;                 /* 2 heads x 2 token halves */
 constexpr int kKB = Q38_PREFILL_KEYS;     /* keys per block */
 constexpr int kKRow = Q38_PREFILL_KROW;   /* bf16 per K row: 16 B pad, conflict-free b128 reads */
 constexpr int kVRow = Q38_PREFILL_VROW;   /* bf16 per transposed V row (one head dim) */
 constexpr int kThreads = 64 * kWaves;
 constexpr int kPieces = Q38_PREFILL_IMAGE_BYTES / 1024; /* 1 KiB direct-to-LDS pieces of an image */
+/* A query's reference max m is its max over the first key block (which
+ * holds key 0, visible to every query) and O is never rescaled: weights
+ * exp2(s - m) stay <= 2^kRefSlack while no later score passes m by more, so
+ * sums over 2^20 keys stay < 2^84, and the largest score's weight is >= 1.
+ * A block whose max does pass m + kRefSlack for some query raises that
+ * query's m and restarts the workgroup's key loop from block 0 (with O and
+ * l cleared) -- never for scores of RMS-normalised q and k, which span a
+ * few tens of log2 units. */
+constexpr float kRefSlack = 64.0f;
 static_assert(Q38_PREFILL_IMAGE_BYTES % 1024 == 0, "image in 1 KiB pieces");
-static_assert(kTiles * kWaves == Q38_ATTN_GROUP * (kQ / 16), "tiles cover the group");
+static_assert(kQ == 2 * kQW && kWaves == 4 && kKB == 32, "2 heads x 2 halves of 32 tokens, 32-key blocks");
+static_assert(2 * Q38_PREFILL_HEAD_PAIRS == Q38_ATTN_GROUP, "head pairs cover the group");
 
 struct Split4 {
     bf16x4 hi, lo;
@@ -70,17 +82,12 @@ Q38_DEV Split4 split4(f32x4 x) {
     return r;
 }
 
-/* slot of key k (0..31) inside a block: 8g + 4kt + i for k = 16kt + 4g + i */
-Q38_DEV int key_slot(int k) { return 8 * ((k & 15) >> 2) + 4 * (k >> 4) + (k & 3); }
-
-Q38_DEV float max_over_groups(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16, 64));
-    return fmaxf(x, __shfl_xor(x, 32, 64));
-}
-
-Q38_DEV float sum_over_groups(float x) {
-    x += __shfl_xor(x, 16, 64);
-    return x + __shfl_xor(x, 32, 64);
+/* slot of key k = 8J + 4h + i (J < 4, h < 2, i < 4) inside a block: the
+ * 8 keys lane half h supplies for k-step t of O += P V (J = 2t, 2t+1) sit
+ * at slots 16t + 8h .. 16t + 8h + 7 */
+Q38_DEV int key_slot(int k) {
+    const int J = k >> 3, h = (k >> 2) & 1, i = k & 3;
+    return 16 * (J >> 1) + 8 * h + 4 * (J & 1) + i;
 }
 
 /* Element offset of key position kp (clamped to the last needed one) in
@@ -140,189 +147,268 @@ extern "C" __global__ __launch_bounds__(256) void q38_kv_split_mfma(q38_prefill_
 extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(q38_prefill_args a) {
     __shared__ __attribute__((aligned(16))) Tile tiles[2];
 
-    /* workgroup -> (kv head, query block): consecutive workgroups go to the
-     * 8 XCDs in turn, so XCDs 2j and 2j+1 take kv head j and its K/V blocks
-     * stay in those two L2s; the longest causal rows start first */
+    /* workgroup -> (kv head j, query block, head pair): consecutive
+     * workgroups go to the 8 XCDs in turn, so XCDs 2j and 2j+1 take kv head
+     * j and its K/V images stay in those two L2s; the 3 head pairs of a
+     * query block run side by side on the same images; the longest causal
+     * rows start first */
     const int L = blockIdx.x;
     const int nq = a.n_qblocks;
-    int j, qi;
+    int j, c;
     if ((nq & 1) == 0) {
         j = (L & 7) >> 1;
-        qi = (L >> 3) * 2 + (L & 1);
+        c = 2 * (L >> 3) + (L & 1);
     } else {
         j = L & 3;
-        qi = L >> 2;
+        c = L >> 2;
     }
+    const int qi = c / Q38_PREFILL_HEAD_PAIRS;
+    const int hp = c - Q38_PREFILL_HEAD_PAIRS * qi;
     const int qb = nq - 1 - qi;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 4;
-    const int c = lane & 15;
-    const int qt0 = qb * kQ;                            /* first query token of the block */
-    const int q_last = min(qt0 + kQ, a.n_tokens) - 1;   /* last real query token */
-    const int kmax = a.base_pos + q_last;               /* last key position any row needs */
+    const int h = lane >> 5;  /* lane half */
+    const int col = lane & 31;
+    const int head = j * Q38_ATTN_GROUP + 2 * hp + (wave & 1);
+    const int q0 = qb * kQ + kQW * (wave >> 1);      /* the wave's first query token */
+    const int q_last = min(qb * kQ + kQ, a.n_tokens) - 1; /* last real query token of the block */
+    const int kmax = a.base_pos + q_last;            /* last key position any row needs */
     const int n_kb = kmax / kKB + 1;
+    const bool active = q0 <= q_last;                /* the wave has real rows */
+    const int pos_first = a.base_pos + q0;           /* the wave's first row's position */
+    const int pos_last = a.base_pos + min(q0 + kQW - 1, q_last);
+    const int qpos = a.base_pos + q0 + col;          /* this lane's query column */
 
-    /* the wave's tiles: (head, 16-query tile) combos 3w .. 3w+2 of the 12 */
-    int head[kTiles], q0[kTiles], qpos[kTiles];
-    bf16x8 q_hi[kTiles][8], q_lo[kTiles][8];
+    /* Q^T as the B operand: lane l holds query col, dims 16ks + 8h .. +7 */
+    bf16x8 q_hi[16], q_lo[16];
+    {
+        const int tq = min(q0 + col, q_last);
+        const float *qp = a.q + ((size_t)tq * Q38_ATTN_HEADS + head) * Q38_ATTN_HEAD_DIM + 8 * h;
 #pragma unroll
-    for (int u = 0; u < kTiles; ++u) {
-        const int combo = kTiles * wave + u;
-        head[u] = j * Q38_ATTN_GROUP + (combo >> 1);
-        q0[u] = qt0 + 16 * (combo & 1);
-        qpos[u] = a.base_pos + q0[u] + c;
-        const int tq = min(q0[u] + c, q_last);
-        const float *qp = a.q + ((size_t)tq * Q38_ATTN_HEADS + head[u]) * Q38_ATTN_HEAD_DIM + 8 * g;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            const Split4 s0 = split4(q38_ld4(qp + 32 * kk));
-            const Split4 s1 = split4(q38_ld4(qp + 32 * kk + 4));
+        for (int ks = 0; ks < 16; ++ks) {
+            const Split4 s0 = split4(q38_ld4(qp + 16 * ks));
+            const Split4 s1 = split4(q38_ld4(qp + 16 * ks + 4));
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                q_hi[u][kk][e] = s0.hi[e];
-                q_hi[u][kk][4 + e] = s1.hi[e];
-                q_lo[u][kk][e] = s0.lo[e];
-                q_lo[u][kk][4 + e] = s1.lo[e];
+                q_hi[ks][e] = s0.hi[e];
+                q_hi[ks][4 + e] = s1.hi[e];
+                q_lo[ks][e] = s0.lo[e];
+                q_lo[ks][4 + e] = s1.lo[e];
             }
+            /* opaque to the compiler, which would otherwise keep f32 Q and
+             * split it again in every block; held in accumulation registers
+             * (the matrix unit reads its B operand from them), which leaves
+             * the vector registers to the scores, P and the fragments */
+            asm volatile("" : "+a"(q_hi[ks]), "+a"(q_lo[ks]));
         }
     }
 
-    float m[kTiles], l[kTiles];
-    f32x4 O[kTiles][16];
+    float m = -INFINITY, l = 0.0f; /* query col's, in both lane halves */
+    f32x16 O[8];                   /* O[n][4J+i] = row 8J+4h+i, dim 32n + col */
+    /* zeros made by the matrix unit (0 x 0 + 0), so the accumulators start,
+     * and stay, in accumulation registers */
+    auto clear_o = [&]() {
+        const bf16x8 z = {};
+        f32x16 zc;
 #pragma unroll
-    for (int u = 0; u < kTiles; ++u) {
-        m[u] = -INFINITY;
-        l[u] = 0.0f;
+        for (int v = 0; v < 16; ++v) zc[v] = 0.0f;
 #pragma unroll
-        for (int n = 0; n < 16; ++n) O[u][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+        for (int n = 0; n < 8; ++n) O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(z, z, zc, 0, 0, 0);
+    };
+    clear_o();
+    /* a wave whose block passed its reference max sets the flag of the
+     * block's parity; every wave reads it after the block's barrier */
+    __shared__ int restart_flag[2];
+    if (tid < 2) restart_flag[tid] = 0;
 
     /* block images go HBM -> LDS by direct-to-LDS loads (no registers):
      * wave w moves 1 KiB pieces w, w+4, ...; lane l's 16 bytes land at the
-     * piece's LDS base + 16 l */
+     * piece's LDS base + 16 l.  Written as assembly so the compiler's
+     * wait-count pass does not see them: it cannot tell the two buffers
+     * apart and would wait for the next block's image before the first read
+     * of the current one.  The loop waits for them itself (s_waitcnt 0 and
+     * the barrier that ends each block).  M0 carries the LDS address; nothing
+     * else in the kernel uses M0. */
     auto fetch = [&](int kb, int buf) {
         const char *img = reinterpret_cast<const char *>(image_of(a, j, kb));
         char *dst = reinterpret_cast<char *>(&tiles[buf]);
-        for (int p = wave; p < kPieces; p += kWaves)
-            __builtin_amdgcn_global_load_lds(img + p * 1024 + lane * 16,
-                                             (__attribute__((address_space(3))) void *)(dst + p * 1024), 16, 0, 0);
+        for (int p = wave; p < kPieces; p += kWaves) {
+            const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) char *)(dst + p * 1024);
+            /* one wait state between the M0 write and the load that reads it */
+            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds),
+                         "v"(img + p * 1024 + lane * 16)
+                         : "memory");
+        }
     };
     fetch(0, 0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    for (int kb = 0; kb < n_kb; ++kb) {
-        const int buf = kb & 1;
-        if (kb + 1 < n_kb) fetch(kb + 1, buf ^ 1);
+    /* this wave's share of an image: pieces wave + 4i, i < kMyPieces */
+    constexpr int kMyPieces = (kPieces + kWaves - 1) / kWaves;
+    static_assert(kMyPieces <= 16 + 3, "pieces fit the QK steps and the first PV steps");
 
-        /* S^T tiles: s[u][kt][i] = score of the tile's query c and key 16kt + 4g + i;
-         * each K fragment read from LDS feeds 3 tiles x 3 products */
-        f32x4 s[kTiles][2];
+    int kb = 0;
+    while (kb < n_kb) {
+        const int buf = kb & 1;
+        /* The next block's image is loaded a piece at a time between the
+         * matrix instructions below: issued all at once, 75 KB per workgroup
+         * queue behind the CU's memory path and stall every wave before its
+         * first product. */
+        const bool prefetch = kb + 1 < n_kb;
+        const char *next_img = reinterpret_cast<const char *>(image_of(a, j, min(kb + 1, n_kb - 1)));
+        char *next_dst = reinterpret_cast<char *>(&tiles[buf ^ 1]);
+        auto piece = [&](int i) {
+            const int p = wave + kWaves * i;
+            if (prefetch && p < kPieces) {
+                const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) char *)(next_dst + p * 1024);
+                asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds),
+                             "v"(next_img + p * 1024 + lane * 16)
+                             : "memory");
+            }
+        };
+        const int key0 = kb * kKB;
+        const bool computes = active && key0 <= pos_last;
+        if (!computes)
+            for (int i = 0; i < kMyPieces; ++i) piece(i);
+        float bm = -INFINITY; /* this block's max for query col (if computed) */
+
+        if (computes) {
+            /* K fragments are read kAhead steps before their products, so
+             * the LDS latency hides behind the matrix work */
+            constexpr int kAhead = 4;
+            f32x16 s;
 #pragma unroll
-        for (int u = 0; u < kTiles; ++u)
+            for (int v = 0; v < 16; ++v) s[v] = 0.0f;
+            bf16x8 kh[kAhead + 1], kl[kAhead + 1];
+            auto read_k = [&](int ks, int r) {
+                kh[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[0][col][16 * ks + 8 * h]);
+                kl[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[1][col][16 * ks + 8 * h]);
+            };
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) s[u][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int ks = 0; ks < kAhead; ++ks) read_k(ks, ks);
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[0][16 * kt + c][32 * kk + 8 * g]);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[1][16 * kt + c][32 * kk + 8 * g]);
-#pragma unroll
-                for (int u = 0; u < kTiles; ++u) {
-                    s[u][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, q_hi[u][kk], s[u][kt], 0, 0, 0);
-                    s[u][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, q_lo[u][kk], s[u][kt], 0, 0, 0);
-                    s[u][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, q_hi[u][kk], s[u][kt], 0, 0, 0);
-                }
-                /* keep each fragment's LDS read inside its step (hoisting them
-                 * all would need 128 more registers) */
+            for (int ks = 0; ks < 16; ++ks) {
+                if (ks + kAhead < 16) read_k(ks + kAhead, (ks + kAhead) % (kAhead + 1));
+                piece(ks);
+                const int r = ks % (kAhead + 1);
+                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[r], q_hi[ks], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[r], q_lo[ks], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl[r], q_hi[ks], s, 0, 0, 0);
+                /* keep the steps in this order: hoisting every read would
+                 * need registers the Q fragments hold */
                 __builtin_amdgcn_sched_barrier(0);
             }
-        }
 
-        bf16x8 p_hi[kTiles], p_lo[kTiles];
+            /* scale, causal mask (only a block that reaches past the wave's
+             * first row needs one), the query's max over the block */
+            const bool full = key0 + kKB - 1 <= pos_first;
 #pragma unroll
-        for (int u = 0; u < kTiles; ++u) {
-            /* scale, causal mask, block max of the row */
-            float bm = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = kb * kKB + 16 * kt + 4 * g + i;
-                    const float x = key <= qpos[u] ? s[u][kt][i] * Q38_SCORE_LOG2 : -INFINITY;
-                    s[u][kt][i] = x;
-                    bm = fmaxf(bm, x);
+            for (int v = 0; v < 16; ++v) {
+                float x = s[v] * Q38_SCORE_LOG2;
+                if (!full) {
+                    const int key = key0 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    x = key <= qpos ? x : -INFINITY;
                 }
-            bm = max_over_groups(bm);
-            const float m_new = fmaxf(m[u], bm); /* finite: key 0 is in every row's block 0 */
-            const float f = q38_exp2(m[u] - m_new); /* 0 while m is -inf */
-            float ps = 0.0f;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = q38_exp2(s[u][kt][i] - m_new);
-                    ps += p;
-                    const __bf16 ph = (__bf16)p;
-                    p_hi[u][4 * kt + i] = ph;
-                    p_lo[u][4 * kt + i] = (__bf16)(p - (float)ph);
-                }
-            l[u] = l[u] * f + sum_over_groups(ps);
-            m[u] = m_new;
-            /* rescale O: lane (g, c) holds rows 4g+i, whose factor lives in lane 4g+i */
-            if (__any(f != 1.0f)) {
-                float fr[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) fr[i] = __shfl(f, 4 * g + i, 64);
-#pragma unroll
-                for (int n = 0; n < 16; ++n)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) O[u][n][i] *= fr[i];
+                s[v] = x;
             }
-        }
+            /* tree reductions: the dependent chains are what one wave per
+             * SIMD cannot hide */
+            {
+                float t8[8];
+#pragma unroll
+                for (int v = 0; v < 8; ++v) t8[v] = fmaxf(s[v], s[v + 8]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) t8[v] = fmaxf(t8[v], t8[v + 4]);
+                bm = fmaxf(fmaxf(t8[0], t8[2]), fmaxf(t8[1], t8[3]));
+            }
+            const q38_halves bh = q38_both_halves(bm);
+            bm = fmaxf(bh.a, bh.b);
+            if (m == -INFINITY) m = bm; /* first block: finite (key 0) */
 
-        /* O += P V: B = V^T rows (head dims 16n + c), key slots 8g .. 8g+7;
-         * each V fragment feeds 3 tiles x 3 products */
+            if (!__any(bm > m + kRefSlack)) {
+                float pv[16];
+                bf16x8 ph[2], pl[2];
 #pragma unroll
-        for (int n = 0; n < 16; ++n) {
-            const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[0][16 * n + c][8 * g]);
-            const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[1][16 * n + c][8 * g]);
+                for (int v = 0; v < 16; ++v) {
+                    const float p = q38_exp2(s[v] - m);
+                    pv[v] = p;
+                    /* key 8J + 4h + i -> k-step J/2, element 4(J%2) + i */
+                    const int t = v >> 3, e = v & 7;
+                    const __bf16 hb = (__bf16)p;
+                    ph[t][e] = hb;
+                    pl[t][e] = (__bf16)(p - (float)hb);
+                }
 #pragma unroll
-            for (int u = 0; u < kTiles; ++u) {
-                O[u][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p_hi[u], vh, O[u][n], 0, 0, 0);
-                O[u][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p_hi[u], vl, O[u][n], 0, 0, 0);
-                O[u][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p_lo[u], vh, O[u][n], 0, 0, 0);
+                for (int v = 0; v < 8; ++v) pv[v] += pv[v + 8];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) pv[v] += pv[v + 4];
+                const float ps = (pv[0] + pv[2]) + (pv[1] + pv[3]);
+                const q38_halves sh = q38_both_halves(ps);
+                l += sh.a + sh.b;
+
+                /* O += P V: B = V^T rows (head dims 32n + col), key slots
+                 * 16t + 8h .. +7 */
+                bf16x8 vh[kAhead + 1], vl[kAhead + 1];
+                auto read_v = [&](int st, int r) {
+                    const int n = st >> 1, t = st & 1;
+                    vh[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[0][32 * n + col][16 * t + 8 * h]);
+                    vl[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[1][32 * n + col][16 * t + 8 * h]);
+                };
+#pragma unroll
+                for (int st = 0; st < kAhead; ++st) read_v(st, st);
+#pragma unroll
+                for (int st = 0; st < 16; ++st) {
+                    if (st + kAhead < 16) read_v(st + kAhead, (st + kAhead) % (kAhead + 1));
+                    if (st < kMyPieces - 16) piece(16 + st);
+                    const int r = st % (kAhead + 1), n = st >> 1, t = st & 1;
+                    O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph[t], vh[r], O[n], 0, 0, 0);
+                    O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph[t], vl[r], O[n], 0, 0, 0);
+                    O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pl[t], vh[r], O[n], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                for (int i = 16; i < kMyPieces; ++i) piece(i);
+                if (lane == 0) restart_flag[kb & 1] = 1;
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
 
         /* the next block's pieces have landed (this wave's), and every wave is
          * done with this block */
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if (restart_flag[kb & 1]) {
+            /* raise the references to cover this block and start over */
+            m = fmaxf(m, bm);
+            l = 0.0f;
+            clear_o();
+            __syncthreads(); /* every wave has read the flag */
+            if (tid < 2) restart_flag[tid] = 0;
+            kb = 0;
+            fetch(0, 0);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            continue;
+        }
+        ++kb;
     }
 
-    /* normalise, gate, store rows 4g+i of each tile */
+    /* normalise, gate, store rows 8J+4h+i (their sums live in lanes 8J+4h+i) */
+    if (!active) return;
 #pragma unroll
-    for (int u = 0; u < kTiles; ++u) {
-        float inv[4];
+    for (int v = 0; v < 16; ++v) {
+        const int r = 8 * (v >> 2) + 4 * h + (v & 3);
+        const float inv = 1.0f / __shfl(l, r, 64);
+        const int t = q0 + r;
+        if (t > q_last) continue;
+        const size_t row = ((size_t)t * Q38_ATTN_HEADS + head) * Q38_ATTN_HEAD_DIM;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) inv[i] = 1.0f / __shfl(l[u], 4 * g + i, 64);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = q0[u] + 4 * g + i;
-            if (t > q_last) continue;
-            const size_t row = ((size_t)t * Q38_ATTN_HEADS + head[u]) * Q38_ATTN_HEAD_DIM;
-#pragma unroll
-            for (int n = 0; n < 16; ++n) {
-                const int d = 16 * n + c;
-                float r = O[u][n][i] * inv[i];
-                if (a.gate != nullptr) r *= q38_sigmoid(a.gate[row + d]);
-                a.out[row + d] = r;
-            }
+        for (int n = 0; n < 8; ++n) {
+            const int d = 32 * n + col;
+            float res = O[n][v] * inv;
+            if (a.gate != nullptr) res *= q38_sigmoid(a.gate[row + d]);
+            a.out[row + d] = res;
         }
     }
 }

@@ -173,10 +173,12 @@ typedef struct {
 } q38_gdn_pre_args;
 
 /* Causal prefill attention of one sequence on bf16 MFMA.  grid
- * (4 * n_qblocks), 4 waves, Q38_PREFILL_QUERIES query tokens of the 6
- * query heads of one kv head per workgroup. */
-#define Q38_PREFILL_KEYS 32   /* keys per K/V block */
-#define Q38_PREFILL_QUERIES 32 /* query tokens per prefill workgroup */
+ * (12 * n_qblocks), 4 waves: a workgroup serves Q38_PREFILL_QUERIES query
+ * tokens of 2 of the 6 query heads of one kv head (3 head pairs per kv
+ * head), one wave per 32 tokens x 1 head. */
+#define Q38_PREFILL_KEYS 32    /* keys per K/V block */
+#define Q38_PREFILL_QUERIES 64 /* query tokens per prefill workgroup */
+#define Q38_PREFILL_HEAD_PAIRS 3
 #define Q38_PREFILL_KROW 264  /* bf16 per K row in a block image (256 + 16 B pad) */
 #define Q38_PREFILL_VROW 40   /* bf16 per transposed V row (32 key slots + 16 B pad) */
 /* One K/V block of one kv head split into bf16 hi/lo, laid out exactly as
