@@ -28,11 +28,14 @@
  *    transposed and slot-permuted); the attention kernel moves each 32-key
  *    image HBM -> LDS with direct-to-LDS loads one block ahead
  *    (double-buffered), one barrier per block, no conversion in its loop;
- *  - online softmax in base 2 per query, the two lane halves of a query
- *    combined with v_permlane32_swap; a query's reference max moves only
- *    when passed by more than 2^8, so rescaling O is rare; blocks wholly
- *    after a wave's queries are skipped, and only diagonal blocks are
- *    masked.
+ *  - softmax in base 2 against a fixed per-query reference max (the max
+ *    over the first key block), so O is never rescaled; the two lane halves
+ *    of a query combine with v_permlane32_swap; a block whose scores pass
+ *    the reference by more than 2^64 restarts the workgroup's key loop with
+ *    a raised reference (kRefSlack below); blocks wholly after a wave's
+ *    queries are skipped, and only diagonal blocks are masked;
+ *  - the loads of block kb+1's image are issued between the MFMA steps of
+ *    block kb, so the direct-to-LDS traffic runs under the matrix work.
  */
 #include "q38_device.h"
 

@@ -318,6 +318,45 @@ def test_prefill_4096_prompt(pkg, ctx, ref):
     assert _prefill_case(pkg, ctx, ref, 0, 4096, 980, rows=rows) <= TOL
 
 
+def test_prefill_reference_restart(pkg, ctx, ref):
+    """Keys far above the first block's scores: the prefill kernel keeps one
+    reference max per query taken from key block 0 and restarts a workgroup's
+    key loop when a later block passes it by more than 2^64.  Heads 0-5 query
+    one direction u; key 70 of kv head 0 scores 60 (natural units) and key 150
+    scores 130, so queries 70.. restart at block 2 and queries 150.. again at
+    block 4.  All rows against the restatement."""
+    from q38amd import synth
+    T = 200
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=T // 16 + 4, max_seqs=1, max_tokens_per_seq=T)
+    try:
+        seq = kv.seq_create()
+        layer = 3
+        K = synth.normal(1001, T * 1024).reshape(T, 4, 256)
+        V = synth.normal(1002, T * 1024).reshape(T, 4, 256)
+        Q = synth.normal(1003, T * 6144).reshape(T, 24, 256)
+        u = synth.normal(1004, 256)
+        Q[:, 0:6, :] = u
+        un = u / np.linalg.norm(u)
+        K[70, 0] = (60.0 * 16.0 / np.linalg.norm(u)) * un
+        K[150, 0] = (130.0 * 16.0 / np.linalg.norm(u)) * un
+        K, V, Q = K.astype(np.float32).reshape(-1), V.astype(np.float32).reshape(-1), Q.astype(np.float32).reshape(-1)
+        d_k, d_v = ctx.array(K), ctx.array(V)
+        d_o = ctx.empty((T, 24, 256))
+        kv.attn_prefill(layer, seq, 0, T, ctx.array(Q), d_k, d_v, d_o)
+        got = d_o.download()
+        Kr, Vr = K.reshape(-1, 1024), V.reshape(-1, 1024)
+        worst = 0.0
+        for t in range(T):
+            want = ref.attn_heads(Q[t * 6144:(t + 1) * 6144], Kr[:t + 1], Vr[:t + 1])
+            worst = max(worst, float(np.max(np.abs(got[t] - want))))
+        # the planted keys dominate: head 0 of query 120 returns v_70, of query 190 v_150
+        assert np.max(np.abs(got[120, 0] - Vr[70, :256])) <= 1e-3
+        assert np.max(np.abs(got[190, 0] - Vr[150, :256])) <= 1e-3
+    finally:
+        kv.close()
+    assert worst <= TOL
+
+
 def test_kv_pages_roundtrip_and_rollback(pkg, ctx, synth):
     """Write/read through a permuted page table; truncate releases whole pages
     past the kept positions; reset releases all."""
