@@ -74,13 +74,20 @@ def attention_decode(pkg, ctx, steps: int, warmup: int):
     for i in range(warmup):
         step(i)
     ctx.sync()
+    # the timed steps: plain launches, bracketed by two stream events
     e0, e1 = ctx.event(), ctx.event()
-    ctx.kernel_timer_start("q38_attn_decode_split", steps)
     ctx.record(e0)
     for i in range(steps):
         step(warmup + i)
     ctx.record(e1)
     ms_total = ctx.elapsed_ms(e0, e1)
+    ctx.sync()
+    # the split kernel's own duration, from the same steps again with each
+    # split launch carrying start/stop events (not part of `value`: the
+    # per-dispatch events are instrumentation)
+    ctx.kernel_timer_start("q38_attn_decode_split", steps)
+    for i in range(steps):
+        step(warmup + i)
     k_ms, k_n = ctx.kernel_timer_stop()
     ctx.sync()
     # merge-kernel time, from a separate short loop (not part of `value`)
@@ -123,12 +130,15 @@ def gdn_steps(pkg, ctx, n_seq: int, n_states: int, steps: int, warmup: int):
         step(i)
     ctx.sync()
     e0, e1 = ctx.event(), ctx.event()
-    ctx.kernel_timer_start("q38_gdn_step_rows", steps)
     ctx.record(e0)
     for i in range(steps):
         step(warmup + i)
     ctx.record(e1)
     ms_total = ctx.elapsed_ms(e0, e1)
+    ctx.sync()
+    ctx.kernel_timer_start("q38_gdn_step_rows", steps)
+    for i in range(steps):
+        step(warmup + i)
     k_ms, k_n = ctx.kernel_timer_stop()
     states.free()
     kern = k_ms / max(k_n, 1)
@@ -216,12 +226,15 @@ def batched_decode(pkg, ctx, steps: int, warmup: int):
         step()
     ctx.sync()
     e0, e1 = ctx.event(), ctx.event()
-    ctx.kernel_timer_start("q38_attn_decode_split", steps)
     ctx.record(e0)
     for _ in range(steps):
         step()
     ctx.record(e1)
     ms = ctx.elapsed_ms(e0, e1) / steps
+    ctx.sync()
+    ctx.kernel_timer_start("q38_attn_decode_split", steps)
+    for _ in range(steps):
+        step()
     k_ms, k_n = ctx.kernel_timer_stop()
     kv.close()
     for b in (rows_k, rows_v, q, g, o, kn, vn):
