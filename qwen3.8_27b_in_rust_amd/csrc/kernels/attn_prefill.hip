@@ -190,8 +190,9 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
         const float *qp = a.q + ((size_t)tq * Q38_ATTN_HEADS + head) * Q38_ATTN_HEAD_DIM + 8 * h;
 #pragma unroll
         for (int ks = 0; ks < 16; ++ks) {
-            const Split4 s0 = split4(q38_ld4(qp + 16 * ks));
-            const Split4 s1 = split4(q38_ld4(qp + 16 * ks + 4));
+            /* scaled to base-2 score units before the split */
+            const Split4 s0 = split4(q38_ld4(qp + 16 * ks) * Q38_SCORE_LOG2);
+            const Split4 s1 = split4(q38_ld4(qp + 16 * ks + 4) * Q38_SCORE_LOG2);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 q_hi[ks][e] = s0.hi[e];
@@ -207,7 +208,8 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
         }
     }
 
-    float m = -INFINITY, l = 0.0f; /* query col's, in both lane halves */
+    float m = -INFINITY; /* query col's reference, in both lane halves */
+    float l = 0.0f;       /* the sum of this lane's weights (its half of the keys) */
     f32x16 O[8];                   /* O[n][4J+i] = row 8J+4h+i, dim 32n + col */
     /* zeros made by the matrix unit (0 x 0 + 0), so the accumulators start,
      * and stay, in accumulation registers */
@@ -304,52 +306,48 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
                 __builtin_amdgcn_sched_barrier(0);
             }
 
-            /* scale, causal mask (only a block that reaches past the wave's
-             * first row needs one), the query's max over the block */
+            /* causal mask (only a block that reaches past the wave's first
+             * row needs one); the scores are already in base-2 units */
             const bool full = key0 + kKB - 1 <= pos_first;
+            if (!full) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                float x = s[v] * Q38_SCORE_LOG2;
-                if (!full) {
+                for (int v = 0; v < 16; ++v) {
                     const int key = key0 + 8 * (v >> 2) + 4 * h + (v & 3);
-                    x = key <= qpos ? x : -INFINITY;
+                    s[v] = key <= qpos ? s[v] : -INFINITY;
                 }
-                s[v] = x;
             }
-            /* tree reductions: the dependent chains are what one wave per
-             * SIMD cannot hide */
+            /* this lane's max over its 16 scores (3-input maxima); the
+             * reference needs the query's max over both lane halves only on
+             * the first block and on a restart */
+            float lm;
             {
-                float t8[8];
+                float t6[6];
 #pragma unroll
-                for (int v = 0; v < 8; ++v) t8[v] = fmaxf(s[v], s[v + 8]);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) t8[v] = fmaxf(t8[v], t8[v + 4]);
-                bm = fmaxf(fmaxf(t8[0], t8[2]), fmaxf(t8[1], t8[3]));
+                for (int v = 0; v < 5; ++v) t6[v] = fmaxf(fmaxf(s[3 * v], s[3 * v + 1]), s[3 * v + 2]);
+                t6[5] = s[15];
+                lm = fmaxf(fmaxf(fmaxf(t6[0], t6[1]), t6[2]), fmaxf(fmaxf(t6[3], t6[4]), t6[5]));
             }
-            const q38_halves bh = q38_both_halves(bm);
-            bm = fmaxf(bh.a, bh.b);
-            if (m == -INFINITY) m = bm; /* first block: finite (key 0) */
+            if (m == -INFINITY) { /* first block: finite (key 0) */
+                const q38_halves bh = q38_both_halves(lm);
+                m = fmaxf(bh.a, bh.b);
+            }
 
-            if (!__any(bm > m + kRefSlack)) {
-                float pv[16];
+            if (!__any(lm > m + kRefSlack)) {
                 bf16x8 ph[2], pl[2];
+                float psum[2] = {0.0f, 0.0f};
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const float p = q38_exp2(s[v] - m);
-                    pv[v] = p;
-                    /* key 8J + 4h + i -> k-step J/2, element 4(J%2) + i */
+                    psum[v & 1] += p;
+                    /* key 8J + 4h + i -> k-step J/2, element 4(J%2) + i.
+                     * hi = p with its low 16 mantissa bits cleared, lo =
+                     * bf16(p - hi) (the difference is exact in f32) */
                     const int t = v >> 3, e = v & 7;
-                    const __bf16 hb = (__bf16)p;
-                    ph[t][e] = hb;
-                    pl[t][e] = (__bf16)(p - (float)hb);
+                    const uint32_t pb = __float_as_uint(p);
+                    ph[t][e] = __builtin_bit_cast(__bf16, (uint16_t)(pb >> 16));
+                    pl[t][e] = (__bf16)(p - __uint_as_float(pb & 0xFFFF0000u));
                 }
-#pragma unroll
-                for (int v = 0; v < 8; ++v) pv[v] += pv[v + 8];
-#pragma unroll
-                for (int v = 0; v < 4; ++v) pv[v] += pv[v + 4];
-                const float ps = (pv[0] + pv[2]) + (pv[1] + pv[3]);
-                const q38_halves sh = q38_both_halves(ps);
-                l += sh.a + sh.b;
+                l += psum[0] + psum[1];
 
                 /* O += P V: B = V^T rows (head dims 32n + col), key slots
                  * 16t + 8h .. +7 */
@@ -372,6 +370,8 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
                     __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
+                const q38_halves bh = q38_both_halves(lm);
+                bm = fmaxf(bh.a, bh.b); /* the query's max over the block: the raised reference */
                 for (int i = 16; i < kMyPieces; ++i) piece(i);
                 if (lane == 0) restart_flag[kb & 1] = 1;
             }
@@ -382,7 +382,8 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (restart_flag[kb & 1]) {
-            /* raise the references to cover this block and start over */
+            /* raise the references to cover this block and start over (a
+             * wave that did not pass its reference keeps bm = -inf) */
             m = fmaxf(m, bm);
             l = 0.0f;
             clear_o();
@@ -399,6 +400,10 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
 
     /* normalise, gate, store rows 8J+4h+i (their sums live in lanes 8J+4h+i) */
     if (!active) return;
+    {
+        const q38_halves lh = q38_both_halves(l); /* both halves of the keys */
+        l = lh.a + lh.b;
+    }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int r = 8 * (v >> 2) + 4 * h + (v & 3);
