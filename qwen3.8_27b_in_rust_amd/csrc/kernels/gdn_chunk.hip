@@ -46,7 +46,7 @@ static_assert(2 * C * WR * 2 <= Q38_GDN_W_BYTES && 2 * C * WR * 2 + 2 * C * BR *
                   2 * D * BR * 2 == Q38_GDN_KT_BYTES,
               "image parts");
 static_assert(kPiecesW % 4 == 0 && kPiecesQB % 4 == 0 && kPiecesKt % 4 == 0,
-              "each of the 4 scan waves moves the same number of pieces of every part");
+              "each of the 4 moving scan waves moves the same number of pieces of every part");
 constexpr int kPrepThreads = 64 * kPrepWaves;
 
 /* One head-chunk record of the workspace: the scan's operand image (bf16
@@ -302,7 +302,13 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chunk_args a) {
+/* 8 waves, two per SIMD: every phase of a chunk is a short dependent chain of
+ * LDS reads and matrix steps, and a second wave per SIMD fills the gaps.
+ * Waves 0-3 move the image (each every 4th piece of a part); all 8 compute. */
+constexpr int kScanWaves = Q38_GDN_SCAN_WAVES;
+static_assert(kScanWaves == 8, "steps a and b give each wave one of 8 tiles");
+
+extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan(q38_gdn_chunk_args a) {
     /* the chunk image in three arrays, one per part, so the compiler sees that
      * loads into one part do not alias reads of another */
     __shared__ __attribute__((aligned(16))) char imgW[Q38_GDN_W_BYTES];
@@ -338,12 +344,12 @@ extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chu
     li.kt_lo = li.kt_hi + D * BR;
 
     /* f32 state of the slab in registers, in the layout of the state-update
-     * tiles: wave w owns tiles 4w..4w+3, tile -> (row block tc, column block tk) */
+     * tiles: wave w owns tiles 2w, 2w+1, tile -> (row block tc, column block tk) */
     float *st = a.state + (size_t)s * a.state_stride + ((size_t)vh * D + c0) * D;
-    float S[4][4];
+    float S[2][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int tile = 4 * wave + q, tc = tile >> 3, tk = tile & 7;
+    for (int q = 0; q < 2; ++q) {
+        const int tile = 2 * wave + q, tc = tile >> 3, tk = tile & 7;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 16 * tc + 4 * g4 + i, col = 16 * tk + r;
@@ -354,11 +360,16 @@ extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chu
 
     /* The next chunk's image streams in behind the compute, each part once
      * the step that reads it is done: W after step a, Q' and Bm (with U')
-     * after step b, K'^T after step c.  Every wave moves every 4th piece of a
-     * part; a wave's waits count its own operations, and the barrier after
-     * the wait makes the pieces of all waves visible. */
-    const int ti = wave;
+     * after step b, K'^T after step c.  Waves 0-3 each move every 4th piece
+     * of a part; a wave's waits count its own operations, and the barrier
+     * after the wait makes the pieces of all waves visible (waves 4-7 move
+     * no pieces, so their waits pass at once). */
+    /* steps a and b: wave w computes token block ti of value-row block tb */
+    const int ti = wave & 3;
+    const int tb = wave >> 2;
+    const bool mover = wave < 4;
     auto fetch = [&](const char *src, char *dst, auto n_pieces) {
+        if (!mover) return;
 #pragma unroll
         for (int j = 0; j < decltype(n_pieces)::value / 4; ++j) {
             const int p = 4 * j + wave;
@@ -374,13 +385,11 @@ extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chu
     auto fetch_kt = [&](const Record &rec) {
         fetch(rec.image + Q38_GDN_W_BYTES + Q38_GDN_QB_BYTES, imgK, PiecesKt{});
     };
-    float up[2][4];
+    float up[4];
     float gamma_c;
     auto fetch_u = [&](const Record &rec) {
 #pragma unroll
-        for (int tc = 0; tc < 2; ++tc)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) up[tc][i] = rec.u[(16 * ti + 4 * g4 + i) * D + c0 + 16 * tc + r];
+        for (int i = 0; i < 4; ++i) up[i] = rec.u[(16 * ti + 4 * g4 + i) * D + c0 + 16 * tb + r];
         gamma_c = *rec.gamma_c;
     };
     {
@@ -399,29 +408,27 @@ extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chu
         const bool more = n + 1 < a.n_chunks;
         const Record next = record_of(a, s, vh, more ? n + 1 : n);
 
-        /* a: U = U' - W S^T (64 x 32): wave w takes token block w; U^T to LDS */
-#pragma unroll
-        for (int tc = 0; tc < 2; ++tc) {
+        /* a: U = U' - W S^T (64 x 32): wave w takes tile (ti, tb); U^T to LDS */
+        {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = q38_mma16_split<D>(acc, li.w_hi + 16 * ti * WR, li.w_lo + 16 * ti * WR, WR, &sSh[16 * tc][0],
-                                     &sSl[16 * tc][0], WR);
+            acc = q38_mma16_split<D>(acc, li.w_hi + 16 * ti * WR, li.w_lo + 16 * ti * WR, WR, &sSh[16 * tb][0],
+                                     &sSl[16 * tb][0], WR);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                split_store(&sUh[0][0], &sUl[0][0], (16 * tc + r) * BR + 16 * ti + 4 * g4 + i, up[tc][i] - acc[i]);
+                split_store(&sUh[0][0], &sUl[0][0], (16 * tb + r) * BR + 16 * ti + 4 * g4 + i, up[i] - acc[i]);
         }
         const float gc = gamma_c;
         q38_barrier_vm<63>(); /* U^T in LDS; W free */
         if (more) fetch_w(next);
 
         /* b: O = (Q' S^T + Bm U) / sqrt(128), Q' = diag(gamma) Q */
-        f32x4 o[2];
-#pragma unroll
-        for (int tc = 0; tc < 2; ++tc) {
+        f32x4 o;
+        {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc = q38_mma16_split<D>(acc, li.q_hi + 16 * ti * WR, li.q_lo + 16 * ti * WR, WR, &sSh[16 * tc][0],
-                                     &sSl[16 * tc][0], WR);
-            o[tc] = q38_mma16_split<C>(acc, li.b_hi + 16 * ti * BR, li.b_lo + 16 * ti * BR, BR, &sUh[16 * tc][0],
-                                       &sUl[16 * tc][0], BR);
+            acc = q38_mma16_split<D>(acc, li.q_hi + 16 * ti * WR, li.q_lo + 16 * ti * WR, WR, &sSh[16 * tb][0],
+                                     &sSl[16 * tb][0], WR);
+            o = q38_mma16_split<C>(acc, li.b_hi + 16 * ti * BR, li.b_lo + 16 * ti * BR, BR, &sUh[16 * tb][0],
+                                   &sUl[16 * tb][0], BR);
         }
         /* this chunk's K'^T has landed: only the next W is younger.  The
          * output stores come after the wait, as their number varies. */
@@ -430,12 +437,10 @@ extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chu
         else
             __builtin_amdgcn_s_waitcnt(q38_waitcnt(0, 15));
 #pragma unroll
-        for (int tc = 0; tc < 2; ++tc)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * ti + 4 * g4 + i;
-                if (t < cnt) a.out[(tok0 + t) * Q38_LIN_V_DIM + vh * D + c0 + 16 * tc + r] = o[tc][i] * query_scale;
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int t = 16 * ti + 4 * g4 + i;
+            if (t < cnt) a.out[(tok0 + t) * Q38_LIN_V_DIM + vh * D + c0 + 16 * tb + r] = o[i] * query_scale;
+        }
         q38_barrier_vm<63>(); /* K'^T of every wave in LDS; Q', Bm free */
         if (more) {
             fetch_qb(next);
@@ -444,8 +449,8 @@ extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chu
 
         /* c: S <- gamma_C S + U^T K' (tiles of the register layout) */
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int tile = 4 * wave + q, tc = tile >> 3, tk = tile & 7;
+        for (int q = 0; q < 2; ++q) {
+            const int tile = 2 * wave + q, tc = tile >> 3, tk = tile & 7;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             acc = q38_mma16_split<C>(acc, &sUh[16 * tc][0], &sUl[16 * tc][0], BR, li.kt_hi + 16 * tk * BR,
                                      li.kt_lo + 16 * tk * BR, BR);
@@ -468,8 +473,8 @@ extern "C" __global__ __launch_bounds__(256) void q38_gdn_chunk_scan(q38_gdn_chu
     }
 
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int tile = 4 * wave + q, tc = tile >> 3, tk = tile & 7;
+    for (int q = 0; q < 2; ++q) {
+        const int tile = 2 * wave + q, tc = tile >> 3, tk = tile & 7;
 #pragma unroll
         for (int i = 0; i < 4; ++i) st[(16 * tc + 4 * g4 + i) * D + 16 * tk + r] = S[q][i];
     }

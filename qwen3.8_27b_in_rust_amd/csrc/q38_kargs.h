@@ -128,6 +128,7 @@ typedef struct {
 #define Q38_GDN_KT_BYTES (36 * 1024) /* K'^T hi, lo */
 #define Q38_GDN_IMAGE_BYTES (Q38_GDN_W_BYTES + Q38_GDN_QB_BYTES + Q38_GDN_KT_BYTES)
 #define Q38_GDN_RECORD_BYTES (Q38_GDN_IMAGE_BYTES + 64 * 128 * 4 + 256)
+#define Q38_GDN_SCAN_WAVES 8 /* waves of a chunk-scan workgroup, two per SIMD */
 typedef struct {
     float *state;      /* seq s at state + s*state_stride: [48][128][128] */
     const float *q;    /* token (s*T + t): q + (s*T + t)*q_stride + kh*128 */
