@@ -49,8 +49,12 @@ static_assert(kPiecesW % 4 == 0 && kPiecesQB % 4 == 0 && kPiecesKt % 4 == 0,
               "each of the 4 moving scan waves moves the same number of pieces of every part");
 constexpr int kPrepThreads = 64 * kPrepWaves;
 
+/* gamma_C sits in the padding after W hi/lo, so it travels with W */
+constexpr int kGammaOffset = 2 * C * WR * 2;
+static_assert(kGammaOffset + 4 <= Q38_GDN_W_BYTES, "gamma_C in the W part");
+
 /* One head-chunk record of the workspace: the scan's operand image (bf16
- * hi/lo, LDS layout), then U' and gamma_C. */
+ * hi/lo, LDS layout; gamma_C in the W part), then U'. */
 struct Record {
     __bf16 *w_hi, *w_lo, *q_hi, *q_lo, *b_hi, *b_lo, *kt_hi, *kt_lo;
     float *u;
@@ -70,7 +74,7 @@ Q38_DEV Record record_at(char *base) {
     r.kt_hi = reinterpret_cast<__bf16 *>(base + Q38_GDN_W_BYTES + Q38_GDN_QB_BYTES);
     r.kt_lo = r.kt_hi + D * BR;
     r.u = reinterpret_cast<float *>(base + Q38_GDN_IMAGE_BYTES);
-    r.gamma_c = r.u + C * D;
+    r.gamma_c = reinterpret_cast<float *>(base + kGammaOffset);
     return r;
 }
 
@@ -79,21 +83,91 @@ Q38_DEV Record record_of(const q38_gdn_chunk_args &a, int s, int vh, int n) {
                      (((size_t)s * Q38_LIN_V_HEADS + vh) * a.n_chunks + n) * Q38_GDN_RECORD_BYTES);
 }
 
+/* LDS byte address of a __shared__ object */
+Q38_DEV uint32_t lds_address(const void *p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+/* One 1 KiB piece, 16 bytes per lane from base + off, straight to LDS at
+ * lds + 16 * lane.  Written in assembly so that the compiler's wait-count
+ * pass does not track it (it would otherwise wait for every piece in flight
+ * at the top of the chunk loop): every read of a piece follows an explicit
+ * vector-memory wait and a barrier.  M0 carries the LDS address; nothing
+ * else in the kernel uses M0. */
+Q38_DEV void dma_piece(uint32_t lds, const void *base, uint32_t off) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off), "s"(base)
+                 : "memory");
+}
+
 Q38_DEV void split_store(__bf16 *hi, __bf16 *lo, int idx, float x) {
     const __bf16 h = (__bf16)x;
     hi[idx] = h;
     lo[idx] = (__bf16)(x - (float)h);
 }
+
+/* 16 x 16 tiles (ti, tj) on or below the block diagonal of a 64 x 64 matrix,
+ * numbered row by row: p = ti (ti + 1) / 2 + tj. */
+constexpr int kLowerTiles = 10;
+Q38_DEV int lower_tile_row(int p) { return p < 1 ? 0 : (p < 3 ? 1 : (p < 6 ? 2 : 3)); }
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+/* x = hi + lo as bf16 (8-byte stores of 4 elements each) */
+Q38_DEV void split4_store(__bf16 *hi, __bf16 *lo, f32x4 x) {
+    bf16x4 h, l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        h[e] = (__bf16)x[e];
+        l[e] = (__bf16)(x[e] - (float)h[e]);
+    }
+    *reinterpret_cast<bf16x4 *>(hi) = h;
+    *reinterpret_cast<bf16x4 *>(lo) = l;
+}
+
+/* One 16 x 16 tile on bf16x3 products, c += A B, with A given by columns,
+ * A(m, k) = a[k * lda_k + m] (8 two-byte reads per fragment half), and B by
+ * columns contiguous in k, B(k, n) = b[n * ldb + k] (one 16-byte read). */
+template <int KD>
+Q38_DEV f32x4 mma16_split_acol(f32x4 c, const __bf16 *a_hi, const __bf16 *a_lo, int lda_k, const __bf16 *b_hi,
+                               const __bf16 *b_lo, int ldb) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    const int r = lane & 15;
+#pragma unroll
+    for (int k0 = 0; k0 < KD; k0 += 32) {
+        bf16x8 ah, al;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            ah[j] = a_hi[(k0 + 8 * g + j) * lda_k + r];
+            al[j] = a_lo[(k0 + 8 * g + j) * lda_k + r];
+        }
+        const int bo = r * ldb + k0 + 8 * g;
+        const bf16x8 bh = *reinterpret_cast<const bf16x8 *>(b_hi + bo);
+        const bf16x8 bl = *reinterpret_cast<const bf16x8 *>(b_lo + bo);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+    }
+    return c;
+}
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q38_gdn_chunk_args a) {
-    __shared__ __attribute__((aligned(16))) float sK[C][P];
-    __shared__ __attribute__((aligned(16))) float sQ[C][P]; /* Q, then the staging of W */
-    __shared__ __attribute__((aligned(16))) float sV[C][P];
-    __shared__ float sA[C][C + 1];
+    /* K and Q as bf16 hi/lo rows (split once, read by every product); once A
+     * and Bm are formed, Q's arrays hold T diag(beta gamma), W's left operand */
+    __shared__ __attribute__((aligned(16))) __bf16 sKh[C][WR];
+    __shared__ __attribute__((aligned(16))) __bf16 sKl[C][WR];
+    __shared__ __attribute__((aligned(16))) __bf16 sQh[C][WR];
+    __shared__ __attribute__((aligned(16))) __bf16 sQl[C][WR];
+    /* V^T as bf16 hi/lo rows of the chunk's 64 tokens */
+    __shared__ __attribute__((aligned(16))) __bf16 sVh[D][BR];
+    __shared__ __attribute__((aligned(16))) __bf16 sVl[D][BR];
+    /* A (f32); once T is complete, T diag(beta) as bf16 hi/lo (U''s left operand) */
+    __shared__ __attribute__((aligned(16))) float sA[C][BR];
     __shared__ __attribute__((aligned(16))) float sT[C][C + 4]; /* staging of Bm, then T */
     __shared__ float sX[3][16][17];
-    __shared__ float sG[C], sBeta[C], sGraw[C], sBG[C], sGam[C], sKd[C];
+    __shared__ float sG[C], sBeta[C], sBG[C], sKd[C];
+    static_assert(2 * C * BR * 2 == sizeof(float) * C * BR && C * BR <= C * WR, "operand images fit");
 
     const int vh = blockIdx.x;
     const int n = blockIdx.y;
@@ -109,99 +183,108 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
     const size_t tok0 = (size_t)s * a.n_tokens + t0;
     Record rec = record_of(a, s, vh, n);
 
-    /* rows of the chunk (zero past the prompt: such rows add nothing) */
-    for (int i = tid; i < C * (D / 4); i += kPrepThreads) {
-        const int t = i >> 5, c4 = i & 31;
-        f32x4 kv = {0.f, 0.f, 0.f, 0.f}, qv = kv, vv = kv;
+    /* rows of the chunk (zero past the prompt: such rows add nothing).  Pass p,
+     * lane l of wave w: token 8 (2p + w/4) + l/8, columns 4c .. 4c+3 with
+     * c = 8 (w%4) + l%8, so 8 lanes read 128 contiguous bytes of a row. */
+    f32x4 kv[4], qv[4], vv[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int t = 8 * (2 * p + (wave >> 2)) + (lane >> 3);
+        const int c4 = 8 * (wave & 3) + (lane & 7);
+        kv[p] = qv[p] = vv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (t < cnt) {
             const size_t tok = tok0 + t;
-            kv = q38_ld4(a.k + tok * a.q_stride + kh * D + 4 * c4);
-            qv = q38_ld4(a.q + tok * a.q_stride + kh * D + 4 * c4);
-            vv = q38_ld4(a.v + tok * a.v_stride + vh * D + 4 * c4);
+            kv[p] = q38_ld4(a.k + tok * a.q_stride + kh * D + 4 * c4);
+            qv[p] = q38_ld4(a.q + tok * a.q_stride + kh * D + 4 * c4);
+            vv[p] = q38_ld4(a.v + tok * a.v_stride + vh * D + 4 * c4);
         }
-        q38_st4(&sK[t][4 * c4], kv);
-        q38_st4(&sQ[t][4 * c4], qv);
-        q38_st4(&sV[t][4 * c4], vv);
     }
-    if (tid < C) {
-        const bool in = tid < cnt;
-        sBeta[tid] = in ? a.beta[(tok0 + tid) * Q38_LIN_V_HEADS + vh] : 0.0f;
-        sGraw[tid] = in ? a.g[(tok0 + tid) * Q38_LIN_V_HEADS + vh] : 0.0f;
-    }
-    __syncthreads();
-    if (tid < C) { /* inclusive prefix sum of the log-decays over the chunk (one wave) */
-        float acc = sGraw[tid];
+    /* inclusive prefix sum of the log-decays over the chunk, one token per
+     * lane, formed by every wave for its own use; wave 0 publishes it */
+    const bool in = lane < cnt;
+    const float beta_l = in ? a.beta[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
+    float acc_g = in ? a.g[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
 #pragma unroll
-        for (int d = 1; d < C; d <<= 1) {
-            const float o = __shfl_up(acc, d, 64);
-            if (tid >= d) acc += o;
+    for (int d = 1; d < C; d <<= 1) {
+        const float o = __shfl_up(acc_g, d, 64);
+        if (lane >= d) acc_g += o;
+    }
+    const float g_last = __shfl(acc_g, C - 1, 64);
+    const float gam_l = expf(acc_g);
+    if (wave == 0) {
+        sG[lane] = acc_g;
+        sBeta[lane] = beta_l;
+        sBG[lane] = beta_l * gam_l;
+        sKd[lane] = expf(g_last - acc_g);
+        if (lane == 0) *rec.gamma_c = expf(g_last);
+    }
+    /* K and Q split into LDS, V split and transposed; Q' = diag(gamma) Q
+     * straight to the record */
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int t = 8 * (2 * p + (wave >> 2)) + (lane >> 3);
+        const int c4 = 8 * (wave & 3) + (lane & 7);
+        split4_store(&sKh[t][4 * c4], &sKl[t][4 * c4], kv[p]);
+        split4_store(&sQh[t][4 * c4], &sQl[t][4 * c4], qv[p]);
+        const float gam = __shfl(gam_l, t, 64);
+        split4_store(rec.q_hi + t * WR + 4 * c4, rec.q_lo + t * WR + 4 * c4, gam * qv[p]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const __bf16 h = (__bf16)vv[p][e];
+            sVh[4 * c4 + e][t] = h;
+            sVl[4 * c4 + e][t] = (__bf16)(vv[p][e] - (float)h);
         }
-        sG[tid] = acc;
-        const float g_last = __shfl(acc, C - 1, 64);
-        sGam[tid] = expf(acc);
-        sBG[tid] = sBeta[tid] * sGam[tid];
-        sKd[tid] = expf(g_last - acc);
-        if (tid == 0) *rec.gamma_c = expf(g_last);
     }
     __syncthreads();
 
     /* A (strictly lower) into LDS and Bm (lower, with the diagonal) staged in
-     * sT: the 16 tile pairs (ti, tj) are 4 per wave; tiles above the diagonal
-     * are zero without a product (2 per wave) */
-    for (int job = wave; job < 16; job += kPrepWaves) {
-        const int ti = job >> 2, tj = job & 3;
-        f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
-        if (tj <= ti) {
-            kk = q38_mma16<D>(kk, [&](int m, int k) { return sK[16 * ti + m][k]; },
-                              [&](int k, int nn) { return sK[16 * tj + nn][k]; });
-            qk = q38_mma16<D>(qk, [&](int m, int k) { return sQ[16 * ti + m][k]; },
-                              [&](int k, int nn) { return sK[16 * tj + nn][k]; });
-        }
+     * sT, over the 10 tiles on or below the block diagonal: 20 products, 5 per
+     * SIMD (waves w and w + 4 share one) */
+    for (int u = wave; u < 2 * kLowerTiles; u += kPrepWaves) {
+        const int p = u >> 1;
+        const bool is_qk = u & 1;
+        const int ti = lower_tile_row(p), tj = p - ti * (ti + 1) / 2;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = q38_mma16_split<D>(acc, is_qk ? &sQh[16 * ti][0] : &sKh[16 * ti][0],
+                                 is_qk ? &sQl[16 * ti][0] : &sKl[16 * ti][0], WR, &sKh[16 * tj][0],
+                                 &sKl[16 * tj][0], WR);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * ti + 4 * g4 + i;
             const int sc = 16 * tj + r;
             const float dec = sc <= t ? expf(sG[t] - sG[sc]) : 0.0f;
-            sA[t][sc] = sc < t ? sBeta[t] * dec * kk[i] : 0.0f;
-            sT[t][sc] = sc <= t ? dec * qk[i] : 0.0f;
+            if (is_qk)
+                sT[t][sc] = sc <= t ? dec * acc[i] : 0.0f;
+            else
+                sA[t][sc] = sc < t ? sBeta[t] * dec * acc[i] : 0.0f;
         }
     }
     __syncthreads();
-    /* Bm out as bf16 hi/lo rows (16-byte stores); Q' = diag(gamma) Q rows;
-     * K'^T = (diag(exp(G_C - G)) K)^T by columns */
+    /* Bm out as bf16 hi/lo rows (zero above the diagonal blocks);
+     * K'^T = (diag(exp(G_C - G)) K)^T by rows of 8 tokens, K read as hi + lo */
     for (int it = tid; it < C * (C / 8); it += kPrepThreads) {
         const int t = it >> 3, c8 = it & 7;
+        const bool upper = (c8 >> 1) > (t >> 4);
         float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sT[t][8 * c8 + e];
+        for (int e = 0; e < 8; ++e) x[e] = upper ? 0.0f : sT[t][8 * c8 + e];
         bf16x8 hi, lo;
         q38_split8(x, hi, lo);
         *reinterpret_cast<bf16x8 *>(rec.b_hi + t * BR + 8 * c8) = hi;
         *reinterpret_cast<bf16x8 *>(rec.b_lo + t * BR + 8 * c8) = lo;
     }
-    for (int it = tid; it < C * (D / 8); it += kPrepThreads) {
-        const int t = it >> 4, c8 = it & 15;
-        const float gam = sGam[t];
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = gam * sQ[t][8 * c8 + e];
-        bf16x8 hi, lo;
-        q38_split8(x, hi, lo);
-        *reinterpret_cast<bf16x8 *>(rec.q_hi + t * WR + 8 * c8) = hi;
-        *reinterpret_cast<bf16x8 *>(rec.q_lo + t * WR + 8 * c8) = lo;
-    }
     for (int it = tid; it < D * (C / 8); it += kPrepThreads) {
-        const int i = it >> 3, t8 = it & 7;
+        const int i = it & (D - 1), t8 = it >> 7;
         float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sKd[8 * t8 + e] * sK[8 * t8 + e][i];
+        for (int e = 0; e < 8; ++e)
+            x[e] = sKd[8 * t8 + e] * ((float)sKh[8 * t8 + e][i] + (float)sKl[8 * t8 + e][i]);
         bf16x8 hi, lo;
         q38_split8(x, hi, lo);
         *reinterpret_cast<bf16x8 *>(rec.kt_hi + i * BR + 8 * t8) = hi;
         *reinterpret_cast<bf16x8 *>(rec.kt_lo + i * BR + 8 * t8) = lo;
     }
     __syncthreads();
-
     /* T = (I + A)^-1, blockwise (16 x 16 blocks).  Diagonal block w: wave w,
      * lane j < 16 keeps column j of the block in registers and substitutes
      * row by row, T_rj = -A_rj - sum_{j<k<r} A_rk T_kj, reading each row of A
@@ -268,37 +351,59 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
         __syncthreads();
     }
 
-    /* W = T diag(beta gamma) K (staged in sQ, then out as bf16 hi/lo rows) and
-     * U' = T diag(beta) V (f32 out): 32 + 32 tiles, 8 per wave */
+    /* the left operands of W and U' as bf16 hi/lo rows: T diag(beta gamma)
+     * over Q's arrays, T diag(beta) over A's (both free now) */
+    __bf16 *const t1h = &sQh[0][0];
+    __bf16 *const t1l = &sQl[0][0];
+    __bf16 *const t2h = reinterpret_cast<__bf16 *>(&sA[0][0]);
+    __bf16 *const t2l = t2h + C * BR;
+    for (int it = tid; it < C * (C / 8); it += kPrepThreads) {
+        const int t = it >> 3, c8 = it & 7;
+        float x1[8], x2[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float tv = sT[t][8 * c8 + e];
+            x1[e] = tv * sBG[8 * c8 + e];
+            x2[e] = tv * sBeta[8 * c8 + e];
+        }
+        bf16x8 hi, lo;
+        q38_split8(x1, hi, lo);
+        *reinterpret_cast<bf16x8 *>(t1h + t * BR + 8 * c8) = hi;
+        *reinterpret_cast<bf16x8 *>(t1l + t * BR + 8 * c8) = lo;
+        q38_split8(x2, hi, lo);
+        *reinterpret_cast<bf16x8 *>(t2h + t * BR + 8 * c8) = hi;
+        *reinterpret_cast<bf16x8 *>(t2l + t * BR + 8 * c8) = lo;
+    }
+    __syncthreads();
+
+    /* W = T diag(beta gamma) K, out as bf16 hi/lo rows, and U' = T diag(beta) V
+     * (f32 out): 32 + 32 tiles, 4 + 4 per wave.  W is formed transposed
+     * (W^T = K^T (T diag(beta gamma))^T) so that a lane holds 4 adjacent
+     * columns of a W row.  Token blocks 0 and 1 contract over tokens 0..31
+     * only: T is lower triangular. */
     for (int tile = wave; tile < 64; tile += kPrepWaves) {
         const bool is_w = tile < 32;
         const int ti = (tile & 31) >> 3, tn = tile & 7;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        if (is_w)
-            acc = q38_mma16<C>(acc, [&](int m, int k) { return sT[16 * ti + m][k]; },
-                               [&](int k, int nn) { return sBG[k] * sK[k][16 * tn + nn]; });
-        else
-            acc = q38_mma16<C>(acc, [&](int m, int k) { return sT[16 * ti + m][k]; },
-                               [&](int k, int nn) { return sBeta[k] * sV[k][16 * tn + nn]; });
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = 16 * ti + 4 * g4 + i, col = 16 * tn + r;
-            if (is_w)
-                sQ[t][col] = acc[i];
+        if (is_w) {
+            if (ti < 2)
+                acc = mma16_split_acol<32>(acc, &sKh[0][16 * tn], &sKl[0][16 * tn], WR, t1h + 16 * ti * BR,
+                                           t1l + 16 * ti * BR, BR);
             else
-                rec.u[t * D + col] = acc[i];
-        }
-    }
-    __syncthreads();
-    for (int it = tid; it < C * (D / 8); it += kPrepThreads) {
-        const int t = it >> 4, c8 = it & 15;
-        float x[8];
+                acc = mma16_split_acol<C>(acc, &sKh[0][16 * tn], &sKl[0][16 * tn], WR, t1h + 16 * ti * BR,
+                                          t1l + 16 * ti * BR, BR);
+            const int t = 16 * ti + r, col = 16 * tn + 4 * g4;
+            split4_store(rec.w_hi + t * WR + col, rec.w_lo + t * WR + col, acc);
+        } else {
+            if (ti < 2)
+                acc = q38_mma16_split<32>(acc, t2h + 16 * ti * BR, t2l + 16 * ti * BR, BR, &sVh[16 * tn][0],
+                                          &sVl[16 * tn][0], BR);
+            else
+                acc = q38_mma16_split<C>(acc, t2h + 16 * ti * BR, t2l + 16 * ti * BR, BR, &sVh[16 * tn][0],
+                                         &sVl[16 * tn][0], BR);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sQ[t][8 * c8 + e];
-        bf16x8 hi, lo;
-        q38_split8(x, hi, lo);
-        *reinterpret_cast<bf16x8 *>(rec.w_hi + t * WR + 8 * c8) = hi;
-        *reinterpret_cast<bf16x8 *>(rec.w_lo + t * WR + 8 * c8) = lo;
+            for (int i = 0; i < 4; ++i) rec.u[(16 * ti + 4 * g4 + i) * D + 16 * tn + r] = acc[i];
+        }
     }
 }
 
@@ -318,6 +423,7 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
     __shared__ __attribute__((aligned(16))) __bf16 sSl[R][WR];
     __shared__ __attribute__((aligned(16))) __bf16 sUh[R][BR]; /* U^T: row = value row, col = token */
     __shared__ __attribute__((aligned(16))) __bf16 sUl[R][BR];
+    __shared__ __attribute__((aligned(16))) float sUp[C][R]; /* the slab's columns of U' */
 
     /* workgroup -> (head, slab): consecutive workgroups go to the 8 XCDs in
      * turn, so a head's 4 slabs share one XCD and its L2 serves the image */
@@ -359,11 +465,13 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
     }
 
     /* The next chunk's image streams in behind the compute, each part once
-     * the step that reads it is done: W after step a, Q' and Bm (with U')
-     * after step b, K'^T after step c.  Waves 0-3 each move every 4th piece
-     * of a part; a wave's waits count its own operations, and the barrier
-     * after the wait makes the pieces of all waves visible (waves 4-7 move
-     * no pieces, so their waits pass at once). */
+     * the step that reads it is done: W after step a, U' with Q' and Bm
+     * after step b, K'^T after step c.  Each part is awaited only before the
+     * step that reads it: W and U' before step a, Q' and Bm before step b,
+     * K'^T before step c.  Waves 0-3 each move every 4th piece of a part; a
+     * wave's waits count its own operations, and the barrier after the wait
+     * makes the pieces of all waves visible (waves 4-7 move no pieces, so
+     * their waits pass at once). */
     /* steps a and b: wave w computes token block ti of value-row block tb */
     const int ti = wave & 3;
     const int tb = wave >> 2;
@@ -373,8 +481,7 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
 #pragma unroll
         for (int j = 0; j < decltype(n_pieces)::value / 4; ++j) {
             const int p = 4 * j + wave;
-            __builtin_amdgcn_global_load_lds(src + p * 1024 + lane * 16,
-                                             (__attribute__((address_space(3))) void *)(dst + p * 1024), 16, 0, 0);
+            dma_piece(lds_address(dst + p * 1024), src, p * 1024 + lane * 16);
         }
     };
     using PiecesW = std::integral_constant<int, kPiecesW>;
@@ -385,12 +492,16 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
     auto fetch_kt = [&](const Record &rec) {
         fetch(rec.image + Q38_GDN_W_BYTES + Q38_GDN_QB_BYTES, imgK, PiecesKt{});
     };
-    float up[4];
-    float gamma_c;
+    /* U' columns c0 .. c0+31: piece j holds rows 8j .. 8j+7 (a lane gathers
+     * 16 bytes of one row), 2 pieces per moving wave */
     auto fetch_u = [&](const Record &rec) {
+        if (!mover) return;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) up[i] = rec.u[(16 * ti + 4 * g4 + i) * D + c0 + 16 * tb + r];
-        gamma_c = *rec.gamma_c;
+        for (int jj = 0; jj < 2; ++jj) {
+            const int j = 4 * jj + wave;
+            const int row = 8 * j + (lane >> 3);
+            dma_piece(lds_address(&sUp[8 * j][0]), rec.u, (row * D + c0 + 4 * (lane & 7)) * 4);
+        }
     };
     {
         const Record rec0 = record_of(a, s, vh, 0);
@@ -408,8 +519,13 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
         const bool more = n + 1 < a.n_chunks;
         const Record next = record_of(a, s, vh, more ? n + 1 : n);
 
-        /* a: U = U' - W S^T (64 x 32): wave w takes tile (ti, tb); U^T to LDS */
+        /* a: U = U' - W S^T (64 x 32): wave w takes tile (ti, tb); U^T to LDS.
+         * gamma_C is read here, before the next W overwrites the W part. */
+        const float gamma_c = *reinterpret_cast<const float *>(imgW + kGammaOffset);
         {
+            float up[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) up[i] = sUp[16 * ti + 4 * g4 + i][16 * tb + r];
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             acc = q38_mma16_split<D>(acc, li.w_hi + 16 * ti * WR, li.w_lo + 16 * ti * WR, WR, &sSh[16 * tb][0],
                                      &sSl[16 * tb][0], WR);
@@ -417,8 +533,9 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
             for (int i = 0; i < 4; ++i)
                 split_store(&sUh[0][0], &sUl[0][0], (16 * tb + r) * BR + 16 * ti + 4 * g4 + i, up[i] - acc[i]);
         }
-        const float gc = gamma_c;
-        q38_barrier_vm<63>(); /* U^T in LDS; W free */
+        /* U^T in LDS, W and U' free; this chunk's Q' and Bm have landed
+         * (only its K'^T is younger) */
+        q38_barrier_vm<kPiecesKt / 4>();
         if (more) fetch_w(next);
 
         /* b: O = (Q' S^T + Bm U) / sqrt(128), Q' = diag(gamma) Q */
@@ -443,8 +560,8 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
         }
         q38_barrier_vm<63>(); /* K'^T of every wave in LDS; Q', Bm free */
         if (more) {
-            fetch_qb(next);
             fetch_u(next);
+            fetch_qb(next);
         }
 
         /* c: S <- gamma_C S + U^T K' (tiles of the register layout) */
@@ -456,19 +573,16 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
                                      li.kt_lo + 16 * tk * BR, BR);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                S[q][i] = __builtin_fmaf(gc, S[q][i], acc[i]);
-                /* opaque stores: the next chunk's Q' and Bm are loading */
-                const int idx = (16 * tc + 4 * g4 + i) * WR + 16 * tk + r;
-                const __bf16 h = (__bf16)S[q][i];
-                q38_lds_store_bf16(&sSh[0][0] + idx, h);
-                q38_lds_store_bf16(&sSl[0][0] + idx, (__bf16)(S[q][i] - (float)h));
+                S[q][i] = __builtin_fmaf(gamma_c, S[q][i], acc[i]);
+                split_store(&sSh[0][0], &sSl[0][0], (16 * tc + 4 * g4 + i) * WR + 16 * tk + r, S[q][i]);
             }
         }
         q38_barrier_vm<63>(); /* the new S in LDS; K'^T free */
         if (more) {
             fetch_kt(next);
-            /* the next W, Q', Bm and U' (every wave); K'^T still in flight */
-            q38_barrier_vm<kPiecesKt / 4>();
+            /* the next W and U'; its Q', Bm and K'^T stay in flight into
+             * step a */
+            q38_barrier_vm<(kPiecesQB + kPiecesKt) / 4>();
         }
     }
 
