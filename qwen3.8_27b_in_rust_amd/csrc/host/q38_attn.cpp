@@ -902,7 +902,7 @@ static int gdn_chunked(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, in
     a.v_stride = v_stride;
     a.n_tokens = n_tokens;
     a.n_chunks = n_chunks;
-    if (ctx->launch(ctx->f_chunk_prep, Q38_LIN_V_HEADS, n_chunks, n_seq, 512, &a)) return -1;
+    if (ctx->launch(ctx->f_chunk_prep, Q38_LIN_QK_HEADS, n_chunks, n_seq, 512, &a)) return -1;
     return ctx->launch(ctx->f_chunk_scan, Q38_LIN_V_HEADS * 4, n_seq, 1, 64 * Q38_GDN_SCAN_WAVES, &a);
 }
 

@@ -83,6 +83,12 @@ Q38_DEV Record record_of(const q38_gdn_chunk_args &a, int s, int vh, int n) {
                      (((size_t)s * Q38_LIN_V_HEADS + vh) * a.n_chunks + n) * Q38_GDN_RECORD_BYTES);
 }
 
+/* Workgroup barrier after this wave's LDS operations: the prep's waves share
+ * data only through LDS, so its barriers need not wait for the record's
+ * global stores (as __syncthreads() would) and those drain behind the
+ * compute. */
+Q38_DEV void lds_barrier() { q38_barrier_vm<63>(); }
+
 /* LDS byte address of a __shared__ object */
 Q38_DEV uint32_t lds_address(const void *p) {
     return (uint32_t)(size_t)(const __attribute__((address_space(3))) char *)p;
@@ -150,145 +156,17 @@ Q38_DEV f32x4 mma16_split_acol(f32x4 c, const __bf16 *a_hi, const __bf16 *a_lo, 
     }
     return c;
 }
-}  // namespace
-
-extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q38_gdn_chunk_args a) {
-    /* K and Q as bf16 hi/lo rows (split once, read by every product); once A
-     * and Bm are formed, Q's arrays hold T diag(beta gamma), W's left operand */
-    __shared__ __attribute__((aligned(16))) __bf16 sKh[C][WR];
-    __shared__ __attribute__((aligned(16))) __bf16 sKl[C][WR];
-    __shared__ __attribute__((aligned(16))) __bf16 sQh[C][WR];
-    __shared__ __attribute__((aligned(16))) __bf16 sQl[C][WR];
-    /* V^T as bf16 hi/lo rows of the chunk's 64 tokens */
-    __shared__ __attribute__((aligned(16))) __bf16 sVh[D][BR];
-    __shared__ __attribute__((aligned(16))) __bf16 sVl[D][BR];
-    /* A (f32); once T is complete, T diag(beta) as bf16 hi/lo (U''s left operand) */
-    __shared__ __attribute__((aligned(16))) float sA[C][BR];
-    __shared__ __attribute__((aligned(16))) float sT[C][C + 4]; /* staging of Bm, then T */
-    __shared__ float sX[3][16][17];
-    __shared__ float sG[C], sBeta[C], sBG[C], sKd[C];
-    static_assert(2 * C * BR * 2 == sizeof(float) * C * BR && C * BR <= C * WR, "operand images fit");
-
-    const int vh = blockIdx.x;
-    const int n = blockIdx.y;
-    const int s = blockIdx.z;
-    const int kh = vh % Q38_LIN_QK_HEADS;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g4 = lane >> 4;
-    const int r = lane & 15;
-    const int t0 = n * C;
-    const int cnt = min(C, a.n_tokens - t0);
-    const size_t tok0 = (size_t)s * a.n_tokens + t0;
-    Record rec = record_of(a, s, vh, n);
-
-    /* rows of the chunk (zero past the prompt: such rows add nothing).  Pass p,
-     * lane l of wave w: token 8 (2p + w/4) + l/8, columns 4c .. 4c+3 with
-     * c = 8 (w%4) + l%8, so 8 lanes read 128 contiguous bytes of a row. */
-    f32x4 kv[4], qv[4], vv[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int t = 8 * (2 * p + (wave >> 2)) + (lane >> 3);
-        const int c4 = 8 * (wave & 3) + (lane & 7);
-        kv[p] = qv[p] = vv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (t < cnt) {
-            const size_t tok = tok0 + t;
-            kv[p] = q38_ld4(a.k + tok * a.q_stride + kh * D + 4 * c4);
-            qv[p] = q38_ld4(a.q + tok * a.q_stride + kh * D + 4 * c4);
-            vv[p] = q38_ld4(a.v + tok * a.v_stride + vh * D + 4 * c4);
-        }
-    }
-    /* inclusive prefix sum of the log-decays over the chunk, one token per
-     * lane, formed by every wave for its own use; wave 0 publishes it */
-    const bool in = lane < cnt;
-    const float beta_l = in ? a.beta[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
-    float acc_g = in ? a.g[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
-#pragma unroll
-    for (int d = 1; d < C; d <<= 1) {
-        const float o = __shfl_up(acc_g, d, 64);
-        if (lane >= d) acc_g += o;
-    }
-    const float g_last = __shfl(acc_g, C - 1, 64);
-    const float gam_l = expf(acc_g);
-    if (wave == 0) {
-        sG[lane] = acc_g;
-        sBeta[lane] = beta_l;
-        sBG[lane] = beta_l * gam_l;
-        sKd[lane] = expf(g_last - acc_g);
-        if (lane == 0) *rec.gamma_c = expf(g_last);
-    }
-    /* K and Q split into LDS, V split and transposed; Q' = diag(gamma) Q
-     * straight to the record */
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const int t = 8 * (2 * p + (wave >> 2)) + (lane >> 3);
-        const int c4 = 8 * (wave & 3) + (lane & 7);
-        split4_store(&sKh[t][4 * c4], &sKl[t][4 * c4], kv[p]);
-        split4_store(&sQh[t][4 * c4], &sQl[t][4 * c4], qv[p]);
-        const float gam = __shfl(gam_l, t, 64);
-        split4_store(rec.q_hi + t * WR + 4 * c4, rec.q_lo + t * WR + 4 * c4, gam * qv[p]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const __bf16 h = (__bf16)vv[p][e];
-            sVh[4 * c4 + e][t] = h;
-            sVl[4 * c4 + e][t] = (__bf16)(vv[p][e] - (float)h);
-        }
-    }
-    __syncthreads();
-
-    /* A (strictly lower) into LDS and Bm (lower, with the diagonal) staged in
-     * sT, over the 10 tiles on or below the block diagonal: 20 products, 5 per
-     * SIMD (waves w and w + 4 share one) */
-    for (int u = wave; u < 2 * kLowerTiles; u += kPrepWaves) {
-        const int p = u >> 1;
-        const bool is_qk = u & 1;
-        const int ti = lower_tile_row(p), tj = p - ti * (ti + 1) / 2;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = q38_mma16_split<D>(acc, is_qk ? &sQh[16 * ti][0] : &sKh[16 * ti][0],
-                                 is_qk ? &sQl[16 * ti][0] : &sKl[16 * ti][0], WR, &sKh[16 * tj][0],
-                                 &sKl[16 * tj][0], WR);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = 16 * ti + 4 * g4 + i;
-            const int sc = 16 * tj + r;
-            const float dec = sc <= t ? expf(sG[t] - sG[sc]) : 0.0f;
-            if (is_qk)
-                sT[t][sc] = sc <= t ? dec * acc[i] : 0.0f;
-            else
-                sA[t][sc] = sc < t ? sBeta[t] * dec * acc[i] : 0.0f;
-        }
-    }
-    __syncthreads();
-    /* Bm out as bf16 hi/lo rows (zero above the diagonal blocks);
-     * K'^T = (diag(exp(G_C - G)) K)^T by rows of 8 tokens, K read as hi + lo */
-    for (int it = tid; it < C * (C / 8); it += kPrepThreads) {
-        const int t = it >> 3, c8 = it & 7;
-        const bool upper = (c8 >> 1) > (t >> 4);
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = upper ? 0.0f : sT[t][8 * c8 + e];
-        bf16x8 hi, lo;
-        q38_split8(x, hi, lo);
-        *reinterpret_cast<bf16x8 *>(rec.b_hi + t * BR + 8 * c8) = hi;
-        *reinterpret_cast<bf16x8 *>(rec.b_lo + t * BR + 8 * c8) = lo;
-    }
-    for (int it = tid; it < D * (C / 8); it += kPrepThreads) {
-        const int i = it & (D - 1), t8 = it >> 7;
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            x[e] = sKd[8 * t8 + e] * ((float)sKh[8 * t8 + e][i] + (float)sKl[8 * t8 + e][i]);
-        bf16x8 hi, lo;
-        q38_split8(x, hi, lo);
-        *reinterpret_cast<bf16x8 *>(rec.kt_hi + i * BR + 8 * t8) = hi;
-        *reinterpret_cast<bf16x8 *>(rec.kt_lo + i * BR + 8 * t8) = lo;
-    }
-    __syncthreads();
-    /* T = (I + A)^-1, blockwise (16 x 16 blocks).  Diagonal block w: wave w,
-     * lane j < 16 keeps column j of the block in registers and substitutes
-     * row by row, T_rj = -A_rj - sum_{j<k<r} A_rk T_kj, reading each row of A
-     * once (the same address in every lane). */
+/* T = (I + A)^-1 for the strictly lower 64 x 64 A, blockwise (16 x 16 blocks).
+ * Diagonal block w: wave w, lane j < 16 keeps column j of the block in
+ * registers and substitutes row by row, T_rj = -A_rj - sum_{j<k<r} A_rk T_kj,
+ * reading each row of A once (the same address in every lane).  Off-diagonal
+ * blocks by distance, block (w + dist, w) by wave w on fp32 matrix steps
+ * (v_mfma_f32_16x16x4_f32): X = sum_{k=j}^{i-1} A_ik T_kj, then
+ * T_ij = -T_ii X.  Each 16x16x16 product runs its contraction index as
+ * k = 4g + s (lane group g, step s), so X, held as the accumulator (lane (g, r):
+ * rows 4g .. 4g+3 of column r), is already the right operand of the second
+ * product.  Blocks above the diagonal are zero.  Ends with a barrier. */
+Q38_DEV void invert_unit_lower(const float (*sA)[BR], float (*sT)[C + 4], int wave, int lane) {
     if (wave < 4 && lane < 16) {
         const int b0 = 16 * wave;
         const int j = lane;
@@ -306,104 +184,284 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
 #pragma unroll
         for (int row = 0; row < 16; ++row) sT[b0 + row][b0 + j] = tc[row];
     }
-    /* above the diagonal blocks T is zero */
-    for (int i = tid; i < C * C; i += kPrepThreads) {
+    for (int i = threadIdx.x; i < C * C; i += kPrepThreads) {
         const int row = i >> 6, col = i & 63;
         if ((col >> 4) > (row >> 4)) sT[row][col] = 0.0f;
     }
-    __syncthreads();
-    /* off-diagonal blocks by distance: X_ij = sum_{k=j}^{i-1} A_ik T_kj, then
-     * T_ij = -T_ii X_ij; wave q handles block q of the current distance, lane l
-     * row l/4 and columns 4(l%4) .. +3 */
+    lds_barrier();
+    const int g = lane >> 4, r = lane & 15;
 #pragma unroll
     for (int dist = 1; dist < 4; ++dist) {
-        const bool mine = wave < 4 - dist;
-        const int bj = wave, bi = wave + dist;
-        const int row = lane >> 2, c4 = 4 * (lane & 3);
-        if (mine) {
-            float x[4] = {0.f, 0.f, 0.f, 0.f};
+        if (wave < 4 - dist) {
+            const int bj = wave, bi = wave + dist;
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int bk = 0; bk < dist; ++bk) {
+            for (int bk = bj; bk < bi; ++bk) {
+                const f32x4 av = *reinterpret_cast<const f32x4 *>(&sA[16 * bi + r][16 * bk + 4 * g]);
 #pragma unroll
-                for (int kk = 0; kk < 16; ++kk) {
-                    const int k = 16 * (bj + bk) + kk;
-                    const float av = sA[16 * bi + row][k];
-                    const f32x4 tv = *reinterpret_cast<const f32x4 *>(&sT[k][16 * bj + c4]);
+                for (int st = 0; st < 4; ++st)
+                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st], sT[16 * bk + 4 * g + st][16 * bj + r], x, 0, 0,
+                                                             0);
+            }
+            const f32x4 tv = *reinterpret_cast<const f32x4 *>(&sT[16 * bi + r][16 * bi + 4 * g]);
+            f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) x[e] = __builtin_fmaf(av, tv[e], x[e]);
+            for (int st = 0; st < 4; ++st) y = __builtin_amdgcn_mfma_f32_16x16x4f32(tv[st], x[st], y, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sT[16 * bi + 4 * g + i][16 * bj + r] = -y[i];
+        }
+        lds_barrier();
+    }
+}
+}  // namespace
+
+/*
+ * One workgroup per (q/k head, chunk): the 3 value heads that read q/k head
+ * kh (value heads kh, kh + 16, kh + 32; ops.rs:691) share K, Q, their bf16
+ * splits and the products K K^T and Q K^T; the decays, betas, T, W, U' and
+ * the images are per value head, formed one head after another.
+ */
+extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q38_gdn_chunk_args a) {
+    constexpr int kGroup = Q38_LIN_V_HEADS / Q38_LIN_QK_HEADS;
+    /* K as bf16 hi/lo rows, for all three heads */
+    __shared__ __attribute__((aligned(16))) __bf16 sKh[C][WR];
+    __shared__ __attribute__((aligned(16))) __bf16 sKl[C][WR];
+    /* the 10 tiles on or below the block diagonal of K K^T and of Q K^T */
+    __shared__ float sKK[kLowerTiles][16][17];
+    __shared__ float sQK[kLowerTiles][16][17];
+    /* Q as bf16 hi/lo rows while K K^T and Q K^T are formed; then V^T of the
+     * current head as bf16 hi/lo rows of the chunk's 64 tokens */
+    __shared__ __attribute__((aligned(16))) __bf16 sVh[D][BR];
+    __shared__ __attribute__((aligned(16))) __bf16 sVl[D][BR];
+    /* A (f32); once T is complete, T diag(beta) as bf16 hi/lo (U''s left operand) */
+    __shared__ __attribute__((aligned(16))) float sA[C][BR];
+    __shared__ __attribute__((aligned(16))) float sT[C][C + 4];
+    /* T diag(beta gamma) as bf16 hi/lo (W's left operand) */
+    __shared__ __attribute__((aligned(16))) __bf16 sWh[C][BR];
+    __shared__ __attribute__((aligned(16))) __bf16 sWl[C][BR];
+    __shared__ float sG[C], sBeta[C], sBG[C], sKd[C];
+    __shared__ float sG3[3][C], sBeta3[3][C]; /* G and beta of the three heads */
+    static_assert(2 * C * BR * 2 == sizeof(float) * C * BR, "T diag(beta) fits over A");
+    static_assert(C * WR <= D * BR, "Q rows fit over V^T");
+    __bf16 *const sQh = &sVh[0][0]; /* [C][WR] */
+    __bf16 *const sQl = &sVl[0][0];
+
+    const int kh = blockIdx.x;
+    const int n = blockIdx.y;
+    const int s = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g4 = lane >> 4;
+    const int r = lane & 15;
+    const int t0 = n * C;
+    const int cnt = min(C, a.n_tokens - t0);
+    const size_t tok0 = (size_t)s * a.n_tokens + t0;
+
+    /* rows of the chunk (zero past the prompt: such rows add nothing).  Pass p,
+     * lane l of wave w: token 8 (2p + w/4) + l/8, columns 4c .. 4c+3 with
+     * c = 8 (w%4) + l%8, so 8 lanes read 128 contiguous bytes of a row. */
+    auto row_t = [&](int p) { return 8 * (2 * p + (wave >> 2)) + (lane >> 3); };
+    auto col_c4 = [&]() { return 8 * (wave & 3) + (lane & 7); };
+    f32x4 kv[4], qv[4], vv[4];
+    auto load_v = [&](int vh) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int t = row_t(p);
+            vv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (t < cnt) vv[p] = q38_ld4(a.v + (tok0 + t) * a.v_stride + vh * D + 4 * col_c4());
+        }
+    };
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int t = row_t(p);
+        kv[p] = qv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (t < cnt) {
+            const size_t tok = tok0 + t;
+            kv[p] = q38_ld4(a.k + tok * a.q_stride + kh * D + 4 * col_c4());
+            qv[p] = q38_ld4(a.q + tok * a.q_stride + kh * D + 4 * col_c4());
+        }
+    }
+    load_v(kh);
+    /* log-decays and betas of the three heads, one token per lane; every
+     * wave forms the inclusive prefix sums G of the log-decays for its own
+     * use */
+    float beta_in[kGroup], acc_g[kGroup];
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+        const int vh = kh + Q38_LIN_QK_HEADS * j;
+        const bool in = lane < cnt;
+        beta_in[j] = in ? a.beta[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
+        acc_g[j] = in ? a.g[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+#pragma unroll
+        for (int d = 1; d < C; d <<= 1) {
+            const float o = __shfl_up(acc_g[j], d, 64);
+            if (lane >= d) acc_g[j] += o;
+        }
+        if (wave == 0) {
+            sG3[j][lane] = acc_g[j];
+            sBeta3[j][lane] = beta_in[j];
+        }
+    }
+    /* K and Q split into LDS; Q' = diag(gamma) Q of every head straight to
+     * its record */
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int t = row_t(p), c4 = col_c4();
+        split4_store(&sKh[t][4 * c4], &sKl[t][4 * c4], kv[p]);
+        split4_store(sQh + t * WR + 4 * c4, sQl + t * WR + 4 * c4, qv[p]);
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            const Record rec = record_of(a, s, kh + Q38_LIN_QK_HEADS * j, n);
+            const float gam = expf(__shfl(acc_g[j], t, 64));
+            split4_store(rec.q_hi + t * WR + 4 * c4, rec.q_lo + t * WR + 4 * c4, gam * qv[p]);
+        }
+    }
+    lds_barrier();
+
+    /* K K^T and Q K^T over the 10 tiles on or below the block diagonal: 20
+     * products, 5 per SIMD (waves w and w + 4 share one) */
+    for (int u = wave; u < 2 * kLowerTiles; u += kPrepWaves) {
+        const int p = u >> 1;
+        const bool is_qk = u & 1;
+        const int ti = lower_tile_row(p), tj = p - ti * (ti + 1) / 2;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = q38_mma16_split<D>(acc, is_qk ? sQh + 16 * ti * WR : &sKh[16 * ti][0],
+                                 is_qk ? sQl + 16 * ti * WR : &sKl[16 * ti][0], WR, &sKh[16 * tj][0],
+                                 &sKl[16 * tj][0], WR);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) (is_qk ? sQK : sKK)[p][4 * g4 + i][r] = acc[i];
+    }
+    lds_barrier();
+
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+        const int vh = kh + Q38_LIN_QK_HEADS * j;
+        const Record rec = record_of(a, s, vh, n);
+
+        /* this head's G and betas (wave 0 publishes them) */
+        if (wave == 0) {
+            const float g_l = sG3[j][lane];
+            const float beta_l = sBeta3[j][lane];
+            const float g_last = __shfl(g_l, C - 1, 64);
+            sG[lane] = g_l;
+            sBeta[lane] = beta_l;
+            sBG[lane] = beta_l * expf(g_l);
+            sKd[lane] = expf(g_last - g_l);
+            if (lane == 0) *rec.gamma_c = expf(g_last);
+        }
+        /* V^T of this head split into LDS */
+        if (j > 0) load_v(vh);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int t = row_t(p), c4 = col_c4();
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const __bf16 h = (__bf16)vv[p][e];
+                sVh[4 * c4 + e][t] = h;
+                sVl[4 * c4 + e][t] = (__bf16)(vv[p][e] - (float)h);
+            }
+        }
+        lds_barrier();
+
+        /* A (strictly lower) into LDS and Bm (lower, with the diagonal; zero
+         * above the diagonal blocks) out as bf16 hi/lo rows: thread (t, c8)
+         * forms columns 8 c8 .. 8 c8 + 7 of row t */
+        {
+            const int t = tid >> 3, c8 = tid & 7;
+            const int ti = t >> 4, tj = c8 >> 1;
+            float bm[8];
+            if (tj > ti) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bm[e] = 0.0f;
+            } else {
+                const int p = ti * (ti + 1) / 2 + tj;
+                const float gt = sG[t], bt = sBeta[t];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int sc = 8 * c8 + e;
+                    const float dec = sc <= t ? expf(gt - sG[sc]) : 0.0f;
+                    sA[t][sc] = sc < t ? bt * dec * sKK[p][t & 15][sc & 15] : 0.0f;
+                    bm[e] = sc <= t ? dec * sQK[p][t & 15][sc & 15] : 0.0f;
                 }
             }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sX[wave][row][c4 + e] = x[e];
+            bf16x8 hi, lo;
+            q38_split8(bm, hi, lo);
+            *reinterpret_cast<bf16x8 *>(rec.b_hi + t * BR + 8 * c8) = hi;
+            *reinterpret_cast<bf16x8 *>(rec.b_lo + t * BR + 8 * c8) = lo;
         }
-        __syncthreads();
-        if (mine) {
-            float y[4] = {0.f, 0.f, 0.f, 0.f};
+        /* K'^T = (diag(exp(G_C - G)) K)^T by rows of 8 tokens, K read as hi + lo */
+        for (int it = tid; it < D * (C / 8); it += kPrepThreads) {
+            const int i = it & (D - 1), t8 = it >> 7;
+            float x[8];
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const float tv = sT[16 * bi + row][16 * bi + k];
+            for (int e = 0; e < 8; ++e)
+                x[e] = sKd[8 * t8 + e] * ((float)sKh[8 * t8 + e][i] + (float)sKl[8 * t8 + e][i]);
+            bf16x8 hi, lo;
+            q38_split8(x, hi, lo);
+            *reinterpret_cast<bf16x8 *>(rec.kt_hi + i * BR + 8 * t8) = hi;
+            *reinterpret_cast<bf16x8 *>(rec.kt_lo + i * BR + 8 * t8) = lo;
+        }
+        lds_barrier();
+
+        invert_unit_lower(sA, sT, wave, lane);
+
+        /* the left operands of W and U' as bf16 hi/lo rows: T diag(beta gamma)
+         * and T diag(beta) (over A, free now) */
+        __bf16 *const t2h = reinterpret_cast<__bf16 *>(&sA[0][0]);
+        __bf16 *const t2l = t2h + C * BR;
+        {
+            const int t = tid >> 3, c8 = tid & 7;
+            float x1[8], x2[8];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[e] = __builtin_fmaf(tv, sX[wave][k][c4 + e], y[e]);
+            for (int e = 0; e < 8; ++e) {
+                const float tv = sT[t][8 * c8 + e];
+                x1[e] = tv * sBG[8 * c8 + e];
+                x2[e] = tv * sBeta[8 * c8 + e];
             }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sT[16 * bi + row][16 * bj + c4 + e] = -y[e];
+            bf16x8 hi, lo;
+            q38_split8(x1, hi, lo);
+            *reinterpret_cast<bf16x8 *>(&sWh[t][8 * c8]) = hi;
+            *reinterpret_cast<bf16x8 *>(&sWl[t][8 * c8]) = lo;
+            q38_split8(x2, hi, lo);
+            *reinterpret_cast<bf16x8 *>(t2h + t * BR + 8 * c8) = hi;
+            *reinterpret_cast<bf16x8 *>(t2l + t * BR + 8 * c8) = lo;
         }
-        __syncthreads();
-    }
+        lds_barrier();
 
-    /* the left operands of W and U' as bf16 hi/lo rows: T diag(beta gamma)
-     * over Q's arrays, T diag(beta) over A's (both free now) */
-    __bf16 *const t1h = &sQh[0][0];
-    __bf16 *const t1l = &sQl[0][0];
-    __bf16 *const t2h = reinterpret_cast<__bf16 *>(&sA[0][0]);
-    __bf16 *const t2l = t2h + C * BR;
-    for (int it = tid; it < C * (C / 8); it += kPrepThreads) {
-        const int t = it >> 3, c8 = it & 7;
-        float x1[8], x2[8];
+        /* W = T diag(beta gamma) K, out as bf16 hi/lo rows, and U' = T diag(beta) V
+         * (f32 out): 32 + 32 tiles, 4 + 4 per wave.  W is formed transposed
+         * (W^T = K^T (T diag(beta gamma))^T) so that a lane holds 4 adjacent
+         * columns of a W row.  Token blocks 0 and 1 contract over tokens 0..31
+         * only: T is lower triangular. */
+        for (int tile = wave; tile < 64; tile += kPrepWaves) {
+            const bool is_w = tile < 32;
+            const int ti = (tile & 31) >> 3, tn = tile & 7;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            if (is_w) {
+                if (ti < 2)
+                    acc = mma16_split_acol<32>(acc, &sKh[0][16 * tn], &sKl[0][16 * tn], WR, &sWh[16 * ti][0],
+                                               &sWl[16 * ti][0], BR);
+                else
+                    acc = mma16_split_acol<C>(acc, &sKh[0][16 * tn], &sKl[0][16 * tn], WR, &sWh[16 * ti][0],
+                                              &sWl[16 * ti][0], BR);
+                const int t = 16 * ti + r, col = 16 * tn + 4 * g4;
+                split4_store(rec.w_hi + t * WR + col, rec.w_lo + t * WR + col, acc);
+            } else {
+                if (ti < 2)
+                    acc = q38_mma16_split<32>(acc, t2h + 16 * ti * BR, t2l + 16 * ti * BR, BR, &sVh[16 * tn][0],
+                                              &sVl[16 * tn][0], BR);
+                else
+                    acc = q38_mma16_split<C>(acc, t2h + 16 * ti * BR, t2l + 16 * ti * BR, BR, &sVh[16 * tn][0],
+                                             &sVl[16 * tn][0], BR);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float tv = sT[t][8 * c8 + e];
-            x1[e] = tv * sBG[8 * c8 + e];
-            x2[e] = tv * sBeta[8 * c8 + e];
+                for (int i = 0; i < 4; ++i) rec.u[(16 * ti + 4 * g4 + i) * D + 16 * tn + r] = acc[i];
+            }
         }
-        bf16x8 hi, lo;
-        q38_split8(x1, hi, lo);
-        *reinterpret_cast<bf16x8 *>(t1h + t * BR + 8 * c8) = hi;
-        *reinterpret_cast<bf16x8 *>(t1l + t * BR + 8 * c8) = lo;
-        q38_split8(x2, hi, lo);
-        *reinterpret_cast<bf16x8 *>(t2h + t * BR + 8 * c8) = hi;
-        *reinterpret_cast<bf16x8 *>(t2l + t * BR + 8 * c8) = lo;
-    }
-    __syncthreads();
-
-    /* W = T diag(beta gamma) K, out as bf16 hi/lo rows, and U' = T diag(beta) V
-     * (f32 out): 32 + 32 tiles, 4 + 4 per wave.  W is formed transposed
-     * (W^T = K^T (T diag(beta gamma))^T) so that a lane holds 4 adjacent
-     * columns of a W row.  Token blocks 0 and 1 contract over tokens 0..31
-     * only: T is lower triangular. */
-    for (int tile = wave; tile < 64; tile += kPrepWaves) {
-        const bool is_w = tile < 32;
-        const int ti = (tile & 31) >> 3, tn = tile & 7;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        if (is_w) {
-            if (ti < 2)
-                acc = mma16_split_acol<32>(acc, &sKh[0][16 * tn], &sKl[0][16 * tn], WR, t1h + 16 * ti * BR,
-                                           t1l + 16 * ti * BR, BR);
-            else
-                acc = mma16_split_acol<C>(acc, &sKh[0][16 * tn], &sKl[0][16 * tn], WR, t1h + 16 * ti * BR,
-                                          t1l + 16 * ti * BR, BR);
-            const int t = 16 * ti + r, col = 16 * tn + 4 * g4;
-            split4_store(rec.w_hi + t * WR + col, rec.w_lo + t * WR + col, acc);
-        } else {
-            if (ti < 2)
-                acc = q38_mma16_split<32>(acc, t2h + 16 * ti * BR, t2l + 16 * ti * BR, BR, &sVh[16 * tn][0],
-                                          &sVl[16 * tn][0], BR);
-            else
-                acc = q38_mma16_split<C>(acc, t2h + 16 * ti * BR, t2l + 16 * ti * BR, BR, &sVh[16 * tn][0],
-                                         &sVl[16 * tn][0], BR);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) rec.u[(16 * ti + 4 * g4 + i) * D + 16 * tn + r] = acc[i];
-        }
+        if (j + 1 < kGroup) lds_barrier(); /* the next head reuses every per-head array */
     }
 }
 
