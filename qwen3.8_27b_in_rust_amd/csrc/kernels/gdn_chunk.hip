@@ -353,8 +353,8 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
             sKd[lane] = expf(g_last - g_l);
             if (lane == 0) *rec.gamma_c = expf(g_last);
         }
-        /* V^T of this head split into LDS */
-        if (j > 0) load_v(vh);
+        /* V^T of this head split into LDS; the next head's V rows load behind
+         * the rest of this head's work */
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const int t = row_t(p), c4 = col_c4();
@@ -365,6 +365,7 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
                 sVl[4 * c4 + e][t] = (__bf16)(vv[p][e] - (float)h);
             }
         }
+        if (j + 1 < kGroup) load_v(vh + Q38_LIN_QK_HEADS);
         lds_barrier();
 
         /* A (strictly lower) into LDS and Bm (lower, with the diagonal; zero
