@@ -260,27 +260,26 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
 
     /* rows of the chunk (zero past the prompt: such rows add nothing).  Pass p,
      * lane l of wave w: token 8 (2p + w/4) + l/8, columns 4c .. 4c+3 with
-     * c = 8 (w%4) + l%8, so 8 lanes read 128 contiguous bytes of a row. */
+     * c = 8 (w%4) + l%8, so 8 lanes read 128 contiguous bytes of a row.  Every
+     * load is unconditional (a row past the prompt reads the chunk's last
+     * row) and rows past the prompt are zeroed where they are used: a load
+     * under a branch makes the compiler wait for it at the branch's end. */
     auto row_t = [&](int p) { return 8 * (2 * p + (wave >> 2)) + (lane >> 3); };
     auto col_c4 = [&]() { return 8 * (wave & 3) + (lane & 7); };
     f32x4 kv[4], qv[4], vv[4];
     auto load_v = [&](int vh) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const int t = row_t(p);
-            vv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (t < cnt) vv[p] = q38_ld4(a.v + (tok0 + t) * a.v_stride + vh * D + 4 * col_c4());
+            const size_t tok = tok0 + min(row_t(p), cnt - 1);
+            vv[p] = q38_ld4(a.v + tok * a.v_stride + vh * D + 4 * col_c4());
         }
     };
+    auto live = [&](int p, f32x4 x) { return row_t(p) < cnt ? x : f32x4{0.f, 0.f, 0.f, 0.f}; };
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const int t = row_t(p);
-        kv[p] = qv[p] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (t < cnt) {
-            const size_t tok = tok0 + t;
-            kv[p] = q38_ld4(a.k + tok * a.q_stride + kh * D + 4 * col_c4());
-            qv[p] = q38_ld4(a.q + tok * a.q_stride + kh * D + 4 * col_c4());
-        }
+        const size_t tok = tok0 + min(row_t(p), cnt - 1);
+        kv[p] = q38_ld4(a.k + tok * a.q_stride + kh * D + 4 * col_c4());
+        qv[p] = q38_ld4(a.q + tok * a.q_stride + kh * D + 4 * col_c4());
     }
     load_v(kh);
     /* log-decays and betas of the three heads, one token per lane; every
@@ -290,9 +289,14 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
 #pragma unroll
     for (int j = 0; j < kGroup; ++j) {
         const int vh = kh + Q38_LIN_QK_HEADS * j;
-        const bool in = lane < cnt;
-        beta_in[j] = in ? a.beta[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
-        acc_g[j] = in ? a.g[(tok0 + lane) * Q38_LIN_V_HEADS + vh] : 0.0f;
+        const size_t tok = tok0 + min(lane, cnt - 1);
+        beta_in[j] = a.beta[tok * Q38_LIN_V_HEADS + vh];
+        acc_g[j] = a.g[tok * Q38_LIN_V_HEADS + vh];
+    }
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+        beta_in[j] = lane < cnt ? beta_in[j] : 0.0f;
+        acc_g[j] = lane < cnt ? acc_g[j] : 0.0f;
     }
 #pragma unroll
     for (int j = 0; j < kGroup; ++j) {
@@ -311,13 +315,14 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         const int t = row_t(p), c4 = col_c4();
-        split4_store(&sKh[t][4 * c4], &sKl[t][4 * c4], kv[p]);
-        split4_store(sQh + t * WR + 4 * c4, sQl + t * WR + 4 * c4, qv[p]);
+        const f32x4 kx = live(p, kv[p]), qx = live(p, qv[p]);
+        split4_store(&sKh[t][4 * c4], &sKl[t][4 * c4], kx);
+        split4_store(sQh + t * WR + 4 * c4, sQl + t * WR + 4 * c4, qx);
 #pragma unroll
         for (int j = 0; j < kGroup; ++j) {
             const Record rec = record_of(a, s, kh + Q38_LIN_QK_HEADS * j, n);
             const float gam = expf(__shfl(acc_g[j], t, 64));
-            split4_store(rec.q_hi + t * WR + 4 * c4, rec.q_lo + t * WR + 4 * c4, gam * qv[p]);
+            split4_store(rec.q_hi + t * WR + 4 * c4, rec.q_lo + t * WR + 4 * c4, gam * qx);
         }
     }
     lds_barrier();
@@ -358,11 +363,12 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const int t = row_t(p), c4 = col_c4();
+            const f32x4 vx = live(p, vv[p]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const __bf16 h = (__bf16)vv[p][e];
+                const __bf16 h = (__bf16)vx[e];
                 sVh[4 * c4 + e][t] = h;
-                sVl[4 * c4 + e][t] = (__bf16)(vv[p][e] - (float)h);
+                sVl[4 * c4 + e][t] = (__bf16)(vx[e] - (float)h);
             }
         }
         if (j + 1 < kGroup) load_v(vh + Q38_LIN_QK_HEADS);
