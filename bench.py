@@ -95,6 +95,16 @@ def attention_decode(pkg, ctx, steps: int, warmup: int):
     for i in range(64):
         step(i)
     m_ms, m_n = ctx.kernel_timer_stop()
+    # the same steps on one layer's cache only (268 MB against the 256 MB
+    # last-level cache: the labelled same-buffer figure, not part of `value`)
+    ctx.sync()
+    e2, e3 = ctx.event(), ctx.event()
+    ctx.record(e2)
+    for i in range(100):
+        kv.attn_decode(LAYERS[0], [seq], [CTX - 1], d_q, d_o, k_new=k_new, v_new=v_new, gate=d_g)
+    ctx.record(e3)
+    same_ms = ctx.elapsed_ms(e2, e3) / 100
+    ctx.sync()
     last_layer = LAYERS[(warmup + steps - 1) % 16]
     # outputs of the last timed layer, for the parity line of the CPU leg
     step(warmup + steps - 1)
@@ -104,6 +114,7 @@ def attention_decode(pkg, ctx, steps: int, warmup: int):
         "kernel_ms": k_ms / max(k_n, 1),
         "kernel_launches": k_n,
         "merge_ms": m_ms / max(m_n, 1),
+        "same_buffer_ms_per_step": same_ms,
         "out": out,
         "layer": last_layer,
         "kv": kv, "seq": seq, "rows": (rows_k, rows_v), "q": d_q, "g": d_g,
@@ -346,11 +357,12 @@ def gdn_prefill(pkg, ctx, reps: int):
                     "bf16x3 MFMA products"}
 
 
-def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float):
+def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float, threads: int = 0):
     """The CPU restatement of the reference's attention (ops.rs:868-938) on the
     32K workload, all cores of this host (heads split across threads as the
-    reference's rayon dispatch does): decode steps per second."""
-    threads = ref.cores()
+    reference's rayon dispatch does), or `threads` of them: decode steps per
+    second."""
+    threads = threads or ref.cores()
     out = ref.attn_heads(q, k_rows, v_rows, gate=gate, threads=threads)  # warm
     n, t0 = 0, time.perf_counter()
     while True:
@@ -430,6 +442,8 @@ def main():
         "step_us": r["ms_per_step"] * 1e3,
         "step_gb_s": step_gbs,
         "step_frac_hbm": step_gbs / HBM_PEAK_GBS,
+        "same_buffer_step_us": r["same_buffer_ms_per_step"] * 1e3,
+        "same_buffer_note": "100 steps on one layer's 268 MB cache (the timed steps rotate over 16 layers' caches)",
         "device": info["name"],
         "cu_count": info["cu_count"],
     }
@@ -447,6 +461,8 @@ def main():
         log(f"cpu baseline: restatement on {ref.cores()} host threads, ~{args.cpu_seconds:.0f} s")
         cpu, want = cpu_baseline(ref, q, K, V, g, args.cpu_seconds)
         extra["parity_max_abs_vs_cpu"] = float(np.max(np.abs(r["out"] - want)))
+        one, _ = cpu_baseline(ref, q, K, V, g, min(args.cpu_seconds, 4.0), threads=1)
+        extra["cpu_1_thread_steps_per_s"] = one["value"]
         log(f"cpu {cpu['value']:.2f} steps/s; GPU vs CPU max-abs {extra['parity_max_abs_vs_cpu']:.2e}")
     r["kv"].close()
 
@@ -467,6 +483,9 @@ def main():
         extra["gdn_step_1"] = gdn_steps(pkg, ctx, 1, 192, 384, 32)
         extra["gdn_step_32"] = gdn_steps(pkg, ctx, 32, 192, 60, 6)
         log(f"gdn: {json.dumps(extra['gdn_step_1'])} {json.dumps(extra['gdn_step_32'])}")
+        # labelled same-buffer figure: one 6.3 MB state stepped in place
+        extra["gdn_step_1_same_state"] = gdn_steps(pkg, ctx, 1, 1, 384, 32)
+        log(f"gdn, one state in place: {json.dumps(extra['gdn_step_1_same_state'])}")
 
     line = {
         "metric": "attn decode-steps/s & achieved HBM GB/s (% of 8 TB/s) at 32K ctx, 1 MI355X",
