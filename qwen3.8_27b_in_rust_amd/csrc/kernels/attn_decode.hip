@@ -315,6 +315,11 @@ extern "C" __global__ __launch_bounds__(256) void q38_attn_decode_merge(q38_merg
     const size_t o_step = (size_t)Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
     const float *po = a.part_o + ((size_t)base * Q38_ATTN_HEADS + h) * Q38_ATTN_HEAD_DIM + d;
     const float *pml = a.part_ml + ((size_t)base * Q38_ATTN_HEADS + h) * 2;
+    /* the gate of the 4 output dims this thread may store, loaded with the
+     * partials rather than after them */
+    const size_t off = (size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d;
+    const bool gated = a.gate != nullptr;
+    const f32x4 gt = gated && sl == 0 ? q38_ld4(a.gate + off) : f32x4{0.f, 0.f, 0.f, 0.f};
 
     float M = -INFINITY, L = 0.0f;
     f32x4 O = {0.f, 0.f, 0.f, 0.f};
@@ -364,9 +369,7 @@ extern "C" __global__ __launch_bounds__(256) void q38_attn_decode_merge(q38_merg
             Ot = q38_fma4(w, red_o[i][dl], Ot);
         }
         f32x4 r = Ot / Lt;
-        const size_t off = (size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d;
-        if (a.gate != nullptr) {
-            const f32x4 gt = q38_ld4(a.gate + off);
+        if (gated) {
             r.x *= q38_sigmoid(gt.x);
             r.y *= q38_sigmoid(gt.y);
             r.z *= q38_sigmoid(gt.z);
