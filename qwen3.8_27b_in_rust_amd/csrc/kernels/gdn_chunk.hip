@@ -1,7 +1,7 @@
 /*
  * Chunked Gated-DeltaNet prefill (gfx950): the recurrence of linear_core
  * (src/model/ops.rs:698-714) over a prompt, 64 tokens at a time, with the
- * intra-chunk products on bf16x3 MFMA (q38_mma16).
+ * intra-chunk products on bf16x3 MFMA (q38_mma16_split).
  *
  * The reference runs the recurrence token by token (ops.rs:1084-1099):
  *     S_t = d_t S_{t-1} + u_t k_t^T,  u_t = beta_t (v_t - d_t S_{t-1} k_t),
@@ -18,10 +18,11 @@
  * Every decay factor is exp of a difference G_t - G_s (s <= t) or of G_t
  * itself, never exp(-G), so nothing overflows when decays are strong.
  *
- * q38_gdn_chunk_prep (grid (48 heads, chunks, sequences)) computes W, U', Bm
- * and G of every chunk in parallel; T comes from a blocked forward
- * substitution in f32 (16x16 diagonal blocks inverted by substitution, the
- * off-diagonal blocks by T_ij = -T_ii sum_k A_ik T_kj).
+ * q38_gdn_chunk_prep (grid (16 q/k heads, chunks, sequences)) computes W, U',
+ * Bm and G of every chunk in parallel, for the 3 value heads that read one
+ * q/k head; T comes from a blocked inverse in f32 (16x16 diagonal blocks by
+ * substitution, the off-diagonal blocks by T_ij = -T_ii sum_k A_ik T_kj on
+ * fp32 matrix instructions).
  * q38_gdn_chunk_scan (grid (48 heads x 4 slabs of 32 value rows, sequences))
  * carries its slab of the state through the chunks: value rows are
  * independent in every formula above, so a slab needs only its own rows.
@@ -32,7 +33,6 @@
 namespace {
 constexpr int C = Q38_GDN_CHUNK;     /* tokens per chunk */
 constexpr int D = Q38_LIN_HEAD_DIM;  /* 128 */
-constexpr int P = D + 4;             /* padded LDS row (floats) */
 constexpr int kSlabs = 4;
 constexpr int R = D / kSlabs;        /* value rows per scan slab */
 constexpr int WR = Q38_GDN_WROW;

@@ -125,16 +125,6 @@ Q38_DEV void q38_barrier_vm() {
     asm volatile("" ::: "memory");
 }
 
-/* Store of one bf16 to LDS that the compiler does not see as a memory access,
- * so its wait-count pass cannot order it after outstanding direct-to-LDS loads
- * into other arrays (it may not tell them apart).  The caller makes it
- * visible with a barrier that waits for lgkmcnt 0. */
-Q38_DEV void q38_lds_store_bf16(__bf16 *p, __bf16 x) {
-    const uint32_t addr = (uint32_t)(size_t)(__attribute__((address_space(3))) __bf16 *)p;
-    const uint32_t v = __builtin_bit_cast(uint16_t, x);
-    asm volatile("ds_write_b16 %0, %1" ::"v"(addr), "v"(v) : "memory");
-}
-
 /* ------------------------------------------------ bf16x3 matrix-core tiles */
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -151,40 +141,14 @@ Q38_DEV void q38_split8(const float (&x)[8], bf16x8 &hi, bf16x8 &lo) {
 }
 
 /*
- * One 16x16 output tile on v_mfma_f32_16x16x32_bf16 with bf16x3 products:
- * c += A B, A(m, k) = fa(m, k) (16 x KD), B(k, n) = fb(k, n) (KD x 16),
- * KD a multiple of 32.  Lane l supplies A row l%16 and B column l%16 at
- * k = k0 + 8(l/16) .. +7; the tile it returns holds rows 4(l/16) + i
- * (i = 0..3) of column l%16.
- */
-template <int KD, class FA, class FB>
-Q38_DEV f32x4 q38_mma16(f32x4 c, FA fa, FB fb) {
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;
-    const int r = lane & 15;
-#pragma unroll
-    for (int k0 = 0; k0 < KD; k0 += 32) {
-        float av[8], bv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            av[j] = fa(r, k0 + 8 * g + j);
-            bv[j] = fb(k0 + 8 * g + j, r);
-        }
-        bf16x8 ah, al, bh, bl;
-        q38_split8(av, ah, al);
-        q38_split8(bv, bh, bl);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
-    }
-    return c;
-}
-
-/*
- * The same tile with both operands already split into bf16 hi/lo arrays
- * (LDS): A row m at a_hi/a_lo + m*lda, and B given by its columns, B(k, n)
- * = b[n*ldb + k], each contiguous in k.  One 16-byte read per fragment half.
- * Row strides and the arrays must keep 16-byte alignment.
+ * One 16x16 output tile on v_mfma_f32_16x16x32_bf16 with bf16x3 products,
+ * c += A B (A 16 x KD, B KD x 16, KD a multiple of 32), both operands already
+ * split into bf16 hi/lo arrays (LDS): A row m at a_hi/a_lo + m*lda, and B
+ * given by its columns, B(k, n) = b[n*ldb + k], each contiguous in k.  Lane l
+ * supplies A row l%16 and B column l%16 at k = k0 + 8(l/16) .. +7 (one 16-byte
+ * read per fragment half); the tile it returns holds rows 4(l/16) + i
+ * (i = 0..3) of column l%16.  Row strides and the arrays must keep 16-byte
+ * alignment.
  */
 template <int KD>
 Q38_DEV f32x4 q38_mma16_split(f32x4 c, const __bf16 *a_hi, const __bf16 *a_lo, int lda, const __bf16 *b_hi,
