@@ -218,3 +218,39 @@ def test_linear_core_prefill_matches_reference(ctx, ref, synth, T):
     assert worst <= 1e-3
     assert np.max(np.abs(d_conv.download() - c_ref)) == 0.0
     assert max(_rel(d_delta.download(), s_ref)) <= 1e-4
+
+
+def test_linear_core_prefill_two_sequences(ctx, ref, synth):
+    """Two sequences' prompts in one call: the chunked kernels' sequence axis
+    (records, state slabs and outputs at (s*T + t)), with a partial last chunk."""
+    n, T = 2, 70
+    conv_w = synth.normal(631, 10240 * 4, sigma=0.5)
+    dt = synth.normal(632, 48)
+    a = -np.abs(synth.normal(633, 48))
+    norm = synth.normal(634, 128, sigma=0.1, mean=1.0)
+    conv_state = synth.normal(635, n * 10240 * 3)
+    delta = synth.normal(636, n * STATE, sigma=0.02)
+    qkv = synth.normal(637, n * T * 10240)
+    z = synth.normal(638, n * T * 6144)
+    b = synth.normal(639, n * T * 48)
+    al = synth.normal(640, n * T * 48)
+    d_conv, d_delta = ctx.array(conv_state), ctx.array(delta)
+    d_out = ctx.empty((n * T, 6144))
+    ctx.linear_core(n, T, *[ctx.array(x) for x in (conv_w, dt, a, norm)], d_conv, d_delta, ctx.array(qkv),
+                    ctx.array(z), ctx.array(b), ctx.array(al), d_out)
+    got = d_out.download().reshape(n * T, 6144)
+    got_conv, got_delta = d_conv.download(), d_delta.download()
+    for s in range(n):
+        c_ref = conv_state[s * 30720:(s + 1) * 30720].copy()
+        s_ref = delta[s * STATE:(s + 1) * STATE].copy()
+        worst = 0.0
+        for t in range(T):
+            r = s * T + t
+            o = ref.linear_core(conv_w, dt, a, norm, c_ref, s_ref, qkv[r * 10240:(r + 1) * 10240],
+                                z[r * 6144:(r + 1) * 6144], b[r * 48:(r + 1) * 48], al[r * 48:(r + 1) * 48],
+                                threads=8)
+            worst = max(worst, float(np.max(np.abs(got[r] - o))))
+        assert worst <= 1e-3, (s, worst)
+        assert np.max(np.abs(got_conv[s * 30720:(s + 1) * 30720] - c_ref)) == 0.0
+        assert max(_rel(got_delta[s * STATE:(s + 1) * STATE], s_ref)) <= 1e-4
+
