@@ -821,15 +821,21 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
         float *qo = static_cast<float *>(ctx->work) + part_floats;
         float *go = qo + (size_t)n * Q38_ATTN_Q_DIM;
         float *ko = go + (size_t)n * Q38_ATTN_Q_DIM;
-        /* positions differ per sequence: one pre launch per sequence keeps
-         * the kernel's position = pos0 + token contract */
-        for (int b = 0; b < n; ++b) {
-            if (q38_attn_pre(ctx, 1, positions[b0 + b], d_q_norm, d_k_norm,
-                             d_q_and_gate + (size_t)(b0 + b) * Q38_ATTN_QG_DIM,
-                             d_key + (size_t)(b0 + b) * Q38_ATTN_KV_DIM, qo + (size_t)b * Q38_ATTN_Q_DIM,
-                             go + (size_t)b * Q38_ATTN_Q_DIM, ko + (size_t)b * Q38_ATTN_KV_DIM))
-                return -1;
-        }
+        /* one pre launch for the chunk's sequences, each at its own position */
+        q38_attn_pre_args p;
+        memset(&p, 0, sizeof(p));
+        p.q_and_gate = d_q_and_gate + (size_t)b0 * Q38_ATTN_QG_DIM;
+        p.key = d_key + (size_t)b0 * Q38_ATTN_KV_DIM;
+        p.q_norm = d_q_norm;
+        p.k_norm = d_k_norm;
+        p.q_out = qo;
+        p.gate_out = go;
+        p.k_out = ko;
+        p.n_tokens = n;
+        p.theta_scale = ctx->rope_theta_scale;
+        p.per_token_positions = 1;
+        for (int b = 0; b < n; ++b) p.positions[b] = positions[b0 + b];
+        if (ctx->launch(ctx->f_attn_pre, n, Q38_ATTN_HEADS + Q38_ATTN_KV_HEADS, 1, 64, &p)) return -1;
         if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, qo, ko,
                          d_value + (size_t)b0 * Q38_ATTN_KV_DIM, go,
                          d_out + (size_t)b0 * Q38_ATTN_Q_DIM))

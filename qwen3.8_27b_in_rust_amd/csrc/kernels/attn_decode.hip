@@ -406,7 +406,7 @@ extern "C" __global__ __launch_bounds__(64) void q38_attn_pre(q38_attn_pre_args 
     const int t = blockIdx.x;
     const int hd = blockIdx.y;
     const int lane = threadIdx.x;
-    const int position = a.positions_dev != nullptr ? a.positions_dev[t] : a.pos0 + t;
+    const int position = a.per_token_positions ? a.positions[t] : a.pos0 + t;
     const bool is_q = hd < Q38_ATTN_HEADS;
     const float *src;
     const float *w;

@@ -84,11 +84,11 @@ typedef struct {
     float *q_out;            /* [n][24][256] */
     float *gate_out;         /* [n][24][256] */
     float *k_out;            /* [n][4][256] */
-    const int32_t *positions_dev; /* [n] or NULL: then position = pos0 + token */
     int32_t pos0;
     int32_t n_tokens;
     float theta_scale; /* 1e7^(-2/64) in f32 */
-    int32_t pad_;
+    int32_t per_token_positions; /* 1: token t's position is positions[t] (t < 64) */
+    int32_t positions[Q38_MAX_BATCH]; /* else position = pos0 + token */
 } q38_attn_pre_args;
 
 /* Gated-DeltaNet recurrence over n_tokens consecutive tokens of each of

@@ -212,6 +212,46 @@ def test_full_core_matches_reference(pkg, ctx, ref):
     assert worst <= TOL
 
 
+def test_full_core_batched_positions(pkg, ctx, ref):
+    """full_core for three sequences at different positions in one call (one
+    pre launch with each sequence's own RoPE position, then the batched
+    decode with appends), each against the reference on its own caches."""
+    from q38amd import synth
+    layer = 3
+    ctx_len = 1024
+    qn = synth.normal(11, 256, sigma=0.2, mean=1.0)
+    kn = synth.normal(12, 256, sigma=0.2, mean=1.0)
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=3 * ctx_len // 16, max_seqs=3, max_tokens_per_seq=ctx_len)
+    positions = [100, 37, 500]
+    seqs = [kv.seq_create() for _ in positions]
+    caches = []
+    for i, (sq, pos) in enumerate(zip(seqs, positions)):
+        K0 = synth.normal(20 + i, pos * 1024)
+        V0 = synth.normal(30 + i, pos * 1024)
+        kc = np.zeros(ctx_len * 1024, np.float32)
+        vc = np.zeros(ctx_len * 1024, np.float32)
+        kc[:pos * 1024] = K0
+        vc[:pos * 1024] = V0
+        d_k0, d_v0 = ctx.array(K0), ctx.array(V0)
+        kv.write(layer, sq, 0, pos, d_k0, d_v0)
+        d_k0.free()
+        d_v0.free()
+        caches.append((kc, vc))
+    qg = synth.normal(40, 3 * 12288)
+    key = synth.normal(41, 3 * 1024)
+    val = synth.normal(42, 3 * 1024)
+    d_o = ctx.empty((3, 24, 256))
+    kv.full_core(layer, seqs, positions, ctx.array(qn), ctx.array(kn), ctx.array(qg), ctx.array(key),
+                 ctx.array(val), d_o)
+    got = d_o.download().reshape(3, 6144)
+    for b, pos in enumerate(positions):
+        kc, vc = caches[b]
+        want, _ = ref.full_core(qn, kn, qg[b * 12288:(b + 1) * 12288], key[b * 1024:(b + 1) * 1024],
+                                val[b * 1024:(b + 1) * 1024], kc, vc, ctx_len, pos, layer, threads=8)
+        assert float(np.max(np.abs(got[b] - np.asarray(want).reshape(-1)))) <= TOL, b
+    kv.close()
+
+
 def test_attn_pre_matches_reference(pkg, ctx, ref):
     """RMSNorm + RoPE prologue alone, bit for bit where the math is exact."""
     from q38amd import synth
