@@ -86,6 +86,7 @@ struct q38_ctx {
     hipFunction_t f_chunk_scan = nullptr;
     hipFunction_t f_gdn_post = nullptr;
     hipFunction_t f_decode_split = nullptr;
+    hipFunction_t f_decode_split_pre = nullptr; /* the same with full_core's pre step fused */
     hipFunction_t f_decode_merge = nullptr;
     hipFunction_t f_kv_copy = nullptr;
     hipFunction_t f_attn_pre = nullptr;
@@ -265,6 +266,7 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_prefill, ctx->mod_prefill, "q38_attn_prefill_mfma"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_split, ctx->mod_prefill, "q38_kv_split_mfma"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split, ctx->mod_decode, "q38_attn_decode_split"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_pre, ctx->mod_decode, "q38_attn_decode_split_pre"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "q38_attn_decode_merge"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_copy, ctx->mod_decode, "q38_kv_copy"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_attn_pre, ctx->mod_decode, "q38_attn_pre"));
@@ -418,6 +420,7 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     hipFunction_t f = nullptr;
     const std::string name(kernel_name);
     if (name == "q38_attn_decode_split") f = ctx->f_decode_split;
+    else if (name == "q38_attn_decode_split_pre") f = ctx->f_decode_split_pre;
     else if (name == "q38_attn_decode_merge") f = ctx->f_decode_merge;
     else if (name == "q38_kv_copy") f = ctx->f_kv_copy;
     else if (name == "q38_attn_pre") f = ctx->f_attn_pre;
@@ -662,9 +665,16 @@ int choose_split_tokens(const q38_ctx *ctx, int n_seq, long total_tokens, long m
     return 0;
 }
 
+/* full_core's pre step fused into the decode kernel: d_q holds raw q|gate
+ * rows, d_k_new raw keys; norm weights for both */
+struct decode_pre {
+    const float *q_norm;
+    const float *k_norm;
+};
+
 int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const int32_t *positions,
                  const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate,
-                 float *d_out) {
+                 float *d_out, const decode_pre *pre = nullptr) {
     q38_ctx *ctx = kv->ctx;
     long total_tokens = 0, max_tokens = 0;
     for (int b = 0; b < n_seq; ++b) {
@@ -684,6 +694,15 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
     a.v_new = d_v_new;
     a.gate = d_gate;
     a.out = d_out;
+    a.gate_head_stride = Q38_ATTN_HEAD_DIM;
+    if (pre != nullptr) {
+        /* q|gate rows: the gate is the second half of each head's 512 */
+        a.gate = d_q + Q38_ATTN_HEAD_DIM;
+        a.gate_head_stride = 2 * Q38_ATTN_HEAD_DIM;
+        a.q_norm = pre->q_norm;
+        a.k_norm = pre->k_norm;
+        a.theta_scale = ctx->rope_theta_scale;
+    }
     a.pt_stride = kv->pt_stride;
     a.n_seq = n_seq;
     a.split_tokens = split_tokens;
@@ -707,13 +726,16 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
         a.part_o = static_cast<float *>(ctx->work);
         a.part_ml = a.part_o + part_o_floats;
     }
-    if (ctx->launch(ctx->f_decode_split, total, Q38_ATTN_KV_HEADS, 1, ctx->decode_block, &a)) return -1;
+    if (ctx->launch(pre != nullptr ? ctx->f_decode_split_pre : ctx->f_decode_split, total, Q38_ATTN_KV_HEADS, 1,
+                    ctx->decode_block, &a))
+        return -1;
     if (any_multi) {
         q38_merge_args m;
         memset(&m, 0, sizeof(m));
         m.part_o = a.part_o;
         m.part_ml = a.part_ml;
-        m.gate = d_gate;
+        m.gate = a.gate;
+        m.gate_head_stride = a.gate_head_stride;
         m.out = d_out;
         m.n_seq = n_seq;
         memcpy(m.split_base, a.split_base, sizeof(m.split_base));
@@ -801,44 +823,14 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
     if (validate_decode(kv, layer, n_seq, seq_ids, positions, true, &slot)) return -1;
     if (n_seq == 0) return 0;
     if (!d_q_norm || !d_k_norm || !d_q_and_gate || !d_key || !d_value || !d_out) return fail("NULL argument");
-    q38_ctx *ctx = kv->ctx;
+    /* the pre step (q/gate split, q and k RMSNorm, RoPE) runs inside the
+     * decode kernel: no separate launch and no intermediate rows */
+    const decode_pre pre{d_q_norm, d_k_norm};
     for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
         const int n = std::min(Q38_MAX_BATCH, n_seq - b0);
-        /* workspace: q [n][6144] | gate [n][6144] | k [n][1024], after the
-         * region decode_chunk uses for its partials */
-        const size_t pre_floats = (size_t)n * (2 * Q38_ATTN_Q_DIM + Q38_ATTN_KV_DIM);
-        long total_tokens = 0, max_tokens = 0;
-        for (int b = 0; b < n; ++b) {
-            total_tokens += positions[b0 + b] + 1;
-            max_tokens = std::max<long>(max_tokens, positions[b0 + b] + 1);
-        }
-        int split = 0;
-        if (choose_split_tokens(ctx, n, total_tokens, max_tokens, &split)) return -1;
-        size_t splits = 0;
-        for (int b = 0; b < n; ++b) splits += (positions[b0 + b] + split) / split;
-        const size_t part_floats = splits * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2);
-        if (ctx->ensure_work((part_floats + pre_floats) * sizeof(float))) return -1;
-        float *qo = static_cast<float *>(ctx->work) + part_floats;
-        float *go = qo + (size_t)n * Q38_ATTN_Q_DIM;
-        float *ko = go + (size_t)n * Q38_ATTN_Q_DIM;
-        /* one pre launch for the chunk's sequences, each at its own position */
-        q38_attn_pre_args p;
-        memset(&p, 0, sizeof(p));
-        p.q_and_gate = d_q_and_gate + (size_t)b0 * Q38_ATTN_QG_DIM;
-        p.key = d_key + (size_t)b0 * Q38_ATTN_KV_DIM;
-        p.q_norm = d_q_norm;
-        p.k_norm = d_k_norm;
-        p.q_out = qo;
-        p.gate_out = go;
-        p.k_out = ko;
-        p.n_tokens = n;
-        p.theta_scale = ctx->rope_theta_scale;
-        p.per_token_positions = 1;
-        for (int b = 0; b < n; ++b) p.positions[b] = positions[b0 + b];
-        if (ctx->launch(ctx->f_attn_pre, n, Q38_ATTN_HEADS + Q38_ATTN_KV_HEADS, 1, 64, &p)) return -1;
-        if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, qo, ko,
-                         d_value + (size_t)b0 * Q38_ATTN_KV_DIM, go,
-                         d_out + (size_t)b0 * Q38_ATTN_Q_DIM))
+        if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, d_q_and_gate + (size_t)b0 * Q38_ATTN_QG_DIM,
+                         d_key + (size_t)b0 * Q38_ATTN_KV_DIM, d_value + (size_t)b0 * Q38_ATTN_KV_DIM, nullptr,
+                         d_out + (size_t)b0 * Q38_ATTN_Q_DIM, &pre))
             return -1;
     }
     return 0;

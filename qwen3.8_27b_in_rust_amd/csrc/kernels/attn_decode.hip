@@ -97,14 +97,123 @@ Q38_DEV void decode_rows(DecodeState &st, const f32x4 (&q0)[Q38_ATTN_GROUP],
     }
 }
 
+/* RMSNorm with weight w (rms_scale / rmsnorm_inplace, ops.rs:476-498: f64 sum
+ * of squares, eps 1e-6), then RoPE on dims 0..63 (ops.rs:595-610: pairs (p,
+ * p+32), theta_0 = position, theta_{p+1} = theta_p * 1e7^(-2/64) by repeated
+ * f32 multiplication) of one 256-dim head held 4 dims per lane by a whole
+ * wave (lane l: dims 4l .. 4l+3).  Every f32 square is exact in f64, so the
+ * f64 sum rounds to the same f32 mean in any order. */
+Q38_DEV void q38_rope_lanes(f32x4 &x, int l, int position, float theta_scale) {
+    /* lanes 0..7 hold dims 0..31, lanes 8..15 their partners 32..63 */
+    f32x4 partner;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) partner[c] = __shfl_xor(x[c], 8, 64);
+    if (l < 16) {
+        const int p0 = 4 * (l & 7);
+        float theta = (float)position;
+        for (int i = 0; i < p0; ++i) theta *= theta_scale;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float cosine = cosf(theta);
+            const float sine = sinf(theta);
+            if (l < 8) {
+                const float x0 = x[c], x1 = partner[c];
+                x[c] = x0 * cosine - x1 * sine;
+            } else {
+                const float x0 = partner[c], x1 = x[c];
+                x[c] = x0 * sine + x1 * cosine;
+            }
+            theta *= theta_scale;
+        }
+    }
+}
+
+/* RoPE angles of one position, once: pair p gets theta_p = position *
+ * scale^p by p repeated f32 multiplications (the reference's rounding), and
+ * cs[p] = (cos, sin) of it; lane p < 32 of the calling wave forms pair p. */
+Q38_DEV void q38_rope_table(float (*cs)[2], int lane, int position, float theta_scale) {
+    if (lane < 32) {
+        float theta = (float)position;
+        for (int i = 0; i < lane; ++i) theta *= theta_scale;
+        cs[lane][0] = cosf(theta);
+        cs[lane][1] = sinf(theta);
+    }
+}
+
+/* q38_rope_lanes with the angles read from a table of q38_rope_table */
+Q38_DEV void q38_rope_lanes_cs(f32x4 &x, int l, const float (*cs)[2]) {
+    f32x4 partner;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) partner[c] = __shfl_xor(x[c], 8, 64);
+    if (l < 16) {
+        const int p0 = 4 * (l & 7);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float cosine = cs[p0 + c][0];
+            const float sine = cs[p0 + c][1];
+            if (l < 8) {
+                const float x0 = x[c], x1 = partner[c];
+                x[c] = x0 * cosine - x1 * sine;
+            } else {
+                const float x0 = partner[c], x1 = x[c];
+                x[c] = x0 * sine + x1 * cosine;
+            }
+        }
+    }
+}
+
+/* RMS scale of a 256-dim head from its f64 sum of squares */
+Q38_DEV float q38_rms_scale_of(double ss) {
+    const float mean = (float)(ss / (double)Q38_ATTN_HEAD_DIM);
+    return 1.0f / sqrtf(mean + 1e-6f);
+}
+
+Q38_DEV void q38_norm_rope4(f32x4 &x, f32x4 w, int lane, int position, float theta_scale) {
+    double ss = (double)x.x * (double)x.x + (double)x.y * (double)x.y + (double)x.z * (double)x.z +
+                (double)x.w * (double)x.w;
+    ss = q38_wave_sum_f64(ss);
+    const float mean = (float)(ss / (double)Q38_ATTN_HEAD_DIM);
+    const float scale = 1.0f / sqrtf(mean + 1e-6f);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[c] = x[c] * scale * w[c];
+    q38_rope_lanes(x, lane, position, theta_scale);
+}
+
+/* The same for a head held by a half-wave, lane li: dims 4li .. 4li+3 (x0)
+ * and 128 + 4li .. (x1); the angles from a q38_rope_table. */
+Q38_DEV void q38_norm_rope8(f32x4 &x0, f32x4 &x1, f32x4 w0, f32x4 w1, int li, const float (*cs)[2]) {
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ss += (double)x0[c] * (double)x0[c] + (double)x1[c] * (double)x1[c];
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float scale = q38_rms_scale_of(ss);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        x0[c] = x0[c] * scale * w0[c];
+        x1[c] = x1[c] * scale * w1[c];
+    }
+    q38_rope_lanes_cs(x0, li, cs);
+}
+
+/* The same for a head held 4 dims per lane by a whole wave */
+Q38_DEV void q38_norm_rope4_cs(f32x4 &x, f32x4 w, int lane, const float (*cs)[2]) {
+    double ss = (double)x.x * (double)x.x + (double)x.y * (double)x.y + (double)x.z * (double)x.z +
+                (double)x.w * (double)x.w;
+    const float scale = q38_rms_scale_of(q38_wave_sum_f64(ss));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) x[c] = x[c] * scale * w[c];
+    q38_rope_lanes_cs(x, lane, cs);
+}
+
 }  // namespace
 
 #ifndef Q38_DECODE_MIN_WGS
 #define Q38_DECODE_MIN_WGS 1 /* workgroups per CU the register budget is sized for */
 #endif
 
-extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split(
-    q38_decode_args a) {
+template <bool kPre>
+Q38_DEV void decode_split(const q38_decode_args &a) {
     constexpr int NW = Q38_DECODE_WAVES;
     __shared__ float red_o[NW][Q38_ATTN_GROUP][Q38_ATTN_HEAD_DIM];
     __shared__ float red_m[NW][Q38_ATTN_GROUP];
@@ -135,11 +244,26 @@ extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WG
     const int32_t *pt = a.page_table + (size_t)seq * a.pt_stride;
     const int n_split_pages = (t_end - t_begin + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS;
     if (tid < n_split_pages) pages[tid] = pt[(t_begin >> 4) + tid];
+    /* with the pre step fused, the split holding `pos` forms the new key row
+     * (RMSNorm and RoPE of the raw key, ops.rs:844-856) in LDS; it is
+     * appended below and scored from there */
+    __shared__ __attribute__((aligned(16))) float k_formed[Q38_ATTN_HEAD_DIM];
+    __shared__ float rope_cs[32][2];
+    const bool holds_pos = pos >= t_begin && pos < t_end;
+    if (kPre) {
+        if (wave == NW - 1) q38_rope_table(rope_cs, lane, pos, a.theta_scale);
+        __syncthreads();
+        if (a.k_new != nullptr && holds_pos && wave == 0) {
+            f32x4 x = q38_ld4(a.k_new + (size_t)b * Q38_ATTN_KV_DIM + j * Q38_ATTN_HEAD_DIM + 4 * lane);
+            q38_norm_rope4_cs(x, q38_ld4(a.k_norm + 4 * lane), lane, rope_cs);
+            q38_st4(&k_formed[4 * lane], x);
+        }
+    }
     __syncthreads();
     const float *k_new_row = nullptr;
     const float *v_new_row = nullptr;
     if (a.k_new != nullptr) {
-        k_new_row = a.k_new + (size_t)b * Q38_ATTN_KV_DIM + j * Q38_ATTN_HEAD_DIM;
+        k_new_row = kPre ? k_formed : a.k_new + (size_t)b * Q38_ATTN_KV_DIM + j * Q38_ATTN_HEAD_DIM;
         v_new_row = a.v_new + (size_t)b * Q38_ATTN_KV_DIM + j * Q38_ATTN_HEAD_DIM;
         /* KV append (ops.rs:858-866): the split that holds `pos` stores the row. */
         if (pos >= t_begin && pos < t_end && wave == 0) {
@@ -172,11 +296,30 @@ extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WG
     }
 
     f32x4 q0[Q38_ATTN_GROUP], q1[Q38_ATTN_GROUP];
-    const float *qb = a.q + ((size_t)b * Q38_ATTN_HEADS + j * Q38_ATTN_GROUP) * Q38_ATTN_HEAD_DIM;
+    if (kPre) {
+        /* the group's query heads from q|gate, RMSNormed and rotated here
+         * (ops.rs:832-856; the same arithmetic as q38_attn_pre), each half-wave
+         * holding a whole head */
+        const float *qb = a.q + ((size_t)b * Q38_ATTN_HEADS + j * Q38_ATTN_GROUP) * 2 * Q38_ATTN_HEAD_DIM;
 #pragma unroll
-    for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
-        q0[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d0) * Q38_SCORE_LOG2;
-        q1[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d1) * Q38_SCORE_LOG2;
+        for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+            q0[hh] = q38_ld4(qb + hh * 2 * Q38_ATTN_HEAD_DIM + d0);
+            q1[hh] = q38_ld4(qb + hh * 2 * Q38_ATTN_HEAD_DIM + d1);
+        }
+        const f32x4 w0 = q38_ld4(a.q_norm + d0), w1 = q38_ld4(a.q_norm + d1);
+#pragma unroll
+        for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+            q38_norm_rope8(q0[hh], q1[hh], w0, w1, li, rope_cs);
+            q0[hh] *= Q38_SCORE_LOG2;
+            q1[hh] *= Q38_SCORE_LOG2;
+        }
+    } else {
+        const float *qb = a.q + ((size_t)b * Q38_ATTN_HEADS + j * Q38_ATTN_GROUP) * Q38_ATTN_HEAD_DIM;
+#pragma unroll
+        for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+            q0[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d0) * Q38_SCORE_LOG2;
+            q1[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d1) * Q38_SCORE_LOG2;
+        }
     }
 
     DecodeState st;
@@ -278,7 +421,8 @@ extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WG
         const int h = j * Q38_ATTN_GROUP + hh;
         if (nsplit == 1) {
             float r = O / L;
-            if (a.gate != nullptr) r *= q38_sigmoid(a.gate[(size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d]);
+            if (a.gate != nullptr)
+                r *= q38_sigmoid(a.gate[((size_t)b * Q38_ATTN_HEADS + h) * a.gate_head_stride + d]);
             a.out[(size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d] = r;
         } else {
             a.part_o[((size_t)g * Q38_ATTN_HEADS + h) * Q38_ATTN_HEAD_DIM + d] = O;
@@ -288,6 +432,19 @@ extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WG
             }
         }
     }
+}
+
+extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split(
+    q38_decode_args a) {
+    decode_split<false>(a);
+}
+
+/* The same with the pre step of full_core fused: q from the raw q|gate rows
+ * and the appended key from the raw key, both RMSNormed and rotated in the
+ * kernel; the gate read from q|gate. */
+extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_pre(
+    q38_decode_args a) {
+    decode_split<true>(a);
 }
 
 /* Combine the splits of each (sequence, head): rescale every partial to the
@@ -319,7 +476,8 @@ extern "C" __global__ __launch_bounds__(256) void q38_attn_decode_merge(q38_merg
      * partials rather than after them */
     const size_t off = (size_t)b * Q38_ATTN_Q_DIM + h * Q38_ATTN_HEAD_DIM + d;
     const bool gated = a.gate != nullptr;
-    const f32x4 gt = gated && sl == 0 ? q38_ld4(a.gate + off) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 gt = gated && sl == 0 ? q38_ld4(a.gate + ((size_t)b * Q38_ATTN_HEADS + h) * a.gate_head_stride + d)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
 
     float M = -INFINITY, L = 0.0f;
     f32x4 O = {0.f, 0.f, 0.f, 0.f};
@@ -406,7 +564,7 @@ extern "C" __global__ __launch_bounds__(64) void q38_attn_pre(q38_attn_pre_args 
     const int t = blockIdx.x;
     const int hd = blockIdx.y;
     const int lane = threadIdx.x;
-    const int position = a.per_token_positions ? a.positions[t] : a.pos0 + t;
+    const int position = a.pos0 + t;
     const bool is_q = hd < Q38_ATTN_HEADS;
     const float *src;
     const float *w;
@@ -424,38 +582,6 @@ extern "C" __global__ __launch_bounds__(64) void q38_attn_pre(q38_attn_pre_args 
         dst = a.k_out + ((size_t)t * Q38_ATTN_KV_HEADS + kh) * Q38_ATTN_HEAD_DIM;
     }
     f32x4 x = q38_ld4(src + 4 * lane);
-    /* rms_scale (ops.rs:476-483): every f32 square is exact in f64, so the
-     * f64 sum rounds to the same f32 mean in any order */
-    double ss = (double)x.x * (double)x.x + (double)x.y * (double)x.y + (double)x.z * (double)x.z +
-                (double)x.w * (double)x.w;
-    ss = q38_wave_sum_f64(ss);
-    const float mean = (float)(ss / (double)Q38_ATTN_HEAD_DIM);
-    const float scale = 1.0f / sqrtf(mean + 1e-6f);
-    const f32x4 wv = q38_ld4(w + 4 * lane);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) x[c] = x[c] * scale * wv[c];
-
-    /* RoPE: lanes 0..7 hold x0 = dims 0..31, lanes 8..15 hold x1 = dims 32..63 */
-    f32x4 partner;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) partner[c] = __shfl_xor(x[c], 8, 64);
-    if (lane < 16) {
-        const int p0 = 4 * (lane & 7);
-        float theta = (float)position;
-        for (int i = 0; i < p0; ++i) theta *= a.theta_scale;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float cosine = cosf(theta);
-            const float sine = sinf(theta);
-            if (lane < 8) {
-                const float x0 = x[c], x1 = partner[c];
-                x[c] = x0 * cosine - x1 * sine;
-            } else {
-                const float x0 = partner[c], x1 = x[c];
-                x[c] = x0 * sine + x1 * cosine;
-            }
-            theta *= a.theta_scale;
-        }
-    }
+    q38_norm_rope4(x, q38_ld4(w + 4 * lane), lane, position, a.theta_scale);
     q38_st4(dst + 4 * lane, x);
 }

@@ -42,13 +42,19 @@ typedef struct {
     float *kpool;              /* this layer's K pages: [max_pages][4][16][256] */
     float *vpool;              /* this layer's V pages */
     const int32_t *page_table; /* [max_seqs][pt_stride] physical page ids */
-    const float *q;            /* [n_seq][24][256], post-norm, post-RoPE */
-    const float *k_new;        /* [n_seq][1024] appended at pos[b] first, or NULL */
+    const float *q;            /* [n_seq][24][256], post-norm, post-RoPE (fused pre step:
+                                  raw [n_seq][24][512] q|gate rows) */
+    const float *k_new;        /* [n_seq][1024] appended at pos[b] first, or NULL (fused pre
+                                  step: the raw key, normed and rotated before the append) */
     const float *v_new;        /* [n_seq][1024] or NULL */
     const float *gate;         /* [n_seq][24][256] output gate logits, or NULL */
     float *out;                /* [n_seq][24][256] */
     float *part_o;             /* [total_splits][24][256] unnormalised partial outputs */
     float *part_ml;            /* [total_splits][24][2]  (running max in log2 units, sum) */
+    const float *q_norm;       /* fused pre step: [256] q RMSNorm weight, else unused */
+    const float *k_norm;       /* fused pre step: [256] k RMSNorm weight */
+    float theta_scale;         /* fused pre step: RoPE 1e7^(-2/64) in f32 */
+    int32_t gate_head_stride;  /* floats between heads' gates: 256, or 512 in q|gate rows */
     int32_t pt_stride;
     int32_t n_seq;
     int32_t split_tokens; /* multiple of 64 */
@@ -84,11 +90,10 @@ typedef struct {
     float *q_out;            /* [n][24][256] */
     float *gate_out;         /* [n][24][256] */
     float *k_out;            /* [n][4][256] */
-    int32_t pos0;
+    int32_t pos0;      /* token t is at position pos0 + t */
     int32_t n_tokens;
     float theta_scale; /* 1e7^(-2/64) in f32 */
-    int32_t per_token_positions; /* 1: token t's position is positions[t] (t < 64) */
-    int32_t positions[Q38_MAX_BATCH]; /* else position = pos0 + token */
+    int32_t pad_;
 } q38_attn_pre_args;
 
 /* Gated-DeltaNet recurrence over n_tokens consecutive tokens of each of
@@ -207,7 +212,7 @@ typedef struct {
     const float *gate;
     float *out;
     int32_t n_seq;
-    int32_t pad_;
+    int32_t gate_head_stride; /* floats between heads' gates: 256, or 512 in q|gate rows */
     int32_t split_base[Q38_MAX_BATCH + 1];
 } q38_merge_args;
 
