@@ -243,7 +243,9 @@ def batched_decode(pkg, ctx, steps: int, warmup: int):
     ctx.record(e1)
     ms = ctx.elapsed_ms(e0, e1) / steps
     ctx.sync()
-    ctx.kernel_timer_start("q38_attn_decode_split", steps)
+    # more than 256 splits in the launch: the form that reads every page id
+    # from the page table
+    ctx.kernel_timer_start("q38_attn_decode_split_many", steps)
     for _ in range(steps):
         step()
     k_ms, k_n = ctx.kernel_timer_stop()

@@ -86,7 +86,9 @@ struct q38_ctx {
     hipFunction_t f_chunk_scan = nullptr;
     hipFunction_t f_gdn_post = nullptr;
     hipFunction_t f_decode_split = nullptr;
+    hipFunction_t f_decode_split_many = nullptr; /* any number of splits */
     hipFunction_t f_decode_split_pre = nullptr; /* the same with full_core's pre step fused */
+    hipFunction_t f_decode_split_pre_many = nullptr;
     hipFunction_t f_decode_merge = nullptr;
     hipFunction_t f_kv_copy = nullptr;
     hipFunction_t f_attn_pre = nullptr;
@@ -266,7 +268,10 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_prefill, ctx->mod_prefill, "q38_attn_prefill_mfma"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_split, ctx->mod_prefill, "q38_kv_split_mfma"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split, ctx->mod_decode, "q38_attn_decode_split"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_many, ctx->mod_decode, "q38_attn_decode_split_many"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_pre, ctx->mod_decode, "q38_attn_decode_split_pre"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_pre_many, ctx->mod_decode,
+                                 "q38_attn_decode_split_pre_many"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "q38_attn_decode_merge"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_copy, ctx->mod_decode, "q38_kv_copy"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_attn_pre, ctx->mod_decode, "q38_attn_pre"));
@@ -420,7 +425,9 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     hipFunction_t f = nullptr;
     const std::string name(kernel_name);
     if (name == "q38_attn_decode_split") f = ctx->f_decode_split;
+    else if (name == "q38_attn_decode_split_many") f = ctx->f_decode_split_many;
     else if (name == "q38_attn_decode_split_pre") f = ctx->f_decode_split_pre;
+    else if (name == "q38_attn_decode_split_pre_many") f = ctx->f_decode_split_pre_many;
     else if (name == "q38_attn_decode_merge") f = ctx->f_decode_merge;
     else if (name == "q38_kv_copy") f = ctx->f_kv_copy;
     else if (name == "q38_attn_pre") f = ctx->f_attn_pre;
@@ -718,6 +725,22 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
     }
     a.split_base[n_seq] = total;
     a.total_splits = total;
+    /* up to 256 splits, each split's first two page ids ride in the launch
+     * arguments (from the host mirror of the page table), so the kernel's
+     * first row loads wait on no page-table load */
+    const bool arg_pages = total <= Q38_HEAD_PAGE_SPLITS;
+    if (arg_pages) {
+        for (int b = 0; b < n_seq; ++b) {
+            const int32_t *row = &kv->page_table[(size_t)seq_ids[b] * kv->pt_stride];
+            const int held = kv->seq_pages[seq_ids[b]];
+            for (int g = a.split_base[b]; g < a.split_base[b + 1]; ++g) {
+                const int lp = (int)(((long)(g - a.split_base[b]) * split_tokens) / Q38_PAGE_TOKENS);
+                if (lp >= held) return fail("sequence %d: split page %d is not reserved", seq_ids[b], lp);
+                a.head_pages[g][0] = row[lp];
+                a.head_pages[g][1] = row[lp + 1 < held ? lp + 1 : lp];
+            }
+        }
+    }
 
     const size_t part_o_floats = (size_t)total * Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
     const size_t part_ml_floats = (size_t)total * Q38_ATTN_HEADS * 2;
@@ -726,9 +749,9 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
         a.part_o = static_cast<float *>(ctx->work);
         a.part_ml = a.part_o + part_o_floats;
     }
-    if (ctx->launch(pre != nullptr ? ctx->f_decode_split_pre : ctx->f_decode_split, total, Q38_ATTN_KV_HEADS, 1,
-                    ctx->decode_block, &a))
-        return -1;
+    hipFunction_t f = pre != nullptr ? (arg_pages ? ctx->f_decode_split_pre : ctx->f_decode_split_pre_many)
+                                     : (arg_pages ? ctx->f_decode_split : ctx->f_decode_split_many);
+    if (ctx->launch(f, total, Q38_ATTN_KV_HEADS, 1, ctx->decode_block, &a)) return -1;
     if (any_multi) {
         q38_merge_args m;
         memset(&m, 0, sizeof(m));

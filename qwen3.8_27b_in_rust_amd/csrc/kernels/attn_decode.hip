@@ -212,7 +212,7 @@ Q38_DEV void q38_norm_rope4_cs(f32x4 &x, f32x4 w, int lane, const float (*cs)[2]
 #define Q38_DECODE_MIN_WGS 1 /* workgroups per CU the register budget is sized for */
 #endif
 
-template <bool kPre>
+template <bool kPre, bool kArgPages>
 Q38_DEV void decode_split(const q38_decode_args &a) {
     constexpr int NW = Q38_DECODE_WAVES;
     __shared__ float red_o[NW][Q38_ATTN_GROUP][Q38_ATTN_HEAD_DIM];
@@ -239,11 +239,53 @@ Q38_DEV void decode_split(const q38_decode_args &a) {
     const int d0 = 4 * li;
     const int d1 = 128 + 4 * li;
 
+    const int n_tok = t_end - t_begin;
+    const int n_hp = (n_tok + 7) / 8;
+    /* every half-page is full except, in the split that holds `pos` (always
+     * the sequence's last position), the last one: that one is handled after
+     * the loop with per-row redirection */
+    const bool has_tail = t_end == pos + 1;
+    const int n_regular = has_tail ? n_hp - 1 : n_hp;
+    const int lane_off = grp * Q38_ATTN_HEAD_DIM + d0;
+
     /* the split's page ids, loaded once: the streaming loop below then has
      * no global load whose address depends on another global load */
     const int32_t *pt = a.page_table + (size_t)seq * a.pt_stride;
     const int n_split_pages = (t_end - t_begin + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS;
-    if (tid < n_split_pages) pages[tid] = pt[(t_begin >> 4) + tid];
+    Rows K, V;
+    f32x4 q0[Q38_ATTN_GROUP], q1[Q38_ATTN_GROUP];
+    /* the group's 6 query rows; with the pre step fused, raw q|gate rows
+     * (each head's q followed by its gate) */
+    const int q_stride = kPre ? 2 * Q38_ATTN_HEAD_DIM : Q38_ATTN_HEAD_DIM;
+    const float *qb = a.q + ((size_t)b * Q38_ATTN_HEADS + j * Q38_ATTN_GROUP) * q_stride;
+    if (kArgPages) {
+        /* software pipeline start: wave w's half-page w lies in the split's
+         * page 0 or 1, whose ids come with the launch, so these loads issue at
+         * once.  A wave with no regular half-page loads page 0's rows (in the
+         * pool, unused) so that no load sits under a branch.  The page-id load
+         * is issued first and every thread stores its result (slots past the
+         * split's pages are never read), so that store waits for it alone. */
+        const int32_t my_page = pt[(t_begin >> 4) + min(tid, n_split_pages - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        const int hp0 = wave < n_regular ? wave : 0;
+        const size_t base = ((size_t)a.head_pages[g][hp0 >> 1] * Q38_ATTN_KV_HEADS + j) * Q38_PAGE_TOKENS *
+                                Q38_ATTN_HEAD_DIM + (size_t)(hp0 & 1) * 8 * Q38_ATTN_HEAD_DIM;
+        load_rows(K, a.kpool, base, lane_off);
+        load_rows(V, a.vpool, base, lane_off);
+#pragma unroll
+        for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+            q0[hh] = q38_ld4(qb + hh * q_stride + d0);
+            q1[hh] = q38_ld4(qb + hh * q_stride + d1);
+        }
+        pages[tid] = my_page;
+    } else {
+#pragma unroll
+        for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
+            q0[hh] = q38_ld4(qb + hh * q_stride + d0);
+            q1[hh] = q38_ld4(qb + hh * q_stride + d1);
+        }
+        if (tid < n_split_pages) pages[tid] = pt[(t_begin >> 4) + tid];
+    }
     /* with the pre step fused, the split holding `pos` forms the new key row
      * (RMSNorm and RoPE of the raw key, ops.rs:844-856) in LDS; it is
      * appended below and scored from there */
@@ -275,37 +317,21 @@ Q38_DEV void decode_split(const q38_decode_args &a) {
         }
     }
 
-    const int n_tok = t_end - t_begin;
-    const int n_hp = (n_tok + 7) / 8;
-    /* every half-page is full except, in the split that holds `pos` (always
-     * the sequence's last position), the last one: that one is handled after
-     * the loop with per-row redirection */
-    const bool has_tail = t_end == pos + 1;
-    const int n_regular = has_tail ? n_hp - 1 : n_hp;
-    const int lane_off = grp * Q38_ATTN_HEAD_DIM + d0;
     const bool all_valid[4] = {true, true, true, true};
 
     /* software pipeline: the K rows of the next half-page are in flight
      * while the current one is scored, and its V rows while the current one
      * is accumulated */
-    Rows K, V;
-    if (wave < n_regular) {
+    if (!kArgPages && wave < n_regular) {
         const size_t base = half_page_base(pages, j, wave * 8);
         load_rows(K, a.kpool, base, lane_off);
         load_rows(V, a.vpool, base, lane_off);
     }
 
-    f32x4 q0[Q38_ATTN_GROUP], q1[Q38_ATTN_GROUP];
     if (kPre) {
-        /* the group's query heads from q|gate, RMSNormed and rotated here
-         * (ops.rs:832-856; the same arithmetic as q38_attn_pre), each half-wave
-         * holding a whole head */
-        const float *qb = a.q + ((size_t)b * Q38_ATTN_HEADS + j * Q38_ATTN_GROUP) * 2 * Q38_ATTN_HEAD_DIM;
-#pragma unroll
-        for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
-            q0[hh] = q38_ld4(qb + hh * 2 * Q38_ATTN_HEAD_DIM + d0);
-            q1[hh] = q38_ld4(qb + hh * 2 * Q38_ATTN_HEAD_DIM + d1);
-        }
+        /* the group's query heads RMSNormed and rotated here (ops.rs:832-856;
+         * the same arithmetic as q38_attn_pre), each half-wave holding a whole
+         * head */
         const f32x4 w0 = q38_ld4(a.q_norm + d0), w1 = q38_ld4(a.q_norm + d1);
 #pragma unroll
         for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
@@ -314,11 +340,10 @@ Q38_DEV void decode_split(const q38_decode_args &a) {
             q1[hh] *= Q38_SCORE_LOG2;
         }
     } else {
-        const float *qb = a.q + ((size_t)b * Q38_ATTN_HEADS + j * Q38_ATTN_GROUP) * Q38_ATTN_HEAD_DIM;
 #pragma unroll
         for (int hh = 0; hh < Q38_ATTN_GROUP; ++hh) {
-            q0[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d0) * Q38_SCORE_LOG2;
-            q1[hh] = q38_ld4(qb + hh * Q38_ATTN_HEAD_DIM + d1) * Q38_SCORE_LOG2;
+            q0[hh] *= Q38_SCORE_LOG2;
+            q1[hh] *= Q38_SCORE_LOG2;
         }
     }
 
@@ -434,17 +459,30 @@ Q38_DEV void decode_split(const q38_decode_args &a) {
     }
 }
 
+/* Launches of at most Q38_HEAD_PAGE_SPLITS splits: the first two page ids of
+ * every split come in a.head_pages. */
 extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split(
     q38_decode_args a) {
-    decode_split<false>(a);
+    decode_split<false, true>(a);
 }
 
-/* The same with the pre step of full_core fused: q from the raw q|gate rows
- * and the appended key from the raw key, both RMSNormed and rotated in the
- * kernel; the gate read from q|gate. */
+/* Any number of splits: every page id read from the page table. */
+extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_many(
+    q38_decode_args a) {
+    decode_split<false, false>(a);
+}
+
+/* The same two with the pre step of full_core fused: q from the raw q|gate
+ * rows and the appended key from the raw key, both RMSNormed and rotated in
+ * the kernel; the gate read from q|gate. */
 extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_pre(
     q38_decode_args a) {
-    decode_split<true>(a);
+    decode_split<true, true>(a);
+}
+
+extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_pre_many(
+    q38_decode_args a) {
+    decode_split<true, false>(a);
 }
 
 /* Combine the splits of each (sequence, head): rescale every partial to the

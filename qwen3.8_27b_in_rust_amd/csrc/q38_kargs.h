@@ -36,6 +36,7 @@
 #define Q38_MAX_SPLITS 4096 /* splits of one sequence in one decode launch */
 #define Q38_MAX_SPLIT_TOKENS 4096 /* context tokens one decode workgroup streams */
 #define Q38_DECODE_WAVES 4 /* waves of a decode workgroup */
+#define Q38_HEAD_PAGE_SPLITS 256 /* splits whose first page ids a decode launch can carry */
 
 /* Split-K paged decode: grid (total_splits, 4 kv heads). */
 typedef struct {
@@ -62,6 +63,9 @@ typedef struct {
     int32_t seq[Q38_MAX_BATCH];
     int32_t pos[Q38_MAX_BATCH]; /* attend over positions 0..pos inclusive */
     int32_t split_base[Q38_MAX_BATCH + 1];
+    int32_t head_pages[Q38_HEAD_PAGE_SPLITS][2]; /* physical ids of split g's first two pages (the
+                                                    second repeats the first where the split has
+                                                    one), when total_splits <= 256 */
 } q38_decode_args;
 
 /* Copy token rows between [n][1024] arrays and a sequence's pages.

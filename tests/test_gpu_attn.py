@@ -171,6 +171,57 @@ def test_decode_batched_paged_permuted(pkg, ctx, ref):
     assert worst <= TOL
 
 
+@pytest.mark.parametrize("split", [None, 128, 64])
+def test_decode_permuted_pages_both_launch_forms(pkg, ctx, ref, split):
+    """Five sequences (one page, two pages, and longer) on a permuted page
+    table.  Launches of at most 256 splits carry each split's first two page
+    ids in their arguments (default and 128-token splits: 135 splits at 128);
+    64-token splits make 267 splits, which read every page id from the table."""
+    from q38amd import synth
+    lens = [5, 17, 3001, 7777, 6100]
+    n = len(lens)
+    rng = np.random.default_rng(0x51333803 + (split or 0))
+    pages_needed = [(c + 15) // 16 for c in lens]
+    pool = sum(pages_needed) + 8
+    kv = pkg.KVCache(ctx, n_slots=1, max_pages=pool, max_seqs=n, max_tokens_per_seq=8192)
+    perm = rng.permutation(pool)
+    old = os.environ.get("Q38_SPLIT_TOKENS")
+    try:
+        seqs, off = [], 0
+        for i in range(n):
+            s = kv.seq_create()
+            kv.seq_set_pages(s, perm[off:off + pages_needed[i]].tolist())
+            off += pages_needed[i]
+            seqs.append(s)
+        Ks, Vs = [], []
+        for i, P in enumerate(lens):
+            K = synth.normal(0x7100 + 2 * i, P * 1024)
+            V = synth.normal(0x7101 + 2 * i, P * 1024)
+            d_k, d_v = ctx.array(K), ctx.array(V)
+            kv.write(3, seqs[i], 0, P, d_k, d_v)
+            d_k.free()
+            d_v.free()
+            Ks.append(K.reshape(P, 1024))
+            Vs.append(V.reshape(P, 1024))
+        Q = synth.normal(0x7200, n * 6144)
+        G = synth.normal(0x7201, n * 6144)
+        d_q, d_g, d_o = ctx.array(Q), ctx.array(G), ctx.empty((n, 24, 256))
+        if split is not None:
+            os.environ["Q38_SPLIT_TOKENS"] = str(split)
+        kv.attn_decode(3, seqs, [P - 1 for P in lens], d_q, d_o, gate=d_g)
+        got = d_o.download()
+    finally:
+        if old is None:
+            os.environ.pop("Q38_SPLIT_TOKENS", None)
+        else:
+            os.environ["Q38_SPLIT_TOKENS"] = old
+        kv.close()
+    for i in range(n):
+        want = ref.attn_heads(Q[i * 6144:(i + 1) * 6144], Ks[i], Vs[i], gate=G[i * 6144:(i + 1) * 6144])
+        err = float(np.max(np.abs(got[i] - want)))
+        assert err <= TOL, (i, lens[i], err)
+
+
 def test_full_core_matches_reference(pkg, ctx, ref):
     """full_core whole: q/gate split, q and k RMSNorm, RoPE, append, attention,
     gate, for consecutive tokens, including a position past 2^16 (RoPE angles
