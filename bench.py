@@ -411,8 +411,8 @@ def main():
                     "(default: next to the library), to compare builds")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards over kv heads or context with one merge step; see DESIGN.md)",
+        print(f"bench.py: one GPU only; --gpus {args.gpus} is not supported "
+              "(the path would shard over kv heads or context, with one split-K merge step)",
               file=sys.stderr)
         sys.exit(2)
 

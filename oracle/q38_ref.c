@@ -1,7 +1,7 @@
 /*
  * q38_ref.c -- CPU restatement of the reference engine's attention path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels and the CPU
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP kernels and the CPU
  * baseline timed beside them.  The product library never links or calls it.
  *
  * Each function cites the reference function it restates
@@ -14,7 +14,7 @@
 
 /* Q38R_MUTANT > 0 plants one known mistake (tests/test_oracle_mutants.py
  * builds each and checks that the fixtures and closed forms reject it).
- * The checker itself is built with Q38R_MUTANT 0. */
+ * The oracle itself is built with Q38R_MUTANT 0. */
 #ifndef Q38R_MUTANT
 #define Q38R_MUTANT 0
 #endif

@@ -1,7 +1,7 @@
 /*
  * q38_ref.h -- CPU restatement of the reference engine's attention path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the HIP
  * kernels are compared against, and the CPU baseline that bench.py times
  * beside them.  Nothing in the product library links, loads or calls it.
  *

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU restatement (oracle/_build/libq38ref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as
-the checker, and by bench.py's cpu_baseline leg.  The product never imports it.
+the oracle its GPU run is compared against, and by bench.py's cpu_baseline leg.  The product never imports it.
 """
 from __future__ import annotations
 

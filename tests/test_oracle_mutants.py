@@ -1,6 +1,6 @@
 """Each planted mistake in the restatement (q38_ref.c built with
 -DQ38R_MUTANT=k) must be rejected by at least one check, so a plausible slip
-in the checker cannot pass unnoticed (CPU only)."""
+in the oracle cannot pass unnoticed (CPU only)."""
 import os
 import subprocess
 
