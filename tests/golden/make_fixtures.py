@@ -113,7 +113,7 @@ def main():
     out["gen_words"] = synth.splitmix64(0x51333800, 0, 8)
     out["gen_normals"] = synth.normal(0x51333800, 8).astype(F64)
 
-    # ---- attention, 256 positions (config shape), with and without gate
+    # ---- attention, 256 positions (24 q / 4 kv heads, head_dim 256), with and without gate
     P = 256
     q = synth.normal(0x51333801, 6144)
     K = synth.normal(0x51333802, P * 1024)
