@@ -222,6 +222,48 @@ def test_decode_permuted_pages_both_launch_forms(pkg, ctx, ref, split):
         assert err <= TOL, (i, lens[i], err)
 
 
+def test_decode_after_rollback_new_pages(pkg, ctx, ref):
+    """A rollback returns pages to the free stack, a second sequence takes some
+    of them, and the first grows again into other physical pages, one row per
+    decode call (64-token splits, so every split's first page ids come from
+    the host copy of the page table, which must follow each change)."""
+    from q38amd import synth
+    P, keep, n_new = 900, 300, 40
+    kv = pkg.KVCache(ctx, n_slots=1, max_pages=80, max_seqs=2, max_tokens_per_seq=1024)
+    old = os.environ.get("Q38_SPLIT_TOKENS")
+    try:
+        a = kv.seq_create()
+        K = synth.normal(0x7300, P * 1024).reshape(P, 1024)
+        V = synth.normal(0x7301, P * 1024).reshape(P, 1024)
+        d_k, d_v = ctx.array(K), ctx.array(V)
+        kv.write(3, a, 0, P, d_k, d_v)
+        kv.seq_truncate(a, keep)
+        b = kv.seq_create()
+        kv.write(3, b, 0, 200, d_k, d_v)  # takes pages that a released
+        os.environ["Q38_SPLIT_TOKENS"] = "64"
+        Kn = synth.normal(0x7304, n_new * 1024).reshape(n_new, 1024)
+        Vn = synth.normal(0x7305, n_new * 1024).reshape(n_new, 1024)
+        Q = synth.normal(0x7306, 6144)
+        G = synth.normal(0x7307, 6144)
+        d_q, d_g, d_o = ctx.array(Q), ctx.array(G), ctx.empty((24, 256))
+        for i in range(n_new):
+            d_kn, d_vn = ctx.array(Kn[i]), ctx.array(Vn[i])
+            kv.attn_decode(3, [a], [keep + i], d_q, d_o, k_new=d_kn, v_new=d_vn, gate=d_g)
+            if i % 13 == 0 or i == n_new - 1:
+                want = ref.attn_heads(Q, np.concatenate([K[:keep], Kn[:i + 1]]),
+                                      np.concatenate([V[:keep], Vn[:i + 1]]), gate=G)
+                err = float(np.max(np.abs(d_o.download() - want)))
+                assert err <= TOL, (i, err)
+            d_kn.free()
+            d_vn.free()
+    finally:
+        if old is None:
+            os.environ.pop("Q38_SPLIT_TOKENS", None)
+        else:
+            os.environ["Q38_SPLIT_TOKENS"] = old
+        kv.close()
+
+
 def test_full_core_matches_reference(pkg, ctx, ref):
     """full_core whole: q/gate split, q and k RMSNorm, RoPE, append, attention,
     gate, for consecutive tokens, including a position past 2^16 (RoPE angles
