@@ -13,7 +13,10 @@
  *
  * Conventions (mirroring the reference's Result<_, i32> with Err(-1)):
  *  - every function returns 0 on success and -1 on failure; q38_last_error()
- *    then gives the reason (thread-local, valid until the next failing call);
+ *    then gives the reason (thread-local, valid until the next failing call).
+ *    Arguments are checked on the host before anything is changed: a call
+ *    that fails its checks launches nothing and leaves the KV cache (pages,
+ *    page tables, sequences) as it was;
  *  - pointers named d_* are device pointers; all other pointers are host
  *    memory that is read during the call and never retained;
  *  - work is stream-ordered on the context's stream; results are visible to
@@ -68,28 +71,12 @@ int q38_upload(q38_ctx *ctx, void *d_dst, const void *src, size_t bytes);
 int q38_download(q38_ctx *ctx, void *dst, const void *d_src, size_t bytes);
 int q38_zero(q38_ctx *ctx, void *d_dst, size_t bytes);
 
-/* Events on the context's stream, for timing. */
-int q38_event_create(q38_ctx *ctx, void **event);
-int q38_event_record(q38_ctx *ctx, void *event);
-int q38_event_elapsed_ms(void *start, void *stop, float *ms);
-int q38_event_destroy(void *event);
-
-/* Time every launch of one kernel of this library (by its symbol name, e.g.
- * "q38_attn_decode_split") with a pair of events on the context's stream,
- * for up to max_launches launches; stop returns the summed kernel time. */
-int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launches);
-int q38_kernel_timer_stop(q38_ctx *ctx, float *total_ms, int *launches);
-
-/* Seeded N(mean, sigma^2) f32 fill on the device: element i equals what the
- * host generator (SplitMix64 + Box-Muller, qwen3.8_27b_in_rust_amd/synth.py)
- * gives for the same seed.  For benchmark inputs of many gigabytes. */
-int q38_fill_normal(q38_ctx *ctx, float *d_out, size_t n, uint64_t seed, float sigma, float mean);
-
-/* Plain device-to-device copy by a kernel of this library (bytes a multiple
- * of 16, pointers 16-byte aligned): reads and writes exactly `bytes` each,
- * the calibration figure for hardware memory counters.  No counterpart in
- * the reference (which has no device). */
-int q38_device_copy(q38_ctx *ctx, void *d_dst, const void *d_src, size_t bytes);
+/* Context tokens one decode workgroup streams (a multiple of 64 in
+ * 64..4096), or 0 (the default) to choose per launch: one workgroup per CU
+ * for one sequence, at most 1024 tokens for batches.  A tuning setting with
+ * no counterpart in the reference (whose rayon split is per head, ops.rs:919-938);
+ * results do not depend on it beyond f32 rounding. */
+int q38_set_decode_split(q38_ctx *ctx, int tokens);
 
 /* ------------------------------------------------------------- paged KV cache */
 

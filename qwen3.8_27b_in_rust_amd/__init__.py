@@ -20,7 +20,8 @@ import numpy as np
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libq38attn.so")
-HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "q38_attn.h")
+INCLUDE_DIR = os.path.join(os.path.dirname(PKG_DIR), "include")
+HEADER_PATH = os.path.join(INCLUDE_DIR, "q38_attn.h")
 
 # shapes: reference src/model/mod.rs:13-24
 ATTN_HEADS, ATTN_KV_HEADS, ATTN_HEAD_DIM = 24, 4, 256
@@ -49,6 +50,7 @@ _SIGNATURES = {
     "q38_ctx_stream": (c_void_p, [_P]),
     "q38_sync": (c_int, [_P]),
     "q38_device_info": (c_int, [_P, POINTER(c_int), POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]),
+    "q38_set_decode_split": (c_int, [_P, c_int]),
     "q38_alloc": (c_int, [_P, c_size_t, POINTER(c_void_p)]),
     "q38_free": (c_int, [_P, _P]),
     "q38_upload": (c_int, [_P, _P, _P, c_size_t]),
@@ -195,6 +197,10 @@ class Context:
                                      ctypes.byref(lds), name, 256), "q38_device_info")
         return {"cu_count": cu.value, "clock_khz": clk.value, "lds_bytes": lds.value,
                 "name": name.value.decode()}
+
+    def set_decode_split(self, tokens: int) -> None:
+        """Context tokens per decode workgroup (multiple of 64), 0 = automatic."""
+        _check(lib().q38_set_decode_split(self.handle, int(tokens)), "q38_set_decode_split")
 
     def stream(self) -> int:
         return lib().q38_ctx_stream(self.handle)
@@ -346,9 +352,13 @@ class KVCache:
                                       _ptr(gate), _ptr(out)), "q38_attn_prefill")
 
 
-def header_functions(path: str = HEADER_PATH) -> list[str]:
-    """Names of the functions include/q38_attn.h declares."""
+def header_functions(paths=None) -> list[str]:
+    """Names of the functions the headers under include/ declare."""
+    import glob
     import re
-    text = open(path).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(q38_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for path in paths or sorted(glob.glob(os.path.join(INCLUDE_DIR, "*.h"))):
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(q38_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)

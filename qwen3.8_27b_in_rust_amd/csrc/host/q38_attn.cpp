@@ -35,6 +35,7 @@ extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalW
 #include <vector>
 
 #include "../../../include/q38_attn.h"
+#include "../../../include/q38_bench.h"
 #include "../q38_kargs.h"
 
 namespace {
@@ -103,7 +104,8 @@ struct q38_ctx {
     std::vector<hipEvent_t> timer_events;
     int timer_used = 0;
     int cu_count = 0;
-    int decode_block = 256; /* threads of a decode workgroup (the kernel's launch bound) */
+    int decode_block = 64 * Q38_DECODE_WAVES; /* threads of a decode workgroup (the kernel's launch bound) */
+    int split_tokens = 0; /* context tokens per decode workgroup; 0: chosen per launch */
     int clock_khz = 0;
     int lds_bytes = 0;
     char name[256] = {0};
@@ -240,7 +242,8 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail("no HIP device available");
     if (device < 0 || device >= n) return fail("device %d out of range (%d devices)", device, n);
-    std::unique_ptr<q38_ctx> ctx(new q38_ctx);
+    /* a failure part-way through set-up releases what was created so far */
+    std::unique_ptr<q38_ctx, int (*)(q38_ctx *)> ctx(new q38_ctx, q38_ctx_destroy);
     ctx->device = device;
     Q38_HIP(hipSetDevice(device));
     hipDeviceProp_t prop;
@@ -280,8 +283,10 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_step_rows, ctx->mod_gdn, "q38_gdn_step_rows"));
     Q38_HIP(hipFuncGetAttribute(&ctx->decode_block, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
                                 ctx->f_decode_split));
-    if (ctx->decode_block < 256 || ctx->decode_block > 1024 || ctx->decode_block % 64 != 0)
-        return fail("decode kernel has an unexpected block size %d", ctx->decode_block);
+    /* the decode kernel's reductions and its page-id array are sized for
+     * exactly Q38_DECODE_WAVES waves */
+    if (ctx->decode_block != 64 * Q38_DECODE_WAVES)
+        return fail("decode kernel has block size %d, expected %d", ctx->decode_block, 64 * Q38_DECODE_WAVES);
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
@@ -313,6 +318,14 @@ void *q38_ctx_stream(q38_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr;
 int q38_sync(q38_ctx *ctx) {
     if (ctx == nullptr) return fail("ctx is NULL");
     Q38_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+int q38_set_decode_split(q38_ctx *ctx, int tokens) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    if (tokens != 0 && (tokens < 64 || tokens > Q38_MAX_SPLIT_TOKENS || tokens % 64 != 0))
+        return fail("split of %d tokens: 0, or a multiple of 64 in 64..%d", tokens, Q38_MAX_SPLIT_TOKENS);
+    ctx->split_tokens = tokens;
     return 0;
 }
 
@@ -476,6 +489,9 @@ int q38_kv_create(q38_ctx *ctx, int n_slots, int max_pages, int max_seqs, int ma
     if (n_slots < 1 || n_slots > 17) return fail("n_slots %d outside 1..17", n_slots);
     if (max_pages < 1 || max_seqs < 1 || max_tokens_per_seq < 1)
         return fail("max_pages, max_seqs and max_tokens_per_seq must be positive");
+    if ((long)max_tokens_per_seq > (long)Q38_MAX_SPLITS * Q38_MAX_SPLIT_TOKENS)
+        return fail("max_tokens_per_seq %d above the decode limit of %ld", max_tokens_per_seq,
+                    (long)Q38_MAX_SPLITS * Q38_MAX_SPLIT_TOKENS);
     std::unique_ptr<q38_kv> kv(new q38_kv);
     kv->ctx = ctx;
     kv->n_slots = n_slots;
@@ -571,19 +587,22 @@ int q38_seq_set_pages(q38_kv *kv, int seq, int n_pages, const int32_t *page_ids)
     if (kv->check_seq(seq)) return -1;
     if (n_pages < 0 || n_pages > kv->pt_stride)
         return fail("n_pages %d outside 0..%d", n_pages, kv->pt_stride);
-    kv->release_from(seq, 0);
-    std::vector<char> is_free(kv->max_pages, 0);
-    for (int32_t p : kv->free_pages) is_free[p] = 1;
+    /* validate first (the sequence's own pages count as available), so a
+     * rejected call keeps the sequence's mapping and the pool unchanged */
+    std::vector<char> avail(kv->max_pages, 0);
+    for (int32_t p : kv->free_pages) avail[p] = 1;
+    for (int i = 0; i < kv->seq_pages[seq]; ++i) avail[kv->page_table[(size_t)seq * kv->pt_stride + i]] = 1;
     for (int i = 0; i < n_pages; ++i) {
         const int32_t p = page_ids[i];
         if (p < 0 || p >= kv->max_pages) return fail("page id %d outside the pool of %d", p, kv->max_pages);
-        if (!is_free[p]) return fail("page %d is not free (held, or listed twice)", p);
-        is_free[p] = 0;
+        if (!avail[p]) return fail("page %d is not free (held, or listed twice)", p);
+        avail[p] = 0;
     }
+    kv->release_from(seq, 0);
     std::vector<int32_t> rest;
     rest.reserve(kv->free_pages.size());
     for (int32_t p : kv->free_pages)
-        if (is_free[p]) rest.push_back(p);
+        if (avail[p]) rest.push_back(p);
     kv->free_pages.swap(rest);
     for (int i = 0; i < n_pages; ++i) kv->page_table[(size_t)seq * kv->pt_stride + i] = page_ids[i];
     kv->seq_pages[seq] = n_pages;
@@ -642,15 +661,13 @@ namespace {
 /* Context tokens per decode workgroup: a multiple of 64, at least 64 and at
  * most Q38_MAX_SPLIT_TOKENS, chosen to give one workgroup per CU for one
  * sequence (the split kernel streams fastest so: 46 us at 32768 tokens
- * against 50 us with two per CU); Q38_SPLIT_TOKENS overrides (rounded up to
- * a multiple of 64). */
+ * against 50 us with two per CU), unless q38_set_decode_split fixed it. */
 constexpr int kMaxSplitsPerSeq = Q38_MAX_SPLITS; /* LDS weights of the merge kernel */
 
 int choose_split_tokens(const q38_ctx *ctx, int n_seq, long total_tokens, long max_tokens, int *split_out) {
     long split = 64;
-    const char *env = getenv("Q38_SPLIT_TOKENS");
-    if (env != nullptr && atoi(env) >= 64) {
-        split = std::min<long>((atoi(env) + 63) / 64 * 64, Q38_MAX_SPLIT_TOKENS);
+    if (ctx->split_tokens > 0) {
+        split = ctx->split_tokens;
     } else {
         const long slots = std::max(ctx->cu_count, 1);
         const long per = (total_tokens * Q38_ATTN_KV_HEADS + slots - 1) / slots;
@@ -672,6 +689,34 @@ int choose_split_tokens(const q38_ctx *ctx, int n_seq, long total_tokens, long m
     return 0;
 }
 
+/* How one decode launch of n_seq sequences is split: tokens per split, the
+ * total number of splits, and the workspace the split-K partials need (0
+ * when every sequence fits one split). */
+struct decode_plan {
+    int split_tokens = 0;
+    int total_splits = 0;
+    size_t work_bytes = 0;
+};
+
+int plan_decode(const q38_ctx *ctx, int n_seq, const int32_t *positions, decode_plan *plan) {
+    long total_tokens = 0, max_tokens = 0;
+    for (int b = 0; b < n_seq; ++b) {
+        total_tokens += positions[b] + 1;
+        max_tokens = std::max<long>(max_tokens, positions[b] + 1);
+    }
+    if (choose_split_tokens(ctx, n_seq, total_tokens, max_tokens, &plan->split_tokens)) return -1;
+    int total = 0;
+    bool any_multi = false;
+    for (int b = 0; b < n_seq; ++b) {
+        const int ns = (positions[b] + plan->split_tokens) / plan->split_tokens; /* ceil((pos+1)/split) */
+        any_multi |= ns > 1;
+        total += ns;
+    }
+    plan->total_splits = total;
+    plan->work_bytes = any_multi ? (size_t)total * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2) * sizeof(float) : 0;
+    return 0;
+}
+
 /* full_core's pre step fused into the decode kernel: d_q holds raw q|gate
  * rows, d_k_new raw keys; norm weights for both */
 struct decode_pre {
@@ -679,18 +724,13 @@ struct decode_pre {
     const float *k_norm;
 };
 
+/* One decode launch (plus the merge) for n_seq <= Q38_MAX_BATCH sequences
+ * whose pages are reserved; `work` holds plan.work_bytes. */
 int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const int32_t *positions,
                  const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate,
-                 float *d_out, const decode_pre *pre = nullptr) {
+                 float *d_out, const decode_plan &plan, void *work, const decode_pre *pre = nullptr) {
     q38_ctx *ctx = kv->ctx;
-    long total_tokens = 0, max_tokens = 0;
-    for (int b = 0; b < n_seq; ++b) {
-        total_tokens += positions[b] + 1;
-        max_tokens = std::max<long>(max_tokens, positions[b] + 1);
-    }
-    int split_tokens = 0;
-    if (choose_split_tokens(ctx, n_seq, total_tokens, max_tokens, &split_tokens)) return -1;
-
+    const int split_tokens = plan.split_tokens;
     q38_decode_args a;
     memset(&a, 0, sizeof(a));
     a.kpool = kv->kslot(slot);
@@ -714,14 +754,11 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
     a.n_seq = n_seq;
     a.split_tokens = split_tokens;
     int total = 0;
-    bool any_multi = false;
     for (int b = 0; b < n_seq; ++b) {
         a.seq[b] = seq_ids[b];
         a.pos[b] = positions[b];
         a.split_base[b] = total;
-        const int ns = (positions[b] + split_tokens) / split_tokens; /* ceil((pos+1)/split) */
-        any_multi |= ns > 1;
-        total += ns;
+        total += (positions[b] + split_tokens) / split_tokens; /* ceil((pos+1)/split) */
     }
     a.split_base[n_seq] = total;
     a.total_splits = total;
@@ -742,12 +779,11 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
         }
     }
 
-    const size_t part_o_floats = (size_t)total * Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
-    const size_t part_ml_floats = (size_t)total * Q38_ATTN_HEADS * 2;
+    const bool any_multi = plan.work_bytes > 0;
     if (any_multi) {
-        if (ctx->ensure_work((part_o_floats + part_ml_floats) * sizeof(float))) return -1;
-        a.part_o = static_cast<float *>(ctx->work);
-        a.part_ml = a.part_o + part_o_floats;
+        if (work == nullptr) return fail("decode workspace missing");
+        a.part_o = static_cast<float *>(work);
+        a.part_ml = a.part_o + (size_t)total * Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
     }
     hipFunction_t f = pre != nullptr ? (arg_pages ? ctx->f_decode_split_pre : ctx->f_decode_split_pre_many)
                                      : (arg_pages ? ctx->f_decode_split : ctx->f_decode_split_many);
@@ -767,28 +803,74 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
     return 0;
 }
 
+/* Every check of a decode call, with nothing changed: the layer is a
+ * full-attention layer with a slot, sequences exist (and are distinct when
+ * the call appends), positions are inside the context limit (the reference's
+ * KV bounds check, ops.rs:860-864, and its context-full check, :1702), and
+ * the pool holds the pages the whole batch must take for its appends; a
+ * call that does not append must find its positions reserved. */
 int validate_decode(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, const int32_t *positions,
                     bool appends, int *slot) {
     if (kv == nullptr) return fail("kv is NULL");
     if (kv->slot_of(layer, slot)) return -1;
     if (n_seq < 0) return fail("negative n_seq");
     if (n_seq > 0 && (seq_ids == nullptr || positions == nullptr)) return fail("NULL seq_ids/positions");
+    long pages_needed = 0;
     for (int b = 0; b < n_seq; ++b) {
-        if (kv->check_seq(seq_ids[b])) return -1;
+        const int s = seq_ids[b];
+        if (kv->check_seq(s)) return -1;
         if (positions[b] < 0) return fail("negative position %d", positions[b]);
-        if (positions[b] + 1 > kv->pt_stride * Q38_PAGE_TOKENS)
+        if ((long)positions[b] + 1 > (long)kv->pt_stride * Q38_PAGE_TOKENS)
             return fail("position %d is past the context limit %d", positions[b],
                         kv->pt_stride * Q38_PAGE_TOKENS);
         for (int c = 0; c < b; ++c)
-            if (seq_ids[c] == seq_ids[b] && appends) return fail("sequence %d appears twice", seq_ids[b]);
-    }
-    for (int b = 0; b < n_seq; ++b) {
-        const int s = seq_ids[b];
+            if (seq_ids[c] == s && appends) return fail("sequence %d appears twice", s);
+        const int need = positions[b] / Q38_PAGE_TOKENS + 1;
         if (appends) {
-            if (kv->reserve(s, positions[b] + 1)) return -1;
-        } else if (positions[b] + 1 > kv->seq_pages[s] * Q38_PAGE_TOKENS) {
+            pages_needed += std::max(0, need - kv->seq_pages[s]);
+        } else if (need > kv->seq_pages[s]) {
             return fail("sequence %d: position %d is not reserved", s, positions[b]);
         }
+    }
+    if (pages_needed > (long)kv->free_pages.size())
+        return fail("KV pool exhausted: the batch needs %ld more pages, %zu free", pages_needed,
+                    kv->free_pages.size());
+    return 0;
+}
+
+/* The decode of n_seq sequences in launches of up to Q38_MAX_BATCH: every
+ * check first, then the workspace, then the page reservations, so that a
+ * call that fails leaves the cache as it was.  `pre` set: full_core's
+ * norm + RoPE fused (d_q holds q|gate rows, d_k_new raw keys). */
+int decode_all(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+               const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate, float *d_out,
+               const decode_pre *pre) {
+    int slot = 0;
+    const bool appends = d_k_new != nullptr;
+    if (validate_decode(kv, layer, n_seq, seq_ids, positions, appends, &slot)) return -1;
+    if (n_seq == 0) return 0;
+    q38_ctx *ctx = kv->ctx;
+    size_t work_bytes = 0;
+    for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
+        decode_plan plan;
+        if (plan_decode(ctx, std::min(Q38_MAX_BATCH, n_seq - b0), positions + b0, &plan)) return -1;
+        work_bytes = std::max(work_bytes, plan.work_bytes);
+    }
+    if (work_bytes > 0 && ctx->ensure_work(work_bytes)) return -1;
+    if (appends)
+        for (int b = 0; b < n_seq; ++b)
+            if (kv->reserve(seq_ids[b], positions[b] + 1)) return -1;
+    const size_t q_rows = pre != nullptr ? Q38_ATTN_QG_DIM : Q38_ATTN_Q_DIM;
+    for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
+        const int n = std::min(Q38_MAX_BATCH, n_seq - b0);
+        decode_plan plan;
+        if (plan_decode(ctx, n, positions + b0, &plan)) return -1;
+        const size_t kvoff = (size_t)b0 * Q38_ATTN_KV_DIM;
+        const size_t qoff = (size_t)b0 * Q38_ATTN_Q_DIM;
+        if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, d_q + (size_t)b0 * q_rows,
+                         d_k_new ? d_k_new + kvoff : nullptr, d_v_new ? d_v_new + kvoff : nullptr,
+                         d_gate ? d_gate + qoff : nullptr, d_out + qoff, plan, ctx->work, pre))
+            return -1;
     }
     return 0;
 }
@@ -798,21 +880,9 @@ int validate_decode(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, co
 int q38_attn_decode(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
                     const int32_t *positions, const float *d_q, const float *d_k_new,
                     const float *d_v_new, const float *d_gate, float *d_out) {
-    int slot = 0;
     if ((d_k_new == nullptr) != (d_v_new == nullptr)) return fail("d_k_new and d_v_new go together");
-    if (validate_decode(kv, layer, n_seq, seq_ids, positions, d_k_new != nullptr, &slot)) return -1;
-    if (n_seq == 0) return 0;
-    if (d_q == nullptr || d_out == nullptr) return fail("NULL q/out");
-    for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
-        const int n = std::min(Q38_MAX_BATCH, n_seq - b0);
-        const size_t qoff = (size_t)b0 * Q38_ATTN_Q_DIM;
-        const size_t kvoff = (size_t)b0 * Q38_ATTN_KV_DIM;
-        if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, d_q + qoff,
-                         d_k_new ? d_k_new + kvoff : nullptr, d_v_new ? d_v_new + kvoff : nullptr,
-                         d_gate ? d_gate + qoff : nullptr, d_out + qoff))
-            return -1;
-    }
-    return 0;
+    if (n_seq > 0 && (d_q == nullptr || d_out == nullptr)) return fail("NULL q/out");
+    return decode_all(kv, layer, n_seq, seq_ids, positions, d_q, d_k_new, d_v_new, d_gate, d_out, nullptr);
 }
 
 int q38_attn_pre(q38_ctx *ctx, int n_tokens, int pos0, const float *d_q_norm, const float *d_k_norm,
@@ -842,21 +912,12 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
                   const int32_t *positions, const float *d_q_norm, const float *d_k_norm,
                   const float *d_q_and_gate, const float *d_key, const float *d_value,
                   float *d_out) {
-    int slot = 0;
-    if (validate_decode(kv, layer, n_seq, seq_ids, positions, true, &slot)) return -1;
-    if (n_seq == 0) return 0;
-    if (!d_q_norm || !d_k_norm || !d_q_and_gate || !d_key || !d_value || !d_out) return fail("NULL argument");
+    if (n_seq > 0 && (!d_q_norm || !d_k_norm || !d_q_and_gate || !d_key || !d_value || !d_out))
+        return fail("NULL argument");
     /* the pre step (q/gate split, q and k RMSNorm, RoPE) runs inside the
      * decode kernel: no separate launch and no intermediate rows */
     const decode_pre pre{d_q_norm, d_k_norm};
-    for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
-        const int n = std::min(Q38_MAX_BATCH, n_seq - b0);
-        if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, d_q_and_gate + (size_t)b0 * Q38_ATTN_QG_DIM,
-                         d_key + (size_t)b0 * Q38_ATTN_KV_DIM, d_value + (size_t)b0 * Q38_ATTN_KV_DIM, nullptr,
-                         d_out + (size_t)b0 * Q38_ATTN_Q_DIM, &pre))
-            return -1;
-    }
-    return 0;
+    return decode_all(kv, layer, n_seq, seq_ids, positions, d_q_and_gate, d_key, d_value, nullptr, d_out, &pre);
 }
 
 int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens, const float *d_q,
@@ -865,10 +926,16 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     if (n_tokens < 0 || base_pos < 0) return fail("negative count or position");
     if (n_tokens == 0) return 0;
     if (!d_q || !d_k || !d_v || !d_out) return fail("NULL argument");
-    /* append the prompt's rows (reserves pages; fails past the context limit) */
-    if (q38_kv_write(kv, layer, seq, base_pos, n_tokens, d_k, d_v)) return -1;
+    if (kv->check_seq(seq)) return -1;
     int slot = 0;
     if (kv->slot_of(layer, &slot)) return -1;
+    const long end = (long)base_pos + n_tokens;
+    if (end > (long)kv->pt_stride * Q38_PAGE_TOKENS)
+        return fail("positions %d..%ld are past the context limit %d", base_pos, end - 1,
+                    kv->pt_stride * Q38_PAGE_TOKENS);
+    const long need = (end + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS - kv->seq_pages[seq];
+    if (need > (long)kv->free_pages.size())
+        return fail("KV pool exhausted: need %ld pages, %zu free", need, kv->free_pages.size());
     q38_ctx *ctx = kv->ctx;
     constexpr int kQueryBlock = Q38_PREFILL_QUERIES; /* query tokens per workgroup of the kernel */
     q38_prefill_args a;
@@ -882,14 +949,17 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     a.base_pos = base_pos;
     a.n_tokens = n_tokens;
     a.n_qblocks = (n_tokens + kQueryBlock - 1) / kQueryBlock;
-    a.n_kblocks = (base_pos + n_tokens - 1) / Q38_PREFILL_KEYS + 1;
-    /* the K/V of positions 0 .. base_pos+n_tokens-1 split once into bf16
-     * hi/lo block images (workspace), then the attention kernel */
-    if (ctx->ensure_work((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES)) return -1;
-    a.images = ctx->work;
-    if (ctx->launch(ctx->f_kv_split, a.n_kblocks, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
+    a.n_kblocks = (int)((end - 1) / Q38_PREFILL_KEYS + 1);
     const size_t n_wg = (size_t)a.n_qblocks * Q38_ATTN_KV_HEADS * Q38_PREFILL_HEAD_PAIRS;
     if (n_wg > 0x7FFFFFFFull) return fail("prompt too long");
+    /* the workspace for the K/V block images before anything is changed */
+    if (ctx->ensure_work((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES)) return -1;
+    a.images = ctx->work;
+    /* append the prompt's rows (reserves pages) */
+    if (q38_kv_write(kv, layer, seq, base_pos, n_tokens, d_k, d_v)) return -1;
+    /* the K/V of positions 0 .. base_pos+n_tokens-1 split once into bf16
+     * hi/lo block images, then the attention kernel */
+    if (ctx->launch(ctx->f_kv_split, a.n_kblocks, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
     return ctx->launch(ctx->f_prefill, (unsigned)n_wg, 1, 1, 256, &a);
 }
 
