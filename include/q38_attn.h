@@ -156,6 +156,27 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
                   const float *d_q_and_gate, const float *d_key, const float *d_value,
                   float *d_out);
 
+/*
+ * q38_full_core with no device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Arguments,
+ * results and errors are those of q38_full_core; the split-K partials live
+ * in a fixed per-device scratch array of Q38_NOALLOC_SCRATCH_BYTES instead
+ * of the context's growable workspace, so a call whose partials need more
+ * (n_seq sequences of P_b cached tokens: sum over b of ceil((P_b+1)/split)
+ * splits x 24,768 bytes) fails with -1 before anything is changed.  The
+ * scratch needs no clearing (every split writes its partials before the
+ * merge reads them).  All calls on one GPU share that array: calls that
+ * overlap on one GPU (other streams or contexts) race on it.  Pages for the
+ * appended rows come from the pool as in q38_full_core, which allocates no
+ * device memory either.
+ */
+#define Q38_NOALLOC_SCRATCH_BYTES (16u << 20)
+int q38_full_core_noalloc(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
+                          const int32_t *positions, const float *d_q_norm, const float *d_k_norm,
+                          const float *d_q_and_gate, const float *d_key, const float *d_value,
+                          float *d_out);
+
 /* The q/k RMSNorm + RoPE prologue of full_core alone (ops.rs:832-856) for
  * n_tokens tokens at positions pos0, pos0+1, ...: writes d_q_out, d_gate_out
  * [n_tokens][24][256] and d_k_out [n_tokens][1024]. */

@@ -30,6 +30,7 @@ LIN_QK_HEADS, LIN_V_HEADS, LIN_HEAD_DIM = 16, 48, 128
 LIN_QK_DIM, LIN_V_DIM, LIN_QKV_DIM = 2048, 6144, 10240
 LIN_STATE_FLOATS = LIN_V_HEADS * LIN_HEAD_DIM * LIN_HEAD_DIM
 PAGE_TOKENS = 16
+NOALLOC_SCRATCH_BYTES = 16 << 20  # Q38_NOALLOC_SCRATCH_BYTES of include/q38_attn.h
 
 
 class Q38Error(RuntimeError):
@@ -78,6 +79,7 @@ _SIGNATURES = {
     "q38_kv_read": (c_int, [_P, c_int, c_int, c_int, c_int, _P, _P]),
     "q38_attn_decode": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P]),
     "q38_full_core": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P, _P]),
+    "q38_full_core_noalloc": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P, _P]),
     "q38_attn_pre": (c_int, [_P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P]),
     "q38_attn_prefill": (c_int, [_P, c_int, c_int, c_int, c_int, _P, _P, _P, _P, _P]),
     "q38_gdn_step": (c_int, [_P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P]),
@@ -346,6 +348,12 @@ class KVCache:
         _check(lib().q38_full_core(self.handle, layer, n, _i32(seq_ids), _i32(positions), _ptr(q_norm),
                                    _ptr(k_norm), _ptr(q_and_gate), _ptr(key), _ptr(value), _ptr(out)),
                "q38_full_core")
+
+    def full_core_noalloc(self, layer, seq_ids, positions, q_norm, k_norm, q_and_gate, key, value, out):
+        n = len(seq_ids)
+        _check(lib().q38_full_core_noalloc(self.handle, layer, n, _i32(seq_ids), _i32(positions), _ptr(q_norm),
+                                           _ptr(k_norm), _ptr(q_and_gate), _ptr(key), _ptr(value), _ptr(out)),
+               "q38_full_core_noalloc")
 
     def attn_prefill(self, layer, seq, base_pos, n_tokens, q, k, v, out, gate=None):
         _check(lib().q38_attn_prefill(self.handle, layer, seq, base_pos, n_tokens, _ptr(q), _ptr(k), _ptr(v),

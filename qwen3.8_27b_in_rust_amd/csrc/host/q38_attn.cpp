@@ -37,6 +37,7 @@ extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalW
 #include "../../../include/q38_attn.h"
 #include "../../../include/q38_bench.h"
 #include "../q38_kargs.h"
+#include "q38_scratch.h"
 
 namespace {
 
@@ -109,6 +110,8 @@ struct q38_ctx {
     int clock_khz = 0;
     int lds_bytes = 0;
     char name[256] = {0};
+    /* this device's copy of the fixed scratch array (q38_full_core_noalloc) */
+    void *scratch = nullptr;
     /* grow-only device workspace (split-K partials, pre-kernel outputs) */
     void *work = nullptr;
     size_t work_bytes = 0;
@@ -255,6 +258,10 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     ctx->lds_bytes = (int)prop.sharedMemPerBlock;
     snprintf(ctx->name, sizeof(ctx->name), "%.200s (%.40s)", prop.name, prop.gcnArchName);
     Q38_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    {
+        const int e = q38_scratch_address(device, &ctx->scratch);
+        if (e != 0) return fail("device scratch lookup failed: %s", hipGetErrorString((hipError_t)e));
+    }
 
     const std::string dir = module_dir != nullptr ? std::string(module_dir) : library_dir();
     const std::string p_decode = dir + "/attn_decode.hsaco";
@@ -844,7 +851,7 @@ int validate_decode(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, co
  * norm + RoPE fused (d_q holds q|gate rows, d_k_new raw keys). */
 int decode_all(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, const int32_t *positions,
                const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate, float *d_out,
-               const decode_pre *pre) {
+               const decode_pre *pre, void *fixed_work = nullptr, size_t fixed_bytes = 0) {
     int slot = 0;
     const bool appends = d_k_new != nullptr;
     if (validate_decode(kv, layer, n_seq, seq_ids, positions, appends, &slot)) return -1;
@@ -856,7 +863,16 @@ int decode_all(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, const i
         if (plan_decode(ctx, std::min(Q38_MAX_BATCH, n_seq - b0), positions + b0, &plan)) return -1;
         work_bytes = std::max(work_bytes, plan.work_bytes);
     }
-    if (work_bytes > 0 && ctx->ensure_work(work_bytes)) return -1;
+    void *work = nullptr;
+    if (fixed_work != nullptr) {
+        /* the caller's fixed area: no allocation, so the call must fit */
+        if (work_bytes > fixed_bytes)
+            return fail("split-K partials need %zu bytes, the fixed scratch holds %zu", work_bytes, fixed_bytes);
+        work = fixed_work;
+    } else {
+        if (work_bytes > 0 && ctx->ensure_work(work_bytes)) return -1;
+        work = ctx->work;
+    }
     if (appends)
         for (int b = 0; b < n_seq; ++b)
             if (kv->reserve(seq_ids[b], positions[b] + 1)) return -1;
@@ -869,7 +885,7 @@ int decode_all(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, const i
         const size_t qoff = (size_t)b0 * Q38_ATTN_Q_DIM;
         if (decode_chunk(kv, slot, n, seq_ids + b0, positions + b0, d_q + (size_t)b0 * q_rows,
                          d_k_new ? d_k_new + kvoff : nullptr, d_v_new ? d_v_new + kvoff : nullptr,
-                         d_gate ? d_gate + qoff : nullptr, d_out + qoff, plan, ctx->work, pre))
+                         d_gate ? d_gate + qoff : nullptr, d_out + qoff, plan, work, pre))
             return -1;
     }
     return 0;
@@ -918,6 +934,19 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
      * decode kernel: no separate launch and no intermediate rows */
     const decode_pre pre{d_q_norm, d_k_norm};
     return decode_all(kv, layer, n_seq, seq_ids, positions, d_q_and_gate, d_key, d_value, nullptr, d_out, &pre);
+}
+
+int q38_full_core_noalloc(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
+                          const int32_t *positions, const float *d_q_norm, const float *d_k_norm,
+                          const float *d_q_and_gate, const float *d_key, const float *d_value,
+                          float *d_out) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (n_seq > 0 && (!d_q_norm || !d_k_norm || !d_q_and_gate || !d_key || !d_value || !d_out))
+        return fail("NULL argument");
+    if (kv->ctx->scratch == nullptr) return fail("device scratch is not set up");
+    const decode_pre pre{d_q_norm, d_k_norm};
+    return decode_all(kv, layer, n_seq, seq_ids, positions, d_q_and_gate, d_key, d_value, nullptr, d_out, &pre,
+                      kv->ctx->scratch, Q38_NOALLOC_SCRATCH_BYTES);
 }
 
 int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens, const float *d_q,

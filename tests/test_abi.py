@@ -67,3 +67,10 @@ def test_kargs_layout_matches_device_expectations():
         out = subprocess.run([os.path.join(d, "p")], capture_output=True, text=True, check=True).stdout
     sizes = [int(x) for x in out.split()]
     assert all(s < 4096 for s in sizes), sizes
+
+
+def test_noalloc_scratch_size_matches_header(pkg):
+    import re
+    text = open(os.path.join(pkg.INCLUDE_DIR, "q38_attn.h")).read()
+    m = re.search(r"#define Q38_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == pkg.NOALLOC_SCRATCH_BYTES
