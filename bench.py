@@ -164,6 +164,78 @@ def gdn_steps(pkg, ctx, n_seq: int, n_states: int, steps: int, warmup: int):
     }
 
 
+def launch_floor(ctx, n: int):
+    """An empty kernel: n launches back to back (events around the loop) and
+    the same launches with dispatch-stamped events (per-launch kernel time)."""
+    for _ in range(16):
+        ctx.noop()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(n):
+        ctx.noop()
+    ctx.record(e1)
+    back_to_back = ctx.elapsed_ms(e0, e1) / n
+    ctx.kernel_timer_start("q38_noop", n)
+    for _ in range(n):
+        ctx.noop()
+    k_ms, k_n = ctx.kernel_timer_stop()
+    return {"us_per_launch_back_to_back": back_to_back * 1e3, "us_event_stamped": k_ms * 1e3 / max(k_n, 1)}
+
+
+# linear_core, one token: DeltaNet state read + written, conv state read +
+# written, raw qkv, conv weights, z and out, gates and norm weight
+LINEAR_CORE_BYTES = (2 * GDN_STATE_BYTES + 2 * 10240 * 3 * 4 + 10240 * 4 + 10240 * 4 * 4 + 2 * 6144 * 4
+                     + 4 * 48 * 4 + 128 * 4)
+
+
+def linear_core_decode(pkg, ctx, tokens: int, warmup: int):
+    """linear_core for one decode token (conv, gates, recurrence, gated norm:
+    one q38_gdn_decode launch) over the 48 DeltaNet layers' states in layer
+    order, back to back: time per layer, and the kernel's own duration."""
+    per = 48 * 128 * 128
+    states = ctx.empty((48 * per,))
+    ctx.fill_normal(states, 48 * per, 0x51334b00, sigma=0.02)
+    conv = ctx.empty((48 * 30720,))
+    ctx.fill_normal(conv, 48 * 30720, 0x51334b01)
+    bufs = {}
+    for name, m in (("conv_w", 40960), ("dt", 48), ("a", 48), ("norm", 128), ("qkv", 10240), ("z", 6144),
+                    ("beta", 48), ("alpha", 48), ("out", 6144)):
+        bufs[name] = ctx.empty((m,))
+        ctx.fill_normal(bufs[name], m, 0x51334b10 + len(bufs))
+    b = bufs
+
+    def token():
+        for li in range(48):
+            ctx.linear_core(1, 1, b["conv_w"], b["dt"], b["a"], b["norm"], conv.offset(li * 30720),
+                            states.offset(li * per), b["qkv"], b["z"], b["beta"], b["alpha"], b["out"])
+
+    for _ in range(warmup):
+        token()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(tokens):
+        token()
+    ctx.record(e1)
+    us_layer = ctx.elapsed_ms(e0, e1) * 1e3 / (48 * tokens)
+    ctx.kernel_timer_start("q38_gdn_decode", 48 * tokens)
+    for _ in range(tokens):
+        token()
+    k_ms, k_n = ctx.kernel_timer_stop()
+    states.free()
+    conv.free()
+    for v in bufs.values():
+        v.free()
+    kern_us = k_ms * 1e3 / max(k_n, 1)
+    return {"layers": 48, "tokens": tokens, "us_per_layer_back_to_back": us_layer, "kernel_us": kern_us,
+            "algorithmic_bytes_per_layer": LINEAR_CORE_BYTES,
+            "gb_s_back_to_back": LINEAR_CORE_BYTES / (us_layer * 1e-6) / 1e9,
+            "kernel_gb_s": LINEAR_CORE_BYTES / (kern_us * 1e-6) / 1e9,
+            "note": "one q38_gdn_decode launch per layer (conv1d, SiLU, L2 norms, gates, recurrence, gated "
+                    "RMSNorm); 48 layers' states (151 MB) rotated"}
+
+
 PREFILL_T = 4096
 # causal attention flops of a 4096-token prompt: per (query t, head) (t+1)
 # keys x 256 dims x 2 (QK^T) + the same for PV
@@ -396,6 +468,26 @@ def copy_calibration(ctx, steps: int) -> None:
                       "gb_s": 2 * COPY_BYTES / (us * 1e-6) / 1e9}), flush=True)
 
 
+EXTRAS = {
+    "prefill_attention_4096": ("prefill attention, 4096-token causal prompt",
+                               lambda pkg, ctx: prefill_attention(pkg, ctx, 5)),
+    "gdn_prefill_4096": ("chunked Gated-DeltaNet prefill, 4096 tokens", lambda pkg, ctx: gdn_prefill(pkg, ctx, 5)),
+    "batched_decode_32": ("batched paged decode, 32 sequences, context ~U[1K, 32K]",
+                          lambda pkg, ctx: batched_decode(pkg, ctx, 20, 3)),
+    "launch_floor": ("empty kernel launches", lambda pkg, ctx: launch_floor(ctx, 500)),
+    "linear_core_decode": ("linear_core decode over 48 DeltaNet layers", lambda pkg, ctx: linear_core_decode(
+        pkg, ctx, 20, 3)),
+    "full_stack_128k": ("64 layers (48 DeltaNet + 16 attention), 128K context, one token",
+                        lambda pkg, ctx: full_stack(pkg, ctx, 10, 2)),
+    "gdn_step_1": ("Gated-DeltaNet step, 1 state per launch over 192 states",
+                   lambda pkg, ctx: gdn_steps(pkg, ctx, 1, 192, 384, 32)),
+    "gdn_step_32": ("Gated-DeltaNet step, 32 states per launch over 192",
+                    lambda pkg, ctx: gdn_steps(pkg, ctx, 32, 192, 60, 6)),
+    "gdn_step_1_same_state": ("Gated-DeltaNet step, one state stepped in place (labelled same-buffer figure)",
+                              lambda pkg, ctx: gdn_steps(pkg, ctx, 1, 1, 384, 32)),
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -403,7 +495,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the DeltaNet measurements")
+    ap.add_argument("--no-extra", action="store_true", help="skip every measurement besides the headline")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated subset of the extra measurements (" + ",".join(EXTRAS) + ")")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the benchmark: time a plain 512 MiB device copy (q38_copy_f32), "
                     "the reference figure that scales the HBM byte counters")
@@ -468,26 +562,15 @@ def main():
         log(f"cpu {cpu['value']:.2f} steps/s; GPU vs CPU max-abs {extra['parity_max_abs_vs_cpu']:.2e}")
     r["kv"].close()
 
-    if not args.no_extra:
-        log("prefill attention: 4096-token causal prompt")
-        extra["prefill_attention_4096"] = prefill_attention(pkg, ctx, 5)
-        log(f"prefill: {json.dumps(extra['prefill_attention_4096'])}")
-        log("chunked Gated-DeltaNet prefill: 4096 tokens")
-        extra["gdn_prefill_4096"] = gdn_prefill(pkg, ctx, 5)
-        log(f"gdn prefill: {json.dumps(extra['gdn_prefill_4096'])}")
-        log("batched paged decode: 32 sequences, context ~U[1K, 32K]")
-        extra["batched_decode_32"] = batched_decode(pkg, ctx, 20, 3)
-        log(f"batched: {json.dumps(extra['batched_decode_32'])}")
-        log("full stack: 64 layers (48 DeltaNet + 16 attention), 128K context, one token")
-        extra["full_stack_128k"] = full_stack(pkg, ctx, 10, 2)
-        log(f"full stack: {json.dumps(extra['full_stack_128k'])}")
-        log("Gated-DeltaNet step: 1 state per launch over 192 states; 32 per launch over 192")
-        extra["gdn_step_1"] = gdn_steps(pkg, ctx, 1, 192, 384, 32)
-        extra["gdn_step_32"] = gdn_steps(pkg, ctx, 32, 192, 60, 6)
-        log(f"gdn: {json.dumps(extra['gdn_step_1'])} {json.dumps(extra['gdn_step_32'])}")
-        # labelled same-buffer figure: one 6.3 MB state stepped in place
-        extra["gdn_step_1_same_state"] = gdn_steps(pkg, ctx, 1, 1, 384, 32)
-        log(f"gdn, one state in place: {json.dumps(extra['gdn_step_1_same_state'])}")
+    wanted = [] if args.no_extra else (args.only.split(",") if args.only else list(EXTRAS))
+    unknown = [w for w in wanted if w not in EXTRAS]
+    if unknown:
+        print(f"bench.py: unknown measurement(s) {unknown}; choose from {list(EXTRAS)}", file=sys.stderr)
+        sys.exit(2)
+    for name in wanted:
+        log(f"{name}: {EXTRAS[name][0]}")
+        extra[name] = EXTRAS[name][1](pkg, ctx)
+        log(f"{name}: {json.dumps(extra[name])}")
 
     line = {
         "metric": "attn decode-steps/s & achieved HBM GB/s (% of 8 TB/s) at 32K ctx, 1 MI355X",

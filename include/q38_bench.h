@@ -38,6 +38,10 @@ int q38_fill_normal(q38_ctx *ctx, float *d_out, size_t n, uint64_t seed, float s
  * the reference (which has no device). */
 int q38_device_copy(q38_ctx *ctx, void *d_dst, const void *d_src, size_t bytes);
 
+/* Launch an empty kernel (one 64-thread workgroup) on the context's
+ * stream: the launch floor that one dependent launch costs. */
+int q38_device_noop(q38_ctx *ctx);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,7 @@ _SIGNATURES = {
     "q38_kernel_timer_stop": (c_int, [_P, POINTER(c_float), POINTER(c_int)]),
     "q38_fill_normal": (c_int, [_P, _P, c_size_t, ctypes.c_uint64, c_float, c_float]),
     "q38_device_copy": (c_int, [_P, _P, _P, c_size_t]),
+    "q38_device_noop": (c_int, [_P]),
     "q38_kv_create": (c_int, [_P, c_int, c_int, c_int, c_int, POINTER(c_void_p)]),
     "q38_kv_destroy": (c_int, [_P]),
     "q38_kv_free_pages": (c_int, [_P, POINTER(c_int)]),
@@ -250,6 +251,10 @@ class Context:
     def fill_normal(self, dst, n: int, seed: int, sigma: float = 1.0, mean: float = 0.0) -> None:
         _check(lib().q38_fill_normal(self.handle, _ptr(dst), n, seed & 0xFFFFFFFFFFFFFFFF, sigma, mean),
                "q38_fill_normal")
+
+    def noop(self) -> None:
+        """Launch an empty kernel (the launch floor)."""
+        _check(lib().q38_device_noop(self.handle), "q38_device_noop")
 
     def copy(self, dst, src, nbytes: int) -> None:
         _check(lib().q38_device_copy(self.handle, _ptr(dst), _ptr(src), nbytes), "q38_device_copy")

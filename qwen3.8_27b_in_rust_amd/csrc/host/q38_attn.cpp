@@ -94,12 +94,13 @@ struct q38_ctx {
     hipFunction_t f_decode_merge = nullptr;
     hipFunction_t f_kv_copy = nullptr;
     hipFunction_t f_attn_pre = nullptr;
-    hipFunction_t f_gdn_recurrent = nullptr;
+    hipFunction_t f_gdn_decode = nullptr;
     hipFunction_t f_gdn_pre = nullptr;
     hipFunction_t f_gdn_step_rows = nullptr;
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
     hipFunction_t f_copy = nullptr;
+    hipFunction_t f_noop = nullptr;
     /* per-kernel event timer (q38_kernel_timer_*) */
     hipFunction_t timed = nullptr;
     std::vector<hipEvent_t> timer_events;
@@ -115,6 +116,26 @@ struct q38_ctx {
     /* grow-only device workspace (split-K partials, pre-kernel outputs) */
     void *work = nullptr;
     size_t work_bytes = 0;
+    /* DeltaNet decode arrival counters [n_seq][Q38_GDN_ARRIVALS], zero
+     * between calls */
+    int32_t *arrivals = nullptr;
+    int arrival_seqs = 0;
+
+    int ensure_arrivals(int n_seq) {
+        if (n_seq <= arrival_seqs) return 0;
+        if (arrivals != nullptr) {
+            Q38_HIP(hipStreamSynchronize(stream));
+            Q38_HIP(hipFree(arrivals));
+            arrivals = nullptr;
+            arrival_seqs = 0;
+        }
+        const int want = std::max(n_seq, 64);
+        const size_t bytes = (size_t)want * Q38_GDN_ARRIVALS * sizeof(int32_t);
+        Q38_HIP(hipMalloc(&arrivals, bytes));
+        Q38_HIP(hipMemsetAsync(arrivals, 0, bytes, stream));
+        arrival_seqs = want;
+        return 0;
+    }
     float rope_theta_scale = 0.0f;
 
     int ensure_work(size_t bytes) {
@@ -285,7 +306,7 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "q38_attn_decode_merge"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_copy, ctx->mod_decode, "q38_kv_copy"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_attn_pre, ctx->mod_decode, "q38_attn_pre"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_recurrent, ctx->mod_gdn, "q38_gdn_recurrent"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_decode, ctx->mod_gdn, "q38_gdn_decode"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_pre, ctx->mod_gdn, "q38_gdn_pre"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_step_rows, ctx->mod_gdn, "q38_gdn_step_rows"));
     Q38_HIP(hipFuncGetAttribute(&ctx->decode_block, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
@@ -298,6 +319,7 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_copy, ctx->mod_synth, "q38_copy_f32"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_noop, ctx->mod_synth, "q38_noop"));
     /* ops.rs:596: 1e7^(-2/64) in f32, computed once with the host's powf */
     ctx->rope_theta_scale = powf(10000000.0f, -2.0f / 64.0f);
     *out = ctx.release();
@@ -309,6 +331,7 @@ int q38_ctx_destroy(q38_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->work) (void)hipFree(ctx->work);
+    if (ctx->arrivals) (void)hipFree(ctx->arrivals);
     if (ctx->mod_decode) (void)hipModuleUnload(ctx->mod_decode);
     if (ctx->mod_gdn) (void)hipModuleUnload(ctx->mod_gdn);
     if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
@@ -439,6 +462,12 @@ int q38_device_copy(q38_ctx *ctx, void *d_dst, const void *d_src, size_t bytes) 
     return ctx->launch(ctx->f_copy, (unsigned)blocks, 1, 1, 256, &a);
 }
 
+int q38_device_noop(q38_ctx *ctx) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    int32_t unused = 0;
+    return ctx->launch(ctx->f_noop, 1, 1, 1, 64, &unused);
+}
+
 int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launches) {
     if (ctx == nullptr || kernel_name == nullptr) return fail("NULL argument");
     if (max_launches < 1) return fail("max_launches must be positive");
@@ -451,10 +480,11 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_attn_decode_merge") f = ctx->f_decode_merge;
     else if (name == "q38_kv_copy") f = ctx->f_kv_copy;
     else if (name == "q38_attn_pre") f = ctx->f_attn_pre;
-    else if (name == "q38_gdn_recurrent") f = ctx->f_gdn_recurrent;
+    else if (name == "q38_gdn_decode") f = ctx->f_gdn_decode;
     else if (name == "q38_gdn_pre") f = ctx->f_gdn_pre;
     else if (name == "q38_gdn_step_rows") f = ctx->f_gdn_step_rows;
     else if (name == "q38_copy_f32") f = ctx->f_copy;
+    else if (name == "q38_noop") f = ctx->f_noop;
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
     else if (name == "q38_gdn_chunk_prep") f = ctx->f_chunk_prep;
@@ -1049,7 +1079,6 @@ int q38_gdn_step(q38_ctx *ctx, int n_seq, float *d_state, int64_t state_stride, 
     a.state_stride = state_stride;
     a.q_stride = Q38_LIN_QK_DIM;
     a.v_stride = Q38_LIN_V_DIM;
-    a.n_tokens = 1;
     a.n_seq = n_seq;
     return ctx->launch(ctx->f_gdn_step_rows, Q38_LIN_V_HEADS * (Q38_LIN_HEAD_DIM / 16), n_seq, 1, 256, &a);
 }
@@ -1077,14 +1106,34 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
         !d_qkv || !d_z || !d_beta || !d_alpha || !d_out)
         return fail("NULL argument");
     if (n_seq > 65535) return fail("n_seq %d above 65535", n_seq);
+    if (n_tokens == 1) {
+        /* decode: conv, gates, recurrence and gated norm in one launch */
+        if (ctx->ensure_arrivals(n_seq)) return -1;
+        q38_gdn_decode_args a;
+        memset(&a, 0, sizeof(a));
+        a.qkv_raw = d_qkv;
+        a.conv_w = w->d_conv_w;
+        a.conv_state = d_conv_state;
+        a.state = d_delta_state;
+        a.z = d_z;
+        a.beta_raw = d_beta;
+        a.alpha_raw = d_alpha;
+        a.dt = w->d_dt;
+        a.a = w->d_a;
+        a.norm_w = w->d_norm;
+        a.out = d_out;
+        a.arrivals = ctx->arrivals;
+        return ctx->launch(ctx->f_gdn_decode, Q38_LIN_V_HEADS, n_seq, 1, 512, &a);
+    }
     const int n_chunks = (n_tokens + 63) / 64;
     const size_t toks = (size_t)n_seq * n_tokens;
     /* workspace: qkv after conv/SiLU/L2 | beta | g | conv state out |
-     * (n_tokens > 1) recurrence output before the norm | chunk products */
+     * recurrence output before the norm | chunk products */
     const size_t conv_floats = (size_t)n_seq * Q38_LIN_QKV_DIM * 3;
     const size_t base_floats = toks * (Q38_LIN_QKV_DIM + 2 * Q38_LIN_V_HEADS) + (n_chunks > 1 ? conv_floats : 0);
-    const size_t o_floats = n_tokens > 1 ? toks * Q38_LIN_V_DIM : 0;
-    const size_t chunk_floats = n_tokens > 1 ? chunk_work_floats(n_seq, n_tokens) : 0;
+    const size_t o_floats = toks * Q38_LIN_V_DIM;
+    const size_t chunk_floats = chunk_work_floats(n_seq, n_tokens);
+    if (toks > 0x7FFFFFFFull) return fail("too many tokens");
     if (ctx->ensure_work((base_floats + o_floats + chunk_floats) * sizeof(float))) return -1;
     float *x = static_cast<float *>(ctx->work);
     float *beta = x + toks * Q38_LIN_QKV_DIM;
@@ -1112,38 +1161,17 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
     if (n_chunks > 1)
         Q38_HIP(hipMemcpyAsync(d_conv_state, conv_out, conv_floats * sizeof(float),
                                hipMemcpyDeviceToDevice, ctx->stream));
-    if (n_tokens > 1) {
-        /* prompt: chunked recurrence, then the gated RMSNorm */
-        if (gdn_chunked(ctx, n_seq, n_tokens, d_delta_state, Q38_LIN_STATE_FLOATS, x, x + Q38_LIN_QK_DIM,
-                        x + 2 * Q38_LIN_QK_DIM, beta, g, o_raw, Q38_LIN_QKV_DIM, Q38_LIN_QKV_DIM, chunk_work))
-            return -1;
-        if (toks > 0x7FFFFFFFull) return fail("too many tokens");
-        q38_gdn_post_args pa;
-        memset(&pa, 0, sizeof(pa));
-        pa.o = o_raw;
-        pa.z = d_z;
-        pa.norm_w = w->d_norm;
-        pa.out = d_out;
-        return ctx->launch(ctx->f_gdn_post, (unsigned)toks, Q38_LIN_V_HEADS, 1, 64, &pa);
-    }
-    /* one token: the recurrence with the gated RMSNorm fused */
-    q38_gdn_args a;
-    memset(&a, 0, sizeof(a));
-    a.state = d_delta_state;
-    a.q = x;
-    a.k = x + Q38_LIN_QK_DIM;
-    a.v = x + 2 * Q38_LIN_QK_DIM;
-    a.beta = beta;
-    a.g = g;
-    a.out = d_out;
-    a.z = d_z;
-    a.norm_w = w->d_norm;
-    a.state_stride = Q38_LIN_STATE_FLOATS;
-    a.q_stride = Q38_LIN_QKV_DIM;
-    a.v_stride = Q38_LIN_QKV_DIM;
-    a.n_tokens = n_tokens;
-    a.n_seq = n_seq;
-    return ctx->launch(ctx->f_gdn_recurrent, Q38_LIN_V_HEADS, n_seq, 1, 512, &a);
+    /* prompt: chunked recurrence, then the gated RMSNorm */
+    if (gdn_chunked(ctx, n_seq, n_tokens, d_delta_state, Q38_LIN_STATE_FLOATS, x, x + Q38_LIN_QK_DIM,
+                    x + 2 * Q38_LIN_QK_DIM, beta, g, o_raw, Q38_LIN_QKV_DIM, Q38_LIN_QKV_DIM, chunk_work))
+        return -1;
+    q38_gdn_post_args pa;
+    memset(&pa, 0, sizeof(pa));
+    pa.o = o_raw;
+    pa.z = d_z;
+    pa.norm_w = w->d_norm;
+    pa.out = d_out;
+    return ctx->launch(ctx->f_gdn_post, (unsigned)toks, Q38_LIN_V_HEADS, 1, 64, &pa);
 }
 
 }  /* extern "C" */

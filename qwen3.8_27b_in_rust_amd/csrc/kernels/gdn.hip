@@ -3,21 +3,12 @@
  *
  * Reference semantics: linear_core, src/model/ops.rs:648-742.
  *
- * q38_gdn_recurrent -- the delta-rule recurrence (ops.rs:698-714): for value
- * head vh (key head vh % 16) and each state row c:
- *     S_c *= exp(g);  pred = S_c.k;  delta = (v_c - pred) * beta;
- *     S_c += k * delta;  o_c = (S_c.q) / sqrt(128)
- * Rows are independent given (q, k, v_c, beta, g).  One workgroup owns one
- * head of one sequence: 512 threads, 16 lanes per row, 4 rows per 16-lane
- * group, lane i holding columns 4i..4i+3 and 64+4i..64+4i+3 of its rows in
- * VGPRs.  The state is read from HBM once, carried in registers through all
- * n_tokens tokens, and written back once: a decode step is n_tokens = 1, a
- * sequential prefill is the same code over the prompt.  Both 128-long dots
- * are 8 FMAs per lane plus a 4-step DPP row reduction (no LDS).  The next
- * token's q/k/v/beta/g are loaded while the current one computes.
+ * q38_gdn_decode -- one linear_core token in one launch: conv1d, SiLU, L2
+ * norms and gates, the delta-rule recurrence with readout, and the gated
+ * RMSNorm, one workgroup per value head.
  *
- * With z != NULL the gated RMSNorm of ops.rs:735-740 is fused as an epilogue:
- * the head's 128 outputs meet in LDS, one wave forms the f64 sum of squares.
+ * q38_gdn_step_rows -- the recurrence alone, one token, 8 workgroups per
+ * value head (the rows of a head are independent).
  *
  * q38_gdn_pre -- conv1d (kernel 4) with state shift (ops.rs:665-675), SiLU
  * (:676), per-head L2 norm of q and k (:678-683) and the beta / decay gates
@@ -25,109 +16,185 @@
  */
 #include "q38_device.h"
 
-namespace {
-
-struct GdnTok {
-    f32x4 k0, k1, q0, q1;
-    f32x4 v; /* v for rows 4*grp .. 4*grp+3 */
-    float beta, g;
-};
-
-Q38_DEV GdnTok gdn_load(const q38_gdn_args &a, size_t tok, int kh, int vh, int grp, int d0,
-                        int d1) {
-    GdnTok x;
-    const float *kp = a.k + tok * a.q_stride + kh * Q38_LIN_HEAD_DIM;
-    const float *qp = a.q + tok * a.q_stride + kh * Q38_LIN_HEAD_DIM;
-    x.k0 = q38_ld4(kp + d0);
-    x.k1 = q38_ld4(kp + d1);
-    x.q0 = q38_ld4(qp + d0);
-    x.q1 = q38_ld4(qp + d1);
-    x.v = q38_ld4(a.v + tok * a.v_stride + vh * Q38_LIN_HEAD_DIM + 4 * grp);
-    x.beta = a.beta[tok * Q38_LIN_V_HEADS + vh];
-    x.g = a.g[tok * Q38_LIN_V_HEADS + vh];
-    return x;
-}
-
-}  // namespace
-
-extern "C" __global__ __launch_bounds__(512) void q38_gdn_recurrent(q38_gdn_args a) {
-    __shared__ float o_lds[2][Q38_LIN_HEAD_DIM];
+/* One linear_core token (ops.rs:648-742) in ONE launch: grid (48 value
+ * heads, n_seq), 512 threads.  The workgroup of value head vh (key head kh =
+ * vh % 16):
+ *  1. issues the loads of its head's 128x128 state first (16 lanes per row,
+ *     4 rows per 16-lane group, lane i holding columns 4i..4i+3 and
+ *     64+4i..64+4i+3), so the state streams in while the prologue runs;
+ *  2. prologue (ops.rs:665-687): threads 0..383 take one channel each -- q
+ *     and k of key head kh and v of value head vh -- conv1d over the 3-tap
+ *     state and the raw input (separate multiplies and adds, left to right),
+ *     SiLU, then the f64 L2 norm of q and k (waves 0-1 and 2-3); thread 384
+ *     forms beta = sigmoid and g = a * softplus(alpha + dt);
+ *  3. the recurrence of ops.rs:698-714 on the 128 rows in registers (decay,
+ *     prediction, delta-rule update and readout; two 4-step DPP reductions
+ *     per row), the new state streamed back with non-temporal stores;
+ *  4. the gated RMSNorm of ops.rs:735-740 over the head's 128 outputs in LDS.
+ * Conv state: the v channels of vh belong to this workgroup alone and are
+ * shifted in place.  The q/k channels of kh are read by the three value
+ * heads kh, kh+16, kh+32: each of their workgroups counts its arrival on
+ * arrivals[s][kh] after its reads have been consumed, and the third to
+ * arrive writes the shifted q/k state and resets the counter to zero for the
+ * next call.  No workgroup waits on another.  The arithmetic is that of
+ * q38_gdn_pre followed by the recurrence, operation for operation. */
+extern "C" __global__ __launch_bounds__(512) void q38_gdn_decode(q38_gdn_decode_args a) {
+    __shared__ __attribute__((aligned(16))) float xqkv[3][Q38_LIN_HEAD_DIM]; /* q, k (normed), v */
+    __shared__ __attribute__((aligned(16))) float o_lds[Q38_LIN_HEAD_DIM];
+    __shared__ double red[4];
+    __shared__ float gates[2];
+    __shared__ int last_arrival;
     const int vh = blockIdx.x;
-    const int s = blockIdx.y;
+    const size_t s = blockIdx.y;
     const int kh = vh % Q38_LIN_QK_HEADS;
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const int grp = tid >> 4; /* 0..31: rows 4*grp .. 4*grp+3 */
     const int li = tid & 15;
     const int d0 = 4 * li;
     const int d1 = 64 + 4 * li;
     const float query_scale = 1.0f / sqrtf((float)Q38_LIN_HEAD_DIM);
 
-    float *st = a.state + (size_t)s * a.state_stride + (size_t)vh * Q38_LIN_HEAD_DIM * Q38_LIN_HEAD_DIM;
+    /* the prologue's loads first: one channel per thread (q, k of key head
+     * kh, v of value head vh; thread 384 the gates) */
+    const int part = tid >> 7; /* 0: q, 1: k, 2: v, 3: gates */
+    const int ci = tid & 127;
+    int c = 0;
+    if (part == 0) c = kh * Q38_LIN_HEAD_DIM + ci;
+    else if (part == 1) c = Q38_LIN_QK_DIM + kh * Q38_LIN_HEAD_DIM + ci;
+    else if (part == 2) c = 2 * Q38_LIN_QK_DIM + vh * Q38_LIN_HEAD_DIM + ci;
+    float *conv = a.conv_state + s * (Q38_LIN_QKV_DIM * 3) + (size_t)c * 3;
+    f32x4 w = {0.f, 0.f, 0.f, 0.f};
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, x = 0.0f, g_beta = 0.0f, g_alpha = 0.0f;
+    if (part < 3) {
+        w = q38_ld4(a.conv_w + (size_t)c * 4);
+        s0 = conv[0];
+        s1 = conv[1];
+        s2 = conv[2];
+        x = a.qkv_raw[s * Q38_LIN_QKV_DIM + c];
+    } else if (ci == 0) {
+        g_beta = a.beta_raw[s * Q38_LIN_V_HEADS + vh];
+        g_alpha = a.alpha_raw[s * Q38_LIN_V_HEADS + vh] + a.dt[vh];
+        g_alpha = a.a[vh] * q38_softplus(g_alpha);
+    }
+    /* the epilogue's gate and norm weight (wave 0 forms the outputs) */
+    float z0 = 0.0f, z1 = 0.0f, nw0 = 0.0f, nw1 = 0.0f;
+    if (tid < 64) {
+        const float *zt = a.z + s * Q38_LIN_V_DIM + vh * Q38_LIN_HEAD_DIM;
+        z0 = zt[tid];
+        z1 = zt[tid + 64];
+        nw0 = a.norm_w[tid];
+        nw1 = a.norm_w[tid + 64];
+    }
+    /* then the state, in flight while the prologue computes (the memory
+     * counter is in issue order, so these stay outstanding) */
+    float *st = a.state + s * Q38_LIN_STATE_FLOATS + (size_t)vh * Q38_LIN_HEAD_DIM * Q38_LIN_HEAD_DIM;
     f32x4 S0[4], S1[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int row = 4 * grp + r;
-        S0[r] = q38_ld4(st + row * Q38_LIN_HEAD_DIM + d0);
-        S1[r] = q38_ld4(st + row * Q38_LIN_HEAD_DIM + d1);
+        S0[r] = q38_ld4_stream(st + row * Q38_LIN_HEAD_DIM + d0);
+        S1[r] = q38_ld4_stream(st + row * Q38_LIN_HEAD_DIM + d1);
     }
 
-    const size_t tok0 = (size_t)s * a.n_tokens;
-    GdnTok cur = gdn_load(a, tok0, kh, vh, grp, d0, d1);
-    for (int t = 0; t < a.n_tokens; ++t) {
-        const size_t tok = tok0 + t;
-        GdnTok nxt = cur;
-        if (t + 1 < a.n_tokens) nxt = gdn_load(a, tok + 1, kh, vh, grp, d0, d1);
-
-        const float decay = expf(cur.g);
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            S0[r] *= decay;
-            S1[r] *= decay;
-            float pred = q38_dot4(S0[r], cur.k0, 0.0f);
-            pred = q38_dot4(S1[r], cur.k1, pred);
-            pred = q38_sum16(pred);
-            const float delta = (cur.v[r] - pred) * cur.beta;
-            S0[r] = q38_fma4(delta, cur.k0, S0[r]);
-            S1[r] = q38_fma4(delta, cur.k1, S1[r]);
-            float res = q38_dot4(S0[r], cur.q0, 0.0f);
-            res = q38_dot4(S1[r], cur.q1, res);
-            res = q38_sum16(res);
-            o[r] = res * query_scale;
-        }
-        float *out_tok = a.out + tok * Q38_LIN_V_DIM + vh * Q38_LIN_HEAD_DIM;
-        if (a.z == nullptr) {
-            if (li == 0) q38_st4(out_tok + 4 * grp, f32x4{o[0], o[1], o[2], o[3]});
-        } else {
-            /* gated RMSNorm epilogue (ops.rs:735-740); double-buffered LDS so
-             * one barrier per token suffices */
-            float *ob = o_lds[t & 1];
-            if (li == 0) q38_st4(ob + 4 * grp, f32x4{o[0], o[1], o[2], o[3]});
-            __syncthreads();
-            if (tid < 64) {
-                const float x0 = ob[tid];
-                const float x1 = ob[tid + 64];
-                double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
-                ss = q38_wave_sum_f64(ss);
-                const float mean = (float)(ss / (double)Q38_LIN_HEAD_DIM);
-                const float scale = 1.0f / sqrtf(mean + 1e-6f);
-                const float *zt = a.z + tok * Q38_LIN_V_DIM + vh * Q38_LIN_HEAD_DIM;
-                float y0 = x0 * scale * a.norm_w[tid];
-                float y1 = x1 * scale * a.norm_w[tid + 64];
-                y0 *= q38_silu(zt[tid]);
-                y1 *= q38_silu(zt[tid + 64]);
-                out_tok[tid] = y0;
-                out_tok[tid + 64] = y1;
-            }
-        }
-        cur = nxt;
+    /* prologue (ops.rs:665-687) */
+    float y = 0.0f;
+    if (part < 3) {
+        y = s0 * w.x;
+        y += s1 * w.y;
+        y += s2 * w.z;
+        y += x * w.w;
+        y = q38_silu(y);
+    } else if (ci == 0) {
+        gates[0] = q38_sigmoid(g_beta);
+        gates[1] = g_alpha;
     }
+    if (part < 2) {
+        /* l2norm (ops.rs:562-571): f64 sum, f32 sqrt, floor 1e-6 */
+        const double ss = q38_wave_sum_f64((double)y * (double)y);
+        if (lane == 0) red[wave] = ss;
+    }
+    __syncthreads();
+    if (part < 2) {
+        const double sum = red[2 * part] + red[2 * part + 1];
+        float norm = sqrtf((float)sum);
+        norm = fmaxf(norm, 1e-6f);
+        y *= 1.0f / norm;
+    }
+    if (part < 3) xqkv[part][ci] = y;
+    if (part == 2) {
+        /* this value head's own channels: shift in place */
+        conv[0] = s1;
+        conv[1] = s2;
+        conv[2] = x;
+    }
+    __syncthreads();
+    /* every q/k conv-state value this workgroup read has been consumed:
+     * count the arrival now, use the count at the end (the atomic's round
+     * trip overlaps the recurrence) */
+    int before = 0;
+    if (tid == 0) before = atomicAdd(&a.arrivals[s * Q38_GDN_ARRIVALS + kh], 1);
 
+    /* 3. the recurrence (ops.rs:698-714) */
+    const f32x4 k0 = q38_ld4(&xqkv[1][d0]), k1 = q38_ld4(&xqkv[1][d1]);
+    const f32x4 q0 = q38_ld4(&xqkv[0][d0]), q1 = q38_ld4(&xqkv[0][d1]);
+    const f32x4 v = q38_ld4(&xqkv[2][4 * grp]);
+    const float beta = gates[0];
+    const float decay = expf(gates[1]);
+    float o[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+        S0[r] *= decay;
+        S1[r] *= decay;
+        float pred = q38_dot4(S0[r], k0, 0.0f);
+        pred = q38_dot4(S1[r], k1, pred);
+        pred = q38_sum16(pred);
+        const float delta = (v[r] - pred) * beta;
+        S0[r] = q38_fma4(delta, k0, S0[r]);
+        S1[r] = q38_fma4(delta, k1, S1[r]);
+        float res = q38_dot4(S0[r], q0, 0.0f);
+        res = q38_dot4(S1[r], q1, res);
+        res = q38_sum16(res);
+        o[r] = res * query_scale;
         const int row = 4 * grp + r;
-        q38_st4(st + row * Q38_LIN_HEAD_DIM + d0, S0[r]);
-        q38_st4(st + row * Q38_LIN_HEAD_DIM + d1, S1[r]);
+        q38_st4_stream(st + row * Q38_LIN_HEAD_DIM + d0, S0[r]);
+        q38_st4_stream(st + row * Q38_LIN_HEAD_DIM + d1, S1[r]);
+    }
+
+    /* 4. gated RMSNorm (ops.rs:735-740) */
+    if (li == 0) q38_st4(&o_lds[4 * grp], f32x4{o[0], o[1], o[2], o[3]});
+    __syncthreads();
+    if (tid < 64) {
+        const float x0 = o_lds[tid];
+        const float x1 = o_lds[tid + 64];
+        double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
+        ss = q38_wave_sum_f64(ss);
+        const float mean = (float)(ss / (double)Q38_LIN_HEAD_DIM);
+        const float scale = 1.0f / sqrtf(mean + 1e-6f);
+        float y0 = x0 * scale * nw0;
+        float y1 = x1 * scale * nw1;
+        y0 *= q38_silu(z0);
+        y1 *= q38_silu(z1);
+        float *out = a.out + s * Q38_LIN_V_DIM + vh * Q38_LIN_HEAD_DIM;
+        out[tid] = y0;
+        out[tid + 64] = y1;
+        /* the count is first read here, so the wait for the atomic lands
+         * here and not before the recurrence */
+        asm volatile("" : "+v"(before));
+        if (tid == 0) last_arrival = before == Q38_LIN_V_HEADS / Q38_LIN_QK_HEADS - 1;
+    }
+    __syncthreads();
+    /* the third of the key head's value heads shifts its q/k conv state */
+    if (last_arrival) {
+        if (part < 2) {
+            conv[0] = s1;
+            conv[1] = s2;
+            conv[2] = x;
+        }
+        if (tid == 0)
+            __hip_atomic_store(&a.arrivals[s * Q38_GDN_ARRIVALS + kh], 0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -212,7 +279,7 @@ extern "C" __global__ __launch_bounds__(128) void q38_gdn_pre(q38_gdn_pre_args a
  * per row, lane i holding columns 4i..4i+3 and 64+4i..64+4i+3.  Every load
  * of a thread (its 8 state values, k, q, v_c, beta, g) is issued at once,
  * so the step costs one memory round trip; the state is read and written
- * exactly once.  Arithmetic per row is the same as q38_gdn_recurrent's. */
+ * exactly once.  Arithmetic per row is the same as q38_gdn_decode's. */
 extern "C" __global__ __launch_bounds__(256) void q38_gdn_step_rows(q38_gdn_args a) {
     constexpr int kRowBlocks = Q38_LIN_HEAD_DIM / 16;
     const int vh = blockIdx.x / kRowBlocks;

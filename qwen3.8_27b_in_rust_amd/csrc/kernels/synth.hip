@@ -48,3 +48,11 @@ extern "C" __global__ __launch_bounds__(256) void q38_copy_f32(q38_copy_args a) 
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < a.n4) a.dst[i] = a.src[i];
 }
+
+/* A kernel that does nothing: its back-to-back launch time is the floor
+ * under every dependent launch of this library. */
+typedef struct {
+    int32_t unused;
+} q38_noop_args;
+
+extern "C" __global__ __launch_bounds__(64) void q38_noop(q38_noop_args a) {}

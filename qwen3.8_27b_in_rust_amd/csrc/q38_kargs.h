@@ -100,25 +100,41 @@ typedef struct {
     int32_t pad_;
 } q38_attn_pre_args;
 
-/* Gated-DeltaNet recurrence over n_tokens consecutive tokens of each of
- * n_seq independent states.  grid (48 value heads, n_seq), 512 threads;
- * the head's 128x128 state stays in registers for all the tokens. */
+/* Gated-DeltaNet recurrence, one token of each of n_seq independent states
+ * (q38_gdn_step_rows: grid (48 value heads x 8 row blocks, n_seq)). */
 typedef struct {
     float *state;      /* seq s at state + s*state_stride: [48][128][128] */
-    const float *q;    /* [(s*T + t)*q_stride + kh*128 ...] */
+    const float *q;    /* [s*q_stride + kh*128 ...] */
     const float *k;
-    const float *v;    /* [(s*T + t)*v_stride + vh*128 ...] */
-    const float *beta; /* [(s*T + t)*48 + vh], post-sigmoid */
+    const float *v;    /* [s*v_stride + vh*128 ...] */
+    const float *beta; /* [s*48 + vh], post-sigmoid */
     const float *g;    /* log-decay, same layout */
-    float *out;        /* [(s*T + t)*6144 + vh*128 + c] */
-    const float *z;        /* post: [(s*T + t)*6144 ...] gate of the gated RMSNorm, or NULL */
-    const float *norm_w;   /* post: [128] */
+    float *out;        /* [s*6144 + vh*128 + c] */
     int64_t state_stride;
-    int32_t q_stride; /* floats between consecutive tokens' q (and k) */
+    int32_t q_stride; /* floats between consecutive sequences' q (and k) */
     int32_t v_stride;
-    int32_t n_tokens;
     int32_t n_seq;
+    int32_t pad_;
 } q38_gdn_args;
+
+/* linear_core whole for one token of each of n_seq sequences in one launch
+ * (q38_gdn_decode: grid (48 value heads, n_seq), 512 threads). */
+typedef struct {
+    const float *qkv_raw;   /* [n_seq][10240] raw projection */
+    const float *conv_w;    /* [10240][4] */
+    float *conv_state;      /* seq s at + s*30720: [10240][3], shifted in place */
+    float *state;           /* seq s at + s*786432: [48][128][128] */
+    const float *z;         /* [n_seq][6144] gate of the gated RMSNorm */
+    const float *beta_raw;  /* [n_seq][48] */
+    const float *alpha_raw; /* [n_seq][48] */
+    const float *dt;        /* [48] */
+    const float *a;         /* [48] */
+    const float *norm_w;    /* [128] */
+    float *out;             /* [n_seq][6144] */
+    int32_t *arrivals;      /* [n_seq][Q38_GDN_ARRIVALS] arrival counters (one per key head),
+                               zero between calls */
+} q38_gdn_decode_args;
+#define Q38_GDN_ARRIVALS 16
 
 /* Chunked Gated-DeltaNet prefill (chunk Q38_GDN_CHUNK tokens).  The prep
  * kernel (grid (48 value heads, n_chunks, n_seq)) writes one record per head
