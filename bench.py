@@ -13,12 +13,15 @@ region (inputs resident in HBM).  `roofline` is for the dominant kernel,
 q38_attn_decode_split (a decode step is this launch plus the small
 q38_attn_decode_merge that combines the split-K partials): algorithmic bytes
 per launch (K + V each read once + q) over its mean duration, from start/stop
-events stamped by each dispatch on the launch stream in the timed region.  `cpu_baseline` times the
-CPU restatement of the reference's attention on the same data.
+events stamped by each dispatch on the launch stream in the timed region.
+`cpu_baseline` times the oracle's attention (a C restatement of the
+reference's) on the same data.
 
-Also measured and reported under "extra": the Gated-DeltaNet decode step
-(48 value heads, 128x128 f32 state per head) for one state and for 32 states
-per launch, each rotating over enough states to defeat the cache.
+Also measured under "extra" (all, or those --only names): prefill attention
+and chunked DeltaNet prefill of a 4096-token prompt, batched paged decode,
+the launch floor, one-token linear_core over 48 layers, the 64-layer full
+stack at 128K, and the bare DeltaNet step for one and for 32 states per
+launch, each rotating over enough states to defeat the cache.
 """
 from __future__ import annotations
 
