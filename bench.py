@@ -434,6 +434,73 @@ def gdn_prefill(pkg, ctx, reps: int):
                     "bf16x3 MFMA products"}
 
 
+FFN_MATS = ((12, 17408, 5120, "gate"), (12, 17408, 5120, "up"), (14, 5120, 17408, "down"))
+QUANT_BLOCK_BYTES = {12: 144, 13: 176, 14: 210}
+GEMV_KERNELS = {12: "q38_gemv_q8k_q4k", 13: "q38_gemv_q8k_q5k", 14: "q38_gemv_q8k_q6k"}
+
+
+def gemv_bytes(ty: int, rows: int, width: int, n_tokens: int) -> int:
+    """Algorithmic bytes of one projection launch: the weight rows once, the
+    Q8_K activations (292 bytes per 256 values per token) and the f32 outputs."""
+    return rows * (width // 256) * QUANT_BLOCK_BYTES[ty] + n_tokens * (width // 256) * 292 + n_tokens * rows * 4
+
+
+def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
+    """The FFN projections of `layers` layers (gate and up 17408x5120 Q4_K,
+    down 5120x17408 Q6_K; 173 MB a layer, 693 MB for 4, beyond the 256 MB
+    last-level cache) for n_tokens tokens, in layer order: per-kernel duration
+    and bandwidth of q38_gemv_q8_k.  Weights are random bytes."""
+    mats = []
+    for li in range(layers):
+        for ty, rows, width, name in FFN_MATS:
+            nbytes = rows * (width // 256) * QUANT_BLOCK_BYTES[ty]
+            w = ctx.empty((nbytes,), np.uint8)
+            ctx.fill_normal(w, nbytes // 4, 0x51335000 + 8 * li + ty)
+            mats.append((ty, rows, width, w))
+    x5 = ctx.empty((n_tokens, 5120))
+    ctx.fill_normal(x5, n_tokens * 5120, 0x51335100)
+    x17 = ctx.empty((n_tokens, 17408))
+    ctx.fill_normal(x17, n_tokens * 17408, 0x51335101)
+    q5 = ctx.empty((ctx.q8k_bytes(n_tokens, 5120),), np.uint8)
+    q17 = ctx.empty((ctx.q8k_bytes(n_tokens, 17408),), np.uint8)
+    ctx.quantize_q8_k(n_tokens, 5120, x5, q5)
+    ctx.quantize_q8_k(n_tokens, 17408, x17, q17)
+    out = ctx.empty((n_tokens, 17408))
+
+    def sweep():
+        for ty, rows, width, w in mats:
+            ctx.gemv_q8_k(ty, rows, width, w, q5 if width == 5120 else q17, n_tokens, out)
+
+    sweep()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(reps):
+        sweep()
+    ctx.record(e1)
+    sweep_us = ctx.elapsed_ms(e0, e1) * 1e3 / reps
+    total_bytes = sum(gemv_bytes(ty, rows, width, n_tokens) for ty, rows, width, _ in mats)
+    res = {"tokens": n_tokens, "layers": layers, "sweep_us": sweep_us,
+           "sweep_gb_s": total_bytes / (sweep_us * 1e-6) / 1e9}
+    for ty, label in ((12, "q4k_17408x5120"), (14, "q6k_5120x17408")):
+        ctx.kernel_timer_start(GEMV_KERNELS[ty], reps * 3 * layers)
+        for _ in range(reps):
+            sweep()
+        k_ms, k_n = ctx.kernel_timer_stop()
+        us = k_ms * 1e3 / max(k_n, 1)
+        rows, width = (17408, 5120) if ty == 12 else (5120, 17408)
+        b = gemv_bytes(ty, rows, width, n_tokens)
+        res[label] = {"kernel_us": us, "launches": k_n, "algorithmic_bytes": b,
+                      "gb_s": b / (us * 1e-6) / 1e9, "frac_hbm": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    for *_, w in mats:
+        w.free()
+    for a in (x5, x17, q5, q17, out):
+        a.free()
+    for e in (e0, e1):
+        ctx.destroy_event(e)
+    return res
+
+
 def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float, threads: int = 0):
     """The CPU restatement of the reference's attention (ops.rs:868-938) on the
     32K workload, all cores of this host (heads split across threads as the
@@ -488,6 +555,10 @@ EXTRAS = {
                     lambda pkg, ctx: gdn_steps(pkg, ctx, 32, 192, 60, 6)),
     "gdn_step_1_same_state": ("Gated-DeltaNet step, one state stepped in place (labelled same-buffer figure)",
                               lambda pkg, ctx: gdn_steps(pkg, ctx, 1, 1, 384, 32)),
+    "ffn_projections_1": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 1 token",
+                          lambda pkg, ctx: ffn_projections(pkg, ctx, 1, 20)),
+    "ffn_projections_8": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 8 tokens",
+                          lambda pkg, ctx: ffn_projections(pkg, ctx, 8, 20)),
 }
 
 

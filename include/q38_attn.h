@@ -237,6 +237,38 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
                     float *d_conv_state, float *d_delta_state, const float *d_qkv,
                     const float *d_z, const float *d_beta, const float *d_alpha, float *d_out);
 
+/* ------------------------------------------------------- weight projections */
+
+/*
+ * The projections on either side of the attention path (project,
+ * ops.rs:623-639): activations quantised to Q8_K once (quantize_input,
+ * ops.rs:617-620) and shared by every projection of the layer, then one
+ * K-quant x Q8_K dot per weight row.
+ *
+ * A device Q8_K buffer for n_tokens rows of `width` floats (width a multiple
+ * of 256) is planar: int8 quants [n_tokens][width] | int16 sums of each 16
+ * quants [n_tokens][width/256][16] | f32 scales [n_tokens][width/256];
+ * q38_q8k_bytes gives its size.
+ */
+int q38_q8k_bytes(int n_tokens, int width, size_t *bytes);
+
+/* quantize_q8_k (src/kernel/quant.rs:97-128, quantize_block :55-95) of
+ * d_x [n_tokens][width]: per 256 values, the first value of largest
+ * magnitude m sets scale m/-127 (stored as 1/(-127/m)), quants are
+ * round-to-nearest-even of x * (-127/m) capped at 127; all-zero blocks give
+ * zeros.  Bit-exact with the reference. */
+int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, void *d_q8k);
+
+/* tensor_gemv_q8_k / tensor_gemm_q8_k (src/kernel/tensor.rs:1131-1173,
+ * :1217-1270) for Q4_K (ggml type 12), Q5_K (13) and Q6_K (14) weights:
+ * d_weights [rows][width/256 blocks] in the GGUF block layout (144, 176,
+ * 210 bytes per block, 16-byte aligned base), d_q8k from
+ * q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the reference's
+ * batched form writes it).  Each element equals the reference's scalar
+ * dot_q*_k_q8_k (tensor.rs:365-457) bit for bit. */
+int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
+                  int n_tokens, float *d_out);
+
 #ifdef __cplusplus
 }
 #endif

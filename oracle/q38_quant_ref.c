@@ -1,0 +1,319 @@
+/*
+ * q38_quant_ref.c -- CPU restatement of the reference engine's weight
+ * projection path: the Q8_K activation quantiser and the K-quant x Q8_K row
+ * dots that tensor_gemv_q8_k / tensor_gemm_q8_k run for every row.
+ *
+ * TEST INFRASTRUCTURE ONLY (the oracle the HIP projection kernels are
+ * compared against); nothing in the product library links or calls it.
+ *
+ * Follows, operation for operation and in the same order:
+ *   f16_to_f32                    src/kernel/quant.rs:22-47
+ *   nearest_int                   src/kernel/quant.rs:16-20
+ *   quantize_block / quantize_q8_k src/kernel/quant.rs:55-128
+ *   scale_min_k4                  src/kernel/tensor.rs:23-32
+ *   dot_q4_k_q8_k_scalar          src/kernel/tensor.rs:365-391
+ *   dot_q5_k_q8_k_scalar          src/kernel/tensor.rs:393-428
+ *   dot_q6_k_q8_k_scalar          src/kernel/tensor.rs:430-457
+ *   gemv_rows / gemm_rows         src/kernel/tensor.rs:954-1002 (every
+ *                                 output element is one row dot, so the
+ *                                 row split across threads does not change it)
+ * Integer sums are exact; the f32 operations (the per-block d * weighted -
+ * dmin * minimum and the running total over blocks) are kept separate and in
+ * block order, as rustc compiles them (no contraction: -ffp-contract=off).
+ *
+ * Q8_K blocks are held planar here, as the device keeps them: for T tokens
+ * of width W (B = W/256 blocks per token) quants int8 [T][W], group sums
+ * int16 [T][B][16], scales f32 [T][B].
+ */
+#include "q38_ref.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <string.h>
+
+float q38r_f16_to_f32(uint16_t value) {
+    const uint32_t sign = (uint32_t)(value & 0x8000) << 16;
+    const uint32_t exponent = (value >> 10) & 0x1f;
+    const uint32_t mantissa = value & 0x03ff;
+    uint32_t bits;
+    if (exponent == 0) {
+        if (mantissa == 0) {
+            bits = sign;
+        } else {
+            uint32_t normalized = mantissa;
+            uint32_t shift = 0;
+            while ((normalized & 0x400) == 0) {
+                normalized <<= 1;
+                shift += 1;
+            }
+            normalized &= 0x3ff;
+            bits = sign | (127u - 14u - shift) << 23 | normalized << 13;
+        }
+    } else if (exponent == 31) {
+        bits = sign | 0x7f800000u | mantissa << 13;
+    } else {
+        bits = sign | (exponent + 112u) << 23 | mantissa << 13;
+    }
+    float out;
+    memcpy(&out, &bits, sizeof(out));
+    return out;
+}
+
+static int32_t nearest_int(float value) {
+#if Q38R_MUTANT == 13
+    return (int32_t)value; /* planted: truncation */
+#endif
+    const float shifted = value + 12582912.0f;
+    uint32_t bits;
+    memcpy(&bits, &shifted, sizeof(bits));
+    return (int32_t)(bits & 0x007fffff) - 0x00400000;
+}
+
+void q38r_quantize_block(const float *values, float *scale, int8_t *quants, int16_t *sums) {
+    float maximum = 0.0f;
+    float absolute_maximum = 0.0f;
+    for (int i = 0; i < Q38R_Q8K_BLOCK; ++i) {
+        const float absolute = fabsf(values[i]);
+#if Q38R_MUTANT == 14
+        if (absolute >= absolute_maximum) { /* planted: the last maximum wins */
+#else
+        if (absolute > absolute_maximum) {
+#endif
+            absolute_maximum = absolute;
+            maximum = values[i];
+        }
+    }
+    if (absolute_maximum == 0.0f) {
+        *scale = 0.0f;
+        memset(quants, 0, Q38R_Q8K_BLOCK);
+        memset(sums, 0, sizeof(int16_t) * Q38R_Q8K_BLOCK / 16);
+        return;
+    }
+    const float inverse_scale = -127.0f / maximum;
+    for (int i = 0; i < Q38R_Q8K_BLOCK; ++i) {
+        int32_t quant = nearest_int(inverse_scale * values[i]);
+        if (quant > 127) quant = 127;
+        quants[i] = (int8_t)quant;
+    }
+    for (int group = 0; group < Q38R_Q8K_BLOCK / 16; ++group) {
+        int32_t sum = 0;
+#if Q38R_MUTANT == 18
+        for (int i = 0; i < 16; ++i) sum += quants[group * 8 + i]; /* planted: wrong groups */
+#else
+        for (int i = 0; i < 16; ++i) sum += quants[group * 16 + i];
+#endif
+        sums[group] = (int16_t)sum;
+    }
+    *scale = 1.0f / inverse_scale;
+}
+
+int q38r_quantize_q8_k(const float *input, int n_tokens, int width, void *planar) {
+    if (width % Q38R_Q8K_BLOCK != 0 || n_tokens < 0) return -1;
+    const int blocks = width / Q38R_Q8K_BLOCK;
+    int8_t *quants = (int8_t *)planar;
+    int16_t *sums = (int16_t *)(quants + (size_t)n_tokens * width);
+    float *scales = (float *)(sums + (size_t)n_tokens * blocks * 16);
+    for (int t = 0; t < n_tokens; ++t)
+        for (int b = 0; b < blocks; ++b) {
+            const size_t k = (size_t)t * blocks + b;
+            q38r_quantize_block(input + (size_t)t * width + (size_t)b * Q38R_Q8K_BLOCK, &scales[k],
+                                quants + k * Q38R_Q8K_BLOCK, sums + k * 16);
+        }
+    return 0;
+}
+
+static uint16_t read_u16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* scale_min_k4, tensor.rs:23-32 */
+static void scale_min_k4(int index, const uint8_t *packed, uint8_t *scale, uint8_t *min) {
+    if (index < 4) {
+        *scale = packed[index] & 63;
+        *min = packed[index + 4] & 63;
+    } else {
+#if Q38R_MUTANT == 15
+        *scale = (packed[index + 4] & 15) | ((packed[index] >> 6) << 4); /* planted: wrong high bits */
+        *min = (packed[index + 4] >> 4) | ((packed[index - 4] >> 6) << 4);
+#else
+        *scale = (packed[index + 4] & 15) | ((packed[index - 4] >> 6) << 4);
+        *min = (packed[index + 4] >> 4) | ((packed[index] >> 6) << 4);
+#endif
+    }
+}
+
+/* One Q8_K block's view: scale, 256 quants, 16 group sums. */
+typedef struct {
+    float scale;
+    const int8_t *quants;
+    const int16_t *sums;
+} q8k_view;
+
+static float dot_q4_k(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *blk = data + (size_t)block * 144;
+        const float d = q38r_f16_to_f32(read_u16(blk)) * b->scale;
+        const float dmin = q38r_f16_to_f32(read_u16(blk + 2)) * b->scale;
+        const uint8_t *scales = blk + 4;
+        const uint8_t *quants = blk + 16;
+        int32_t weighted = 0, minimum = 0;
+        for (int chunk = 0; chunk < 4; ++chunk) {
+            uint8_t scale0, min0, scale1, min1;
+            scale_min_k4(chunk * 2, scales, &scale0, &min0);
+            scale_min_k4(chunk * 2 + 1, scales, &scale1, &min1);
+            int32_t dot0 = 0, dot1 = 0;
+            for (int i = 0; i < 32; ++i) {
+                dot0 += (int32_t)(quants[chunk * 32 + i] & 15) * b->quants[chunk * 64 + i];
+                dot1 += (int32_t)(quants[chunk * 32 + i] >> 4) * b->quants[chunk * 64 + 32 + i];
+            }
+            weighted += (int32_t)scale0 * dot0 + (int32_t)scale1 * dot1;
+            minimum += (int32_t)min0 * (int32_t)(b->sums[chunk * 4] + b->sums[chunk * 4 + 1]);
+            minimum += (int32_t)min1 * (int32_t)(b->sums[chunk * 4 + 2] + b->sums[chunk * 4 + 3]);
+        }
+        total += d * (float)weighted - dmin * (float)minimum;
+    }
+    return total;
+}
+
+static float dot_q5_k(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *blk = data + (size_t)block * 176;
+        const float d = q38r_f16_to_f32(read_u16(blk)) * b->scale;
+        const float dmin = q38r_f16_to_f32(read_u16(blk + 2)) * b->scale;
+        const uint8_t *scales = blk + 4;
+        const uint8_t *high = blk + 16;
+        const uint8_t *low = blk + 48;
+        int32_t minimum = 0, weighted = 0;
+        uint8_t high0 = 1, high1 = 2;
+        for (int chunk = 0; chunk < 4; ++chunk) {
+            uint8_t scale0, min0, scale1, min1;
+            scale_min_k4(chunk * 2, scales, &scale0, &min0);
+            scale_min_k4(chunk * 2 + 1, scales, &scale1, &min1);
+            int32_t dot0 = 0, dot1 = 0;
+            for (int i = 0; i < 32; ++i) {
+                const int32_t qv0 = (int32_t)(low[chunk * 32 + i] & 15) + ((high[i] & high0) ? 16 : 0);
+                const int32_t qv1 = (int32_t)(low[chunk * 32 + i] >> 4) + ((high[i] & high1) ? 16 : 0);
+                dot0 += qv0 * b->quants[chunk * 64 + i];
+                dot1 += qv1 * b->quants[chunk * 64 + 32 + i];
+            }
+            weighted += (int32_t)scale0 * dot0 + (int32_t)scale1 * dot1;
+            minimum += (int32_t)min0 * (int32_t)(b->sums[chunk * 4] + b->sums[chunk * 4 + 1]);
+            minimum += (int32_t)min1 * (int32_t)(b->sums[chunk * 4 + 2] + b->sums[chunk * 4 + 3]);
+#if Q38R_MUTANT != 17 /* planted: high bits not advanced per chunk */
+            high0 = (uint8_t)(high0 << 2);
+            high1 = (uint8_t)(high1 << 2);
+#endif
+        }
+        total += d * (float)weighted - dmin * (float)minimum;
+    }
+    return total;
+}
+
+static float dot_q6_k(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *blk = data + (size_t)block * 210;
+        const float d = q38r_f16_to_f32(read_u16(blk + 208)) * b->scale;
+        const uint8_t *scales = blk + 192;
+        int32_t weighted = 0;
+        for (int half = 0; half < 2; ++half) {
+            for (int i = 0; i < 32; ++i) {
+                const int si = half * 8 + i / 16;
+                const int base = half * 128;
+                const uint8_t low_i = blk[half * 64 + i];
+                const uint8_t low_i2 = blk[half * 64 + i + 32];
+                const uint8_t h = blk[128 + half * 32 + i];
+                const int32_t q0 = (int32_t)((low_i & 15) | ((h & 3) << 4)) - 32;
+                const int32_t q1 = (int32_t)((low_i2 & 15) | (((h >> 2) & 3) << 4)) - 32;
+#if Q38R_MUTANT == 16
+                const int32_t q2 = (int32_t)((low_i >> 4) | (((h >> 2) & 3) << 4)) - 32; /* planted */
+#else
+                const int32_t q2 = (int32_t)((low_i >> 4) | (((h >> 4) & 3) << 4)) - 32;
+#endif
+                const int32_t q3 = (int32_t)((low_i2 >> 4) | (((h >> 6) & 3) << 4)) - 32;
+                weighted += (int32_t)(int8_t)scales[si] * q0 * b->quants[base + i];
+                weighted += (int32_t)(int8_t)scales[si + 2] * q1 * b->quants[base + 32 + i];
+                weighted += (int32_t)(int8_t)scales[si + 4] * q2 * b->quants[base + 64 + i];
+                weighted += (int32_t)(int8_t)scales[si + 6] * q3 * b->quants[base + 96 + i];
+            }
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
+int q38r_quant_block_bytes(int ggml_type) {
+    switch (ggml_type) {
+    case Q38R_GGML_Q4_K: return 144;
+    case Q38R_GGML_Q5_K: return 176;
+    case Q38R_GGML_Q6_K: return 210;
+    default: return 0;
+    }
+}
+
+float q38r_dot_q8_k(int ggml_type, const uint8_t *row, const void *planar, int n_tokens, int width, int token) {
+    const int blocks = width / Q38R_Q8K_BLOCK;
+    const int8_t *quants = (const int8_t *)planar;
+    const int16_t *sums = (const int16_t *)(quants + (size_t)n_tokens * width);
+    const float *scales = (const float *)(sums + (size_t)n_tokens * blocks * 16);
+    q8k_view view[256];
+    if (blocks > 256) return NAN;
+    for (int b = 0; b < blocks; ++b) {
+        const size_t k = (size_t)token * blocks + b;
+        view[b].scale = scales[k];
+        view[b].quants = quants + k * Q38R_Q8K_BLOCK;
+        view[b].sums = sums + k * 16;
+    }
+    switch (ggml_type) {
+    case Q38R_GGML_Q4_K: return dot_q4_k(row, view, blocks);
+    case Q38R_GGML_Q5_K: return dot_q5_k(row, view, blocks);
+    case Q38R_GGML_Q6_K: return dot_q6_k(row, view, blocks);
+    default: return NAN;
+    }
+}
+
+typedef struct {
+    int type, rows, width, n_tokens, row0, row1;
+    const uint8_t *weights;
+    const void *planar;
+    float *out;
+} gemv_job;
+
+static void *gemv_worker(void *arg) {
+    const gemv_job *j = (const gemv_job *)arg;
+    const size_t row_bytes = (size_t)(j->width / Q38R_Q8K_BLOCK) * q38r_quant_block_bytes(j->type);
+    for (int row = j->row0; row < j->row1; ++row)
+        for (int t = 0; t < j->n_tokens; ++t)
+            j->out[(size_t)t * j->rows + row] =
+                q38r_dot_q8_k(j->type, j->weights + row * row_bytes, j->planar, j->n_tokens, j->width, t);
+    return NULL;
+}
+
+int q38r_gemv_q8_k(int ggml_type, int rows, int width, const void *weights, const void *planar, int n_tokens,
+                   float *out, int n_threads) {
+    if (q38r_quant_block_bytes(ggml_type) == 0 || width % Q38R_Q8K_BLOCK != 0 || width / Q38R_Q8K_BLOCK > 256)
+        return -1;
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > 64) n_threads = 64;
+    pthread_t th[64];
+    int created[64] = {0};
+    gemv_job jobs[64];
+    const int per = (rows + n_threads - 1) / n_threads;
+    for (int i = 0; i < n_threads; ++i) {
+        const int row0 = i * per;
+        const int row1 = (i + 1) * per < rows ? (i + 1) * per : rows;
+        if (row0 >= row1) break;
+        jobs[i] = (gemv_job){ggml_type, rows, width, n_tokens, row0, row1, (const uint8_t *)weights, planar, out};
+        if (n_threads > 1 && pthread_create(&th[i], NULL, gemv_worker, &jobs[i]) == 0)
+            created[i] = 1;
+        else
+            gemv_worker(&jobs[i]);
+    }
+    for (int i = 0; i < n_threads; ++i)
+        if (created[i]) pthread_join(th[i], NULL);
+    return 0;
+}

@@ -97,6 +97,29 @@ void q38r_linear_core(const float *conv_w, const float *dt, const float *a,
                       float *qkv, const float *z, float *beta, float *alpha,
                       float *attention, int n_threads);
 
+/* ---- weight projections: src/kernel/quant.rs, src/kernel/tensor.rs ---- */
+#define Q38R_Q8K_BLOCK 256
+#define Q38R_GGML_Q4_K 12
+#define Q38R_GGML_Q5_K 13
+#define Q38R_GGML_Q6_K 14
+
+float q38r_f16_to_f32(uint16_t value);                                   /* quant.rs:22-47 */
+/* quantize_block, quant.rs:55-95: one 256-value block. */
+void q38r_quantize_block(const float *values, float *scale, int8_t *quants, int16_t *sums);
+/* quantize_q8_k, quant.rs:97-128, for n_tokens rows of `width` floats,
+ * written planar: quants int8 [T][W] | sums int16 [T][W/256][16] |
+ * scales f32 [T][W/256].  Returns -1 when width is not a multiple of 256. */
+int q38r_quantize_q8_k(const float *input, int n_tokens, int width, void *planar);
+/* Bytes of one 256-weight block of a K-quant type (0 if unsupported). */
+int q38r_quant_block_bytes(int ggml_type);
+/* dot_q4/q5/q6_k_q8_k_scalar (tensor.rs:365-457): one weight row against
+ * token `token` of a planar Q8_K buffer of n_tokens rows. */
+float q38r_dot_q8_k(int ggml_type, const uint8_t *row, const void *planar, int n_tokens, int width, int token);
+/* tensor_gemv_q8_k / tensor_gemm_q8_k (tensor.rs:1131-1173, :1217-1270):
+ * out[t*rows + row] for every row and token; rows split over threads. */
+int q38r_gemv_q8_k(int ggml_type, int rows, int width, const void *weights, const void *planar, int n_tokens,
+                   float *out, int n_threads);
+
 /* Layer slot maps, ops.rs:38-47. */
 int q38r_is_full_attention(int layer);
 int q38r_recurrent_index(int layer);

@@ -64,6 +64,10 @@ def open_library(path: str):
                                    c_uint32, c_int, c_int]),
         "q38r_gdn_heads": (None, [_F, _F, _F, _F, _F, _F, _F, c_int]),
         "q38r_linear_core": (None, [_F, _F, _F, _F, _F, _F, _F, _F, _F, _F, _F, c_int]),
+        "q38r_f16_to_f32": (c_float, [ctypes.c_uint16]),
+        "q38r_quantize_q8_k": (c_int, [_F, c_int, c_int, ctypes.c_void_p]),
+        "q38r_quant_block_bytes": (c_int, [c_int]),
+        "q38r_gemv_q8_k": (c_int, [c_int, c_int, c_int, ctypes.c_void_p, ctypes.c_void_p, c_int, _F, c_int]),
         "q38r_is_full_attention": (c_int, [c_int]),
         "q38r_recurrent_index": (c_int, [c_int]),
         "q38r_available_cores": (c_int, []),
@@ -175,4 +179,51 @@ def linear_core(conv_w, dt, a, norm_w, conv_state, delta_state, qkv, z, beta, al
                            _f(conv_state), _f(delta_state), _f(qkv),
                            _f(np.ascontiguousarray(z, np.float32).reshape(-1)), _f(beta), _f(alpha), _f(out),
                            threads)
+    return out
+
+
+# ------------------------------------------------------- weight projections
+GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 12, 13, 14
+QUANT_BLOCK_BYTES = {GGML_Q4_K: 144, GGML_Q5_K: 176, GGML_Q6_K: 210}
+
+
+def q8k_bytes(n_tokens: int, width: int) -> int:
+    """Bytes of a planar Q8_K buffer: int8 quants, int16 group sums, f32 scales."""
+    blocks = width // 256
+    return n_tokens * blocks * (256 + 32 + 4)
+
+
+def q8k_split(planar: np.ndarray, n_tokens: int, width: int):
+    """(quants int8 [T][W], sums int16 [T][B][16], scales f32 [T][B]) views."""
+    blocks = width // 256
+    buf = np.asarray(planar, np.uint8).reshape(-1)
+    q = buf[:n_tokens * width].view(np.int8).reshape(n_tokens, width)
+    off = n_tokens * width
+    sums = buf[off:off + n_tokens * blocks * 32].view(np.int16).reshape(n_tokens, blocks, 16)
+    off += n_tokens * blocks * 32
+    scales = buf[off:off + n_tokens * blocks * 4].view(np.float32).reshape(n_tokens, blocks)
+    return q, sums, scales
+
+
+def quantize_q8_k(x: np.ndarray) -> np.ndarray:
+    """quantize_q8_k (quant.rs:97-128) of x [T][W] into a planar uint8 buffer."""
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    T, W = x.shape
+    out = np.zeros(q8k_bytes(T, W), np.uint8)
+    if lib().q38r_quantize_q8_k(_f(x), T, W, out.ctypes.data) != 0:
+        raise ValueError("width is not a multiple of 256")
+    return out
+
+
+def gemv_q8_k(ggml_type: int, weights: np.ndarray, planar: np.ndarray, n_tokens: int, width: int,
+              threads: int = 1) -> np.ndarray:
+    """tensor_gemv_q8_k / tensor_gemm_q8_k: out [T][rows] for weights [rows][row_bytes]."""
+    w = np.ascontiguousarray(weights, np.uint8)
+    rows = w.shape[0]
+    out = np.empty((n_tokens, rows), np.float32)
+    p = np.ascontiguousarray(planar, np.uint8)
+    if lib().q38r_gemv_q8_k(ggml_type, rows, width, w.ctypes.data, p.ctypes.data, n_tokens, _f(out), threads) != 0:
+        raise ValueError("unsupported type or width")
     return out

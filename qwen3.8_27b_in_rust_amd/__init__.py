@@ -82,6 +82,9 @@ _SIGNATURES = {
     "q38_full_core": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P, _P]),
     "q38_full_core_noalloc": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P, _P]),
     "q38_attn_pre": (c_int, [_P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "q38_q8k_bytes": (c_int, [c_int, c_int, POINTER(c_size_t)]),
+    "q38_quantize_q8_k": (c_int, [_P, c_int, c_int, _P, _P]),
+    "q38_gemv_q8_k": (c_int, [_P, c_int, c_int, c_int, _P, _P, c_int, _P]),
     "q38_attn_prefill": (c_int, [_P, c_int, c_int, c_int, c_int, _P, _P, _P, _P, _P]),
     "q38_gdn_step": (c_int, [_P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P]),
     "q38_gdn_prefill": (c_int, [_P, _P, c_int, _P, _P, _P, _P, _P, _P]),
@@ -276,6 +279,20 @@ class Context:
         _check(lib().q38_linear_core(self.handle, n_seq, n_tokens, ctypes.byref(w), _ptr(conv_state),
                                      _ptr(delta_state), _ptr(qkv), _ptr(z), _ptr(beta), _ptr(alpha),
                                      _ptr(out)), "q38_linear_core")
+
+    # -- weight projections
+    @staticmethod
+    def q8k_bytes(n_tokens: int, width: int) -> int:
+        n = c_size_t()
+        _check(lib().q38_q8k_bytes(n_tokens, width, ctypes.byref(n)), "q38_q8k_bytes")
+        return n.value
+
+    def quantize_q8_k(self, n_tokens, width, x, q8k):
+        _check(lib().q38_quantize_q8_k(self.handle, n_tokens, width, _ptr(x), _ptr(q8k)), "q38_quantize_q8_k")
+
+    def gemv_q8_k(self, ggml_type, rows, width, weights, q8k, n_tokens, out):
+        _check(lib().q38_gemv_q8_k(self.handle, ggml_type, rows, width, _ptr(weights), _ptr(q8k), n_tokens,
+                                   _ptr(out)), "q38_gemv_q8_k")
 
     def attn_pre(self, n_tokens, pos0, q_norm, k_norm, q_and_gate, key, q_out, gate_out, k_out):
         _check(lib().q38_attn_pre(self.handle, n_tokens, pos0, _ptr(q_norm), _ptr(k_norm), _ptr(q_and_gate),

@@ -97,6 +97,11 @@ struct q38_ctx {
     hipFunction_t f_gdn_decode = nullptr;
     hipFunction_t f_gdn_pre = nullptr;
     hipFunction_t f_gdn_step_rows = nullptr;
+    hipModule_t mod_proj = nullptr;
+    hipFunction_t f_quantize_q8k = nullptr;
+    hipFunction_t f_gemv_q4k = nullptr;
+    hipFunction_t f_gemv_q5k = nullptr;
+    hipFunction_t f_gemv_q6k = nullptr;
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
     hipFunction_t f_copy = nullptr;
@@ -315,6 +320,12 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
      * exactly Q38_DECODE_WAVES waves */
     if (ctx->decode_block != 64 * Q38_DECODE_WAVES)
         return fail("decode kernel has block size %d, expected %d", ctx->decode_block, 64 * Q38_DECODE_WAVES);
+    const std::string p_proj = dir + "/proj.hsaco";
+    Q38_HIP(hipModuleLoad(&ctx->mod_proj, p_proj.c_str()));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_quantize_q8k, ctx->mod_proj, "q38_quantize_q8k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q4k, ctx->mod_proj, "q38_gemv_q8k_q4k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q5k, ctx->mod_proj, "q38_gemv_q8k_q5k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q6k, ctx->mod_proj, "q38_gemv_q8k_q6k"));
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
@@ -337,6 +348,7 @@ int q38_ctx_destroy(q38_ctx *ctx) {
     if (ctx->mod_prefill) (void)hipModuleUnload(ctx->mod_prefill);
     if (ctx->mod_gdn_chunk) (void)hipModuleUnload(ctx->mod_gdn_chunk);
     if (ctx->mod_synth) (void)hipModuleUnload(ctx->mod_synth);
+    if (ctx->mod_proj) (void)hipModuleUnload(ctx->mod_proj);
     for (hipEvent_t e : ctx->timer_events) (void)hipEventDestroy(e);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -485,6 +497,10 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gdn_step_rows") f = ctx->f_gdn_step_rows;
     else if (name == "q38_copy_f32") f = ctx->f_copy;
     else if (name == "q38_noop") f = ctx->f_noop;
+    else if (name == "q38_quantize_q8k") f = ctx->f_quantize_q8k;
+    else if (name == "q38_gemv_q8k_q4k") f = ctx->f_gemv_q4k;
+    else if (name == "q38_gemv_q8k_q5k") f = ctx->f_gemv_q5k;
+    else if (name == "q38_gemv_q8k_q6k") f = ctx->f_gemv_q6k;
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
     else if (name == "q38_gdn_chunk_prep") f = ctx->f_chunk_prep;
@@ -1172,6 +1188,65 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
     pa.norm_w = w->d_norm;
     pa.out = d_out;
     return ctx->launch(ctx->f_gdn_post, (unsigned)toks, Q38_LIN_V_HEADS, 1, 64, &pa);
+}
+
+/* ------------------------------------------------------------ projections */
+
+int q38_q8k_bytes(int n_tokens, int width, size_t *bytes) {
+    if (bytes == nullptr) return fail("bytes is NULL");
+    if (n_tokens < 0 || width <= 0 || width % Q38_Q8K_BLOCK != 0)
+        return fail("width %d is not a positive multiple of %d (or n_tokens %d < 0)", width, Q38_Q8K_BLOCK, n_tokens);
+    *bytes = Q38_Q8K_BYTES(n_tokens, width);
+    return 0;
+}
+
+int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, void *d_q8k) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    if (n_tokens < 0) return fail("negative n_tokens");
+    if (width <= 0 || width % Q38_Q8K_BLOCK != 0)
+        return fail("input length %d is not a multiple of %d", width, Q38_Q8K_BLOCK); /* quant.rs:100-104 */
+    if (n_tokens == 0) return 0;
+    if (d_x == nullptr || d_q8k == nullptr) return fail("NULL argument");
+    if (((uintptr_t)d_x | (uintptr_t)d_q8k) % 16 != 0) return fail("d_x and d_q8k must be 16-byte aligned");
+    if (width / Q38_Q8K_BLOCK > 65535 || n_tokens > 65535) return fail("too many blocks or tokens");
+    q38_quantize_args a;
+    memset(&a, 0, sizeof(a));
+    a.x = d_x;
+    a.q8k = d_q8k;
+    a.width = width;
+    a.n_tokens = n_tokens;
+    return ctx->launch(ctx->f_quantize_q8k, width / Q38_Q8K_BLOCK, n_tokens, 1, 64, &a);
+}
+
+int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
+                  int n_tokens, float *d_out) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    hipFunction_t f = nullptr;
+    if (ggml_type == Q38_GGML_Q4_K) f = ctx->f_gemv_q4k;
+    else if (ggml_type == Q38_GGML_Q5_K) f = ctx->f_gemv_q5k;
+    else if (ggml_type == Q38_GGML_Q6_K) f = ctx->f_gemv_q6k;
+    else return fail("unsupported quant type %d (Q4_K 12, Q5_K 13, Q6_K 14)", ggml_type);
+    if (rows < 0 || n_tokens < 0) return fail("negative rows or n_tokens");
+    if (width <= 0 || width % Q38_Q8K_BLOCK != 0)
+        return fail("width %d is not a multiple of %d", width, Q38_Q8K_BLOCK);
+    if (width / Q38_Q8K_BLOCK > Q38_GEMV_MAX_BLOCKS)
+        return fail("width %d above %d", width, Q38_GEMV_MAX_BLOCKS * Q38_Q8K_BLOCK);
+    if (rows == 0 || n_tokens == 0) return 0;
+    if (d_weights == nullptr || d_q8k == nullptr || d_out == nullptr) return fail("NULL argument");
+    if ((uintptr_t)d_weights % 16 != 0 || (uintptr_t)d_q8k % 16 != 0)
+        return fail("d_weights and d_q8k must be 16-byte aligned");
+    const long wgs = ((long)rows + 3) / 4;
+    const long tok_groups = ((long)n_tokens + Q38_GEMV_TOKENS - 1) / Q38_GEMV_TOKENS;
+    if (wgs > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
+    q38_gemv_args a;
+    memset(&a, 0, sizeof(a));
+    a.weights = static_cast<const uint8_t *>(d_weights);
+    a.q8k = d_q8k;
+    a.out = d_out;
+    a.rows = rows;
+    a.width = width;
+    a.n_tokens = n_tokens;
+    return ctx->launch(f, (unsigned)wgs, (unsigned)tok_groups, 1, 256, &a);
 }
 
 }  /* extern "C" */

@@ -225,6 +225,37 @@ typedef struct {
     int32_t n_kblocks;         /* blocks of keys 0 .. base_pos + n_tokens - 1 */
 } q38_prefill_args;
 
+/* Weight projections.  Q8_K activations are planar: for T tokens of width
+ * W (B = W/256 blocks each) int8 quants [T][W] | int16 group sums [T][B][16]
+ * | f32 scales [T][B] -- Q38_Q8K_BYTES(T, W) bytes. */
+#define Q38_Q8K_BLOCK 256
+#define Q38_Q8K_BYTES(T, W) ((size_t)(T) * ((W) / Q38_Q8K_BLOCK) * (Q38_Q8K_BLOCK + 32 + 4))
+#define Q38_GGML_Q4_K 12
+#define Q38_GGML_Q5_K 13
+#define Q38_GGML_Q6_K 14
+#define Q38_GEMV_TOKENS 8 /* tokens one GEMV workgroup serves per pass over its weights */
+#define Q38_GEMV_MAX_BLOCKS 256 /* 256-wide blocks per row (width 65536) */
+
+/* quantize_q8_k: grid (B, T), 64 threads (one wave per block). */
+typedef struct {
+    const float *x; /* [T][W] */
+    void *q8k;      /* planar, Q38_Q8K_BYTES(T, W) */
+    int32_t width;
+    int32_t n_tokens;
+} q38_quantize_args;
+
+/* K-quant x Q8_K GEMV / GEMM: grid (ceil(rows / 4), ceil(T / 8)), 256
+ * threads, one row per wave. */
+typedef struct {
+    const uint8_t *weights; /* [rows][B * block_bytes], 16-byte aligned */
+    const void *q8k;        /* planar Q8_K of T tokens */
+    float *out;             /* [T][rows] */
+    int32_t rows;
+    int32_t width;
+    int32_t n_tokens;
+    int32_t pad_;
+} q38_gemv_args;
+
 /* Merge of split-K partials.  grid (n_seq, 24, 4). */
 typedef struct {
     const float *part_o;

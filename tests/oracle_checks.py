@@ -289,4 +289,157 @@ def check_layer_maps(ref, synth):
     return None if rec == list(range(48)) else "recurrent indices are not 0..47 in order"
 
 
+# ------------------------------------------------------- weight projections
+# Independent formulations of the projection path (src/kernel/quant.rs,
+# src/kernel/tensor.rs): the Q8_K quantiser restated with numpy's float32
+# arithmetic and round-half-to-even, and the K-quant weights DEQUANTISED the
+# way the reference's decoded path reads them (dot_q4/q5/q6_k_scalar,
+# tensor.rs:187-327) and multiplied out in float64 -- against the integer
+# dots (tensor.rs:365-457) the oracle restates.
+
+def _np_quantize_q8_k(x):
+    """quantize_block (quant.rs:55-95) in numpy: first maximum of |x| sets the
+    sign, float32 -127/max, round half to even, clamp at 127, 16-wide sums."""
+    blocks = np.asarray(x, np.float32).reshape(-1, 256)
+    q = np.zeros(blocks.shape, np.int8)
+    sums = np.zeros((blocks.shape[0], 16), np.int16)
+    scales = np.zeros(blocks.shape[0], np.float32)
+    for b, blk in enumerate(blocks):
+        k = int(np.argmax(np.abs(blk)))  # first occurrence
+        if np.abs(blk[k]) == 0:
+            continue
+        inv = np.float32(-127.0) / np.float32(blk[k])
+        v = np.rint((inv * blk).astype(np.float32))
+        q[b] = np.minimum(v, 127).astype(np.int8)
+        sums[b] = q[b].astype(np.int32).reshape(16, 16).sum(1).astype(np.int16)
+        scales[b] = np.float32(1.0) / inv
+    return q, sums, scales
+
+
+def _q8k_dequant(planar, T, W, ref):
+    q, _, sc = ref.q8k_split(planar, T, W)
+    return q.reshape(T, W // 256, 256).astype(np.float64) * sc.astype(np.float64)[:, :, None]
+
+
+def _f16(b0, b1):
+    return np.frombuffer(np.array([b0, b1], np.uint8).tobytes(), np.float16)[0].astype(np.float64)
+
+
+def _scale_min(s, j):
+    if j < 4:
+        return s[j] & 63, s[j + 4] & 63
+    return (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4), (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
+
+
+def _dequant_row(ty, row):
+    """A weight row's values the way the decoded path reads them."""
+    out = []
+    bb = {12: 144, 13: 176, 14: 210}[ty]
+    for blk in np.asarray(row, np.uint8).reshape(-1, bb).astype(np.int64):
+        w = np.zeros(256)
+        if ty in (12, 13):
+            d, dmin = _f16(blk[0], blk[1]), _f16(blk[2], blk[3])
+            s = blk[4:16]
+            qs = blk[16:144] if ty == 12 else blk[48:176]
+            qh = blk[16:48] if ty == 13 else None
+            for c in range(4):
+                sc0, m0 = _scale_min(s, 2 * c)
+                sc1, m1 = _scale_min(s, 2 * c + 1)
+                lo = qs[32 * c:32 * c + 32] & 15
+                hi = qs[32 * c:32 * c + 32] >> 4
+                if qh is not None:
+                    lo = lo + 16 * ((qh >> (2 * c)) & 1)
+                    hi = hi + 16 * ((qh >> (2 * c + 1)) & 1)
+                w[64 * c:64 * c + 32] = d * sc0 * lo - dmin * m0
+                w[64 * c + 32:64 * c + 64] = d * sc1 * hi - dmin * m1
+        else:
+            ql, qh, sc = blk[0:128], blk[128:192], blk[192:208].astype(np.uint8).view(np.int8).astype(np.int64)
+            d = _f16(blk[208], blk[209])
+            for h in range(2):
+                i = np.arange(32)
+                a, b2, hh = ql[64 * h + i], ql[64 * h + 32 + i], qh[32 * h + i]
+                parts = [(a & 15) | ((hh & 3) << 4), (b2 & 15) | (((hh >> 2) & 3) << 4),
+                         (a >> 4) | (((hh >> 4) & 3) << 4), (b2 >> 4) | (((hh >> 6) & 3) << 4)]
+                for k, qv in enumerate(parts):
+                    w[128 * h + 32 * k + i] = d * sc[8 * h + i // 16 + 2 * k] * (qv - 32)
+        out.append(w)
+    return np.concatenate(out)
+
+
+def _random_kquant(ty, rows, width, seed):
+    """Weight rows of random bytes with finite, moderate f16 scales."""
+    rng = np.random.default_rng(seed)
+    bb = {12: 144, 13: 176, 14: 210}[ty]
+    w = rng.integers(0, 256, (rows, width // 256, bb), dtype=np.uint8)
+    f16 = lambda lo, hi, n: np.frombuffer(rng.uniform(lo, hi, n).astype(np.float16).tobytes(), np.uint8).reshape(n, 2)
+    n = rows * (width // 256)
+    if ty in (12, 13):
+        w.reshape(n, bb)[:, 0:2] = f16(1e-3, 4e-2, n)
+        w.reshape(n, bb)[:, 2:4] = f16(1e-3, 4e-2, n)
+    else:
+        w.reshape(n, bb)[:, 208:210] = f16(1e-3, 4e-2, n)
+    return w.reshape(rows, -1)
+
+
+def check_q8k_quantize(ref, synth):
+    rng = np.random.default_rng(0x51333870)
+    x = rng.standard_normal((3, 1024)).astype(np.float32) * np.float32(3.0)
+    x[0, :256] = 0.0                                   # an all-zero block
+    x[1, 256:512] = 0.25
+    x[1, 256 + 2] = -3.0
+    x[1, 256 + 5] = 3.0                                # |max| tie: the first (negative) sets the sign
+    x[2, :256] = 0.0
+    x[2, 0] = -127.0                                   # inverse scale 1: halves round to even
+    x[2, 1:9] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5, 126.5]
+    # the reference's own activation pattern (tensor.rs:582-586)
+    x[2, 256:512] = ((np.arange(256) * 7919) % 101) / np.float32(50.0) - np.float32(1.0)
+    p = ref.quantize_q8_k(x)
+    q, sums, scales = ref.q8k_split(p, 3, 1024)
+    nq, nsums, nscales = _np_quantize_q8_k(x.reshape(-1))
+    if not np.array_equal(q.reshape(-1, 256), nq):
+        return "Q8_K quants differ from the numpy formulation"
+    if not np.array_equal(sums.reshape(-1, 16), nsums):
+        return "Q8_K group sums differ"
+    if not np.array_equal(scales.reshape(-1).view(np.uint32), nscales.view(np.uint32)):
+        return "Q8_K scales differ"
+    if not (q[1, 256 + 2] == -127 and q[1, 256 + 5] == 127 and scales[1, 1] > 0):
+        return "the first |maximum| does not set the sign"
+    if list(q[2, 1:9]) != [2, 4, -2, -4, 0, 0, 2, 126]:
+        return f"rounding is not half-to-even: {list(q[2, 1:9])}"
+    return None
+
+
+def check_kquant_dots_against_dequantised_rows(ref, synth):
+    """Integer dots of every K-quant type equal the float64 dot of the
+    dequantised weights with the dequantised activations."""
+    W, T = 1024, 3
+    rng = np.random.default_rng(0x51333871)
+    x = rng.standard_normal((T, W)).astype(np.float32)
+    x[1] = ((np.arange(W) * 7919) % 101) / np.float32(50.0) - np.float32(1.0)
+    p = ref.quantize_q8_k(x)
+    a = _q8k_dequant(p, T, W, ref).reshape(T, W)
+    for ty in (ref.GGML_Q4_K, ref.GGML_Q5_K, ref.GGML_Q6_K):
+        wb = _random_kquant(ty, 7, W, 0x51333872 + ty)
+        got = ref.gemv_q8_k(ty, wb, p, T, W)
+        for r in range(7):
+            w = _dequant_row(ty, wb[r])
+            for t in range(T):
+                want = float(np.dot(w, a[t]))
+                scale = float(np.dot(np.abs(w), np.abs(a[t])))
+                if abs(got[t, r] - want) > 2e-6 * scale:
+                    return f"type {ty} row {r} token {t}: {got[t, r]} vs {want} (scale {scale:.3e})"
+    return None
+
+
+def check_gemv_serial_equals_threaded(ref, synth):
+    W = 512
+    x = np.random.default_rng(0x51333873).standard_normal((2, W)).astype(np.float32)
+    p = ref.quantize_q8_k(x)
+    for ty in (ref.GGML_Q4_K, ref.GGML_Q6_K):
+        wb = _random_kquant(ty, 37, W, 0x51333874 + ty)
+        if not np.array_equal(ref.gemv_q8_k(ty, wb, p, 2, W, threads=1), ref.gemv_q8_k(ty, wb, p, 2, W, threads=5)):
+            return f"type {ty}: threaded GEMV differs from serial"
+    return None
+
+
 CHECKS = [v for k, v in sorted(globals().items()) if k.startswith("check_")]

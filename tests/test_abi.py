@@ -21,7 +21,7 @@ def test_binding_covers_every_declared_function(pkg):
 
 
 def test_code_objects_are_built_for_gfx950(pkg):
-    for name in ("attn_decode", "gdn", "synth"):
+    for name in ("attn_decode", "attn_prefill", "gdn", "gdn_chunk", "proj", "synth"):
         path = os.path.join(pkg.LIB_DIR, name + ".hsaco")
         assert os.path.exists(path), path
         with open(path, "rb") as f:

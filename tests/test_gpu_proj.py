@@ -1,0 +1,134 @@
+"""The weight projections on the GPU (q38_quantize_q8_k, q38_gemv_q8_k)
+against the oracle's restatement of quantize_q8_k (src/kernel/quant.rs:55-128)
+and of the scalar K-quant x Q8_K row dots (src/kernel/tensor.rs:365-457)
+driven per row as tensor_gemv_q8_k / tensor_gemm_q8_k do
+(tensor.rs:1131-1173, :1217-1270).  The integer parts and the f32 block terms
+follow the reference's operation order, so both are held bit-exact."""
+import numpy as np
+import pytest
+from oracle_checks import _random_kquant
+from parity import check_attn
+
+pytestmark = pytest.mark.gpu
+
+TYPES = {"Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+HIDDEN = 5120
+
+
+def _activations(T, W, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((T, W)) * rng.uniform(0.1, 4.0, (T, 1))).astype(np.float32)
+    if T > 1:
+        x[1] = ((np.arange(W) * 7919) % 101) / np.float32(50.0) - np.float32(1.0)  # tensor.rs:582-586
+    if W >= 512:
+        x[0, 256:512] = 0.0                      # an all-zero block
+        x[0, 600] = -9.0
+        x[0, 601] = 9.0                          # a |max| tie in block 2: the first sets the sign
+    return x
+
+
+def _quantize_on_device(ctx, x):
+    T, W = x.shape
+    d_x = ctx.array(x)
+    d_q = ctx.empty((ctx.q8k_bytes(T, W),), np.uint8)
+    ctx.quantize_q8_k(T, W, d_x, d_q)
+    return d_q
+
+
+@pytest.mark.parametrize("T,W", [(1, 256), (3, HIDDEN), (9, 17408)])
+def test_quantize_q8_k_bit_exact(ctx, ref, T, W):
+    x = _activations(T, W, 0x51333880 + W)
+    got = _quantize_on_device(ctx, x).download()
+    want = ref.quantize_q8_k(x)
+    assert got.shape == want.shape
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", sorted(TYPES))
+@pytest.mark.parametrize("rows,W,T", [(257, HIDDEN, 1), (61, 768, 3), (33, 1280, 9), (4, 256, 17)])
+def test_gemv_q8_k_bit_exact(ctx, ref, name, rows, W, T):
+    """Partial groups of 4 blocks (3 and 5 blocks), rows not a multiple of 4,
+    token counts across the 8-token passes."""
+    ty = TYPES[name]
+    x = _activations(T, W, 0x51333890 + T)
+    d_q = _quantize_on_device(ctx, x)
+    wb = _random_kquant(ty, rows, W, 0x513338A0 + ty + rows)
+    d_w = ctx.array(wb, np.uint8)
+    d_o = ctx.empty((T, rows))
+    ctx.gemv_q8_k(ty, rows, W, d_w, d_q, T, d_o)
+    got = d_o.download()
+    want = ref.gemv_q8_k(ty, wb, ref.quantize_q8_k(x), T, W, threads=16)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.max(np.abs(got - want)))
+
+
+@pytest.mark.parametrize("name", sorted(TYPES))
+def test_gemv_q8_k_model_shapes(ctx, ref, name):
+    """One token through an FFN-sized matrix (17408 rows of 5120)."""
+    ty = TYPES[name]
+    rows, W = 17408, HIDDEN
+    x = _activations(1, W, 0x513338B0)
+    d_q = _quantize_on_device(ctx, x)
+    wb = _random_kquant(ty, rows, W, 0x513338B1 + ty)
+    d_w = ctx.array(wb, np.uint8)
+    d_o = ctx.empty((1, rows))
+    ctx.gemv_q8_k(ty, rows, W, d_w, d_q, 1, d_o)
+    want = ref.gemv_q8_k(ty, wb, ref.quantize_q8_k(x), 1, W, threads=16)
+    assert np.array_equal(d_o.download().view(np.uint32), want.view(np.uint32))
+
+
+def test_projection_argument_checks(pkg, ctx):
+    x = ctx.empty((300,))
+    q = ctx.empty((4096,), np.uint8)
+    o = ctx.empty((16,))
+    with pytest.raises(pkg.Q38Error, match="multiple of 256"):
+        ctx.quantize_q8_k(1, 300, x, q)
+    with pytest.raises(pkg.Q38Error, match="unsupported quant type"):
+        ctx.gemv_q8_k(8, 4, 256, q, q, 1, o)
+    with pytest.raises(pkg.Q38Error, match="multiple of 256"):
+        ctx.gemv_q8_k(12, 4, 300, q, q, 1, o)
+    with pytest.raises(pkg.Q38Error, match="multiple of 256"):
+        pkg.Context.q8k_bytes(1, 100)
+
+
+def test_projections_feed_full_core(pkg, ctx, ref, margin, synth):
+    """The reference's full_attention (ops.rs:942-982) around full_core: the
+    layer input quantised once (quantize_input), q|gate (12288 rows, Q4_K),
+    k and v (1024 rows each, Q6_K) projected on the device and handed to
+    q38_full_core as device pointers, against the oracle running the same
+    chain."""
+    layer, ctx_len, pos = 3, 2048, 1500
+    x = _activations(1, HIDDEN, 0x513338C0)
+    wq = _random_kquant(12, 12288, HIDDEN, 0x513338C1)
+    wk = _random_kquant(14, 1024, HIDDEN, 0x513338C2)
+    wv = _random_kquant(14, 1024, HIDDEN, 0x513338C3)
+    qn = synth.normal(0x513338C4, 256, sigma=0.2, mean=1.0)
+    kn = synth.normal(0x513338C5, 256, sigma=0.2, mean=1.0)
+    K0 = synth.normal(0x513338C6, pos * 1024)
+    V0 = synth.normal(0x513338C7, pos * 1024)
+    kv = pkg.KVCache(ctx, n_slots=1, max_pages=ctx_len // 16, max_seqs=1, max_tokens_per_seq=ctx_len)
+    try:
+        seq = kv.seq_create()
+        d_k0, d_v0 = ctx.array(K0), ctx.array(V0)
+        kv.write(layer, seq, 0, pos, d_k0, d_v0)
+        d_q8 = _quantize_on_device(ctx, x)
+        d_qg, d_key, d_val = ctx.empty((1, 12288)), ctx.empty((1, 1024)), ctx.empty((1, 1024))
+        ctx.gemv_q8_k(12, 12288, HIDDEN, ctx.array(wq, np.uint8), d_q8, 1, d_qg)
+        ctx.gemv_q8_k(14, 1024, HIDDEN, ctx.array(wk, np.uint8), d_q8, 1, d_key)
+        ctx.gemv_q8_k(14, 1024, HIDDEN, ctx.array(wv, np.uint8), d_q8, 1, d_val)
+        d_o = ctx.empty((24, 256))
+        kv.full_core(layer, [seq], [pos], ctx.array(qn), ctx.array(kn), d_qg, d_key, d_val, d_o)
+        got = d_o.download()
+        # the oracle's chain
+        q8 = ref.quantize_q8_k(x)
+        qg = ref.gemv_q8_k(12, wq, q8, 1, HIDDEN, threads=16)[0]
+        key = ref.gemv_q8_k(14, wk, q8, 1, HIDDEN, threads=16)[0]
+        val = ref.gemv_q8_k(14, wv, q8, 1, HIDDEN, threads=16)[0]
+        assert np.array_equal(d_qg.download()[0], qg)
+        kc = np.zeros(ctx_len * 1024, np.float32)
+        vc = np.zeros(ctx_len * 1024, np.float32)
+        kc[:pos * 1024] = K0
+        vc[:pos * 1024] = V0
+        want, _ = ref.full_core(qn, kn, qg, key, val, kc, vc, ctx_len, pos, layer, threads=16)
+        check_attn(margin, got, want)
+    finally:
+        kv.close()

@@ -22,6 +22,12 @@ MUTANTS = {
     10: "output gate silu instead of sigmoid",
     11: "delta sign flipped",
     12: "DeltaNet readout without 1/sqrt(128)",
+    13: "Q8_K rounding by truncation",
+    14: "Q8_K scale signed by the last |maximum|",
+    15: "Q4_K/Q5_K 6-bit scales with the wrong high bits",
+    16: "Q6_K third quarter with the wrong high bits",
+    17: "Q5_K fifth bit not advanced per chunk",
+    18: "Q8_K group sums over the wrong groups",
 }
 
 
@@ -29,7 +35,8 @@ MUTANTS = {
 def test_mutant_is_rejected(mutant, ref, synth, tmp_path):
     so = tmp_path / f"libq38ref_m{mutant}.so"
     subprocess.run(["gcc", "-O2", "-mfma", "-ffp-contract=off", "-fPIC", "-shared", f"-DQ38R_MUTANT={mutant}",
-                    "-o", str(so), os.path.join(ROOT, "oracle", "q38_ref.c"), "-lm", "-lpthread"], check=True)
+                    "-o", str(so), os.path.join(ROOT, "oracle", "q38_ref.c"),
+                    os.path.join(ROOT, "oracle", "q38_quant_ref.c"), "-lm", "-lpthread"], check=True)
     prev = ref.use_library(str(so))
     try:
         failures = []
