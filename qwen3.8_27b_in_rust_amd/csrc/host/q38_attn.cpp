@@ -157,17 +157,18 @@ struct q38_ctx {
         return 0;
     }
 
-    int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned block, void *args) {
+    int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned block, void *args,
+               unsigned lds_bytes = 0) {
         void *params[] = {args};
         const bool timing = f == timed && timer_used + 2 <= (int)timer_events.size();
         if (timing) {
             /* start/stop timestamps taken by the dispatch itself */
-            Q38_HIP(hipExtModuleLaunchKernel(f, gx * block, gy, gz, block, 1, 1, 0, stream, params, nullptr,
-                                             timer_events[timer_used], timer_events[timer_used + 1], 0));
+            Q38_HIP(hipExtModuleLaunchKernel(f, gx * block, gy, gz, block, 1, 1, lds_bytes, stream, params,
+                                             nullptr, timer_events[timer_used], timer_events[timer_used + 1], 0));
             timer_used += 2;
             return 0;
         }
-        Q38_HIP(hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, 0, stream, params, nullptr));
+        Q38_HIP(hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, lds_bytes, stream, params, nullptr));
         return 0;
     }
 };
@@ -1235,9 +1236,20 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
     if (d_weights == nullptr || d_q8k == nullptr || d_out == nullptr) return fail("NULL argument");
     if ((uintptr_t)d_weights % 16 != 0 || (uintptr_t)d_q8k % 16 != 0)
         return fail("d_weights and d_q8k must be 16-byte aligned");
-    const long wgs = ((long)rows + 3) / 4;
-    const long tok_groups = ((long)n_tokens + Q38_GEMV_TOKENS - 1) / Q38_GEMV_TOKENS;
+    /* tokens per pass: as many as Q38_GEMV_ACT_LDS holds (one at least), up to 8 */
+    const int blocks = width / Q38_Q8K_BLOCK;
+    int tok_pass = std::max(1, std::min(Q38_GEMV_TOKENS, Q38_GEMV_ACT_LDS / (blocks * Q38_GEMV_REC_BYTES)));
+    tok_pass = std::min(tok_pass, n_tokens);
+    /* rows per workgroup: up to Q38_GEMV_UNITS_MAX units (four per lane), and
+     * the per-token terms in at most 16 KiB of LDS; fewer rows when that
+     * leaves under 256 workgroups (small matrices), so every CU gets work */
+    const int max_units = std::min(Q38_GEMV_UNITS_MAX, 4096 / tok_pass);
+    int per_wg = max_units / blocks;
+    if (((long)rows + per_wg - 1) / per_wg < 256) per_wg = std::max(1, std::min(per_wg, rows / 256));
+    const long wgs = ((long)rows + per_wg - 1) / per_wg;
+    const long tok_groups = ((long)n_tokens + tok_pass - 1) / tok_pass;
     if (wgs > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
+    const unsigned lds = (unsigned)(tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * per_wg * blocks * 4);
     q38_gemv_args a;
     memset(&a, 0, sizeof(a));
     a.weights = static_cast<const uint8_t *>(d_weights);
@@ -1246,7 +1258,9 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
     a.rows = rows;
     a.width = width;
     a.n_tokens = n_tokens;
-    return ctx->launch(f, (unsigned)wgs, (unsigned)tok_groups, 1, 256, &a);
+    a.rows_per_wg = per_wg;
+    a.tok_pass = tok_pass;
+    return ctx->launch(f, (unsigned)wgs, (unsigned)tok_groups, 1, 256, &a, lds);
 }
 
 }  /* extern "C" */

@@ -18,30 +18,24 @@
  * IEEE divisions; each quant is the reference's round-to-nearest-even by
  * adding 1.5 * 2^23 and reading the mantissa, clamped at 127.  Bit-exact.
  *
- * q38_gemv_q8k_*: one wave per weight row, 16 lanes per 256-weight block, so a
- * wave covers 4 blocks per step.  Each lane unpacks its share of the block's
- * 4-bit (plus fifth or fifth-and-sixth bit) weights into bytes and multiplies
- * them with the Q8_K quants on v_dot4_i32_i8; the block's integer sums meet
- * in a 16-lane reduction, exactly (integer arithmetic).  Each block's f32
- * term -- d * weighted - dmin * minimum, d and dmin the f16 scales times the
- * activation scale -- is formed with the reference's separate multiplies
- * and subtraction, and the terms are added to the row total in block order,
- * so the result equals the reference's bit for bit.  Up to 8 tokens reuse
- * the weights loaded for a step (the batched form's token loop).
+ * q38_gemv_q8k_*: one lane per 256-weight block of one row (a "unit"): the
+ * lane loads the block whole (rows are contiguous, so a wave's loads cover a
+ * contiguous stretch of the matrix), unpacks its 4-bit (plus fifth, or fifth
+ * and sixth, bit) weights into bytes and multiplies them with the token's
+ * Q8_K quants, staged in LDS, on v_dot4_i32_i8.  The block's integer sums are
+ * exact; its f32 term -- d * weighted - dmin * minimum, d and dmin the f16
+ * scales times the activation scale -- is formed with the reference's
+ * separate multiplies and subtraction, and one lane per row adds the terms
+ * in block order, so the result equals the reference's bit for bit.  Up to
+ * 8 tokens reuse the weights a lane holds (the batched form's token loop).
  */
 #include "q38_device.h"
 
 namespace {
 
-/* f16_to_f32 (quant.rs:22-47): subnormals are m * 2^-24 exactly. */
-Q38_DEV float q38_f16(uint32_t h) {
-    const uint32_t sign = (h & 0x8000u) << 16;
-    const uint32_t e = (h >> 10) & 0x1fu;
-    const uint32_t m = h & 0x3ffu;
-    if (e == 0) return __uint_as_float(__float_as_uint((float)m * 5.9604644775390625e-8f) | sign);
-    if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 13));
-    return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-}
+/* f16_to_f32 (quant.rs:22-47): the hardware conversion is exact for every
+ * half (subnormals included; f16 denormals are not flushed). */
+Q38_DEV float q38_f16(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xffffu)); }
 
 /* nearest_int (quant.rs:16-20) */
 Q38_DEV int q38_nearest_int(float v) {
@@ -50,13 +44,6 @@ Q38_DEV int q38_nearest_int(float v) {
 }
 
 Q38_DEV int q38_sdot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
-
-/* integer sum over the 16 lanes of a lane's group */
-Q38_DEV int q38_isum16(int x) {
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) x += __shfl_xor(x, m, 64);
-    return x;
-}
 
 /* Byte i (0..11) of the 12 packed scale bytes held in three words. */
 Q38_DEV int q38_sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
@@ -75,165 +62,249 @@ Q38_DEV void q38_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc
     }
 }
 
-/* A 32-bit word at a 2-byte-aligned address (Q6_K blocks are 210 bytes). */
-Q38_DEV uint32_t q38_ld_u32_a2(const uint8_t *p) {
-    const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
-    return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-}
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-struct Q8kView {
-    const int8_t *quants;  /* [T][W] */
-    const int16_t *sums;   /* [T][B][16] */
-    const float *scales;   /* [T][B] */
+/* LDS bytes of one block's 256 int8 quants, padded to 272 (68 dwords) so that
+ * 16 lanes reading consecutive blocks with 16-byte reads touch distinct
+ * banks. */
+constexpr int kRec = 272;
+
+template <int TYPE> struct KQuant;
+template <> struct KQuant<Q38_GGML_Q4_K> { static constexpr int bytes = 144, words = 36; };
+template <> struct KQuant<Q38_GGML_Q5_K> { static constexpr int bytes = 176, words = 44; };
+template <> struct KQuant<Q38_GGML_Q6_K> { static constexpr int bytes = 210, words = 52; };
+
+/* One 256-weight block of one row (a "unit"), held by one lane. */
+template <int TYPE> struct Unit {
+    uint32_t w[KQuant<TYPE>::words];
+    uint32_t dh; /* Q6_K: the f16 scale (bytes 208-209) */
 };
 
-Q38_DEV Q8kView q8k_view(const void *q8k, int n_tokens, int width) {
-    const int blocks = width / Q38_Q8K_BLOCK;
-    Q8kView v;
-    v.quants = static_cast<const int8_t *>(q8k);
-    v.sums = reinterpret_cast<const int16_t *>(v.quants + (size_t)n_tokens * width);
-    v.scales = reinterpret_cast<const float *>(v.sums + (size_t)n_tokens * blocks * 16);
-    return v;
-}
-
-/* The weights of one block that one lane needs, loaded once per step. */
-struct WLane {
-    uint32_t h0, s0, s1, s2; /* Q4_K/Q5_K header: d | dmin << 16, 12 scale bytes; Q6_K: d in h0 */
-    uint32_t q[2];           /* Q4_K/Q5_K: 8 bytes of 4-bit pairs; Q6_K: low quants of i0.. and i0+32.. */
-    uint32_t x[2];           /* Q5_K: 8 bytes of fifth bits; Q6_K: x[0] high-bit byte quad */
-    int sc6[4];              /* Q6_K: the lane's 4 signed scales */
-};
-
+/* Unit g of the matrix (row-major: g = row * B + block).  Q4_K and Q5_K
+ * blocks are multiples of 16 bytes and start 16-byte aligned.  Q6_K blocks
+ * are 210 bytes and start 2-byte aligned: the 208 bytes before the scale are
+ * read as 52 dwords from the dword boundary at or below the start (16-byte
+ * reads need dword alignment only) plus the halfword at 206, and shifted into
+ * place; the scale is its own halfword.  Every byte read lies in the block. */
 template <int TYPE>
-Q38_DEV WLane load_weights(const uint8_t *blk, int t) {
-    WLane w{};
+Q38_DEV void load_unit(const uint8_t *weights, size_t g, Unit<TYPE> &u) {
     if (TYPE == Q38_GGML_Q6_K) {
-        const int h = t >> 3, i0 = 4 * (t & 7);
-        w.q[0] = q38_ld_u32_a2(blk + 64 * h + i0);
-        w.q[1] = q38_ld_u32_a2(blk + 64 * h + 32 + i0);
-        w.x[0] = q38_ld_u32_a2(blk + 128 + 32 * h + i0);
-        const int si = 8 * h + (t & 7) / 4;
+        const size_t s = g * 210;
+        const uint32_t o = (uint32_t)(s & 3); /* 0 or 2 */
+        const uint32_t *base = reinterpret_cast<const uint32_t *>(weights + (s - o));
+        uint32_t win[53];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) w.sc6[k] = (int)(int8_t)blk[192 + si + 2 * k];
-        w.h0 = *reinterpret_cast<const uint16_t *>(blk + 208);
-    } else {
-        const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
-        w.h0 = hdr.x;
-        w.s0 = hdr.y;
-        w.s1 = hdr.z;
-        w.s2 = hdr.w;
-        const int c = t >> 2, sub = t & 3;
-        const int qs_off = (TYPE == Q38_GGML_Q4_K ? 16 : 48) + 32 * c + 8 * sub;
-        const uint2 qs = *reinterpret_cast<const uint2 *>(blk + qs_off);
-        w.q[0] = qs.x;
-        w.q[1] = qs.y;
-        if (TYPE == Q38_GGML_Q5_K) {
-            const uint2 qh = *reinterpret_cast<const uint2 *>(blk + 16 + 8 * sub);
-            w.x[0] = qh.x;
-            w.x[1] = qh.y;
+        for (int i = 0; i < 13; ++i) {
+            u32x4 v;
+            __builtin_memcpy(&v, base + 4 * i, 16);
+            win[4 * i] = v.x;
+            win[4 * i + 1] = v.y;
+            win[4 * i + 2] = v.z;
+            win[4 * i + 3] = v.w;
         }
+        win[52] = *reinterpret_cast<const uint16_t *>(weights + s + 206);
+        u.dh = *reinterpret_cast<const uint16_t *>(weights + s + 208);
+#pragma unroll
+        for (int j = 0; j < 52; ++j) u.w[j] = __builtin_amdgcn_alignbyte(win[j + 1], win[j], o);
+    } else {
+        const uint4 *p = reinterpret_cast<const uint4 *>(weights + g * KQuant<TYPE>::bytes);
+#pragma unroll
+        for (int i = 0; i < KQuant<TYPE>::words / 4; ++i) {
+            const uint4 v = p[i];
+            u.w[4 * i] = v.x;
+            u.w[4 * i + 1] = v.y;
+            u.w[4 * i + 2] = v.z;
+            u.w[4 * i + 3] = v.w;
+        }
+        u.dh = 0;
     }
-    return w;
 }
 
-/* The f32 term of one block against one token (lane 0 of the block's 16
- * lanes holds it): dot_q4/q5/q6_k_q8_k's per-block update. */
+/* Per-unit constants: the 8 (Q4_K/Q5_K: scale, min) pairs or the 16 signed
+ * Q6_K scales, and the f16 scales as f32. */
+template <int TYPE> struct UnitScales {
+    int sc[16];
+    int mn[8];
+    float d, dmin;
+};
+
 template <int TYPE>
-Q38_DEV float block_term(const WLane &w, const Q8kView &qv, int width, int blocks, int tok, int blk, int t) {
-    const int8_t *qa = qv.quants + (size_t)tok * width + (size_t)blk * Q38_Q8K_BLOCK;
-    const float a_scale = qv.scales[(size_t)tok * blocks + blk];
+Q38_DEV void unit_scales(const Unit<TYPE> &u, UnitScales<TYPE> &s) {
     if (TYPE == Q38_GGML_Q6_K) {
-        const int h = t >> 3, i0 = 4 * (t & 7);
-        const uint32_t lo = w.q[0], lo2 = w.q[1], hb = w.x[0];
-        const uint32_t q[4] = {(lo & 0x0F0F0F0Fu) | ((hb & 0x03030303u) << 4),
-                               (lo2 & 0x0F0F0F0Fu) | (((hb >> 2) & 0x03030303u) << 4),
-                               ((lo >> 4) & 0x0F0F0F0Fu) | (((hb >> 4) & 0x03030303u) << 4),
-                               ((lo2 >> 4) & 0x0F0F0F0Fu) | (((hb >> 6) & 0x03030303u) << 4)};
-        int weighted = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t a4 = *reinterpret_cast<const uint32_t *>(qa + 128 * h + 32 * k + i0);
-            /* sum of (q - 32) * a over the 4 bytes */
-            const int dot = q38_sdot4(q[k], a4, 0) - 32 * q38_sdot4(0x01010101u, a4, 0);
-            weighted += w.sc6[k] * dot;
-        }
-        weighted = q38_isum16(weighted);
-        const float d = q38_f16(w.h0) * a_scale;
-        return d * (float)weighted;
+        for (int g = 0; g < 16; ++g) s.sc[g] = (int)(int8_t)((u.w[48 + g / 4] >> (8 * (g & 3))) & 255u);
+        s.d = q38_f16(u.dh);
+        s.dmin = 0.0f;
     } else {
-        const int c = t >> 2, sub = t & 3;
-        const uint2 alo = *reinterpret_cast<const uint2 *>(qa + 64 * c + 8 * sub);
-        const uint2 ahi = *reinterpret_cast<const uint2 *>(qa + 64 * c + 32 + 8 * sub);
-        uint32_t wl[2], wh[2];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            wl[k] = w.q[k] & 0x0F0F0F0Fu;
-            wh[k] = (w.q[k] >> 4) & 0x0F0F0F0Fu;
-            if (TYPE == Q38_GGML_Q5_K) {
-                wl[k] |= ((w.x[k] >> (2 * c)) & 0x01010101u) << 4;
-                wh[k] |= ((w.x[k] >> (2 * c + 1)) & 0x01010101u) << 4;
+        for (int j = 0; j < 8; ++j) q38_scale_min(u.w[1], u.w[2], u.w[3], j, s.sc[j], s.mn[j]);
+        s.d = q38_f16(u.w[0]);
+        s.dmin = q38_f16(u.w[0] >> 16);
+    }
+}
+
+/* The f32 term of one unit against one token's activation block `rec`:
+ * dot_q4_k_q8_k / dot_q5_k_q8_k / dot_q6_k_q8_k's per-block update
+ * (tensor.rs:365-457).  The integer sums are exact in any order; the f32
+ * part is the reference's: d = f16(d) * a.d, then d * weighted - dmin *
+ * minimum (Q6_K: d * weighted). */
+template <int TYPE>
+Q38_DEV float unit_term(const Unit<TYPE> &u, const UnitScales<TYPE> &s, const uint8_t *rec, const int16_t *gsums,
+                        float a_scale) {
+    const u32x4 *aq = reinterpret_cast<const u32x4 *>(rec);
+    const u32x4 bs4[2] = {reinterpret_cast<const u32x4 *>(gsums)[0], reinterpret_cast<const u32x4 *>(gsums)[1]};
+    int bsum[16];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t v = bs4[k / 4][k & 3];
+        bsum[2 * k] = (int)(int16_t)(v & 0xffffu);
+        bsum[2 * k + 1] = (int)(int16_t)(v >> 16);
+    }
+    if (TYPE == Q38_GGML_Q6_K) {
+        int dg[16];
+#pragma unroll
+        for (int g = 0; g < 16; ++g) dg[g] = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i4 = 0; i4 < 8; i4 += 4) {
+                /* activation dwords of values 128h + 32k + 4i4 .. +15, k = 0..3 */
+                u32x4 av[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) av[k] = aq[(128 * h + 32 * k + 4 * i4) / 16];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t lo = u.w[16 * h + i4 + c], hi = u.w[16 * h + 8 + i4 + c];
+                    const uint32_t qh = u.w[32 + 8 * h + i4 + c];
+                    const uint32_t q0 = (lo & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
+                    const uint32_t q1 = (hi & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+                    const uint32_t q2 = ((lo >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+                    const uint32_t q3 = ((hi >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+                    const int g = 8 * h + i4 / 4;
+                    dg[g] = q38_sdot4(q0, av[0][c], dg[g]);
+                    dg[g + 2] = q38_sdot4(q1, av[1][c], dg[g + 2]);
+                    dg[g + 4] = q38_sdot4(q2, av[2][c], dg[g + 4]);
+                    dg[g + 6] = q38_sdot4(q3, av[3][c], dg[g + 6]);
+                }
             }
         }
-        const int dot0 = q38_sdot4(wl[1], alo.y, q38_sdot4(wl[0], alo.x, 0));
-        const int dot1 = q38_sdot4(wh[1], ahi.y, q38_sdot4(wh[0], ahi.x, 0));
-        int sc0, m0, sc1, m1;
-        q38_scale_min(w.s0, w.s1, w.s2, 2 * c, sc0, m0);
-        q38_scale_min(w.s0, w.s1, w.s2, 2 * c + 1, sc1, m1);
-        int weighted = sc0 * dot0 + sc1 * dot1;
-        int minimum = 0;
-        if (sub == 0) {
-            const int16_t *bs = qv.sums + ((size_t)tok * blocks + blk) * 16 + 4 * c;
-            const uint2 b4 = *reinterpret_cast<const uint2 *>(bs);
-            const int b0 = (int)(int16_t)(b4.x & 0xffffu), b1 = (int)(int16_t)(b4.x >> 16);
-            const int b2 = (int)(int16_t)(b4.y & 0xffffu), b3 = (int)(int16_t)(b4.y >> 16);
-            minimum = m0 * (b0 + b1) + m1 * (b2 + b3);
+        int weighted = 0;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) weighted += s.sc[g] * (dg[g] - 32 * bsum[g]);
+        const float d = s.d * a_scale;
+        return d * (float)weighted;
+    } else {
+        int weighted = 0, minimum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int dot0 = 0, dot1 = 0;
+#pragma unroll
+            for (int i4 = 0; i4 < 8; i4 += 4) {
+                const u32x4 alo = aq[(64 * j + 4 * i4) / 16];
+                const u32x4 ahi = aq[(64 * j + 32 + 4 * i4) / 16];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int i = i4 + c;
+                    uint32_t ql, qh;
+                    if (TYPE == Q38_GGML_Q4_K) {
+                        const uint32_t q = u.w[4 + 8 * j + i];
+                        ql = q & 0x0F0F0F0Fu;
+                        qh = (q >> 4) & 0x0F0F0F0Fu;
+                    } else {
+                        const uint32_t q = u.w[12 + 8 * j + i], hb = u.w[4 + i];
+                        ql = (q & 0x0F0F0F0Fu) | (((hb >> (2 * j)) & 0x01010101u) << 4);
+                        qh = ((q >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * j + 1)) & 0x01010101u) << 4);
+                    }
+                    dot0 = q38_sdot4(ql, alo[c], dot0);
+                    dot1 = q38_sdot4(qh, ahi[c], dot1);
+                }
+            }
+            weighted += s.sc[2 * j] * dot0 + s.sc[2 * j + 1] * dot1;
+            minimum += s.mn[2 * j] * (bsum[4 * j] + bsum[4 * j + 1]) + s.mn[2 * j + 1] * (bsum[4 * j + 2] + bsum[4 * j + 3]);
         }
-        weighted = q38_isum16(weighted);
-        minimum = q38_isum16(minimum);
-        const float d = q38_f16(w.h0 & 0xffffu) * a_scale;
-        const float dmin = q38_f16(w.h0 >> 16) * a_scale;
+        const float d = s.d * a_scale;
+        const float dmin = s.dmin * a_scale;
         return d * (float)weighted - dmin * (float)minimum;
     }
 }
 
+/*
+ * A workgroup owns rows [row0, row0 + R) and the tokens [tok0, tok0 + tp);
+ * its R * B units (at most Q38_GEMV_UNITS_MAX) are taken by the 256 lanes in
+ * steps of 256:
+ *   1. each lane issues the loads of its first unit, then the workgroup
+ *      copies the tp tokens' Q8_K blocks into LDS (quants [t][b] in
+ *      kRec-byte records, group sums [t][b][16], scales [t][b]);
+ *   2. at each step a lane issues the loads of its next unit before it
+ *      computes the current one (past the workgroup's last unit it loads
+ *      that unit again, a cache hit, so the wait counts are static), and
+ *      writes the unit's f32 term per token into LDS;
+ *   3. one lane per (row, token) adds the row's B terms in block order, the
+ *      reference's `total += ...` sequence, and stores the result.
+ * The host sizes R and tp (LDS: tp * B * Q38_GEMV_REC_BYTES + tp * R * B * 4).
+ */
 template <int TYPE>
 Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
-    constexpr int kBlockBytes = TYPE == Q38_GGML_Q4_K ? 144 : (TYPE == Q38_GGML_Q5_K ? 176 : 210);
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + wave;
-    if (row >= a.rows) return; /* the whole wave; the kernel has no barrier */
-    const int tok0 = blockIdx.y * Q38_GEMV_TOKENS;
-    const int ntok = min(Q38_GEMV_TOKENS, a.n_tokens - tok0);
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x;
     const int width = a.width;
-    const int blocks = width / Q38_Q8K_BLOCK;
-    const int grp = lane >> 4;
-    const int t = lane & 15;
-    const Q8kView qv = q8k_view(a.q8k, a.n_tokens, width);
-    const uint8_t *wrow = a.weights + (size_t)row * blocks * kBlockBytes;
-    float total[Q38_GEMV_TOKENS];
-#pragma unroll
-    for (int k = 0; k < Q38_GEMV_TOKENS; ++k) total[k] = 0.0f;
+    const int B = width / Q38_Q8K_BLOCK;
+    const int R = a.rows_per_wg;
+    const int row0 = blockIdx.x * R;
+    const int rows_here = min(R, a.rows - row0);
+    const int units = rows_here * B;
+    const int steps = (units + 255) >> 8;
+    const int tok0 = blockIdx.y * a.tok_pass;
+    const int tp = min(a.tok_pass, a.n_tokens - tok0);
+    const int nrec = a.tok_pass * B;
+    uint8_t *recs = lds;                                                     /* [tp][B] x kRec */
+    int16_t *lsums = reinterpret_cast<int16_t *>(lds + (size_t)nrec * kRec); /* [tp][B][16] */
+    float *lscales = reinterpret_cast<float *>(lsums + (size_t)nrec * 16);   /* [tp][B] */
+    float *terms = lscales + nrec;                                           /* [tp][units] */
+    const size_t g0 = (size_t)row0 * B;
 
-    for (int b0 = 0; b0 < blocks; b0 += 4) {
-        const int blk = b0 + grp;
-        const int blkc = blk < blocks ? blk : b0; /* a block that exists; its term is not added */
-        const WLane w = load_weights<TYPE>(wrow + (size_t)blkc * kBlockBytes, t);
-        const int n_here = min(4, blocks - b0);
+    Unit<TYPE> w[2];
+    load_unit<TYPE>(a.weights, g0 + min(tid, units - 1), w[0]);
+
+    /* the tokens' blocks are contiguous from token tok0 in each of the three
+     * planes: quants [T][W], sums [T][B][16], scales [T][B] */
+    const int8_t *quants = static_cast<const int8_t *>(a.q8k) + (size_t)tok0 * width;
+    const int16_t *sums = reinterpret_cast<const int16_t *>(quants - (size_t)tok0 * width + (size_t)a.n_tokens * width);
+    const float *scales = reinterpret_cast<const float *>(sums + (size_t)a.n_tokens * B * 16) + (size_t)tok0 * B;
+    sums += (size_t)tok0 * B * 16;
+    const int nblk = tp * B;
+    for (int p = tid; p < nblk * 16; p += 256)
+        *reinterpret_cast<u32x4 *>(recs + (p >> 4) * kRec + (p & 15) * 16) =
+            *reinterpret_cast<const u32x4 *>(quants + (size_t)p * 16);
+    for (int p = tid; p < nblk * 2; p += 256)
+        *reinterpret_cast<u32x4 *>(lsums + p * 8) = *reinterpret_cast<const u32x4 *>(sums + (size_t)p * 8);
+    for (int p = tid; p < nblk; p += 256) lscales[p] = scales[p];
+    __syncthreads();
+
 #pragma unroll
-        for (int k = 0; k < Q38_GEMV_TOKENS; ++k) {
-            if (k >= ntok) break;
-            const float term = block_term<TYPE>(w, qv, width, blocks, tok0 + k, blkc, t);
-            /* the row total in block order: blocks b0, b0+1, ... */
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                if (g < n_here)
-                    total[k] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term), 16 * g));
+    for (int k = 0; k < Q38_GEMV_UNITS_MAX / 256; ++k) {
+        if (k >= steps) break;
+        const int u = tid + 256 * k;
+        load_unit<TYPE>(a.weights, g0 + min(u + 256, units - 1), w[(k + 1) & 1]);
+        if (u < units) {
+            UnitScales<TYPE> s;
+            unit_scales<TYPE>(w[k & 1], s);
+            const int b = u % B;
+            for (int t = 0; t < tp; ++t) {
+                const int r = t * B + b;
+                terms[t * units + u] = unit_term<TYPE>(w[k & 1], s, recs + r * kRec, lsums + r * 16, lscales[r]);
+            }
         }
     }
-#pragma unroll
-    for (int k = 0; k < Q38_GEMV_TOKENS; ++k)
-        if (k < ntok && lane == k) a.out[(size_t)(tok0 + k) * a.rows + row] = total[k];
+    __syncthreads();
+
+    for (int i = tid; i < tp * rows_here; i += 256) {
+        const int t = i / rows_here, r = i - t * rows_here;
+        const float *tr = terms + t * units + r * B;
+        float total = 0.0f;
+        for (int b = 0; b < B; ++b) total += tr[b];
+        a.out[(size_t)(tok0 + t) * a.rows + row0 + r] = total;
+    }
 }
 
 }  // namespace

@@ -233,8 +233,11 @@ typedef struct {
 #define Q38_GGML_Q4_K 12
 #define Q38_GGML_Q5_K 13
 #define Q38_GGML_Q6_K 14
-#define Q38_GEMV_TOKENS 8 /* tokens one GEMV workgroup serves per pass over its weights */
-#define Q38_GEMV_MAX_BLOCKS 256 /* 256-wide blocks per row (width 65536) */
+#define Q38_GEMV_TOKENS 8 /* most tokens one GEMV workgroup serves per pass over its weights */
+#define Q38_GEMV_MAX_BLOCKS 192 /* 256-wide blocks per row (width 49152): one token's blocks fit LDS */
+#define Q38_GEMV_UNITS_MAX 1024 /* (row, block) units per GEMV workgroup: four steps of 256 */
+#define Q38_GEMV_REC_BYTES (272 + 32 + 4) /* LDS bytes of one staged Q8_K block: padded quants, sums, scale */
+#define Q38_GEMV_ACT_LDS (48 * 1024) /* LDS for staged activations when tokens > 1 */
 
 /* quantize_q8_k: grid (B, T), 64 threads (one wave per block). */
 typedef struct {
@@ -244,8 +247,10 @@ typedef struct {
     int32_t n_tokens;
 } q38_quantize_args;
 
-/* K-quant x Q8_K GEMV / GEMM: grid (ceil(rows / 4), ceil(T / 8)), 256
- * threads, one row per wave. */
+/* K-quant x Q8_K GEMV / GEMM: grid (ceil(rows / rows_per_wg),
+ * ceil(T / tok_pass)), 256 threads, one lane per (row, block) unit,
+ * rows_per_wg * B <= Q38_GEMV_UNITS_MAX; dynamic LDS tok_pass * B *
+ * Q38_GEMV_REC_BYTES + tok_pass * rows_per_wg * B * 4 bytes. */
 typedef struct {
     const uint8_t *weights; /* [rows][B * block_bytes], 16-byte aligned */
     const void *q8k;        /* planar Q8_K of T tokens */
@@ -253,6 +258,8 @@ typedef struct {
     int32_t rows;
     int32_t width;
     int32_t n_tokens;
+    int32_t rows_per_wg;
+    int32_t tok_pass;
     int32_t pad_;
 } q38_gemv_args;
 

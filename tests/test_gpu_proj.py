@@ -45,10 +45,12 @@ def test_quantize_q8_k_bit_exact(ctx, ref, T, W):
 
 
 @pytest.mark.parametrize("name", sorted(TYPES))
-@pytest.mark.parametrize("rows,W,T", [(257, HIDDEN, 1), (61, 768, 3), (33, 1280, 9), (4, 256, 17)])
+@pytest.mark.parametrize("rows,W,T", [(257, HIDDEN, 1), (61, 768, 3), (33, 1280, 9), (4, 256, 17),
+                                      (1100, 17408, 4), (700, 2304, 1)])
 def test_gemv_q8_k_bit_exact(ctx, ref, name, rows, W, T):
-    """Partial groups of 4 blocks (3 and 5 blocks), rows not a multiple of 4,
-    token counts across the 8-token passes."""
+    """Row counts that leave a partial last workgroup, several token passes
+    (9 and 17 tokens), a width whose token passes hold 2 tokens (17408), and
+    matrices small enough to get one row per workgroup."""
     ty = TYPES[name]
     x = _activations(T, W, 0x51333890 + T)
     d_q = _quantize_on_device(ctx, x)
@@ -59,6 +61,29 @@ def test_gemv_q8_k_bit_exact(ctx, ref, name, rows, W, T):
     got = d_o.download()
     want = ref.gemv_q8_k(ty, wb, ref.quantize_q8_k(x), T, W, threads=16)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.max(np.abs(got - want)))
+
+
+@pytest.mark.parametrize("name", sorted(TYPES))
+def test_gemv_q8_k_subnormal_scales_and_widest_rows(ctx, ref, name):
+    """f16 block scales that are subnormal (m * 2^-24) or zero, and the widest
+    accepted row (49152 weights, 192 blocks: one token per pass)."""
+    ty = TYPES[name]
+    for rows, W, T in ((45, 1024, 2), (5, 49152, 2)):
+        x = _activations(T, W, 0x513338A8 + W)
+        d_q = _quantize_on_device(ctx, x)
+        wb = _random_kquant(ty, rows, W, 0x513338A9 + ty)
+        blocks = wb.reshape(rows * (W // 256), -1)
+        off = 208 if ty == 14 else 0
+        sub = np.array([0x0001, 0x03ff, 0x8200, 0x0000, 0x8000], np.uint16)
+        for i in range(0, blocks.shape[0], 3):
+            blocks[i, off:off + 2] = np.frombuffer(sub[i % 5].tobytes(), np.uint8)
+        if ty != 14:
+            blocks[1::4, 2:4] = np.frombuffer(np.uint16(0x0155).tobytes(), np.uint8)
+        d_w = ctx.array(wb, np.uint8)
+        d_o = ctx.empty((T, rows))
+        ctx.gemv_q8_k(ty, rows, W, d_w, d_q, T, d_o)
+        want = ref.gemv_q8_k(ty, wb, ref.quantize_q8_k(x), T, W, threads=16)
+        assert np.array_equal(d_o.download().view(np.uint32), want.view(np.uint32)), (rows, W, T)
 
 
 @pytest.mark.parametrize("name", sorted(TYPES))
@@ -86,6 +111,8 @@ def test_projection_argument_checks(pkg, ctx):
         ctx.gemv_q8_k(8, 4, 256, q, q, 1, o)
     with pytest.raises(pkg.Q38Error, match="multiple of 256"):
         ctx.gemv_q8_k(12, 4, 300, q, q, 1, o)
+    with pytest.raises(pkg.Q38Error, match="above 49152"):
+        ctx.gemv_q8_k(12, 4, 49408, q, q, 1, o)
     with pytest.raises(pkg.Q38Error, match="multiple of 256"):
         pkg.Context.q8k_bytes(1, 100)
 
