@@ -20,8 +20,9 @@ reference's) on the same data.
 Also measured under "extra" (all, or those --only names): prefill attention
 and chunked DeltaNet prefill of a 4096-token prompt, batched paged decode,
 the launch floor, one-token linear_core over 48 layers, the 64-layer full
-stack at 128K, and the bare DeltaNet step for one and for 32 states per
-launch, each rotating over enough states to defeat the cache.
+stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
+the Q4_K/Q6_K FFN projections for 1 and 8 tokens, and the recurrent-state
+checkpoint, each rotating over enough buffers to defeat the cache.
 """
 from __future__ import annotations
 
@@ -501,6 +502,28 @@ def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
     return res
 
 
+def recurrent_checkpoint(pkg, ctx, reps: int):
+    """checkpoint_state's device form: conv_state (5.9 MB) and delta_state
+    (151 MB) of a sequence copied to the checkpoint; each copy reads and
+    writes its bytes once."""
+    n_conv, n_delta = 48 * 30720, 48 * 786432
+    bufs = [ctx.empty((n,)) for n in (n_conv, n_delta, n_conv, n_delta)]
+    pkg.recurrent_checkpoint(ctx, bufs[0], bufs[1], n_conv, n_delta, bufs[2], bufs[3])
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(reps):
+        pkg.recurrent_checkpoint(ctx, bufs[0], bufs[1], n_conv, n_delta, bufs[2], bufs[3])
+    ctx.record(e1)
+    us = ctx.elapsed_ms(e0, e1) * 1e3 / reps
+    for b in bufs:
+        b.free()
+    for e in (e0, e1):
+        ctx.destroy_event(e)
+    moved = 2 * 4 * (n_conv + n_delta)
+    return {"us": us, "bytes_read_and_written": moved, "gb_s": moved / (us * 1e-6) / 1e9}
+
+
 def cpu_baseline(ref, q, k_rows, v_rows, gate, budget_s: float, threads: int = 0):
     """The CPU restatement of the reference's attention (ops.rs:868-938) on the
     32K workload, all cores of this host (heads split across threads as the
@@ -555,6 +578,8 @@ EXTRAS = {
                     lambda pkg, ctx: gdn_steps(pkg, ctx, 32, 192, 60, 6)),
     "gdn_step_1_same_state": ("Gated-DeltaNet step, one state stepped in place (labelled same-buffer figure)",
                               lambda pkg, ctx: gdn_steps(pkg, ctx, 1, 1, 384, 32)),
+    "recurrent_checkpoint": ("recurrent-state checkpoint of one sequence (157 MB)",
+                             lambda pkg, ctx: recurrent_checkpoint(pkg, ctx, 20)),
     "ffn_projections_1": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 1 token",
                           lambda pkg, ctx: ffn_projections(pkg, ctx, 1, 20)),
     "ffn_projections_8": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 8 tokens",

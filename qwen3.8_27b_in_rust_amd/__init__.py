@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_void_p
 
 import numpy as np
 
@@ -89,6 +89,17 @@ _SIGNATURES = {
     "q38_gdn_step": (c_int, [_P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P]),
     "q38_gdn_prefill": (c_int, [_P, _P, c_int, _P, _P, _P, _P, _P, _P]),
     "q38_linear_core": (c_int, [_P, c_int, c_int, POINTER(_LinearWeights), _P, _P, _P, _P, _P, _P, _P]),
+    "q38_gguf_open": (c_int, [c_char_p, POINTER(c_void_p)]),
+    "q38_gguf_close": (c_int, [_P]),
+    "q38_gguf_info": (c_int, [_P, POINTER(c_uint32), POINTER(c_uint32), POINTER(ctypes.c_uint64), POINTER(c_int),
+                              POINTER(c_int)]),
+    "q38_gguf_find_tensor": (c_int, [_P, c_char_p, POINTER(c_int)]),
+    "q38_gguf_tensor": (c_int, [_P, c_int, POINTER(c_char_p), POINTER(c_int), POINTER(c_int),
+                                POINTER(ctypes.c_uint64), POINTER(ctypes.c_uint64), POINTER(ctypes.c_uint64)]),
+    "q38_gguf_meta_u32": (c_int, [_P, c_char_p, POINTER(c_uint32)]),
+    "q38_gguf_upload": (c_int, [_P, _P, POINTER(c_void_p), POINTER(c_size_t)]),
+    "q38_recurrent_checkpoint": (c_int, [_P, _P, _P, c_size_t, c_size_t, _P, _P]),
+    "q38_recurrent_restore": (c_int, [_P, _P, _P, c_size_t, c_size_t, _P, _P]),
 }
 
 _lib = None
@@ -380,6 +391,73 @@ class KVCache:
     def attn_prefill(self, layer, seq, base_pos, n_tokens, q, k, v, out, gate=None):
         _check(lib().q38_attn_prefill(self.handle, layer, seq, base_pos, n_tokens, _ptr(q), _ptr(k), _ptr(v),
                                       _ptr(gate), _ptr(out)), "q38_attn_prefill")
+
+
+class Gguf:
+    """A parsed GGUF file (q38_gguf_open); host-only until upload()."""
+
+    MAX_DIMS = 8
+
+    def __init__(self, path: str):
+        h = c_void_p()
+        _check(lib().q38_gguf_open(os.fsencode(path), ctypes.byref(h)), "q38_gguf_open")
+        self.handle = h.value
+
+    def close(self) -> None:
+        if self.handle:
+            lib().q38_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def info(self) -> dict:
+        v, al, off = c_uint32(), c_uint32(), ctypes.c_uint64()
+        nt, nm = c_int(), c_int()
+        _check(lib().q38_gguf_info(self.handle, ctypes.byref(v), ctypes.byref(al), ctypes.byref(off),
+                                   ctypes.byref(nt), ctypes.byref(nm)), "q38_gguf_info")
+        return {"version": v.value, "alignment": al.value, "data_offset": off.value, "n_tensors": nt.value,
+                "n_metadata": nm.value}
+
+    def find_tensor(self, name: str) -> int:
+        i = c_int()
+        _check(lib().q38_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(i)), "q38_gguf_find_tensor")
+        return i.value
+
+    def tensor(self, index: int) -> dict:
+        name = c_char_p()
+        ty, nd = c_int(), c_int()
+        shape = (ctypes.c_uint64 * self.MAX_DIMS)()
+        off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib().q38_gguf_tensor(self.handle, index, ctypes.byref(name), ctypes.byref(ty), ctypes.byref(nd),
+                                     shape, ctypes.byref(off), ctypes.byref(nb)), "q38_gguf_tensor")
+        return {"name": name.value.decode(), "type": ty.value, "shape": list(shape[:nd.value]),
+                "offset": off.value, "nbytes": nb.value}
+
+    def meta_u32(self, key: str) -> int:
+        v = c_uint32()
+        _check(lib().q38_gguf_meta_u32(self.handle, key.encode(), ctypes.byref(v)), "q38_gguf_meta_u32")
+        return v.value
+
+    def upload(self, ctx: "Context") -> tuple[int, int]:
+        """(device base pointer, bytes); free with ctx's q38_free."""
+        p, n = c_void_p(), c_size_t()
+        _check(lib().q38_gguf_upload(ctx.handle, self.handle, ctypes.byref(p), ctypes.byref(n)),
+               "q38_gguf_upload")
+        return p.value, n.value
+
+
+def recurrent_checkpoint(ctx: "Context", conv_state, delta_state, n_conv, n_delta, conv_ckpt, delta_ckpt):
+    _check(lib().q38_recurrent_checkpoint(ctx.handle, _ptr(conv_state), _ptr(delta_state), n_conv, n_delta,
+                                          _ptr(conv_ckpt), _ptr(delta_ckpt)), "q38_recurrent_checkpoint")
+
+
+def recurrent_restore(ctx: "Context", conv_ckpt, delta_ckpt, n_conv, n_delta, conv_state, delta_state):
+    _check(lib().q38_recurrent_restore(ctx.handle, _ptr(conv_ckpt), _ptr(delta_ckpt), n_conv, n_delta,
+                                       _ptr(conv_state), _ptr(delta_state)), "q38_recurrent_restore")
 
 
 def header_functions(paths=None) -> list[str]:

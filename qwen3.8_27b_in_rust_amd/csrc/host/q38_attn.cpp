@@ -53,6 +53,21 @@ int fail(const char *fmt, ...) {
     return -1;
 }
 
+}  // namespace
+
+/* The error slot for the library's other host files (q38_gguf.cpp). */
+__attribute__((visibility("hidden"))) int q38_fail(const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return -1;
+}
+
+namespace {
+
 #define Q38_HIP(call)                                                                   \
     do {                                                                                \
         hipError_t e_ = (call);                                                         \
