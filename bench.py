@@ -483,6 +483,35 @@ def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
     total_bytes = sum(gemv_bytes(ty, rows, width, n_tokens) for ty, rows, width, _ in mats)
     res = {"tokens": n_tokens, "layers": layers, "sweep_us": sweep_us,
            "sweep_gb_s": total_bytes / (sweep_us * 1e-6) / 1e9}
+    # gate and up of a layer read the same input: one q38_gemv_q8_k_multi
+    # launch for the pair, then down
+    out2 = ctx.empty((n_tokens, 17408))
+
+    def sweep_fused():
+        for li in range(layers):
+            g, u, d = mats[3 * li: 3 * li + 3]
+            ctx.gemv_q8_k_multi(12, [17408, 17408], 5120, [g[3], u[3]], q5, n_tokens, [out, out2])
+            ctx.gemv_q8_k(d[0], d[1], d[2], d[3], q17, n_tokens, out)
+
+    sweep_fused()
+    ctx.sync()
+    ctx.record(e0)
+    for _ in range(reps):
+        sweep_fused()
+    ctx.record(e1)
+    fused_us = ctx.elapsed_ms(e0, e1) * 1e3 / reps
+    res["fused_gate_up_sweep_us"] = fused_us
+    res["fused_gate_up_sweep_gb_s"] = total_bytes / (fused_us * 1e-6) / 1e9
+    ctx.kernel_timer_start(GEMV_KERNELS[12], reps * layers)
+    for _ in range(reps):
+        sweep_fused()
+    k_ms, k_n = ctx.kernel_timer_stop()
+    us = k_ms * 1e3 / max(k_n, 1)
+    b = 2 * gemv_bytes(12, 17408, 5120, n_tokens)
+    res["q4k_gate_up_2x17408x5120"] = {"kernel_us": us, "launches": k_n, "algorithmic_bytes": b,
+                                       "gb_s": b / (us * 1e-6) / 1e9,
+                                       "frac_hbm": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    out2.free()
     for ty, label in ((12, "q4k_17408x5120"), (14, "q6k_5120x17408")):
         ctx.kernel_timer_start(GEMV_KERNELS[ty], reps * 3 * layers)
         for _ in range(reps):

@@ -269,6 +269,17 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
                   int n_tokens, float *d_out);
 
+/* Several projections of one layer that read the same quantised input
+ * (project called in turn on one `quantized` buffer: q|gate, k and v in
+ * full_attention, ops.rs:954-958; ffn gate and up, ops.rs:1600-1613): up
+ * to 4 matrices of one type and width, matrix i with rows[i] rows at
+ * d_weights[i], its output at d_out[i] [n_tokens][rows[i]], in one launch.
+ * Each output equals q38_gemv_q8_k's for that matrix bit for bit; the
+ * launch streams the matrices back to back, so the start and end of a
+ * launch are paid once. */
+int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
+                        const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1234,48 +1234,70 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
     return ctx->launch(ctx->f_quantize_q8k, width / Q38_Q8K_BLOCK, n_tokens, 1, 64, &a);
 }
 
-int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
-                  int n_tokens, float *d_out) {
+int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
+                        const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out) {
     if (ctx == nullptr) return fail("ctx is NULL");
     hipFunction_t f = nullptr;
     if (ggml_type == Q38_GGML_Q4_K) f = ctx->f_gemv_q4k;
     else if (ggml_type == Q38_GGML_Q5_K) f = ctx->f_gemv_q5k;
     else if (ggml_type == Q38_GGML_Q6_K) f = ctx->f_gemv_q6k;
     else return fail("unsupported quant type %d (Q4_K 12, Q5_K 13, Q6_K 14)", ggml_type);
-    if (rows < 0 || n_tokens < 0) return fail("negative rows or n_tokens");
+    if (n_mats < 1 || n_mats > Q38_GEMV_MAX_MATS) return fail("n_mats %d outside 1..%d", n_mats, Q38_GEMV_MAX_MATS);
+    if (rows == nullptr || d_weights == nullptr || d_out == nullptr) return fail("NULL argument");
+    if (n_tokens < 0) return fail("negative n_tokens");
+    for (int i = 0; i < n_mats; ++i)
+        if (rows[i] < 0) return fail("negative rows (matrix %d)", i);
     if (width <= 0 || width % Q38_Q8K_BLOCK != 0)
         return fail("width %d is not a multiple of %d", width, Q38_Q8K_BLOCK);
     if (width / Q38_Q8K_BLOCK > Q38_GEMV_MAX_BLOCKS)
         return fail("width %d above %d", width, Q38_GEMV_MAX_BLOCKS * Q38_Q8K_BLOCK);
-    if (rows == 0 || n_tokens == 0) return 0;
-    if (d_weights == nullptr || d_q8k == nullptr || d_out == nullptr) return fail("NULL argument");
-    if ((uintptr_t)d_weights % 16 != 0 || (uintptr_t)d_q8k % 16 != 0)
-        return fail("d_weights and d_q8k must be 16-byte aligned");
+    if (n_tokens == 0) return 0;
     /* tokens per pass: as many as Q38_GEMV_ACT_LDS holds (one at least), up to 8 */
     const int blocks = width / Q38_Q8K_BLOCK;
     int tok_pass = std::max(1, std::min(Q38_GEMV_TOKENS, Q38_GEMV_ACT_LDS / (blocks * Q38_GEMV_REC_BYTES)));
     tok_pass = std::min(tok_pass, n_tokens);
     /* rows per workgroup: up to Q38_GEMV_UNITS_MAX units (four per lane), and
      * the per-token terms in at most 16 KiB of LDS; fewer rows when that
-     * leaves under 256 workgroups (small matrices), so every CU gets work */
+     * leaves a matrix under 256 workgroups (small matrices), so every CU gets
+     * work */
     const int max_units = std::min(Q38_GEMV_UNITS_MAX, 4096 / tok_pass);
-    int per_wg = max_units / blocks;
-    if (((long)rows + per_wg - 1) / per_wg < 256) per_wg = std::max(1, std::min(per_wg, rows / 256));
-    const long wgs = ((long)rows + per_wg - 1) / per_wg;
-    const long tok_groups = ((long)n_tokens + tok_pass - 1) / tok_pass;
-    if (wgs > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
-    const unsigned lds = (unsigned)(tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * per_wg * blocks * 4);
     q38_gemv_args a;
     memset(&a, 0, sizeof(a));
-    a.weights = static_cast<const uint8_t *>(d_weights);
+    long wgs = 0;
+    int max_per_wg = 1;
+    int kept = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        if (rows[i] == 0) continue; /* nothing to compute for an empty matrix */
+        if (d_weights[i] == nullptr || d_out[i] == nullptr) return fail("NULL weights or output (matrix %d)", i);
+        if ((uintptr_t)d_weights[i] % 16 != 0) return fail("d_weights[%d] must be 16-byte aligned", i);
+        int per_wg = max_units / blocks;
+        if (((long)rows[i] + per_wg - 1) / per_wg < 256) per_wg = std::max(1, std::min(per_wg, rows[i] / 256));
+        a.weights[kept] = static_cast<const uint8_t *>(d_weights[i]);
+        a.out[kept] = d_out[i];
+        a.rows[kept] = rows[i];
+        a.rows_per_wg[kept] = per_wg;
+        a.wg_begin[kept] = (int32_t)wgs;
+        wgs += ((long)rows[i] + per_wg - 1) / per_wg;
+        max_per_wg = std::max(max_per_wg, per_wg);
+        ++kept;
+    }
+    if (kept == 0) return 0;
+    if (d_q8k == nullptr || (uintptr_t)d_q8k % 16 != 0) return fail("d_q8k is NULL or not 16-byte aligned");
+    const long tok_groups = ((long)n_tokens + tok_pass - 1) / tok_pass;
+    if (wgs > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
+    a.wg_begin[kept] = (int32_t)wgs;
+    a.n_mats = kept;
     a.q8k = d_q8k;
-    a.out = d_out;
-    a.rows = rows;
     a.width = width;
     a.n_tokens = n_tokens;
-    a.rows_per_wg = per_wg;
     a.tok_pass = tok_pass;
+    const unsigned lds = (unsigned)(tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * max_per_wg * blocks * 4);
     return ctx->launch(f, (unsigned)wgs, (unsigned)tok_groups, 1, 256, &a, lds);
+}
+
+int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
+                  int n_tokens, float *d_out) {
+    return q38_gemv_q8_k_multi(ctx, ggml_type, 1, &rows, width, &d_weights, d_q8k, n_tokens, &d_out);
 }
 
 }  /* extern "C" */

@@ -229,7 +229,8 @@ Q38_DEV float unit_term(const Unit<TYPE> &u, const UnitScales<TYPE> &s, const ui
 }
 
 /*
- * A workgroup owns rows [row0, row0 + R) and the tokens [tok0, tok0 + tp);
+ * A workgroup owns rows [row0, row0 + R) of one of up to Q38_GEMV_MAX_MATS
+ * matrices that read the same activations, and the tokens [tok0, tok0 + tp);
  * its R * B units (at most Q38_GEMV_UNITS_MAX) are taken by the 256 lanes in
  * steps of 256:
  *   1. each lane issues the loads of its first unit, then the workgroup
@@ -249,9 +250,17 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     const int tid = threadIdx.x;
     const int width = a.width;
     const int B = width / Q38_Q8K_BLOCK;
-    const int R = a.rows_per_wg;
-    const int row0 = blockIdx.x * R;
-    const int rows_here = min(R, a.rows - row0);
+    /* the matrix of this workgroup: matrices share the activations and
+     * take consecutive ranges of blockIdx.x */
+    int mat = 0;
+#pragma unroll
+    for (int i = 1; i < Q38_GEMV_MAX_MATS; ++i) mat += (i < a.n_mats && (int)blockIdx.x >= a.wg_begin[i]) ? 1 : 0;
+    const uint8_t *weights = a.weights[mat];
+    float *out = a.out[mat];
+    const int rows = a.rows[mat];
+    const int R = a.rows_per_wg[mat];
+    const int row0 = ((int)blockIdx.x - a.wg_begin[mat]) * R;
+    const int rows_here = min(R, rows - row0);
     const int units = rows_here * B;
     const int steps = (units + 255) >> 8;
     const int tok0 = blockIdx.y * a.tok_pass;
@@ -264,7 +273,7 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     const size_t g0 = (size_t)row0 * B;
 
     Unit<TYPE> w[2];
-    load_unit<TYPE>(a.weights, g0 + min(tid, units - 1), w[0]);
+    load_unit<TYPE>(weights, g0 + min(tid, units - 1), w[0]);
 
     /* the tokens' blocks are contiguous from token tok0 in each of the three
      * planes: quants [T][W], sums [T][B][16], scales [T][B] */
@@ -285,7 +294,7 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     for (int k = 0; k < Q38_GEMV_UNITS_MAX / 256; ++k) {
         if (k >= steps) break;
         const int u = tid + 256 * k;
-        load_unit<TYPE>(a.weights, g0 + min(u + 256, units - 1), w[(k + 1) & 1]);
+        load_unit<TYPE>(weights, g0 + min(u + 256, units - 1), w[(k + 1) & 1]);
         if (u < units) {
             UnitScales<TYPE> s;
             unit_scales<TYPE>(w[k & 1], s);
@@ -303,7 +312,7 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
         const float *tr = terms + t * units + r * B;
         float total = 0.0f;
         for (int b = 0; b < B; ++b) total += tr[b];
-        a.out[(size_t)(tok0 + t) * a.rows + row0 + r] = total;
+        out[(size_t)(tok0 + t) * rows + row0 + r] = total;
     }
 }
 

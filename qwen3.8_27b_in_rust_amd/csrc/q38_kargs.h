@@ -247,18 +247,23 @@ typedef struct {
     int32_t n_tokens;
 } q38_quantize_args;
 
-/* K-quant x Q8_K GEMV / GEMM: grid (ceil(rows / rows_per_wg),
- * ceil(T / tok_pass)), 256 threads, one lane per (row, block) unit,
- * rows_per_wg * B <= Q38_GEMV_UNITS_MAX; dynamic LDS tok_pass * B *
- * Q38_GEMV_REC_BYTES + tok_pass * rows_per_wg * B * 4 bytes. */
+/* K-quant x Q8_K GEMV / GEMM over up to Q38_GEMV_MAX_MATS matrices of one
+ * type and width that read the same activations: grid (wg_begin[n_mats],
+ * ceil(T / tok_pass)), 256 threads, one lane per (row, block) unit; matrix
+ * i takes workgroups wg_begin[i] .. wg_begin[i+1]-1, rows_per_wg[i] * B <=
+ * Q38_GEMV_UNITS_MAX; dynamic LDS tok_pass * B * Q38_GEMV_REC_BYTES +
+ * tok_pass * max_i(rows_per_wg[i]) * B * 4 bytes. */
+#define Q38_GEMV_MAX_MATS 4
 typedef struct {
-    const uint8_t *weights; /* [rows][B * block_bytes], 16-byte aligned */
-    const void *q8k;        /* planar Q8_K of T tokens */
-    float *out;             /* [T][rows] */
-    int32_t rows;
+    const uint8_t *weights[Q38_GEMV_MAX_MATS]; /* [rows][B * block_bytes], 16-byte aligned */
+    float *out[Q38_GEMV_MAX_MATS];             /* [T][rows] */
+    int32_t rows[Q38_GEMV_MAX_MATS];
+    int32_t rows_per_wg[Q38_GEMV_MAX_MATS];
+    int32_t wg_begin[Q38_GEMV_MAX_MATS + 1];
+    int32_t n_mats;
+    const void *q8k; /* planar Q8_K of T tokens */
     int32_t width;
     int32_t n_tokens;
-    int32_t rows_per_wg;
     int32_t tok_pass;
     int32_t pad_;
 } q38_gemv_args;

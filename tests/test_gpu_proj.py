@@ -101,6 +101,34 @@ def test_gemv_q8_k_model_shapes(ctx, ref, name):
     assert np.array_equal(d_o.download().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("name", sorted(TYPES))
+@pytest.mark.parametrize("T", [1, 3, 9])
+def test_gemv_multi_equals_single(ctx, ref, name, T):
+    """Several matrices on one input in one launch (q|gate, k, v of a layer
+    are 12288, 1024, 1024 rows; here smaller, with an empty matrix and a
+    one-row one): every output bit for bit as the single-matrix launch and
+    the oracle."""
+    ty = TYPES[name]
+    W = 1280
+    x = _activations(T, W, 0x513338E0 + T)
+    d_q = _quantize_on_device(ctx, x)
+    q8 = ref.quantize_q8_k(x)
+    rows = [1500, 0, 96, 1]
+    wbs = [_random_kquant(ty, max(r, 1), W, 0x513338E1 + ty + i)[:r] for i, r in enumerate(rows)]
+    d_ws = [ctx.array(wb, np.uint8) if r else None for wb, r in zip(wbs, rows)]
+    d_os = [ctx.empty((T, max(r, 1))) for r in rows]
+    ctx.gemv_q8_k_multi(ty, rows, W, d_ws, d_q, T, d_os)
+    for wb, r, d_w, d_o in zip(wbs, rows, d_ws, d_os):
+        if r == 0:
+            continue
+        got = d_o.download()
+        single = ctx.empty((T, r))
+        ctx.gemv_q8_k(ty, r, W, d_w, d_q, T, single)
+        assert np.array_equal(got.view(np.uint32), single.download().view(np.uint32))
+        want = ref.gemv_q8_k(ty, wb, q8, T, W, threads=16)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_projection_argument_checks(pkg, ctx):
     x = ctx.empty((300,))
     q = ctx.empty((4096,), np.uint8)
@@ -113,6 +141,10 @@ def test_projection_argument_checks(pkg, ctx):
         ctx.gemv_q8_k(12, 4, 300, q, q, 1, o)
     with pytest.raises(pkg.Q38Error, match="above 49152"):
         ctx.gemv_q8_k(12, 4, 49408, q, q, 1, o)
+    with pytest.raises(pkg.Q38Error, match="n_mats 5 outside"):
+        ctx.gemv_q8_k_multi(12, [4] * 5, 256, [q] * 5, q, 1, [o] * 5)
+    with pytest.raises(pkg.Q38Error, match="NULL weights or output"):
+        ctx.gemv_q8_k_multi(12, [4, 4], 256, [q, None], q, 1, [o, o])
     with pytest.raises(pkg.Q38Error, match="multiple of 256"):
         pkg.Context.q8k_bytes(1, 100)
 
