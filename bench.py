@@ -531,6 +531,42 @@ def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
     return res
 
 
+INT8_PEAK_TOPS = 5000.0
+GEMM_KERNELS = {12: "q38_gemm_q8k_q4k", 13: "q38_gemm_q8k_q5k", 14: "q38_gemm_q8k_q6k"}
+
+
+def prompt_projections(pkg, ctx, n_tokens: int, reps: int):
+    """The FFN projections of one layer for a prompt of n_tokens (gate
+    17408 x 5120 Q4_K, down 5120 x 17408 Q6_K; the int8 matrix-unit form
+    from 16 tokens on): kernel time and int8 operations per second
+    (2 x rows x width x tokens; the K-quant expansion and the block terms
+    are not counted)."""
+    res = {"tokens": n_tokens}
+    for ty, rows, width, label in ((12, 17408, 5120, "q4k_17408x5120"), (14, 5120, 17408, "q6k_5120x17408")):
+        nbytes = rows * (width // 256) * QUANT_BLOCK_BYTES[ty]
+        w = ctx.empty((nbytes,), np.uint8)
+        ctx.fill_normal(w, nbytes // 4, 0x51335200 + ty)
+        x = ctx.empty((n_tokens, width))
+        ctx.fill_normal(x, n_tokens * width, 0x51335201)
+        q = ctx.empty((ctx.q8k_bytes(n_tokens, width),), np.uint8)
+        ctx.quantize_q8_k(n_tokens, width, x, q)
+        out = ctx.empty((n_tokens, rows))
+        ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
+        ctx.sync()
+        kern = GEMM_KERNELS[ty] if n_tokens >= 16 else GEMV_KERNELS[ty]
+        ctx.kernel_timer_start(kern, reps * 64)
+        for _ in range(reps):
+            ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
+        k_ms, k_n = ctx.kernel_timer_stop()
+        ms = k_ms / max(k_n, 1) * (k_n / reps if reps else 1)
+        ops = 2.0 * rows * width * n_tokens
+        res[label] = {"kernel": kern, "ms": ms, "int8_tops": ops / (ms * 1e-3) / 1e12,
+                      "frac_int8_peak": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}
+        for arr in (w, x, q, out):
+            arr.free()
+    return res
+
+
 def recurrent_checkpoint(pkg, ctx, reps: int):
     """checkpoint_state's device form: conv_state (5.9 MB) and delta_state
     (151 MB) of a sequence copied to the checkpoint; each copy reads and
@@ -609,6 +645,10 @@ EXTRAS = {
                               lambda pkg, ctx: gdn_steps(pkg, ctx, 1, 1, 384, 32)),
     "recurrent_checkpoint": ("recurrent-state checkpoint of one sequence (157 MB)",
                              lambda pkg, ctx: recurrent_checkpoint(pkg, ctx, 20)),
+    "prompt_projections_64": ("FFN projections of one layer for 64 prompt tokens",
+                              lambda pkg, ctx: prompt_projections(pkg, ctx, 64, 5)),
+    "prompt_projections_4096": ("FFN projections of one layer for a 4096-token prompt",
+                                lambda pkg, ctx: prompt_projections(pkg, ctx, 4096, 3)),
     "ffn_projections_1": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 1 token",
                           lambda pkg, ctx: ffn_projections(pkg, ctx, 1, 20)),
     "ffn_projections_8": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 8 tokens",

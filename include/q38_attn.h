@@ -265,7 +265,9 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
  * 210 bytes per block, 16-byte aligned base), d_q8k from
  * q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the reference's
  * batched form writes it).  width is at most 49152.  Each element equals the
- * reference's scalar dot_q*_k_q8_k (tensor.rs:365-457) bit for bit. */
+ * reference's scalar dot_q*_k_q8_k (tensor.rs:365-457) bit for bit.  From 32
+ * tokens (16 for matrices of 8192 rows or more) the integer dots run on the
+ * int8 matrix unit; the result is the same bit for bit. */
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
                   int n_tokens, float *d_out);
 

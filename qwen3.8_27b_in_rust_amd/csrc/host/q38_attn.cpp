@@ -114,6 +114,7 @@ struct q38_ctx {
     hipFunction_t f_gdn_step_rows = nullptr;
     hipModule_t mod_proj = nullptr;
     hipFunction_t f_quantize_q8k = nullptr;
+    hipFunction_t f_gemm[3] = {nullptr, nullptr, nullptr}; /* Q4_K, Q5_K, Q6_K on the matrix unit */
     hipFunction_t f_gemv_q4k = nullptr;
     hipFunction_t f_gemv_q5k = nullptr;
     hipFunction_t f_gemv_q6k = nullptr;
@@ -342,6 +343,9 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q4k, ctx->mod_proj, "q38_gemv_q8k_q4k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q5k, ctx->mod_proj, "q38_gemv_q8k_q5k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q6k, ctx->mod_proj, "q38_gemv_q8k_q6k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[0], ctx->mod_proj, "q38_gemm_q8k_q4k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[1], ctx->mod_proj, "q38_gemm_q8k_q5k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[2], ctx->mod_proj, "q38_gemm_q8k_q6k"));
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
@@ -514,6 +518,9 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_copy_f32") f = ctx->f_copy;
     else if (name == "q38_noop") f = ctx->f_noop;
     else if (name == "q38_quantize_q8k") f = ctx->f_quantize_q8k;
+    else if (name == "q38_gemm_q8k_q4k") f = ctx->f_gemm[0];
+    else if (name == "q38_gemm_q8k_q5k") f = ctx->f_gemm[1];
+    else if (name == "q38_gemm_q8k_q6k") f = ctx->f_gemm[2];
     else if (name == "q38_gemv_q8k_q4k") f = ctx->f_gemv_q4k;
     else if (name == "q38_gemv_q8k_q5k") f = ctx->f_gemv_q5k;
     else if (name == "q38_gemv_q8k_q6k") f = ctx->f_gemv_q6k;
@@ -1283,6 +1290,32 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     }
     if (kept == 0) return 0;
     if (d_q8k == nullptr || (uintptr_t)d_q8k % 16 != 0) return fail("d_q8k is NULL or not 16-byte aligned");
+    /* many tokens: the int8 matrix-unit form, one launch per matrix, 128
+     * rows x 64 tokens per workgroup; from 16 tokens on when a matrix has
+     * rows for 64+ workgroups, else from 32 (measured crossovers: 17408 x
+     * 5120 Q4_K at 16 tokens, 5120 x 17408 Q6_K at 32) */
+    long min_rows = rows[0];
+    for (int i = 1; i < n_mats; ++i) min_rows = std::min<long>(min_rows, rows[i]);
+    if (n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
+        (n_tokens >= Q38_GEMM_MIN_TOKENS && min_rows >= 64L * Q38_GEMM_ROWS)) {
+        const int ti = ggml_type == Q38_GGML_Q4_K ? 0 : ggml_type == Q38_GGML_Q5_K ? 1 : 2;
+        const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
+        if (tok_tiles > 65535) return fail("too many tokens");
+        for (int i = 0; i < kept; ++i) {
+            q38_gemv_args g;
+            memset(&g, 0, sizeof(g));
+            g.weights[0] = a.weights[i];
+            g.out[0] = a.out[i];
+            g.rows[0] = a.rows[i];
+            g.n_mats = 1;
+            g.q8k = d_q8k;
+            g.width = width;
+            g.n_tokens = n_tokens;
+            const long row_tiles = ((long)a.rows[i] + Q38_GEMM_ROWS - 1) / Q38_GEMM_ROWS;
+            if (ctx->launch(ctx->f_gemm[ti], (unsigned)row_tiles, (unsigned)tok_tiles, 1, 256, &g)) return -1;
+        }
+        return 0;
+    }
     const long tok_groups = ((long)n_tokens + tok_pass - 1) / tok_pass;
     if (wgs > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
     a.wg_begin[kept] = (int32_t)wgs;

@@ -316,6 +316,235 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     }
 }
 
+/*
+ * The batched form for many tokens (tensor_gemm_q8_k, tensor.rs:1217-1270):
+ * the same per-block integer sums and f32 block terms, with the integer
+ * dot products on the int8 matrix unit (v_mfma_i32_32x32x32_i8, exact).
+ * A workgroup of 4 waves owns 128 rows x 64 tokens; wave w owns rows
+ * 128 bx + 32 w .. + 31 (lane l: row l % 32, k half l / 32 of each 32-value
+ * step) and both 32-token tiles (the weights it unpacks serve both).  The activations are the MFMA's first
+ * operand (tokens x k, from LDS, the next block's copied in while this one
+ * is computed), the weights its second (k x rows, unpacked in registers from
+ * the lane's own copy of its row's block), so every lane's accumulator
+ * column is its own row: element 4J+i of a tile is token 8J + 4(l/32) + i.
+ *  - the sub-block scale goes into the weights: w = sc q (Q4_K, Q5_K: a k
+ *    step is one 32-value sub-block) or w = sc (q - 32) (Q6_K: a k step holds
+ *    two 16-value groups, one per lane half), |w| <= 4096, split into byte
+ *    planes w = 128 hi + lo (hi signed, lo in 0..127); two MFMAs per step
+ *    accumulate over the block and weighted = 128 C_hi + C_lo;
+ *  - Q4_K / Q5_K's minimum term sum_j m_j bsum_j is a third MFMA, of the
+ *    activations against m_j splatted over its sub-block (sum_i m_j(i) a_i).
+ * Every integer is exact; the f32 block term and the row total follow the
+ * reference's operation order, so the result equals q38_gemv_q8_k's (and
+ * the reference's) bit for bit.
+ */
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+/* LDS writes complete, then a workgroup barrier; vector-memory loads in
+ * flight stay in flight (gfx9 s_waitcnt: vmcnt 63, expcnt 7, lgkmcnt 0) */
+Q38_DEV void lds_barrier_bare() {
+    __builtin_amdgcn_s_waitcnt((15 | (3 << 14)) | (7 << 4) | (0 << 8));
+    __builtin_amdgcn_s_barrier();
+}
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+constexpr int kGemmRows = 128;
+constexpr int kGemmTokens = Q38_GEMM_TOKENS; /* tiles of 32 */
+constexpr int kGemmTiles = kGemmTokens / 32;
+constexpr int kStagePieces = kGemmTokens * 16 / 256; /* 16-byte activation pieces per thread and block */
+constexpr int kActRow = 272; /* LDS bytes of one token's 256 quants: 16-byte pad, conflict-free reads */
+
+Q38_DEV i32x16 mfma_i8(i32x4 a, i32x4 b, i32x16 c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
+
+/* Four weights w = sc * (q - off) (q the unpacked bytes, |w| <= 4096) split
+ * into byte planes w = 128 hi + lo, hi signed, lo in 0..127; the arithmetic
+ * runs on packed 16-bit lanes (even and odd bytes). */
+Q38_DEV void split_weights(uint32_t q, int sc, short off, uint32_t &hi, uint32_t &lo) {
+    const s16x2 s2 = {(short)sc, (short)sc};
+    const s16x2 o2 = {off, off};
+    const s16x2 e = __builtin_bit_cast(s16x2, q & 0x00FF00FFu) - o2;
+    const s16x2 o = __builtin_bit_cast(s16x2, (q >> 8) & 0x00FF00FFu) - o2;
+    const s16x2 ve = e * s2, vo = o * s2;
+    const s16x2 sh = {7, 7};
+    const uint32_t he = __builtin_bit_cast(uint32_t, ve >> sh) & 0x00FF00FFu;
+    const uint32_t ho = __builtin_bit_cast(uint32_t, vo >> sh) & 0x00FF00FFu;
+    const uint32_t le = __builtin_bit_cast(uint32_t, ve) & 0x007F007Fu;
+    const uint32_t lo_ = __builtin_bit_cast(uint32_t, vo) & 0x007F007Fu;
+    hi = he | (ho << 8);
+    lo = le | (lo_ << 8);
+}
+
+template <int TYPE>
+Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
+    __shared__ __align__(16) int8_t act[2][kGemmTokens][kActRow];
+    __shared__ float ascale[2][kGemmTokens];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const int width = a.width;
+    const int B = width / Q38_Q8K_BLOCK;
+    const int rows = a.rows[0];
+    const int row = blockIdx.x * kGemmRows + wave * 32 + (lane & 31);
+    const int rowc = min(row, rows - 1);
+    const int t0 = blockIdx.y * kGemmTokens;
+    const int T = a.n_tokens;
+    const int8_t *quants = static_cast<const int8_t *>(a.q8k);
+    const int16_t *sums = reinterpret_cast<const int16_t *>(quants + (size_t)T * width);
+    const float *scales = reinterpret_cast<const float *>(sums + (size_t)T * B * 16);
+
+    /* a block's activations: thread p copies pieces p, p + 256, ... (16
+     * bytes of token p / 16, block b); tokens past the prompt are zeros */
+    u32x4 stage[kStagePieces];
+    float stage_scale = 0.0f;
+    /* tokens past the prompt read the last token (no branch around a load,
+     * so the loop's wait counts stay exact); they only feed their own
+     * outputs, which are not stored */
+    auto fetch = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < kStagePieces; ++i) {
+            const int p = tid + 256 * i, t = min(t0 + (p >> 4), T - 1), c = p & 15;
+            stage[i] = *reinterpret_cast<const u32x4 *>(quants + (size_t)t * width + b * 256 + c * 16);
+        }
+        stage_scale = scales[(size_t)min(t0 + (tid & (kGemmTokens - 1)), T - 1) * B + b]; /* threads < kGemmTokens */
+    };
+    auto put = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < kStagePieces; ++i) {
+            const int p = tid + 256 * i, t = p >> 4, c = p & 15;
+            *reinterpret_cast<u32x4 *>(&act[buf][t][c * 16]) = stage[i];
+        }
+        if (tid < kGemmTokens) ascale[buf][tid] = stage_scale;
+    };
+
+    float total[kGemmTiles][16];
+#pragma unroll
+    for (int tt = 0; tt < kGemmTiles; ++tt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) total[tt][e] = 0.0f;
+
+    /* the compute of one block from LDS buffer buf and weights u */
+    auto compute = [&](const Unit<TYPE> &u, int buf, bool real) {
+        UnitScales<TYPE> s;
+        unit_scales<TYPE>(u, s);
+        /* word k + 4 h of the block: both candidates are fixed registers and
+         * the lane half selects (an index that depends on the lane would put
+         * the block in scratch memory) */
+        auto word = [&](int k) { return h ? u.w[k + 4] : u.w[k]; };
+        const int8_t *arow[kGemmTiles];
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt) arow[tt] = &act[buf][32 * tt + (lane & 31)][16 * h];
+        /* the block's integer sums per tile: weighted, and minimum (Q4_K, Q5_K) */
+        i32x16 wsum[kGemmTiles], msum[kGemmTiles];
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt) {
+            wsum[tt] = i32x16{};
+            msum[tt] = i32x16{};
+        }
+        /* two byte planes of the scaled weights per k step (values 32 st +
+         * 16 h .. + 15 of the block): w = sc q (Q4_K, Q5_K: the step is one
+         * 32-value sub-block) or w = sc (q - 32) (Q6_K: group 2 st + h);
+         * weighted = 128 C_hi + C_lo.  Q4_K / Q5_K's minimum is a third
+         * product, the activations against m splatted over the sub-block. */
+        i32x16 lsum[kGemmTiles];
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt) lsum[tt] = i32x16{};
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            i32x4 bh, bl;
+            int sc;
+            if (TYPE == Q38_GGML_Q6_K) sc = h ? s.sc[2 * st + 1] : s.sc[2 * st];
+            else sc = s.sc[st];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t q;
+                if (TYPE == Q38_GGML_Q6_K) {
+                    const int hf = st >> 2, kq = st & 3;
+                    const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
+                    const uint32_t qh = word(32 + 8 * hf + j);
+                    q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
+                } else {
+                    const int c = st >> 1, nib = st & 1;
+                    const uint32_t qs = TYPE == Q38_GGML_Q4_K ? word(4 + 8 * c + j) : word(12 + 8 * c + j);
+                    q = (qs >> (4 * nib)) & 0x0F0F0F0Fu;
+                    if (TYPE == Q38_GGML_Q5_K) q |= ((word(4 + j) >> st) & 0x01010101u) << 4;
+                }
+                uint32_t hi, lo;
+                split_weights(q, sc, TYPE == Q38_GGML_Q6_K ? (short)32 : (short)0, hi, lo);
+                bh[j] = (int)hi;
+                bl[j] = (int)lo;
+            }
+#pragma unroll
+            for (int tt = 0; tt < kGemmTiles; ++tt) {
+                const i32x4 A = *reinterpret_cast<const i32x4 *>(arow[tt] + 32 * st);
+                wsum[tt] = mfma_i8(A, bh, wsum[tt]);
+                lsum[tt] = mfma_i8(A, bl, lsum[tt]);
+                if (TYPE != Q38_GGML_Q6_K) {
+                    const int m4 = s.mn[st] * 0x01010101;
+                    const i32x4 bm = {m4, m4, m4, m4};
+                    msum[tt] = mfma_i8(A, bm, msum[tt]);
+                }
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) wsum[tt][e] = wsum[tt][e] * 128 + lsum[tt][e];
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int tok = 32 * tt + 8 * (e >> 2) + 4 * h + (e & 3);
+                const float as = ascale[buf][tok];
+                const float d = s.d * as;
+                float term;
+                if (TYPE == Q38_GGML_Q6_K) {
+                    term = d * (float)wsum[tt][e];
+                } else {
+                    const float dmin = s.dmin * as;
+                    term = d * (float)wsum[tt][e] - dmin * (float)msum[tt][e];
+                }
+                /* a step past the last block repeats it and adds nothing */
+                total[tt][e] = real ? total[tt][e] + term : total[tt][e];
+            }
+        }
+    };
+
+    /* Weights and activations one block ahead: weights in the other of two
+     * register sets (the loop is unrolled by two), activations through the
+     * other LDS buffer.  The barriers are bare (LDS writes only): a fence
+     * would also wait for the weights in flight.  Every step issues the same
+     * loads and the same compute (no branch in the loop, so the wait counts
+     * stay exact); a step past the last block repeats it and adds nothing. */
+    Unit<TYPE> w[2];
+    fetch(0);
+    load_unit<TYPE>(a.weights[0], (size_t)rowc * B, w[0]);
+    put(0);
+    lds_barrier_bare();
+    auto step = [&](int b, Unit<TYPE> &cur, Unit<TYPE> &ahead) {
+        fetch(min(b + 1, B - 1));
+        load_unit<TYPE>(a.weights[0], (size_t)rowc * B + min(b + 1, B - 1), ahead);
+        __builtin_amdgcn_sched_barrier(0); /* the loads issue before the compute */
+        compute(cur, b & 1, b < B);
+        put((b + 1) & 1);
+        lds_barrier_bare();
+    };
+    for (int b = 0; b < B; b += 2) {
+        step(b, w[0], w[1]);
+        step(b + 1, w[1], w[0]);
+    }
+
+    if (row < rows) {
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int tok = t0 + 32 * tt + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (tok < T) a.out[0][(size_t)tok * rows + row] = total[tt][e];
+            }
+    }
+}
+
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(64) void q38_quantize_q8k(q38_quantize_args a) {
@@ -375,3 +604,6 @@ extern "C" __global__ __launch_bounds__(64) void q38_quantize_q8k(q38_quantize_a
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q4k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q5k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q5_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q6k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q6_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q4k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q4_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q5k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q5_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q6k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q6_K>(a); }

@@ -254,6 +254,12 @@ typedef struct {
  * Q38_GEMV_UNITS_MAX; dynamic LDS tok_pass * B * Q38_GEMV_REC_BYTES +
  * tok_pass * max_i(rows_per_wg[i]) * B * 4 bytes. */
 #define Q38_GEMV_MAX_MATS 4
+/* From this many tokens (twice as many for matrices of under 8192 rows) the
+ * projections run on the int8 matrix unit (q38_gemm_q8k_*: grid (ceil(rows /
+ * 128), ceil(T / 64)), 256 threads, the same arguments with one matrix). */
+#define Q38_GEMM_MIN_TOKENS 16
+#define Q38_GEMM_ROWS 128
+#define Q38_GEMM_TOKENS 64
 typedef struct {
     const uint8_t *weights[Q38_GEMV_MAX_MATS]; /* [rows][B * block_bytes], 16-byte aligned */
     float *out[Q38_GEMV_MAX_MATS];             /* [T][rows] */

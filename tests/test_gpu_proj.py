@@ -129,6 +129,26 @@ def test_gemv_multi_equals_single(ctx, ref, name, T):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("name", sorted(TYPES))
+@pytest.mark.parametrize("rows,W,T", [(130, 1280, 32), (33, 256, 65), (300, HIDDEN, 130), (129, 2304, 64),
+                                      (8200, 256, 16)])
+def test_gemm_many_tokens_bit_exact(ctx, ref, name, rows, W, T):
+    """The matrix-unit form (32 tokens and more, 16 for 8192+ rows): partial
+    row and token tiles, one and several 64-token tiles, bit for bit against
+    the oracle."""
+    ty = TYPES[name]
+    x = _activations(T, W, 0x513338F0 + T + W)
+    d_q = _quantize_on_device(ctx, x)
+    wb = _random_kquant(ty, rows, W, 0x513338F1 + ty + rows)
+    d_w = ctx.array(wb, np.uint8)
+    d_o = ctx.empty((T, rows))
+    ctx.gemv_q8_k(ty, rows, W, d_w, d_q, T, d_o)
+    got = d_o.download()
+    want = ref.gemv_q8_k(ty, wb, ref.quantize_q8_k(x), T, W, threads=16)
+    bad = np.flatnonzero(got.view(np.uint32).reshape(-1) != want.view(np.uint32).reshape(-1))
+    assert bad.size == 0, (bad.size, bad[:5], got.reshape(-1)[bad[:5]], want.reshape(-1)[bad[:5]])
+
+
 def test_projection_argument_checks(pkg, ctx):
     x = ctx.empty((300,))
     q = ctx.empty((4096,), np.uint8)
