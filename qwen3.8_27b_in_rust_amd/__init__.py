@@ -433,7 +433,8 @@ class Gguf:
 
     def find_tensor(self, name: str) -> int:
         i = c_int()
-        _check(lib().q38_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(i)), "q38_gguf_find_tensor")
+        _check(lib().q38_gguf_find_tensor(self.handle, name.encode("utf-8", "surrogateescape"), ctypes.byref(i)),
+               "q38_gguf_find_tensor")
         return i.value
 
     def tensor(self, index: int) -> dict:
@@ -443,12 +444,16 @@ class Gguf:
         off, nb = ctypes.c_uint64(), ctypes.c_uint64()
         _check(lib().q38_gguf_tensor(self.handle, index, ctypes.byref(name), ctypes.byref(ty), ctypes.byref(nd),
                                      shape, ctypes.byref(off), ctypes.byref(nb)), "q38_gguf_tensor")
-        return {"name": name.value.decode(), "type": ty.value, "shape": list(shape[:nd.value]),
+        # names are bytes in the file (not necessarily UTF-8); surrogateescape
+        # round-trips them through find_tensor
+        return {"name": name.value.decode("utf-8", "surrogateescape"), "type": ty.value,
+                "shape": list(shape[:nd.value]),
                 "offset": off.value, "nbytes": nb.value}
 
     def meta_u32(self, key: str) -> int:
         v = c_uint32()
-        _check(lib().q38_gguf_meta_u32(self.handle, key.encode(), ctypes.byref(v)), "q38_gguf_meta_u32")
+        _check(lib().q38_gguf_meta_u32(self.handle, key.encode("utf-8", "surrogateescape"), ctypes.byref(v)),
+               "q38_gguf_meta_u32")
         return v.value
 
     def upload(self, ctx: "Context") -> tuple[int, int]:
