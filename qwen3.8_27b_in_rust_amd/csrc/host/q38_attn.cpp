@@ -1294,8 +1294,8 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
      * rows x 64 tokens per workgroup; from 16 tokens on when a matrix has
      * rows for 64+ workgroups, else from 32 (measured crossovers: 17408 x
      * 5120 Q4_K at 16 tokens, 5120 x 17408 Q6_K at 32) */
-    long min_rows = rows[0];
-    for (int i = 1; i < n_mats; ++i) min_rows = std::min<long>(min_rows, rows[i]);
+    long min_rows = a.rows[0];
+    for (int i = 1; i < kept; ++i) min_rows = std::min<long>(min_rows, a.rows[i]); /* non-empty matrices */
     if (n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
         (n_tokens >= Q38_GEMM_MIN_TOKENS && min_rows >= 64L * Q38_GEMM_ROWS)) {
         const int ti = ggml_type == Q38_GGML_Q4_K ? 0 : ggml_type == Q38_GGML_Q5_K ? 1 : 2;
