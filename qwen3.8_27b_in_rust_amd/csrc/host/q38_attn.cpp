@@ -1067,7 +1067,8 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
  * loop of ops.rs:1088-1099 in 64-token chunks); work holds
  * chunk_work_floats(n_seq, n_tokens) floats. */
 static size_t chunk_work_floats(int n_seq, int n_tokens) {
-    const size_t n_chunks = ((size_t)n_tokens + Q38_GDN_CHUNK - 1) / Q38_GDN_CHUNK;
+    const size_t n_chunks =
+        std::min<size_t>(((size_t)n_tokens + Q38_GDN_CHUNK - 1) / Q38_GDN_CHUNK, Q38_GDN_STAGE_CHUNKS);
     return (size_t)n_seq * Q38_LIN_V_HEADS * n_chunks * (Q38_GDN_RECORD_BYTES / sizeof(float));
 }
 
@@ -1090,9 +1091,15 @@ static int gdn_chunked(q38_ctx *ctx, int n_seq, int n_tokens, float *d_state, in
     a.q_stride = q_stride;
     a.v_stride = v_stride;
     a.n_tokens = n_tokens;
-    a.n_chunks = n_chunks;
-    if (ctx->launch(ctx->f_chunk_prep, Q38_LIN_QK_HEADS, n_chunks, n_seq, 512, &a)) return -1;
-    return ctx->launch(ctx->f_chunk_scan, Q38_LIN_V_HEADS * 4, n_seq, 1, 64 * Q38_GDN_SCAN_WAVES, &a);
+    /* stages of Q38_GDN_STAGE_CHUNKS chunks: the scan reads each stage's
+     * records right after the prep wrote them */
+    for (int c0 = 0; c0 < n_chunks; c0 += Q38_GDN_STAGE_CHUNKS) {
+        a.chunk0 = c0;
+        a.n_chunks = std::min(Q38_GDN_STAGE_CHUNKS, n_chunks - c0);
+        if (ctx->launch(ctx->f_chunk_prep, Q38_LIN_QK_HEADS, a.n_chunks, n_seq, 512, &a)) return -1;
+        if (ctx->launch(ctx->f_chunk_scan, Q38_LIN_V_HEADS * 4, n_seq, 1, 64 * Q38_GDN_SCAN_WAVES, &a)) return -1;
+    }
+    return 0;
 }
 
 int q38_gdn_step(q38_ctx *ctx, int n_seq, float *d_state, int64_t state_stride, const float *d_q,

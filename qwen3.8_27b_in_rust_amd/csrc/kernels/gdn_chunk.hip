@@ -254,7 +254,7 @@ extern "C" __global__ __launch_bounds__(kPrepThreads) void q38_gdn_chunk_prep(q3
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g4 = lane >> 4;
     const int r = lane & 15;
-    const int t0 = n * C;
+    const int t0 = (a.chunk0 + n) * C;
     const int cnt = min(C, a.n_tokens - t0);
     const size_t tok0 = (size_t)s * a.n_tokens + t0;
 
@@ -578,7 +578,7 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
     }
 
     for (int n = 0; n < a.n_chunks; ++n) {
-        const int t0 = n * C;
+        const int t0 = (a.chunk0 + n) * C;
         const int cnt = min(C, a.n_tokens - t0);
         const size_t tok0 = (size_t)s * a.n_tokens + t0;
         const bool more = n + 1 < a.n_chunks;

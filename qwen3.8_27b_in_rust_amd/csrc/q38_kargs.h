@@ -167,8 +167,13 @@ typedef struct {
     int32_t q_stride;
     int32_t v_stride;
     int32_t n_tokens;
-    int32_t n_chunks;
+    int32_t n_chunks;  /* chunks of this launch: chunk0 .. chunk0 + n_chunks - 1 */
+    int32_t chunk0;
+    int32_t pad_;
 } q38_gdn_chunk_args;
+/* chunks per prep/scan launch pair: a stage's records (16 x 48 x 158 KB, ~121 MB
+ * per sequence) stay in the last-level cache between the two launches */
+#define Q38_GDN_STAGE_CHUNKS 16
 
 /* Gated RMSNorm of ops.rs:735-740 on [n][48][128] recurrence outputs:
  * grid (n_tokens * n_seq, 48), 64 threads. */
