@@ -221,10 +221,12 @@ def test_linear_core_prefill_matches_reference(ctx, ref, synth, margin, T):
     check_state(margin, d_delta.download(), s_ref)
 
 
-def test_linear_core_prefill_two_sequences(ctx, ref, synth):
+@pytest.mark.parametrize("T", [70, 1100])
+def test_linear_core_prefill_two_sequences(ctx, ref, synth, T):
     """Two sequences' prompts in one call: the chunked kernels' sequence axis
-    (records, state slabs and outputs at (s*T + t)), with a partial last chunk."""
-    n, T = 2, 70
+    (records, state slabs and outputs at (s*T + t)), with a partial last chunk;
+    1100 tokens are two stages of chunks (16 and 2), the second partial."""
+    n = 2
     conv_w = synth.normal(631, 10240 * 4, sigma=0.5)
     dt = synth.normal(632, 48)
     a = -np.abs(synth.normal(633, 48))
