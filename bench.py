@@ -18,7 +18,8 @@ events stamped by each dispatch on the launch stream in the timed region.
 reference's) on the same data.
 
 Also measured under "extra" (all, or those --only names): prefill attention
-and chunked DeltaNet prefill of a 4096-token prompt, batched paged decode,
+and chunked DeltaNet prefill of a 4096-token prompt, linear_core over that
+prompt (with its conv/L2/gates and gated-norm kernels), batched paged decode,
 the launch floor, one-token linear_core over 48 layers, the 64-layer full
 stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
 the Q4_K/Q6_K FFN projections for 1 and 8 tokens, and the recurrent-state
@@ -435,6 +436,56 @@ def gdn_prefill(pkg, ctx, reps: int):
                     "bf16x3 MFMA products"}
 
 
+# linear_core over a prompt, per token: the conv/SiLU/L2/gates kernel reads
+# the raw qkv row (40,960 B) and the two raw gates (384 B) and writes the
+# same again; the gated RMSNorm reads o and z (2 x 24,576 B) and writes the
+# output (24,576 B)
+LC_PRE_BYTES_PER_TOKEN = 2 * (10240 * 4 + 2 * 48 * 4)
+LC_POST_BYTES_PER_TOKEN = 3 * 6144 * 4
+
+
+def linear_core_prefill(pkg, ctx, reps: int):
+    """linear_core over a 4096-token prompt of one layer (conv, SiLU, L2
+    norms and gates; the chunked recurrence; the gated RMSNorm): time per
+    call, and the two elementwise kernels' durations and bandwidth."""
+    T = PREFILL_T
+    sizes = {"conv_w": 10240 * 4, "dt": 48, "a": 48, "norm": 128}
+    w = {k: ctx.empty((n,)) for k, n in sizes.items()}
+    for i, (k, buf) in enumerate(w.items()):
+        ctx.fill_normal(buf, sizes[k], 0x51334c00 + i, sigma=0.1)
+    conv, delta = ctx.empty((30720,)), ctx.empty((48 * 128 * 128,))
+    ctx.fill_normal(conv, 30720, 0x51334c10)
+    ctx.fill_normal(delta, 48 * 128 * 128, 0x51334c11, sigma=0.02)
+    ins = [ctx.empty((T * n,)) for n in (10240, 6144, 48, 48)]
+    for i, (buf, n) in enumerate(zip(ins, (10240, 6144, 48, 48))):
+        ctx.fill_normal(buf, T * n, 0x51334c20 + i)
+    out = ctx.empty((T * 6144,))
+
+    def call():
+        ctx.linear_core(1, T, w["conv_w"], w["dt"], w["a"], w["norm"], conv, delta, *ins, out)
+
+    call()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    for _ in range(reps):
+        call()
+    ctx.record(e1)
+    ms = ctx.elapsed_ms(e0, e1) / reps
+    res = {"tokens": T, "ms": ms}
+    for name, per_token in (("q38_gdn_pre", LC_PRE_BYTES_PER_TOKEN), ("q38_gdn_post", LC_POST_BYTES_PER_TOKEN)):
+        ctx.kernel_timer_start(name, reps)
+        for _ in range(reps):
+            call()
+        k_ms, k_n = ctx.kernel_timer_stop()
+        us = k_ms * 1e3 / max(k_n, 1)
+        res[name] = {"us": us, "algorithmic_bytes": per_token * T,
+                     "gb_s": per_token * T / (us * 1e-6) / 1e9}
+    for b in (conv, delta, out, *ins, *w.values()):
+        b.free()
+    return res
+
+
 FFN_MATS = ((12, 17408, 5120, "gate"), (12, 17408, 5120, "up"), (14, 5120, 17408, "down"))
 QUANT_BLOCK_BYTES = {12: 144, 13: 176, 14: 210}
 GEMV_KERNELS = {12: "q38_gemv_q8k_q4k", 13: "q38_gemv_q8k_q5k", 14: "q38_gemv_q8k_q6k"}
@@ -630,6 +681,8 @@ EXTRAS = {
     "prefill_attention_4096": ("prefill attention, 4096-token causal prompt",
                                lambda pkg, ctx: prefill_attention(pkg, ctx, 5)),
     "gdn_prefill_4096": ("chunked Gated-DeltaNet prefill, 4096 tokens", lambda pkg, ctx: gdn_prefill(pkg, ctx, 5)),
+    "linear_core_prefill_4096": ("linear_core over a 4096-token prompt (one layer)",
+                                 lambda pkg, ctx: linear_core_prefill(pkg, ctx, 5)),
     "batched_decode_32": ("batched paged decode, 32 sequences, context ~U[1K, 32K]",
                           lambda pkg, ctx: batched_decode(pkg, ctx, 20, 3)),
     "launch_floor": ("empty kernel launches", lambda pkg, ctx: launch_floor(ctx, 500)),

@@ -231,7 +231,8 @@ typedef struct {
  * ops.rs:1084-1099, with n_seq 1).  Sequence s: d_conv_state + s*30720
  * ([10240][3]), d_delta_state + s*786432 ([48][128][128]).  Per token
  * (index s*n_tokens + t): d_qkv [10240] raw projection, d_z [6144], d_beta,
- * d_alpha [48] raw; d_out [6144] receives rmsnorm(o) * silu(z).
+ * d_alpha [48] raw; d_out [6144] receives rmsnorm(o) * silu(z).  With
+ * n_tokens > 1, d_conv_state, d_qkv, d_z and d_out must be 16-byte aligned.
  */
 int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weights *w,
                     float *d_conv_state, float *d_delta_state, const float *d_qkv,

@@ -1171,12 +1171,16 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
         a.arrivals = ctx->arrivals;
         return ctx->launch(ctx->f_gdn_decode, Q38_LIN_V_HEADS, n_seq, 1, 512, &a);
     }
-    const int n_chunks = (n_tokens + 63) / 64;
+    if (((uintptr_t)d_conv_state | (uintptr_t)d_qkv | (uintptr_t)d_z | (uintptr_t)d_out) % 16 != 0)
+        return fail("d_conv_state, d_qkv, d_z and d_out must be 16-byte aligned");
+    /* the conv runs of q38_gdn_pre read conv_state_in while the last run
+     * writes the shifted state: a separate buffer when there are several */
+    const int pre_runs = (n_tokens + Q38_GDN_PRE_TOKENS - 1) / Q38_GDN_PRE_TOKENS;
     const size_t toks = (size_t)n_seq * n_tokens;
     /* workspace: qkv after conv/SiLU/L2 | beta | g | conv state out |
      * recurrence output before the norm | chunk products */
     const size_t conv_floats = (size_t)n_seq * Q38_LIN_QKV_DIM * 3;
-    const size_t base_floats = toks * (Q38_LIN_QKV_DIM + 2 * Q38_LIN_V_HEADS) + (n_chunks > 1 ? conv_floats : 0);
+    const size_t base_floats = toks * (Q38_LIN_QKV_DIM + 2 * Q38_LIN_V_HEADS) + (pre_runs > 1 ? conv_floats : 0);
     const size_t o_floats = toks * Q38_LIN_V_DIM;
     const size_t chunk_floats = chunk_work_floats(n_seq, n_tokens);
     if (toks > 0x7FFFFFFFull) return fail("too many tokens");
@@ -1184,7 +1188,7 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
     float *x = static_cast<float *>(ctx->work);
     float *beta = x + toks * Q38_LIN_QKV_DIM;
     float *g = beta + toks * Q38_LIN_V_HEADS;
-    float *conv_out = n_chunks > 1 ? g + toks * Q38_LIN_V_HEADS : d_conv_state;
+    float *conv_out = pre_runs > 1 ? g + toks * Q38_LIN_V_HEADS : d_conv_state;
     float *o_raw = x + base_floats;
     float *chunk_work = o_raw + o_floats;
 
@@ -1203,8 +1207,8 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
     p.g_out = g;
     p.n_tokens = n_tokens;
     p.n_seq = n_seq;
-    if (ctx->launch(ctx->f_gdn_pre, 81, n_chunks, n_seq, 128, &p)) return -1;
-    if (n_chunks > 1)
+    if (ctx->launch(ctx->f_gdn_pre, Q38_LIN_QKV_DIM / 1024 + 1, pre_runs, n_seq, 256, &p)) return -1;
+    if (pre_runs > 1)
         Q38_HIP(hipMemcpyAsync(d_conv_state, conv_out, conv_floats * sizeof(float),
                                hipMemcpyDeviceToDevice, ctx->stream));
     /* prompt: chunked recurrence, then the gated RMSNorm */
@@ -1217,7 +1221,8 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
     pa.z = d_z;
     pa.norm_w = w->d_norm;
     pa.out = d_out;
-    return ctx->launch(ctx->f_gdn_post, (unsigned)toks, Q38_LIN_V_HEADS, 1, 64, &pa);
+    /* 16 (token, value head) rows per workgroup; toks * 48 rows */
+    return ctx->launch(ctx->f_gdn_post, (unsigned)(toks * (Q38_LIN_V_HEADS / 16)), 1, 1, 256, &pa);
 }
 
 /* ------------------------------------------------------------ projections */

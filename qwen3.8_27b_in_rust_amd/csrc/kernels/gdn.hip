@@ -198,77 +198,164 @@ extern "C" __global__ __launch_bounds__(512) void q38_gdn_decode(q38_gdn_decode_
     }
 }
 
-/* grid (81, n_chunks, n_seq), 128 threads.  x < 80: channels 128x..128x+127
- * (x < 16 the q heads, 16 <= x < 32 the k heads, then v) for tokens
- * 64y..64y+63; x == 80: the gates of those tokens.  Each thread rebuilds its
- * channel's 3-tap window from the raw inputs of the three previous tokens (or
- * from conv_state_in before the first token), so chunks are independent; the
- * chunk holding the last token writes the shifted state to conv_state_out,
- * which must differ from conv_state_in when there is more than one chunk. */
-extern "C" __global__ __launch_bounds__(128) void q38_gdn_pre(q38_gdn_pre_args a) {
-    __shared__ double red[2][2];
+/* grid (11, ceil(n_tokens / C), n_seq), 256 threads, C = Q38_GDN_PRE_TOKENS.
+ * x < 10: channels 1024x..1024x+1023, 4 adjacent channels per lane, so a
+ * half-wave holds one 128-channel head (x < 2 the q heads, 2 <= x < 4 the k
+ * heads, then v), for tokens Cy..Cy+C-1; x == 10: the gates of those tokens.
+ * Each lane rebuilds its channels' 3-tap windows from the raw inputs of the
+ * three previous tokens (or from conv_state_in before the first token), so
+ * runs are independent; the run holding the last token writes the shifted
+ * state to conv_state_out, which must differ from conv_state_in when there is
+ * more than one run.
+ *
+ * A lane issues the 16-byte loads of all its tokens at once (one memory round
+ * trip per workgroup, not one per token), runs the conv backwards in place
+ * over the window + tokens array, and the q/k half-waves form the C per-token
+ * L2 norms with one transposing reduction: at each xor distance a lane keeps
+ * the half of its partial sums whose token bit it owns and adds the partner's
+ * copy of that half, so after distances 16, 8, ... every lane holds one
+ * token's sum over the head (C/2 + C/4 + ... exchanges instead of 5 per
+ * token), and the owner of each token hands its norm to the other lanes. */
+extern "C" __global__ __launch_bounds__(256) void q38_gdn_pre(q38_gdn_pre_args a) {
+    constexpr int C = Q38_GDN_PRE_TOKENS;
+    constexpr int kLanesPerToken = 32 / C; /* lanes of a half-wave holding one token's sum */
+    static_assert(C >= 4 && C <= 32 && (C & (C - 1)) == 0, "tokens per run: a power of two, 4 to 32");
+    constexpr int kGroups = Q38_LIN_QKV_DIM / 1024;
     const int gx = blockIdx.x;
-    const int chunk = blockIdx.y;
+    const int run = blockIdx.y;
     const int s = blockIdx.z;
     const int tid = threadIdx.x;
     const int T = a.n_tokens;
-    const int t0 = chunk * 64;
-    const int t1 = min(T, t0 + 64);
-    const size_t tok0 = (size_t)s * T;
+    const int t0 = run * C;
+    const int n = min(T - t0, C);
+    const size_t tok0 = (size_t)s * T + t0;
 
-    if (gx == 80) {
-        for (int i = tid; i < (t1 - t0) * Q38_LIN_V_HEADS; i += 128) {
-            const int t = t0 + i / Q38_LIN_V_HEADS;
+    if (gx == kGroups) {
+        /* n * 48 gates, up to C * 48 / 256 per thread: every load before
+         * the first store */
+        constexpr int kPer = (C * Q38_LIN_V_HEADS + 255) / 256;
+        const int m = n * Q38_LIN_V_HEADS;
+        const float *br = a.beta_raw + tok0 * Q38_LIN_V_HEADS;
+        const float *ar = a.alpha_raw + tok0 * Q38_LIN_V_HEADS;
+        float bv[kPer], av[kPer], dtv[kPer], aav[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = min(tid + 256 * j, m - 1);
             const int h = i % Q38_LIN_V_HEADS;
-            const size_t at = (tok0 + t) * Q38_LIN_V_HEADS + h;
-            a.beta_out[at] = q38_sigmoid(a.beta_raw[at]);
-            a.g_out[at] = a.a[h] * q38_softplus(a.alpha_raw[at] + a.dt[h]);
+            bv[j] = br[i];
+            av[j] = ar[i];
+            dtv[j] = a.dt[h];
+            aav[j] = a.a[h];
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = tid + 256 * j;
+            if (i < m) {
+                a.beta_out[tok0 * Q38_LIN_V_HEADS + i] = q38_sigmoid(bv[j]);
+                a.g_out[tok0 * Q38_LIN_V_HEADS + i] = aav[j] * q38_softplus(av[j] + dtv[j]);
+            }
         }
         return;
     }
 
-    const int c = gx * 128 + tid;
-    const float w0 = a.conv_w[(size_t)c * 4 + 0];
-    const float w1 = a.conv_w[(size_t)c * 4 + 1];
-    const float w2 = a.conv_w[(size_t)c * 4 + 2];
-    const float w3 = a.conv_w[(size_t)c * 4 + 3];
-    const float *st_in = a.conv_state_in + (size_t)s * Q38_LIN_QKV_DIM * 3 + (size_t)c * 3;
-    /* window of the three raw inputs before t0: x_{t0-3}, x_{t0-2}, x_{t0-1} */
-    float win[3];
+    const int c = gx * 1024 + 4 * tid;
+    f32x4 w[4]; /* w[k]: tap k of the 4 channels */
+    {
+        f32x4 r[4];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        const int tp = t0 - 3 + i;
-        win[i] = tp < 0 ? st_in[tp + 3] : a.qkv_raw[(tok0 + tp) * Q38_LIN_QKV_DIM + c];
+        for (int j = 0; j < 4; ++j) r[j] = q38_ld4(a.conv_w + (size_t)(c + j) * 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = f32x4{r[0][k], r[1][k], r[2][k], r[3][k]};
     }
-    const bool normed = gx < 32;
-    const int wave = tid >> 6;
-    for (int t = t0; t < t1; ++t) {
-        const float x = a.qkv_raw[(tok0 + t) * Q38_LIN_QKV_DIM + c];
-        float y = win[0] * w0;
-        y += win[1] * w1;
-        y += win[2] * w2;
-        y += x * w3;
-        win[0] = win[1];
-        win[1] = win[2];
-        win[2] = x;
-        y = q38_silu(y);
-        if (normed) {
-            /* l2norm (ops.rs:562-571): f64 sum, f32 sqrt, floor 1e-6 */
-            double ss = q38_wave_sum_f64((double)y * (double)y);
-            if ((tid & 63) == 0) red[t & 1][wave] = ss;
-            __syncthreads();
-            const double sum = red[t & 1][0] + red[t & 1][1];
-            float norm = sqrtf((float)sum);
-            norm = fmaxf(norm, 1e-6f);
-            y *= 1.0f / norm;
+    const float *st_in = a.conv_state_in + (size_t)s * Q38_LIN_QKV_DIM * 3 + (size_t)c * 3;
+    const float *src = a.qkv_raw + tok0 * Q38_LIN_QKV_DIM + c;
+    /* e[0..2]: x_{t0-3}, x_{t0-2}, x_{t0-1}; e[3+i]: x_{t0+i} (the last
+     * token repeated past n) */
+    f32x4 e[3 + C];
+    if (t0 == 0) {
+        /* [4 channels][3 taps] from the state */
+        const f32x4 r0 = q38_ld4(st_in), r1 = q38_ld4(st_in + 4), r2 = q38_ld4(st_in + 8);
+        e[0] = f32x4{r0.x, r0.w, r1.z, r2.y};
+        e[1] = f32x4{r0.y, r1.x, r1.w, r2.z};
+        e[2] = f32x4{r0.z, r1.y, r2.x, r2.w};
+    } else {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) e[i] = q38_ld4(src - (long)(3 - i) * Q38_LIN_QKV_DIM);
+    }
+#pragma unroll
+    for (int i = 0; i < C; ++i) e[3 + i] = q38_ld4(src + (size_t)min(i, n - 1) * Q38_LIN_QKV_DIM);
+    /* conv1d + SiLU, last token first so e[3+i] is overwritten only after
+     * the windows of tokens i+1..i+3 have read it */
+#pragma unroll
+    for (int i = C - 1; i >= 0; --i) {
+        f32x4 y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v = e[i][j] * w[0][j];
+            v += e[i + 1][j] * w[1][j];
+            v += e[i + 2][j] * w[2][j];
+            v += e[i + 3][j] * w[3][j];
+            y[j] = q38_silu(v);
         }
-        a.qkv_out[(tok0 + t) * Q38_LIN_QKV_DIM + c] = y;
+        e[i + 3] = y;
     }
-    if (t1 == T) {
+    if (gx < 4) {
+        /* l2norm (ops.rs:562-571): f64 sum, f32 sqrt, floor 1e-6 */
+        const int lane = tid & 63;
+        double p[C];
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            const f32x4 y = e[3 + i];
+            p[i] = (double)y.x * (double)y.x + (double)y.y * (double)y.y + (double)y.z * (double)y.z +
+                   (double)y.w * (double)y.w;
+        }
+        int cnt = C; /* partial sums a lane still holds */
+#pragma unroll
+        for (int d = 16; d >= 1; d >>= 1) {
+            if (cnt > 1) {
+                const int h = cnt / 2;
+                const bool hi = lane & d;
+#pragma unroll
+                for (int j = 0; j < h; ++j) {
+                    const double keep = hi ? p[h + j] : p[j];
+                    const double send = hi ? p[j] : p[h + j];
+                    p[j] = keep + __shfl_xor(send, d, 64);
+                }
+                cnt = h;
+            } else {
+                p[0] += __shfl_xor(p[0], d, 64);
+            }
+        }
+        /* lane l of a half-wave holds token (l % 32) / kLanesPerToken */
+        float norm = sqrtf((float)p[0]);
+        norm = fmaxf(norm, 1e-6f);
+        const float inv = 1.0f / norm;
+        const int half = lane & 32;
+#pragma unroll
+        for (int i = 0; i < C; ++i) e[3 + i] *= __shfl(inv, half + i * kLanesPerToken, 64);
+    }
+    float *dst = a.qkv_out + tok0 * Q38_LIN_QKV_DIM + c;
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+        if (i < n) q38_st4(dst + (size_t)i * Q38_LIN_QKV_DIM, e[3 + i]);
+    if (t0 + n == T) {
+        /* the window after the last token: x_{T-3}, x_{T-2}, x_{T-1} */
+        const float *raw = a.qkv_raw + (size_t)s * T * Q38_LIN_QKV_DIM + c;
+        f32x4 v[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int tp = T - 3 + i;
+            if (tp >= 0) {
+                v[i] = q38_ld4(raw + (size_t)tp * Q38_LIN_QKV_DIM);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[i][j] = st_in[3 * j + tp + 3];
+            }
+        }
         float *st_out = a.conv_state_out + (size_t)s * Q38_LIN_QKV_DIM * 3 + (size_t)c * 3;
-        st_out[0] = win[0];
-        st_out[1] = win[1];
-        st_out[2] = win[2];
+        q38_st4(st_out, f32x4{v[0].x, v[1].x, v[2].x, v[0].y});
+        q38_st4(st_out + 4, f32x4{v[1].y, v[2].y, v[0].z, v[1].z});
+        q38_st4(st_out + 8, f32x4{v[2].z, v[0].w, v[1].w, v[2].w});
     }
 }
 

@@ -659,23 +659,40 @@ extern "C" __global__ __launch_bounds__(64 * kScanWaves) void q38_gdn_chunk_scan
     }
 }
 
-/* Gated RMSNorm (ops.rs:735-740) of one (token, value head): rmsnorm of the
- * 128 outputs with the f64 sum of squares, weight, times silu(z). */
-extern "C" __global__ __launch_bounds__(64) void q38_gdn_post(q38_gdn_post_args a) {
-    const size_t tok = blockIdx.x;
-    const int vh = blockIdx.y;
-    const int lane = threadIdx.x;
-    const size_t base = tok * Q38_LIN_V_DIM + vh * D;
-    const float x0 = a.o[base + lane];
-    const float x1 = a.o[base + lane + 64];
-    double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
-    ss = q38_wave_sum_f64(ss);
-    const float mean = (float)(ss / (double)D);
-    const float scale = 1.0f / sqrtf(mean + 1e-6f);
-    float y0 = x0 * scale * a.norm_w[lane];
-    float y1 = x1 * scale * a.norm_w[lane + 64];
-    y0 *= q38_silu(a.z[base + lane]);
-    y1 *= q38_silu(a.z[base + lane + 64]);
-    a.out[base + lane] = y0;
-    a.out[base + lane + 64] = y1;
+/* Gated RMSNorm (ops.rs:735-740) of (token, value head) rows: rmsnorm of the
+ * 128 outputs with the f64 sum of squares, weight, times silu(z).  grid
+ * (n_rows / 16), 256 threads: each wave takes 4 rows, a half-wave one row
+ * at a time with 4 consecutive columns per lane, both rows' loads issued
+ * before the first reduction. */
+extern "C" __global__ __launch_bounds__(256) void q38_gdn_post(q38_gdn_post_args a) {
+    const int lane = threadIdx.x & 63;
+    const int col = 4 * (lane & 31);
+    const size_t row0 = ((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 5);
+    const f32x4 nw = q38_ld4(a.norm_w + col);
+    f32x4 x[2], z[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const size_t at = (row0 + 2 * p) * D + col;
+        x[p] = q38_ld4(a.o + at);
+        z[p] = q38_ld4(a.z + at);
+    }
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        double ss = (double)x[p].x * (double)x[p].x + (double)x[p].y * (double)x[p].y +
+                    (double)x[p].z * (double)x[p].z + (double)x[p].w * (double)x[p].w;
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        const float mean = (float)(ss / (double)D);
+        const float scale = 1.0f / sqrtf(mean + 1e-6f);
+        f32x4 y;
+        y.x = x[p].x * scale * nw.x;
+        y.y = x[p].y * scale * nw.y;
+        y.z = x[p].z * scale * nw.z;
+        y.w = x[p].w * scale * nw.w;
+        y.x *= q38_silu(z[p].x);
+        y.y *= q38_silu(z[p].y);
+        y.z *= q38_silu(z[p].z);
+        y.w *= q38_silu(z[p].w);
+        q38_st4(a.out + (row0 + 2 * p) * D + col, y);
+    }
 }

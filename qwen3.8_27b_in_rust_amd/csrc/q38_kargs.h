@@ -176,7 +176,8 @@ typedef struct {
 #define Q38_GDN_STAGE_CHUNKS 16
 
 /* Gated RMSNorm of ops.rs:735-740 on [n][48][128] recurrence outputs:
- * grid (n_tokens * n_seq, 48), 64 threads. */
+ * grid (n_tokens * n_seq * 3), 256 threads, 16 rows per workgroup; every
+ * pointer 16-byte aligned. */
 typedef struct {
     const float *o;    /* [(s*T + t)*6144 + vh*128 + c] */
     const float *z;    /* same layout */
@@ -186,7 +187,10 @@ typedef struct {
 
 /* conv1d(k=4) with state shift, SiLU, per-head L2 norm of q and k, and the
  * beta / decay gates, for n_tokens consecutive tokens of n_seq sequences.
- * grid (81, n_seq): x < 80 is a 128-channel group, x == 80 the gates. */
+ * grid (11, ceil(n_tokens / Q38_GDN_PRE_TOKENS), n_seq), 256 threads: x < 10
+ * is a 1024-channel group, x == 10 the gates, y a run of Q38_GDN_PRE_TOKENS
+ * tokens.  qkv_raw, conv_state_in and conv_state_out 16-byte aligned. */
+#define Q38_GDN_PRE_TOKENS 16
 typedef struct {
     const float *qkv_raw;   /* [(s*T + t)*10240] */
     const float *conv_w;    /* [10240][4] */

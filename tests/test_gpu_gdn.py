@@ -192,7 +192,7 @@ def test_linear_core_decode_matches_reference(ctx, ref, synth, margin):
     check_state(margin, d_delta.download(), s_ref)
 
 
-@pytest.mark.parametrize("T", [5, 70, 200])
+@pytest.mark.parametrize("T", [5, 40, 70, 200])
 def test_linear_core_prefill_matches_reference(ctx, ref, synth, margin, T):
     """batch_linear_attention's token loop (ops.rs:1088-1099) in one call."""
     conv_w = synth.normal(611, 10240 * 4, sigma=0.5)
