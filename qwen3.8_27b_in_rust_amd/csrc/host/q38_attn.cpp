@@ -131,6 +131,8 @@ struct q38_ctx {
     int split_tokens = 0; /* context tokens per decode workgroup; 0: chosen per launch */
     int clock_khz = 0;
     int lds_bytes = 0;
+    int lds_per_cu = 0;
+    int gemv_occupancy[3] = {1, 1, 1}; /* Q4_K, Q5_K, Q6_K GEMV workgroups a CU holds (registers) */
     char name[256] = {0};
     /* this device's copy of the fixed scratch array (q38_full_core_noalloc) */
     void *scratch = nullptr;
@@ -299,6 +301,7 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     ctx->cu_count = prop.multiProcessorCount;
     ctx->clock_khz = prop.clockRate;
     ctx->lds_bytes = (int)prop.sharedMemPerBlock;
+    ctx->lds_per_cu = (int)prop.maxSharedMemoryPerMultiProcessor;
     snprintf(ctx->name, sizeof(ctx->name), "%.200s (%.40s)", prop.name, prop.gcnArchName);
     Q38_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
     {
@@ -343,6 +346,14 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q4k, ctx->mod_proj, "q38_gemv_q8k_q4k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q5k, ctx->mod_proj, "q38_gemv_q8k_q5k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q6k, ctx->mod_proj, "q38_gemv_q8k_q6k"));
+    {
+        const hipFunction_t gv[3] = {ctx->f_gemv_q4k, ctx->f_gemv_q5k, ctx->f_gemv_q6k};
+        for (int i = 0; i < 3; ++i) {
+            int n = 0;
+            Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, gv[i], 256, 0));
+            ctx->gemv_occupancy[i] = std::max(1, n);
+        }
+    }
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[0], ctx->mod_proj, "q38_gemm_q8k_q4k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[1], ctx->mod_proj, "q38_gemm_q8k_q5k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[2], ctx->mod_proj, "q38_gemm_q8k_q6k"));
@@ -1275,11 +1286,25 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     const int blocks = width / Q38_Q8K_BLOCK;
     int tok_pass = std::max(1, std::min(Q38_GEMV_TOKENS, Q38_GEMV_ACT_LDS / (blocks * Q38_GEMV_REC_BYTES)));
     tok_pass = std::min(tok_pass, n_tokens);
-    /* rows per workgroup: up to Q38_GEMV_UNITS_MAX units (four per lane), and
-     * the per-token terms in at most 16 KiB of LDS; fewer rows when that
-     * leaves a matrix under 256 workgroups (small matrices), so every CU gets
-     * work */
+    /* rows per workgroup: up to Q38_GEMV_UNITS_MAX units (four per lane), the
+     * per-token terms in at most 16 KiB of LDS, and few enough rows that the
+     * launch has about as many workgroups as the CUs hold at once: a lane
+     * keeps one 144-210 byte block in flight, so the bytes a CU has in
+     * flight -- and with them its share of the bandwidth -- grow with the
+     * workgroups it runs side by side */
     const int max_units = std::min(Q38_GEMV_UNITS_MAX, 4096 / tok_pass);
+    const int ti_occ = ggml_type == Q38_GGML_Q4_K ? 0 : ggml_type == Q38_GGML_Q5_K ? 1 : 2;
+    const long tok_groups_all = ((long)n_tokens + tok_pass - 1) / tok_pass;
+    int target_per_wg = max_units / blocks;
+    {
+        long all_rows = 0;
+        for (int i = 0; i < n_mats; ++i) all_rows += std::max(rows[i], 0);
+        const long lds_max = (long)tok_pass * blocks * Q38_GEMV_REC_BYTES + (long)tok_pass * max_units * 4;
+        long occ = ctx->gemv_occupancy[ti_occ];
+        if (ctx->lds_per_cu > 0) occ = std::max(1L, std::min(occ, ctx->lds_per_cu / lds_max));
+        const long slots = std::max(1L, (long)ctx->cu_count * occ / std::max(1L, tok_groups_all));
+        target_per_wg = (int)std::max(1L, std::min((long)target_per_wg, (all_rows + slots - 1) / slots));
+    }
     q38_gemv_args a;
     memset(&a, 0, sizeof(a));
     long wgs = 0;
@@ -1289,8 +1314,7 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
         if (rows[i] == 0) continue; /* nothing to compute for an empty matrix */
         if (d_weights[i] == nullptr || d_out[i] == nullptr) return fail("NULL weights or output (matrix %d)", i);
         if ((uintptr_t)d_weights[i] % 16 != 0) return fail("d_weights[%d] must be 16-byte aligned", i);
-        int per_wg = max_units / blocks;
-        if (((long)rows[i] + per_wg - 1) / per_wg < 256) per_wg = std::max(1, std::min(per_wg, rows[i] / 256));
+        const int per_wg = target_per_wg;
         a.weights[kept] = static_cast<const uint8_t *>(d_weights[i]);
         a.out[kept] = d_out[i];
         a.rows[kept] = rows[i];
