@@ -159,5 +159,16 @@ def test_gdn_and_split_argument_checks(pkg, ctx):
     for bad in (1, 63, 100, 8192, -64):
         _fails(pkg, lambda: ctx.set_decode_split(bad), "multiple of 64")
     ctx.set_decode_split(0)
+    # linear_core over a prompt reads and writes 16-byte vectors: a buffer
+    # one float off is refused before anything is launched
+    T = 4
+    w = [ctx.empty((n,)) for n in (40960, 48, 48, 128)]
+    bufs = {"conv": ctx.empty((30720 + 4,)), "qkv": ctx.empty((T * 10240 + 4,)), "z": ctx.empty((T * 6144 + 4,)),
+            "out": ctx.empty((T * 6144 + 4,))}
+    delta, gates = ctx.empty((786432,)), ctx.empty((2 * T * 48,))
+    for bad in bufs:
+        p = {k: (v.offset(1) if k == bad else v.ptr) for k, v in bufs.items()}
+        _fails(pkg, lambda: ctx.linear_core(1, T, *w, p["conv"], delta, p["qkv"], p["z"], gates, gates.offset(T * 48),
+                                            p["out"]), "16-byte aligned")
     with pytest.raises(pkg.Q38Error, match="decode limit"):
         pkg.KVCache(ctx, n_slots=1, max_pages=1, max_seqs=1, max_tokens_per_seq=(1 << 24) + 16)
