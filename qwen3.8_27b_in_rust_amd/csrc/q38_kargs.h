@@ -190,7 +190,7 @@ typedef struct {
  * grid (11, ceil(n_tokens / Q38_GDN_PRE_TOKENS), n_seq), 256 threads: x < 10
  * is a 1024-channel group, x == 10 the gates, y a run of Q38_GDN_PRE_TOKENS
  * tokens.  qkv_raw, conv_state_in and conv_state_out 16-byte aligned. */
-#define Q38_GDN_PRE_TOKENS 16
+#define Q38_GDN_PRE_TOKENS 8
 typedef struct {
     const float *qkv_raw;   /* [(s*T + t)*10240] */
     const float *conv_w;    /* [10240][4] */
