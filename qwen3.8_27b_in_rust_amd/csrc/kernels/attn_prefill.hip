@@ -119,8 +119,12 @@ Q38_DEV const uint4 *image_of(const q38_prefill_args &a, int j, int kb) {
 /* Split K/V blocks 0 .. n_kblocks-1 of kv head blockIdx.y into bf16 hi/lo
  * block images (grid (n_kblocks, 4), 256 threads).  Keys past the prompt's
  * last position read that position (finite data; the causal mask gives them
- * weight 0 in every row that can see them). */
+ * weight 0 in every row that can see them).  The K part goes out row by row;
+ * the transposed V part is assembled in LDS (a 4-byte write per key pair and
+ * dim) and then streamed to the image in 16-byte stores, so neither part is
+ * written with scattered small stores. */
 extern "C" __global__ __launch_bounds__(256) void q38_kv_split_mfma(q38_prefill_args a) {
+    __shared__ __attribute__((aligned(16))) __bf16 vimg[2][Q38_ATTN_HEAD_DIM][kVRow];
     const int kb = blockIdx.x;
     const int j = blockIdx.y;
     const int tid = threadIdx.x;
@@ -141,10 +145,15 @@ extern "C" __global__ __launch_bounds__(256) void q38_kv_split_mfma(q38_prefill_
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int d = 4 * c4 + e;
-            *reinterpret_cast<bf16x2 *>(&img->vt[0][d][slot]) = bf16x2{s0.hi[e], s1.hi[e]};
-            *reinterpret_cast<bf16x2 *>(&img->vt[1][d][slot]) = bf16x2{s0.lo[e], s1.lo[e]};
+            *reinterpret_cast<bf16x2 *>(&vimg[0][d][slot]) = bf16x2{s0.hi[e], s1.hi[e]};
+            *reinterpret_cast<bf16x2 *>(&vimg[1][d][slot]) = bf16x2{s0.lo[e], s1.lo[e]};
         }
     }
+    __syncthreads();
+    /* the V part, padding included, as 16-byte pieces */
+    const uint4 *src = reinterpret_cast<const uint4 *>(&vimg[0][0][0]);
+    uint4 *dst = reinterpret_cast<uint4 *>(&img->vt[0][0][0]);
+    for (int i = tid; i < (int)(sizeof(vimg) / 16); i += 256) dst[i] = src[i];
 }
 
 extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(q38_prefill_args a) {
