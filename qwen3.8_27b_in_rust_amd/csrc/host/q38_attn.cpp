@@ -1001,7 +1001,8 @@ int q38_attn_pre(q38_ctx *ctx, int n_tokens, int pos0, const float *d_q_norm, co
     a.pos0 = pos0;
     a.n_tokens = n_tokens;
     a.theta_scale = ctx->rope_theta_scale;
-    return ctx->launch(ctx->f_attn_pre, n_tokens, Q38_ATTN_HEADS + Q38_ATTN_KV_HEADS, 1, 64, &a);
+    static_assert((Q38_ATTN_HEADS + Q38_ATTN_KV_HEADS) % 4 == 0, "4 heads per workgroup");
+    return ctx->launch(ctx->f_attn_pre, n_tokens, (Q38_ATTN_HEADS + Q38_ATTN_KV_HEADS) / 4, 1, 256, &a);
 }
 
 int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,

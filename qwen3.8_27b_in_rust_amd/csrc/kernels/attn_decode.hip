@@ -97,37 +97,6 @@ Q38_DEV void decode_rows(DecodeState &st, const f32x4 (&q0)[Q38_ATTN_GROUP],
     }
 }
 
-/* RMSNorm with weight w (rms_scale / rmsnorm_inplace, ops.rs:476-498: f64 sum
- * of squares, eps 1e-6), then RoPE on dims 0..63 (ops.rs:595-610: pairs (p,
- * p+32), theta_0 = position, theta_{p+1} = theta_p * 1e7^(-2/64) by repeated
- * f32 multiplication) of one 256-dim head held 4 dims per lane by a whole
- * wave (lane l: dims 4l .. 4l+3).  Every f32 square is exact in f64, so the
- * f64 sum rounds to the same f32 mean in any order. */
-Q38_DEV void q38_rope_lanes(f32x4 &x, int l, int position, float theta_scale) {
-    /* lanes 0..7 hold dims 0..31, lanes 8..15 their partners 32..63 */
-    f32x4 partner;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) partner[c] = __shfl_xor(x[c], 8, 64);
-    if (l < 16) {
-        const int p0 = 4 * (l & 7);
-        float theta = (float)position;
-        for (int i = 0; i < p0; ++i) theta *= theta_scale;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float cosine = cosf(theta);
-            const float sine = sinf(theta);
-            if (l < 8) {
-                const float x0 = x[c], x1 = partner[c];
-                x[c] = x0 * cosine - x1 * sine;
-            } else {
-                const float x0 = partner[c], x1 = x[c];
-                x[c] = x0 * sine + x1 * cosine;
-            }
-            theta *= theta_scale;
-        }
-    }
-}
-
 /* RoPE angles of one position, once: pair p gets theta_p = position *
  * scale^p by p repeated f32 multiplications (the reference's rounding), and
  * cs[p] = (cos, sin) of it; lane p < 32 of the calling wave forms pair p. */
@@ -140,7 +109,10 @@ Q38_DEV void q38_rope_table(float (*cs)[2], int lane, int position, float theta_
     }
 }
 
-/* q38_rope_lanes with the angles read from a table of q38_rope_table */
+/* RoPE on dims 0..63 (ops.rs:595-610: pairs (p, p+32), theta_0 = position,
+ * theta_{p+1} = theta_p * 1e7^(-2/64) by repeated f32 multiplication) of one
+ * 256-dim head held 4 dims per lane by a whole wave (lane l: dims 4l ..
+ * 4l+3), with the angles' cosines and sines from a q38_rope_table */
 Q38_DEV void q38_rope_lanes_cs(f32x4 &x, int l, const float (*cs)[2]) {
     f32x4 partner;
 #pragma unroll
@@ -168,17 +140,6 @@ Q38_DEV float q38_rms_scale_of(double ss) {
     return 1.0f / sqrtf(mean + 1e-6f);
 }
 
-Q38_DEV void q38_norm_rope4(f32x4 &x, f32x4 w, int lane, int position, float theta_scale) {
-    double ss = (double)x.x * (double)x.x + (double)x.y * (double)x.y + (double)x.z * (double)x.z +
-                (double)x.w * (double)x.w;
-    ss = q38_wave_sum_f64(ss);
-    const float mean = (float)(ss / (double)Q38_ATTN_HEAD_DIM);
-    const float scale = 1.0f / sqrtf(mean + 1e-6f);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) x[c] = x[c] * scale * w[c];
-    q38_rope_lanes(x, lane, position, theta_scale);
-}
-
 /* The same for a head held by a half-wave, lane li: dims 4li .. 4li+3 (x0)
  * and 128 + 4li .. (x1); the angles from a q38_rope_table. */
 Q38_DEV void q38_norm_rope8(f32x4 &x0, f32x4 &x1, f32x4 w0, f32x4 w1, int li, const float (*cs)[2]) {
@@ -196,7 +157,10 @@ Q38_DEV void q38_norm_rope8(f32x4 &x0, f32x4 &x1, f32x4 w0, f32x4 w1, int li, co
     q38_rope_lanes_cs(x0, li, cs);
 }
 
-/* The same for a head held 4 dims per lane by a whole wave */
+/* RMSNorm with weight w (rms_scale / rmsnorm_inplace, ops.rs:476-498: f64 sum
+ * of squares, eps 1e-6), then the RoPE of q38_rope_lanes_cs, of a head held 4
+ * dims per lane by a whole wave.  Every f32 square is exact in f64, so the f64
+ * sum rounds to the same f32 mean in any order. */
 Q38_DEV void q38_norm_rope4_cs(f32x4 &x, f32x4 w, int lane, const float (*cs)[2]) {
     double ss = (double)x.x * (double)x.x + (double)x.y * (double)x.y + (double)x.z * (double)x.z +
                 (double)x.w * (double)x.w;
@@ -597,11 +561,15 @@ extern "C" __global__ __launch_bounds__(256) void q38_kv_copy(q38_kv_copy_args a
 
 /* q/gate split + q RMSNorm (ops.rs:832-843), k RMSNorm (ops.rs:844-850) and
  * RoPE on lanes (p, p+32), p < 32 (ops.rs:595-610, applied :851-856).
- * grid (n_tokens, 28), one wave per head, lane i holds dims 4i..4i+3. */
-extern "C" __global__ __launch_bounds__(64) void q38_attn_pre(q38_attn_pre_args a) {
+ * grid (n_tokens, 7), 256 threads: one wave per head (4 per workgroup), lane i
+ * holds dims 4i..4i+3.  The token's 32 RoPE angles and their cosines and
+ * sines are formed once per workgroup (wave 0, while every wave's loads are
+ * in flight) and read from LDS by its 4 heads. */
+extern "C" __global__ __launch_bounds__(256) void q38_attn_pre(q38_attn_pre_args a) {
+    __shared__ float cs[32][2];
     const int t = blockIdx.x;
-    const int hd = blockIdx.y;
-    const int lane = threadIdx.x;
+    const int hd = 4 * blockIdx.y + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int position = a.pos0 + t;
     const bool is_q = hd < Q38_ATTN_HEADS;
     const float *src;
@@ -620,6 +588,9 @@ extern "C" __global__ __launch_bounds__(64) void q38_attn_pre(q38_attn_pre_args 
         dst = a.k_out + ((size_t)t * Q38_ATTN_KV_HEADS + kh) * Q38_ATTN_HEAD_DIM;
     }
     f32x4 x = q38_ld4(src + 4 * lane);
-    q38_norm_rope4(x, q38_ld4(w + 4 * lane), lane, position, a.theta_scale);
+    const f32x4 wv = q38_ld4(w + 4 * lane);
+    if (threadIdx.x < 64) q38_rope_table(cs, lane, position, a.theta_scale);
+    __syncthreads();
+    q38_norm_rope4_cs(x, wv, lane, cs);
     q38_st4(dst + 4 * lane, x);
 }
