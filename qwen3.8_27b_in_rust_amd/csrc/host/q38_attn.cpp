@@ -1030,6 +1030,79 @@ int q38_full_core_noalloc(q38_kv *kv, int layer, int n_seq, const int32_t *seq_i
                       kv->ctx->scratch, Q38_NOALLOC_SCRATCH_BYTES);
 }
 
+namespace {
+
+/* Spread the 3 * n_qblocks (head pair, query block) jobs of one kv head over
+ * Q38_PREFILL_BINS bins of at most Q38_PREFILL_JOBS_MAX jobs, a job weighing
+ * the key blocks its workgroup streams: longest first onto the lightest bin,
+ * then moves and swaps out of the heaviest bin while they lower it.  Writes
+ * the table (0xFF past a bin's last job) and returns the jobs per bin. */
+int place_prefill_jobs(int base_pos, int n_tokens, int n_qblocks, uint8_t *table) {
+    struct Job {
+        int weight;
+        uint8_t code;
+    };
+    std::vector<Job> jobs;
+    for (int qb = 0; qb < n_qblocks; ++qb) {
+        const int q_last = std::min((qb + 1) * Q38_PREFILL_QUERIES, n_tokens) - 1;
+        const int weight = (base_pos + q_last) / Q38_PREFILL_KEYS + 1;
+        for (int hp = 0; hp < Q38_PREFILL_HEAD_PAIRS; ++hp) jobs.push_back({weight, (uint8_t)(hp << 6 | qb)});
+    }
+    std::stable_sort(jobs.begin(), jobs.end(), [](const Job &x, const Job &y) { return x.weight > y.weight; });
+    constexpr int kBins = Q38_PREFILL_BINS, kMax = Q38_PREFILL_JOBS_MAX;
+    std::vector<std::vector<Job>> bins(kBins);
+    std::vector<long> load(kBins, 0);
+    for (const Job &jb : jobs) {
+        int best = -1;
+        for (int b = 0; b < kBins; ++b)
+            if ((int)bins[b].size() < kMax && (best < 0 || load[b] < load[best])) best = b;
+        bins[best].push_back(jb);
+        load[best] += jb.weight;
+    }
+    for (int it = 0; it < 4096; ++it) {
+        const int hi = (int)(std::max_element(load.begin(), load.end()) - load.begin());
+        long best_max = load[hi];
+        int bb = -1, bx = -1, by = -1; /* by < 0: a move */
+        for (int b = 0; b < kBins; ++b) {
+            if (b == hi) continue;
+            for (int x = 0; x < (int)bins[hi].size(); ++x) {
+                const long wx = bins[hi][x].weight;
+                if ((int)bins[b].size() < kMax) {
+                    const long m = std::max(load[hi] - wx, load[b] + wx);
+                    if (m < best_max) best_max = m, bb = b, bx = x, by = -1;
+                }
+                for (int y = 0; y < (int)bins[b].size(); ++y) {
+                    const long wy = bins[b][y].weight;
+                    const long m = std::max(load[hi] - wx + wy, load[b] - wy + wx);
+                    if (m < best_max) best_max = m, bb = b, bx = x, by = y;
+                }
+            }
+        }
+        if (bb < 0) break;
+        const Job jx = bins[hi][bx];
+        if (by < 0) {
+            bins[hi].erase(bins[hi].begin() + bx);
+            bins[bb].push_back(jx);
+            load[hi] -= jx.weight;
+            load[bb] += jx.weight;
+        } else {
+            const Job jy = bins[bb][by];
+            bins[hi][bx] = jy;
+            bins[bb][by] = jx;
+            load[hi] += jy.weight - jx.weight;
+            load[bb] += jx.weight - jy.weight;
+        }
+    }
+    int per = 1;
+    for (const auto &b : bins) per = std::max(per, (int)b.size());
+    memset(table, 0xFF, (size_t)kBins * kMax);
+    for (int b = 0; b < kBins; ++b)
+        for (int i = 0; i < (int)bins[b].size(); ++i) table[b * per + i] = bins[b][i].code;
+    return per;
+}
+
+}  // namespace
+
 int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens, const float *d_q,
                      const float *d_k, const float *d_v, const float *d_gate, float *d_out) {
     if (kv == nullptr) return fail("kv is NULL");
@@ -1060,8 +1133,15 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     a.n_tokens = n_tokens;
     a.n_qblocks = (n_tokens + kQueryBlock - 1) / kQueryBlock;
     a.n_kblocks = (int)((end - 1) / Q38_PREFILL_KEYS + 1);
-    const size_t n_wg = (size_t)a.n_qblocks * Q38_ATTN_KV_HEADS * Q38_PREFILL_HEAD_PAIRS;
+    size_t n_wg = (size_t)a.n_qblocks * Q38_ATTN_KV_HEADS * Q38_PREFILL_HEAD_PAIRS;
     if (n_wg > 0x7FFFFFFFull) return fail("prompt too long");
+    if (a.n_qblocks <= 64) {
+        /* few jobs per CU: placed here so that every bin (one workgroup per CU)
+         * gets the same number of key blocks, which the hardware's
+         * longest-first order cannot do with 3 jobs per CU */
+        a.jobs_per_wg = place_prefill_jobs(base_pos, n_tokens, a.n_qblocks, a.jobs);
+        n_wg = (size_t)Q38_ATTN_KV_HEADS * Q38_PREFILL_BINS;
+    }
     /* the workspace for the K/V block images before anything is changed */
     if (ctx->ensure_work((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES)) return -1;
     a.images = ctx->work;

@@ -158,274 +158,316 @@ extern "C" __global__ __launch_bounds__(256) void q38_kv_split_mfma(q38_prefill_
 
 extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(q38_prefill_args a) {
     __shared__ __attribute__((aligned(16))) Tile tiles[2];
-
-    /* workgroup -> (kv head j, query block, head pair): consecutive
-     * workgroups go to the 8 XCDs in turn, so XCDs 2j and 2j+1 take kv head
-     * j and its K/V images stay in those two L2s; the 3 head pairs of a
-     * query block run side by side on the same images; the longest causal
-     * rows start first */
-    const int L = blockIdx.x;
-    const int nq = a.n_qblocks;
-    int j, c;
-    if ((nq & 1) == 0) {
-        j = (L & 7) >> 1;
-        c = 2 * (L >> 3) + (L & 1);
-    } else {
-        j = L & 3;
-        c = L >> 2;
-    }
-    const int qi = c / Q38_PREFILL_HEAD_PAIRS;
-    const int hp = c - Q38_PREFILL_HEAD_PAIRS * qi;
-    const int qb = nq - 1 - qi;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5;  /* lane half */
-    const int col = lane & 31;
-    const int head = j * Q38_ATTN_GROUP + 2 * hp + (wave & 1);
-    const int q0 = qb * kQ + kQW * (wave >> 1);      /* the wave's first query token */
-    const int q_last = min(qb * kQ + kQ, a.n_tokens) - 1; /* last real query token of the block */
-    const int kmax = a.base_pos + q_last;            /* last key position any row needs */
-    const int n_kb = kmax / kKB + 1;
-    const bool active = q0 <= q_last;                /* the wave has real rows */
-    const int pos_first = a.base_pos + q0;           /* the wave's first row's position */
-    const int pos_last = a.base_pos + min(q0 + kQW - 1, q_last);
-    const int qpos = a.base_pos + q0 + col;          /* this lane's query column */
-
-    /* Q^T as the B operand: lane l holds query col, dims 16ks + 8h .. +7 */
-    bf16x8 q_hi[16], q_lo[16];
-    {
-        const int tq = min(q0 + col, q_last);
-        const float *qp = a.q + ((size_t)tq * Q38_ATTN_HEADS + head) * Q38_ATTN_HEAD_DIM + 8 * h;
-#pragma unroll
-        for (int ks = 0; ks < 16; ++ks) {
-            /* scaled to base-2 score units before the split */
-            const Split4 s0 = split4(q38_ld4(qp + 16 * ks) * Q38_SCORE_LOG2);
-            const Split4 s1 = split4(q38_ld4(qp + 16 * ks + 4) * Q38_SCORE_LOG2);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                q_hi[ks][e] = s0.hi[e];
-                q_hi[ks][4 + e] = s1.hi[e];
-                q_lo[ks][e] = s0.lo[e];
-                q_lo[ks][4 + e] = s1.lo[e];
-            }
-            /* opaque to the compiler, which would otherwise keep f32 Q and
-             * split it again in every block; held in accumulation registers
-             * (the matrix unit reads its B operand from them), which leaves
-             * the vector registers to the scores, P and the fragments */
-            asm volatile("" : "+a"(q_hi[ks]), "+a"(q_lo[ks]));
-        }
-    }
-
-    float m = -INFINITY; /* query col's reference, in both lane halves */
-    float l = 0.0f;       /* the sum of this lane's weights (its half of the keys) */
-    f32x16 O[8];                   /* O[n][4J+i] = row 8J+4h+i, dim 32n + col */
-    /* zeros made by the matrix unit (0 x 0 + 0), so the accumulators start,
-     * and stay, in accumulation registers */
-    auto clear_o = [&]() {
-        const bf16x8 z = {};
-        f32x16 zc;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) zc[v] = 0.0f;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(z, z, zc, 0, 0, 0);
-    };
-    clear_o();
     /* a wave whose block passed its reference max sets the flag of the
      * block's parity; every wave reads it after the block's barrier */
     __shared__ int restart_flag[2];
-    if (tid < 2) restart_flag[tid] = 0;
+    if (threadIdx.x < 2) restart_flag[threadIdx.x] = 0;
 
-    /* block images go HBM -> LDS by direct-to-LDS loads (no registers):
-     * wave w moves 1 KiB pieces w, w+4, ...; lane l's 16 bytes land at the
-     * piece's LDS base + 16 l.  Written as assembly so the compiler's
-     * wait-count pass does not see them: it cannot tell the two buffers
-     * apart and would wait for the next block's image before the first read
-     * of the current one.  The loop waits for them itself (s_waitcnt 0 and
-     * the barrier that ends each block).  M0 carries the LDS address; nothing
-     * else in the kernel uses M0. */
-    auto fetch = [&](int kb, int buf) {
-        const char *img = reinterpret_cast<const char *>(image_of(a, j, kb));
-        char *dst = reinterpret_cast<char *>(&tiles[buf]);
-        for (int p = wave; p < kPieces; p += kWaves) {
-            const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) char *)(dst + p * 1024);
-            /* one wait state between the M0 write and the load that reads it */
-            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds),
-                         "v"(img + p * 1024 + lane * 16)
-                         : "memory");
+    /* Jobs: (kv head j, head pair, query block).  Consecutive workgroups go
+     * to the 8 XCDs in turn, so XCDs 2j and 2j+1 take kv head j and its K/V
+     * images stay in those two L2s.  With a job table (jobs_per_wg > 0) the
+     * grid is 4 kv heads x Q38_PREFILL_BINS workgroups and each runs the jobs
+     * the host placed in its bin, so that every CU gets the same number of key
+     * blocks; without one, one job per workgroup, the longest causal rows
+     * first, the 3 head pairs of a query block side by side. */
+    const int L = blockIdx.x;
+    const int nq = a.n_qblocks;
+    const int n_jobs = a.jobs_per_wg > 0 ? a.jobs_per_wg : 1;
+    for (int job = 0; job < n_jobs; ++job) {
+        int j, hp, qb;
+        if (a.jobs_per_wg > 0) {
+            j = (L & 7) >> 1;
+            const int code = a.jobs[(2 * (L >> 3) + (L & 1)) * a.jobs_per_wg + job];
+            if (code == 0xFF) break; /* the bin's jobs are done (the same for every wave) */
+            hp = code >> 6;
+            qb = code & 63;
+        } else {
+            int c;
+            if ((nq & 1) == 0) {
+                j = (L & 7) >> 1;
+                c = 2 * (L >> 3) + (L & 1);
+            } else {
+                j = L & 3;
+                c = L >> 2;
+            }
+            const int qi = c / Q38_PREFILL_HEAD_PAIRS;
+            hp = c - Q38_PREFILL_HEAD_PAIRS * qi;
+            qb = nq - 1 - qi;
         }
-    };
-    fetch(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+        const int tid = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int h = lane >> 5;  /* lane half */
+        const int col = lane & 31;
+        const int head = j * Q38_ATTN_GROUP + 2 * hp + (wave & 1);
+        const int q0 = qb * kQ + kQW * (wave >> 1);      /* the wave's first query token */
+        const int q_last = min(qb * kQ + kQ, a.n_tokens) - 1; /* last real query token of the block */
+        const int kmax = a.base_pos + q_last;            /* last key position any row needs */
+        const int n_kb = kmax / kKB + 1;
+        const bool active = q0 <= q_last;                /* the wave has real rows */
+        const int pos_first = a.base_pos + q0;           /* the wave's first row's position */
+        const int pos_last = a.base_pos + min(q0 + kQW - 1, q_last);
+        const int qpos = a.base_pos + q0 + col;          /* this lane's query column */
 
-    /* this wave's share of an image: pieces wave + 4i, i < kMyPieces */
-    constexpr int kMyPieces = (kPieces + kWaves - 1) / kWaves;
-    static_assert(kMyPieces <= 16 + 3, "pieces fit the QK steps and the first PV steps");
+        /* Q^T as the B operand: lane l holds query col, dims 16ks + 8h .. +7 */
+        bf16x8 q_hi[16], q_lo[16];
+        {
+            const int tq = min(q0 + col, q_last);
+            const float *qp = a.q + ((size_t)tq * Q38_ATTN_HEADS + head) * Q38_ATTN_HEAD_DIM + 8 * h;
+#pragma unroll
+            for (int ks = 0; ks < 16; ++ks) {
+                /* scaled to base-2 score units before the split */
+                const Split4 s0 = split4(q38_ld4(qp + 16 * ks) * Q38_SCORE_LOG2);
+                const Split4 s1 = split4(q38_ld4(qp + 16 * ks + 4) * Q38_SCORE_LOG2);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    q_hi[ks][e] = s0.hi[e];
+                    q_hi[ks][4 + e] = s1.hi[e];
+                    q_lo[ks][e] = s0.lo[e];
+                    q_lo[ks][4 + e] = s1.lo[e];
+                }
+                /* opaque to the compiler, which would otherwise keep f32 Q and
+                 * split it again in every block; held in accumulation registers
+                 * (the matrix unit reads its B operand from them), which leaves
+                 * the vector registers to the scores, P and the fragments */
+                asm volatile("" : "+a"(q_hi[ks]), "+a"(q_lo[ks]));
+            }
+        }
 
-    int kb = 0;
-    while (kb < n_kb) {
-        const int buf = kb & 1;
-        /* The next block's image is loaded a piece at a time between the
-         * matrix instructions below: issued all at once, 75 KB per workgroup
-         * queue behind the CU's memory path and stall every wave before its
-         * first product. */
-        const bool prefetch = kb + 1 < n_kb;
-        const char *next_img = reinterpret_cast<const char *>(image_of(a, j, min(kb + 1, n_kb - 1)));
-        char *next_dst = reinterpret_cast<char *>(&tiles[buf ^ 1]);
-        auto piece = [&](int i) {
-            const int p = wave + kWaves * i;
-            if (prefetch && p < kPieces) {
-                const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) char *)(next_dst + p * 1024);
+        float m = -INFINITY; /* query col's reference, in both lane halves */
+        float l = 0.0f;       /* the sum of this lane's weights (its half of the keys) */
+        f32x16 O[8];                   /* O[n][4J+i] = row 8J+4h+i, dim 32n + col */
+        /* zeros made by the matrix unit (0 x 0 + 0), so the accumulators start,
+         * and stay, in accumulation registers */
+        auto clear_o = [&]() {
+            const bf16x8 z = {};
+            f32x16 zc;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) zc[v] = 0.0f;
+#pragma unroll
+            for (int n = 0; n < 8; ++n) O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(z, z, zc, 0, 0, 0);
+        };
+        clear_o();
+
+        /* block images go HBM -> LDS by direct-to-LDS loads (no registers):
+         * wave w moves 1 KiB pieces w, w+4, ...; lane l's 16 bytes land at the
+         * piece's LDS base + 16 l.  Written as assembly so the compiler's
+         * wait-count pass does not see them: it cannot tell the two buffers
+         * apart and would wait for the next block's image before the first read
+         * of the current one.  The loop waits for them itself (s_waitcnt 0 and
+         * the barrier that ends each block).  M0 carries the LDS address; nothing
+         * else in the kernel uses M0. */
+        auto fetch = [&](int kb, int buf) {
+            const char *img = reinterpret_cast<const char *>(image_of(a, j, kb));
+            char *dst = reinterpret_cast<char *>(&tiles[buf]);
+            for (int p = wave; p < kPieces; p += kWaves) {
+                const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) char *)(dst + p * 1024);
+                /* one wait state between the M0 write and the load that reads it */
                 asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds),
-                             "v"(next_img + p * 1024 + lane * 16)
+                             "v"(img + p * 1024 + lane * 16)
                              : "memory");
             }
         };
-        const int key0 = kb * kKB;
-        const bool computes = active && key0 <= pos_last;
-        if (!computes)
-            for (int i = 0; i < kMyPieces; ++i) piece(i);
-        float bm = -INFINITY; /* this block's max for query col (if computed) */
-
-        if (computes) {
-            /* K fragments are read kAhead steps before their products, so
-             * the LDS latency hides behind the matrix work */
-            constexpr int kAhead = 4;
-            f32x16 s;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s[v] = 0.0f;
-            bf16x8 kh[kAhead + 1], kl[kAhead + 1];
-            auto read_k = [&](int ks, int r) {
-                kh[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[0][col][16 * ks + 8 * h]);
-                kl[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[1][col][16 * ks + 8 * h]);
-            };
-#pragma unroll
-            for (int ks = 0; ks < kAhead; ++ks) read_k(ks, ks);
-#pragma unroll
-            for (int ks = 0; ks < 16; ++ks) {
-                if (ks + kAhead < 16) read_k(ks + kAhead, (ks + kAhead) % (kAhead + 1));
-                piece(ks);
-                const int r = ks % (kAhead + 1);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[r], q_hi[ks], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[r], q_lo[ks], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl[r], q_hi[ks], s, 0, 0, 0);
-                /* keep the steps in this order: hoisting every read would
-                 * need registers the Q fragments hold */
-                __builtin_amdgcn_sched_barrier(0);
-            }
-
-            /* causal mask (only a block that reaches past the wave's first
-             * row needs one); the scores are already in base-2 units */
-            const bool full = key0 + kKB - 1 <= pos_first;
-            if (!full) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int key = key0 + 8 * (v >> 2) + 4 * h + (v & 3);
-                    s[v] = key <= qpos ? s[v] : -INFINITY;
-                }
-            }
-            /* this lane's max over its 16 scores (3-input maxima); the
-             * reference needs the query's max over both lane halves only on
-             * the first block and on a restart */
-            float lm;
-            {
-                float t6[6];
-#pragma unroll
-                for (int v = 0; v < 5; ++v) t6[v] = fmaxf(fmaxf(s[3 * v], s[3 * v + 1]), s[3 * v + 2]);
-                t6[5] = s[15];
-                lm = fmaxf(fmaxf(fmaxf(t6[0], t6[1]), t6[2]), fmaxf(fmaxf(t6[3], t6[4]), t6[5]));
-            }
-            if (m == -INFINITY) { /* first block: finite (key 0) */
-                const q38_halves bh = q38_both_halves(lm);
-                m = fmaxf(bh.a, bh.b);
-            }
-
-            if (!__any(lm > m + kRefSlack)) {
-                bf16x8 ph[2], pl[2];
-                float psum[2] = {0.0f, 0.0f};
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const float p = q38_exp2(s[v] - m);
-                    psum[v & 1] += p;
-                    /* key 8J + 4h + i -> k-step J/2, element 4(J%2) + i.
-                     * hi = p with its low 16 mantissa bits cleared, lo =
-                     * bf16(p - hi) (the difference is exact in f32) */
-                    const int t = v >> 3, e = v & 7;
-                    const uint32_t pb = __float_as_uint(p);
-                    ph[t][e] = __builtin_bit_cast(__bf16, (uint16_t)(pb >> 16));
-                    pl[t][e] = (__bf16)(p - __uint_as_float(pb & 0xFFFF0000u));
-                }
-                l += psum[0] + psum[1];
-
-                /* O += P V: B = V^T rows (head dims 32n + col), key slots
-                 * 16t + 8h .. +7 */
-                bf16x8 vh[kAhead + 1], vl[kAhead + 1];
-                auto read_v = [&](int st, int r) {
-                    const int n = st >> 1, t = st & 1;
-                    vh[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[0][32 * n + col][16 * t + 8 * h]);
-                    vl[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[1][32 * n + col][16 * t + 8 * h]);
-                };
-#pragma unroll
-                for (int st = 0; st < kAhead; ++st) read_v(st, st);
-#pragma unroll
-                for (int st = 0; st < 16; ++st) {
-                    if (st + kAhead < 16) read_v(st + kAhead, (st + kAhead) % (kAhead + 1));
-                    if (st < kMyPieces - 16) piece(16 + st);
-                    const int r = st % (kAhead + 1), n = st >> 1, t = st & 1;
-                    O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph[t], vh[r], O[n], 0, 0, 0);
-                    O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph[t], vl[r], O[n], 0, 0, 0);
-                    O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pl[t], vh[r], O[n], 0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            } else {
-                const q38_halves bh = q38_both_halves(lm);
-                bm = fmaxf(bh.a, bh.b); /* the query's max over the block: the raised reference */
-                for (int i = 16; i < kMyPieces; ++i) piece(i);
-                if (lane == 0) restart_flag[kb & 1] = 1;
-            }
-        }
-
-        /* the next block's pieces have landed (this wave's), and every wave is
-         * done with this block */
+        fetch(0, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (restart_flag[kb & 1]) {
-            /* raise the references to cover this block and start over (a
-             * wave that did not pass its reference keeps bm = -inf) */
-            m = fmaxf(m, bm);
-            l = 0.0f;
-            clear_o();
-            __syncthreads(); /* every wave has read the flag */
-            if (tid < 2) restart_flag[tid] = 0;
-            kb = 0;
-            fetch(0, 0);
+
+        /* this wave's share of an image: pieces wave + 4i, i < kMyPieces */
+        constexpr int kMyPieces = (kPieces + kWaves - 1) / kWaves;
+        static_assert(kMyPieces <= 16 + 3, "pieces fit the QK steps and the first PV steps");
+
+        int kb = 0;
+        while (kb < n_kb) {
+            const int buf = kb & 1;
+            /* The next block's image is loaded a piece at a time between the
+             * matrix instructions below: issued all at once, 75 KB per workgroup
+             * queue behind the CU's memory path and stall every wave before its
+             * first product. */
+            const bool prefetch = kb + 1 < n_kb;
+            const char *next_img = reinterpret_cast<const char *>(image_of(a, j, min(kb + 1, n_kb - 1)));
+            char *next_dst = reinterpret_cast<char *>(&tiles[buf ^ 1]);
+            auto piece = [&](int i) {
+                const int p = wave + kWaves * i;
+                if (prefetch && p < kPieces) {
+                    const uint32_t lds = (uint32_t)(size_t)(__attribute__((address_space(3))) char *)(next_dst + p * 1024);
+                    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds),
+                                 "v"(next_img + p * 1024 + lane * 16)
+                                 : "memory");
+                }
+            };
+            const int key0 = kb * kKB;
+            const bool computes = active && key0 <= pos_last;
+            if (!computes)
+                for (int i = 0; i < kMyPieces; ++i) piece(i);
+            float bm = -INFINITY; /* this block's max for query col (if computed) */
+
+            if (computes) {
+                /* K fragments are read kAhead steps before their products, so
+                 * the LDS latency hides behind the matrix work */
+                constexpr int kAhead = 4;
+                f32x16 s;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) s[v] = 0.0f;
+                bf16x8 kh[kAhead + 1], kl[kAhead + 1];
+                auto read_k = [&](int ks, int r) {
+                    kh[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[0][col][16 * ks + 8 * h]);
+                    kl[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].k[1][col][16 * ks + 8 * h]);
+                };
+#pragma unroll
+                for (int ks = 0; ks < kAhead; ++ks) read_k(ks, ks);
+#pragma unroll
+                for (int ks = 0; ks < 16; ++ks) {
+                    if (ks + kAhead < 16) read_k(ks + kAhead, (ks + kAhead) % (kAhead + 1));
+                    piece(ks);
+                    const int r = ks % (kAhead + 1);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[r], q_hi[ks], s, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh[r], q_lo[ks], s, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl[r], q_hi[ks], s, 0, 0, 0);
+                    /* keep the steps in this order: hoisting every read would
+                     * need registers the Q fragments hold */
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+
+                /* causal mask (only a block that reaches past the wave's first
+                 * row needs one); the scores are already in base-2 units */
+                const bool full = key0 + kKB - 1 <= pos_first;
+                if (!full) {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int key = key0 + 8 * (v >> 2) + 4 * h + (v & 3);
+                        s[v] = key <= qpos ? s[v] : -INFINITY;
+                    }
+                }
+                /* this lane's max over its 16 scores (3-input maxima); the
+                 * reference needs the query's max over both lane halves only on
+                 * the first block and on a restart */
+                float lm;
+                {
+                    float t6[6];
+#pragma unroll
+                    for (int v = 0; v < 5; ++v) t6[v] = fmaxf(fmaxf(s[3 * v], s[3 * v + 1]), s[3 * v + 2]);
+                    t6[5] = s[15];
+                    lm = fmaxf(fmaxf(fmaxf(t6[0], t6[1]), t6[2]), fmaxf(fmaxf(t6[3], t6[4]), t6[5]));
+                }
+                if (m == -INFINITY) { /* first block: finite (key 0) */
+                    const q38_halves bh = q38_both_halves(lm);
+                    m = fmaxf(bh.a, bh.b);
+                }
+
+                if (!__any(lm > m + kRefSlack)) {
+                    bf16x8 ph[2], pl[2];
+                    float psum[2] = {0.0f, 0.0f};
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const float p = q38_exp2(s[v] - m);
+                        psum[v & 1] += p;
+                        /* key 8J + 4h + i -> k-step J/2, element 4(J%2) + i.
+                         * hi = p with its low 16 mantissa bits cleared, lo =
+                         * bf16(p - hi) (the difference is exact in f32) */
+                        const int t = v >> 3, e = v & 7;
+                        const uint32_t pb = __float_as_uint(p);
+                        ph[t][e] = __builtin_bit_cast(__bf16, (uint16_t)(pb >> 16));
+                        pl[t][e] = (__bf16)(p - __uint_as_float(pb & 0xFFFF0000u));
+                    }
+                    l += psum[0] + psum[1];
+
+                    /* O += P V: B = V^T rows (head dims 32n + col), key slots
+                     * 16t + 8h .. +7 */
+                    bf16x8 vh[kAhead + 1], vl[kAhead + 1];
+                    auto read_v = [&](int st, int r) {
+                        const int n = st >> 1, t = st & 1;
+                        vh[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[0][32 * n + col][16 * t + 8 * h]);
+                        vl[r] = *reinterpret_cast<const bf16x8 *>(&tiles[buf].vt[1][32 * n + col][16 * t + 8 * h]);
+                    };
+#pragma unroll
+                    for (int st = 0; st < kAhead; ++st) read_v(st, st);
+#pragma unroll
+                    for (int st = 0; st < 16; ++st) {
+                        if (st + kAhead < 16) read_v(st + kAhead, (st + kAhead) % (kAhead + 1));
+                        if (st < kMyPieces - 16) piece(16 + st);
+                        const int r = st % (kAhead + 1), n = st >> 1, t = st & 1;
+                        O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph[t], vh[r], O[n], 0, 0, 0);
+                        O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ph[t], vl[r], O[n], 0, 0, 0);
+                        O[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pl[t], vh[r], O[n], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                } else {
+                    const q38_halves bh = q38_both_halves(lm);
+                    bm = fmaxf(bh.a, bh.b); /* the query's max over the block: the raised reference */
+                    for (int i = 16; i < kMyPieces; ++i) piece(i);
+                    if (lane == 0) restart_flag[kb & 1] = 1;
+                }
+            }
+
+            /* the next block's pieces have landed (this wave's), and every wave is
+             * done with this block */
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            continue;
+            if (restart_flag[kb & 1]) {
+                /* raise the references to cover this block and start over (a
+                 * wave that did not pass its reference keeps bm = -inf) */
+                m = fmaxf(m, bm);
+                l = 0.0f;
+                clear_o();
+                __syncthreads(); /* every wave has read the flag */
+                if (tid < 2) restart_flag[tid] = 0;
+                kb = 0;
+                fetch(0, 0);
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+                continue;
+            }
+            ++kb;
         }
-        ++kb;
-    }
 
-    /* normalise, gate, store rows 8J+4h+i (their sums live in lanes 8J+4h+i) */
-    if (!active) return;
-    {
-        const q38_halves lh = q38_both_halves(l); /* both halves of the keys */
-        l = lh.a + lh.b;
-    }
+        /* normalise, gate, store rows 8J+4h+i (their sums live in lanes 8J+4h+i);
+         * the last block's barrier has released the tiles for the next job */
+        if (!active) continue;
+        {
+            const q38_halves lh = q38_both_halves(l); /* both halves of the keys */
+            l = lh.a + lh.b;
+        }
+        /* The inverse sums of this lane's 16 rows; then, per 32 output dims,
+         * the 16 rows' gate factors (loads and sigmoids in one straight
+         * block) before their stores.  Every branch here is uniform: out may
+         * alias gate as far as the compiler knows, and a load or its use
+         * after a store or a branch makes it wait for everything in flight,
+         * one memory round trip per output. */
+        float inv[16];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int r = 8 * (v >> 2) + 4 * h + (v & 3);
-        const float inv = 1.0f / __shfl(l, r, 64);
-        const int t = q0 + r;
-        if (t > q_last) continue;
-        const size_t row = ((size_t)t * Q38_ATTN_HEADS + head) * Q38_ATTN_HEAD_DIM;
+        for (int v = 0; v < 16; ++v) inv[v] = 1.0f / __shfl(l, 8 * (v >> 2) + 4 * h + (v & 3), 64);
+        const bool gated = a.gate != nullptr;
+        const bool all_rows = q0 + kQW - 1 <= q_last; /* the wave's 32 rows are all real */
+        float *const out0 = a.out + (size_t)head * Q38_ATTN_HEAD_DIM;
+        const float *const gate0 = a.gate + (size_t)head * Q38_ATTN_HEAD_DIM;
+        constexpr size_t kRow = (size_t)Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
 #pragma unroll
         for (int n = 0; n < 8; ++n) {
             const int d = 32 * n + col;
-            float res = O[n][v] * inv;
-            if (a.gate != nullptr) res *= q38_sigmoid(a.gate[row + d]);
-            a.out[row + d] = res;
+            float gf[16];
+            if (gated) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    gf[v] = gate0[(size_t)min(q0 + 8 * (v >> 2) + 4 * h + (v & 3), q_last) * kRow + d];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) gf[v] = q38_sigmoid(gf[v]);
+            }
+            if (all_rows) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    float res = O[n][v] * inv[v];
+                    if (gated) res *= gf[v];
+                    out0[(size_t)(q0 + 8 * (v >> 2) + 4 * h + (v & 3)) * kRow + d] = res;
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int t = q0 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    float res = O[n][v] * inv[v];
+                    if (gated) res *= gf[v];
+                    if (t <= q_last) out0[(size_t)t * kRow + d] = res;
+                }
+            }
         }
     }
 }

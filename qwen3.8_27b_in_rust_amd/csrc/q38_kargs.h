@@ -214,6 +214,8 @@ typedef struct {
 #define Q38_PREFILL_KEYS 32    /* keys per K/V block */
 #define Q38_PREFILL_QUERIES 64 /* query tokens per prefill workgroup */
 #define Q38_PREFILL_HEAD_PAIRS 3
+#define Q38_PREFILL_BINS 64     /* workgroups per kv head when the host places the jobs */
+#define Q38_PREFILL_JOBS_MAX 4  /* jobs per such workgroup */
 #define Q38_PREFILL_KROW 264  /* bf16 per K row in a block image (256 + 16 B pad) */
 #define Q38_PREFILL_VROW 40   /* bf16 per transposed V row (32 key slots + 16 B pad) */
 /* One K/V block of one kv head split into bf16 hi/lo, laid out exactly as
@@ -232,6 +234,14 @@ typedef struct {
     int32_t n_tokens;
     int32_t n_qblocks;
     int32_t n_kblocks;         /* blocks of keys 0 .. base_pos + n_tokens - 1 */
+    /* 0: grid (12 * n_qblocks), one (kv head, head pair, query block) job per
+     * workgroup.  Else grid (4 * Q38_PREFILL_BINS): workgroup L serves kv head
+     * (L % 8) / 2 and runs the jobs of bin 2 (L / 8) + L % 2, job i of bin b at
+     * jobs[b * jobs_per_wg + i] = head pair << 6 | query block (0xFF: none);
+     * n_qblocks <= 64. */
+    int32_t jobs_per_wg;
+    int32_t pad_;
+    uint8_t jobs[Q38_PREFILL_BINS * Q38_PREFILL_JOBS_MAX];
 } q38_prefill_args;
 
 /* Weight projections.  Q8_K activations are planar: for T tokens of width
