@@ -282,12 +282,33 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     const float *scales = reinterpret_cast<const float *>(sums + (size_t)a.n_tokens * B * 16) + (size_t)tok0 * B;
     sums += (size_t)tok0 * B * 16;
     const int nblk = tp * B;
-    for (int p = tid; p < nblk * 16; p += 256)
+    const int nq16 = nblk * 16, ns16 = nblk * 2; /* 16-byte pieces of quants and of sums */
+    {
+        /* the first 4 quant pieces, one sums piece and one scale of every
+         * thread loaded before any is written (one memory round trip; a
+         * copy loop would wait for each load in turn); indices past the end
+         * reload the last piece and are not written */
+        u32x4 qv[4], sv;
+        float sc;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            qv[k] = *reinterpret_cast<const u32x4 *>(quants + (size_t)min(256 * k + tid, nq16 - 1) * 16);
+        sv = *reinterpret_cast<const u32x4 *>(sums + (size_t)min(tid, ns16 - 1) * 8);
+        sc = scales[min(tid, nblk - 1)];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int p = 256 * k + tid;
+            if (p < nq16) *reinterpret_cast<u32x4 *>(recs + (p >> 4) * kRec + (p & 15) * 16) = qv[k];
+        }
+        if (tid < ns16) *reinterpret_cast<u32x4 *>(lsums + tid * 8) = sv;
+        if (tid < nblk) lscales[tid] = sc;
+    }
+    for (int p = 1024 + tid; p < nq16; p += 256)
         *reinterpret_cast<u32x4 *>(recs + (p >> 4) * kRec + (p & 15) * 16) =
             *reinterpret_cast<const u32x4 *>(quants + (size_t)p * 16);
-    for (int p = tid; p < nblk * 2; p += 256)
+    for (int p = 256 + tid; p < ns16; p += 256)
         *reinterpret_cast<u32x4 *>(lsums + p * 8) = *reinterpret_cast<const u32x4 *>(sums + (size_t)p * 8);
-    for (int p = tid; p < nblk; p += 256) lscales[p] = scales[p];
+    for (int p = 256 + tid; p < nblk; p += 256) lscales[p] = scales[p];
     __syncthreads();
 
 #pragma unroll
