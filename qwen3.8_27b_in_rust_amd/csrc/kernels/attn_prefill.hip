@@ -93,15 +93,6 @@ Q38_DEV int key_slot(int k) {
     return 16 * (J >> 1) + 8 * h + 4 * (J & 1) + i;
 }
 
-/* Element offset of key position kp (clamped to the last needed one) in
- * kv head j's pages. */
-Q38_DEV size_t key_row(const q38_prefill_args &a, int j, int kp, int kmax) {
-    kp = min(kp, kmax);
-    const int phys = a.page_table[kp >> 4];
-    return ((size_t)phys * Q38_ATTN_KV_HEADS + j) * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM +
-           (size_t)(kp & 15) * Q38_ATTN_HEAD_DIM;
-}
-
 /* The LDS tile of one block, and the image of the same bytes in HBM. */
 struct Tile {
     __bf16 k[2][kKB][kKRow];                /* [hi/lo][key][dim] */
@@ -131,17 +122,49 @@ extern "C" __global__ __launch_bounds__(256) void q38_kv_split_mfma(q38_prefill_
     const int kmax = a.base_pos + a.n_tokens - 1;
     Tile *img = reinterpret_cast<Tile *>(static_cast<char *>(a.images) +
                                          ((size_t)j * a.n_kblocks + kb) * Q38_PREFILL_IMAGE_BYTES);
-    for (int i = tid; i < kKB * Q38_ATTN_HEAD_DIM / 4; i += 256) {
+    /* the block's two page ids first, then every K and V row load of this
+     * thread at once (one memory round trip each, where a copy loop would
+     * wait for each page id and row in turn).  Keys past the last position
+     * read it: key r is at min(kb*32 + r, kmax), whose page is the block's
+     * first for r < 16 and its second otherwise. */
+    const int kp0 = kb * kKB;
+    const int pg0 = a.page_table[min(kp0, kmax) >> 4];
+    const int pg1 = a.page_table[min(kp0 + 16, kmax) >> 4];
+    auto row_of = [&](const float *pool, int r) {
+        const int kp = min(kp0 + r, kmax);
+        return pool + ((size_t)(r < 16 ? pg0 : pg1) * Q38_ATTN_KV_HEADS + j) * Q38_PAGE_TOKENS * Q38_ATTN_HEAD_DIM +
+               (size_t)(kp & 15) * Q38_ATTN_HEAD_DIM;
+    };
+    constexpr int kKPer = kKB * Q38_ATTN_HEAD_DIM / 4 / 256;     /* K float4s per thread */
+    constexpr int kVPer = kKB / 2 * Q38_ATTN_HEAD_DIM / 4 / 256; /* V key pairs per thread */
+    f32x4 kx[kKPer], vx[2 * kVPer];
+#pragma unroll
+    for (int m = 0; m < kKPer; ++m) {
+        const int i = tid + 256 * m;
+        kx[m] = q38_ld4(row_of(a.kpool, i >> 6) + 4 * (i & 63));
+    }
+#pragma unroll
+    for (int m = 0; m < kVPer; ++m) {
+        const int i = tid + 256 * m;
+        const int r = 2 * (i >> 6), c4 = i & 63;
+        vx[2 * m] = q38_ld4(row_of(a.vpool, r) + 4 * c4);
+        vx[2 * m + 1] = q38_ld4(row_of(a.vpool, r + 1) + 4 * c4);
+    }
+#pragma unroll
+    for (int m = 0; m < kKPer; ++m) {
+        const int i = tid + 256 * m;
         const int r = i >> 6, c4 = i & 63;
-        const Split4 sp = split4(q38_ld4(a.kpool + key_row(a, j, kb * kKB + r, kmax) + 4 * c4));
+        const Split4 sp = split4(kx[m]);
         *reinterpret_cast<bf16x4 *>(&img->k[0][r][4 * c4]) = sp.hi;
         *reinterpret_cast<bf16x4 *>(&img->k[1][r][4 * c4]) = sp.lo;
     }
-    for (int i = tid; i < kKB / 2 * Q38_ATTN_HEAD_DIM / 4; i += 256) {
+#pragma unroll
+    for (int m = 0; m < kVPer; ++m) {
+        const int i = tid + 256 * m;
         const int r = 2 * (i >> 6), c4 = i & 63;
         const int slot = key_slot(r); /* key r+1 sits at slot + 1 */
-        const Split4 s0 = split4(q38_ld4(a.vpool + key_row(a, j, kb * kKB + r, kmax) + 4 * c4));
-        const Split4 s1 = split4(q38_ld4(a.vpool + key_row(a, j, kb * kKB + r + 1, kmax) + 4 * c4));
+        const Split4 s0 = split4(vx[2 * m]);
+        const Split4 s1 = split4(vx[2 * m + 1]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int d = 4 * c4 + e;
