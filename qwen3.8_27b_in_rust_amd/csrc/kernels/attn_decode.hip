@@ -579,17 +579,19 @@ extern "C" __global__ __launch_bounds__(256) void q38_attn_pre(q38_attn_pre_args
         src = a.q_and_gate + ((size_t)t * Q38_ATTN_HEADS + hd) * 2 * Q38_ATTN_HEAD_DIM;
         w = a.q_norm;
         dst = a.q_out + ((size_t)t * Q38_ATTN_HEADS + hd) * Q38_ATTN_HEAD_DIM;
-        q38_st4(a.gate_out + ((size_t)t * Q38_ATTN_HEADS + hd) * Q38_ATTN_HEAD_DIM + 4 * lane,
-                q38_ld4(src + Q38_ATTN_HEAD_DIM + 4 * lane));
     } else {
         const int kh = hd - Q38_ATTN_HEADS;
         src = a.key + ((size_t)t * Q38_ATTN_KV_HEADS + kh) * Q38_ATTN_HEAD_DIM;
         w = a.k_norm;
         dst = a.k_out + ((size_t)t * Q38_ATTN_KV_HEADS + kh) * Q38_ATTN_HEAD_DIM;
     }
+    /* every load before the first store (the outputs may alias the inputs
+     * as far as the compiler knows, and a load after a store waits for it) */
     f32x4 x = q38_ld4(src + 4 * lane);
     const f32x4 wv = q38_ld4(w + 4 * lane);
+    const f32x4 gt = is_q ? q38_ld4(src + Q38_ATTN_HEAD_DIM + 4 * lane) : f32x4{0.f, 0.f, 0.f, 0.f};
     if (threadIdx.x < 64) q38_rope_table(cs, lane, position, a.theta_scale);
+    if (is_q) q38_st4(a.gate_out + ((size_t)t * Q38_ATTN_HEADS + hd) * Q38_ATTN_HEAD_DIM + 4 * lane, gt);
     __syncthreads();
     q38_norm_rope4_cs(x, wv, lane, cs);
     q38_st4(dst + 4 * lane, x);
