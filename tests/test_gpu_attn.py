@@ -474,6 +474,17 @@ def test_prefill_4096_prompt(pkg, ctx, ref, margin):
     _check_rows(margin, _prefill_case(pkg, ctx, ref, 0, 4096, 980))
 
 
+def test_prefill_past_64_query_blocks(pkg, ctx, ref, margin):
+    """Prompts of more than 64 query blocks run one job per workgroup in the
+    grid's own order (shorter ones on host-placed jobs): 4160 tokens after a
+    100-token prefix, rows of the first, last and ragged query blocks and
+    samples between."""
+    T = 4160
+    rows = sorted(set([0, 1, 63, 64, 2047, 4095, 4096, 4127, 4128, T - 1] +
+                      list(np.random.default_rng(11).integers(0, T, 12))))
+    _check_rows(margin, _prefill_case(pkg, ctx, ref, 100, T, 990, rows=rows))
+
+
 def test_prefill_reference_restart(pkg, ctx, ref, margin):
     """Keys far above the first block's scores: the prefill kernel keeps one
     reference max per query taken from key block 0 and restarts a workgroup's
