@@ -19,7 +19,8 @@ reference's) on the same data.
 
 Also measured under "extra" (all, or those --only names): prefill attention
 and chunked DeltaNet prefill of a 4096-token prompt, linear_core over that
-prompt (with its conv/L2/gates and gated-norm kernels), batched paged decode,
+prompt (with its conv/L2/gates and gated-norm kernels), the decode step at 1K
+to 128K context, batched paged decode,
 the launch floor, one-token linear_core over 48 layers, the 64-layer full
 stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
 the Q4_K/Q6_K FFN projections for 1 and 8 tokens, and the recurrent-state
@@ -277,6 +278,58 @@ def prefill_attention(pkg, ctx, reps: int):
             "mfma_tflop_s_executed": 3 * tflops,
             "note": "bf16x3 (hi*hi + hi*lo + lo*hi) MFMA products with f32 accumulation; "
                     "algorithmic flops count each product once"}
+
+
+def decode_context_sweep(pkg, ctx, contexts=(1024, 4096, 16384, 65536, 131072), steps: int = 48):
+    """The headline's decode step (batch 1, append + gate) at other context
+    lengths, rotating over the 16 full-attention layers as the headline does
+    (16 x ctx x 8 KiB of K/V: 128 MB at 1K tokens sits in the 256 MB
+    last-level cache, as a 16-layer model's whole cache would; from 4K tokens
+    on every step streams from HBM).  Per context: step, split and merge
+    times and the step's bandwidth."""
+    res = {}
+    for c in contexts:
+        kv = pkg.KVCache(ctx, n_slots=16, max_pages=c // 16, max_seqs=1, max_tokens_per_seq=c)
+        seq = kv.seq_create()
+        rows_k, rows_v = ctx.empty((c, 1024)), ctx.empty((c, 1024))
+        for i, layer in enumerate(LAYERS):
+            ctx.fill_normal(rows_k, c * 1024, 0x51333a00 + 2 * i)
+            ctx.fill_normal(rows_v, c * 1024, 0x51333a01 + 2 * i)
+            kv.write(layer, seq, 0, c, rows_k, rows_v)
+        d_q, d_g, d_o = ctx.empty((24, 256)), ctx.empty((24, 256)), ctx.empty((24, 256))
+        ctx.fill_normal(d_q, 6144, 0x51333a90)
+        ctx.fill_normal(d_g, 6144, 0x51333a91)
+        k_new, v_new = rows_k.offset((c - 1) * 1024), rows_v.offset((c - 1) * 1024)
+
+        def step(i):
+            kv.attn_decode(LAYERS[i % 16], [seq], [c - 1], d_q, d_o, k_new=k_new, v_new=v_new, gate=d_g)
+
+        for i in range(16):
+            step(i)
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for i in range(steps):
+            step(i)
+        ctx.record(e1)
+        step_us = ctx.elapsed_ms(e0, e1) * 1e3 / steps
+        timed = {}
+        for name in ("q38_attn_decode_split", "q38_attn_decode_merge"):
+            ctx.kernel_timer_start(name, steps)
+            for i in range(steps):
+                step(i)
+            k_ms, k_n = ctx.kernel_timer_stop()
+            timed[name] = k_ms * 1e3 / max(k_n, 1) if k_n else 0.0
+        nbytes = c * 8192 + 2 * 24 * 256 * 4
+        res[str(c)] = {"step_us": step_us, "split_us": timed["q38_attn_decode_split"],
+                       "merge_us": timed["q38_attn_decode_merge"], "step_gb_s": nbytes / (step_us * 1e-6) / 1e9,
+                       "step_frac_hbm": nbytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+        for e in (e0, e1):
+            ctx.destroy_event(e)
+        for b in (rows_k, rows_v, d_q, d_g, d_o):
+            b.free()
+        kv.close()
+    return res
 
 
 def batched_decode(pkg, ctx, steps: int, warmup: int):
@@ -683,6 +736,8 @@ EXTRAS = {
     "gdn_prefill_4096": ("chunked Gated-DeltaNet prefill, 4096 tokens", lambda pkg, ctx: gdn_prefill(pkg, ctx, 5)),
     "linear_core_prefill_4096": ("linear_core over a 4096-token prompt (one layer)",
                                  lambda pkg, ctx: linear_core_prefill(pkg, ctx, 5)),
+    "decode_context_sweep": ("decode step at 1K-128K context (16 layers rotated)",
+                             lambda pkg, ctx: decode_context_sweep(pkg, ctx)),
     "batched_decode_32": ("batched paged decode, 32 sequences, context ~U[1K, 32K]",
                           lambda pkg, ctx: batched_decode(pkg, ctx, 20, 3)),
     "launch_floor": ("empty kernel launches", lambda pkg, ctx: launch_floor(ctx, 500)),

@@ -71,8 +71,8 @@ int q38_upload(q38_ctx *ctx, void *d_dst, const void *src, size_t bytes);
 int q38_download(q38_ctx *ctx, void *dst, const void *d_src, size_t bytes);
 int q38_zero(q38_ctx *ctx, void *d_dst, size_t bytes);
 
-/* Context tokens one decode workgroup streams (a multiple of 64 in
- * 64..4096), or 0 (the default) to choose per launch: one workgroup per CU
+/* Context tokens one decode workgroup streams (a multiple of 16, the page
+ * size, in 16..4096), or 0 (the default) to choose per launch: one workgroup per CU
  * for one sequence, at most 1024 tokens for batches.  A tuning setting with
  * no counterpart in the reference (whose rayon split is per head, ops.rs:919-938);
  * results do not depend on it beyond f32 rounding. */

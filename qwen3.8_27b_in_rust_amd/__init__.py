@@ -218,7 +218,7 @@ class Context:
                 "name": name.value.decode()}
 
     def set_decode_split(self, tokens: int) -> None:
-        """Context tokens per decode workgroup (multiple of 64), 0 = automatic."""
+        """Context tokens per decode workgroup (multiple of 16), 0 = automatic."""
         _check(lib().q38_set_decode_split(self.handle, int(tokens)), "q38_set_decode_split")
 
     def stream(self) -> int:

@@ -396,8 +396,9 @@ int q38_sync(q38_ctx *ctx) {
 
 int q38_set_decode_split(q38_ctx *ctx, int tokens) {
     if (ctx == nullptr) return fail("ctx is NULL");
-    if (tokens != 0 && (tokens < 64 || tokens > Q38_MAX_SPLIT_TOKENS || tokens % 64 != 0))
-        return fail("split of %d tokens: 0, or a multiple of 64 in 64..%d", tokens, Q38_MAX_SPLIT_TOKENS);
+    if (tokens != 0 && (tokens < Q38_PAGE_TOKENS || tokens > Q38_MAX_SPLIT_TOKENS || tokens % Q38_PAGE_TOKENS != 0))
+        return fail("split of %d tokens: 0, or a multiple of %d in %d..%d", tokens, Q38_PAGE_TOKENS, Q38_PAGE_TOKENS,
+                    Q38_MAX_SPLIT_TOKENS);
     ctx->split_tokens = tokens;
     return 0;
 }
@@ -745,20 +746,24 @@ int q38_kv_read(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float *d
 
 namespace {
 
-/* Context tokens per decode workgroup: a multiple of 64, at least 64 and at
- * most Q38_MAX_SPLIT_TOKENS, chosen to give one workgroup per CU for one
+/* Context tokens per decode workgroup: a whole number of pages, at most
+ * Q38_MAX_SPLIT_TOKENS, chosen to give one workgroup per CU for one
  * sequence (the split kernel streams fastest so: 46 us at 32768 tokens
- * against 50 us with two per CU), unless q38_set_decode_split fixed it. */
+ * against 50 us with two per CU; at 1024 tokens 16-token splits, 256
+ * workgroups, take 13.2-13.8 us per step against 14.4-14.8 us with 64),
+ * unless q38_set_decode_split fixed it. */
 constexpr int kMaxSplitsPerSeq = Q38_MAX_SPLITS; /* LDS weights of the merge kernel */
 
 int choose_split_tokens(const q38_ctx *ctx, int n_seq, long total_tokens, long max_tokens, int *split_out) {
-    long split = 64;
+    long split = Q38_PAGE_TOKENS;
     if (ctx->split_tokens > 0) {
         split = ctx->split_tokens;
     } else {
         const long slots = std::max(ctx->cu_count, 1);
         const long per = (total_tokens * Q38_ATTN_KV_HEADS + slots - 1) / slots;
-        split = std::min<long>(std::max<long>((per + 63) / 64 * 64, 64), Q38_MAX_SPLIT_TOKENS);
+        split = std::min<long>((per + Q38_PAGE_TOKENS - 1) / Q38_PAGE_TOKENS * Q38_PAGE_TOKENS,
+                               Q38_MAX_SPLIT_TOKENS);
+        split = std::max<long>(split, Q38_PAGE_TOKENS);
         /* sequences of different lengths make workgroups of different
          * lengths; past one round of workgroups, 1024-token splits balance
          * them best (32 sequences of 1K-32K tokens: 74% of HBM against 64%

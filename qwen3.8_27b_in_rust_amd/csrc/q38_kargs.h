@@ -58,7 +58,7 @@ typedef struct {
     int32_t gate_head_stride;  /* floats between heads' gates: 256, or 512 in q|gate rows */
     int32_t pt_stride;
     int32_t n_seq;
-    int32_t split_tokens; /* multiple of 64 */
+    int32_t split_tokens; /* multiple of Q38_PAGE_TOKENS */
     int32_t total_splits;
     int32_t seq[Q38_MAX_BATCH];
     int32_t pos[Q38_MAX_BATCH]; /* attend over positions 0..pos inclusive */

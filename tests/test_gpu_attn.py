@@ -53,9 +53,11 @@ def test_decode_ragged_lengths(pkg, ctx, ref, margin, P):
     check_attn(margin, got, ref.attn_heads(Q, K, V, gate=G))
 
 
-@pytest.mark.parametrize("split", [64, 128, 512, 1024, 2048, 4096])
+@pytest.mark.parametrize("split", [16, 32, 48, 64, 128, 512, 1024, 2048, 4096])
 def test_decode_split_invariance(pkg, ctx, ref, margin, split):
-    """Splits from one page per wave to the whole context in one workgroup."""
+    """Splits from one page per workgroup (two waves of four idle; 188 splits
+    over 3000 tokens, the last one 8 tokens) to the whole context in one
+    workgroup; 48-token splits (three pages) are no power of two."""
     got, Q, K, V, G = _decode_one(pkg, ctx, 3000, 9100, gate=True, split=split)
     check_attn(margin, got, ref.attn_heads(Q, K, V, gate=G))
 

@@ -156,8 +156,8 @@ def test_gdn_and_split_argument_checks(pkg, ctx):
     state = ctx.empty((2 * 48 * 128 * 128,))
     x = ctx.empty((2 * 6144,))
     _fails(pkg, lambda: ctx.gdn_step(2, state, x, x, x, x, x, x, state_stride=100), "overlaps states")
-    for bad in (1, 63, 100, 8192, -64):
-        _fails(pkg, lambda: ctx.set_decode_split(bad), "multiple of 64")
+    for bad in (1, 8, 15, 63, 100, 8192, -64):
+        _fails(pkg, lambda: ctx.set_decode_split(bad), "multiple of 16")
     ctx.set_decode_split(0)
     # linear_core over a prompt reads and writes 16-byte vectors: a buffer
     # one float off is refused before anything is launched
