@@ -12,7 +12,7 @@ import __graft_entry__ as entry  # noqa: E402
 # Measured errors of the GPU parity checks, one entry per check: the value,
 # the bound the test asserts, and the headroom (bound / value).  Written at
 # the end of the session to $Q38_MARGINS_PATH, by default
-# gpurun_out/parity_margins.json (the folder a GPU run returns).
+# gpurun_out/parity_margins.json (beside the run's other outputs).
 _MARGINS = []
 
 
