@@ -19,8 +19,9 @@ reference's) on the same data.
 
 Also measured under "extra" (all, or those --only names): prefill attention
 and chunked DeltaNet prefill of a 4096-token prompt, linear_core over that
-prompt (with its conv/L2/gates and gated-norm kernels), the decode step at 1K
-to 128K context, batched paged decode,
+prompt (with its conv/L2/gates and gated-norm kernels), prefill attention at
+512-8192-token prompts and after a prefix, the decode step at 1K to 128K
+context, batched paged decode,
 the launch floor, one-token linear_core over 48 layers, the 64-layer full
 stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
 the Q4_K/Q6_K FFN projections for 1 and 8 tokens, and the recurrent-state
@@ -249,35 +250,59 @@ PREFILL_FLOPS = 24 * 4 * 256 * (PREFILL_T * (PREFILL_T + 1) // 2)
 BF16_PEAK_TFLOPS = 2500.0
 
 
-def prefill_attention(pkg, ctx, reps: int):
-    """Causal prefill attention of a 4096-token prompt (batch_full_attention,
-    ops.rs:1153-1172) on the bf16x3 MFMA kernel: kernel time per prompt."""
-    T = PREFILL_T
-    kv = pkg.KVCache(ctx, n_slots=1, max_pages=T // 16, max_seqs=1, max_tokens_per_seq=T)
+def prefill_attention(pkg, ctx, reps: int, T: int = PREFILL_T, base: int = 0):
+    """Causal prefill attention of a T-token prompt after a base-token prefix
+    (batch_full_attention, ops.rs:1153-1172) on the bf16x3 MFMA kernel: kernel
+    time per prompt (the attention kernel, plus the merge of split jobs where
+    the host cut any; the K/V split apart)."""
+    n = base + T
+    flops = 24 * 1024 * (T * base + T * (T + 1) // 2)
+    kv = pkg.KVCache(ctx, n_slots=1, max_pages=(n + 15) // 16, max_seqs=1, max_tokens_per_seq=n)
     seq = kv.seq_create()
-    k, v = ctx.empty((T, 1024)), ctx.empty((T, 1024))
+    k, v = ctx.empty((n, 1024)), ctx.empty((n, 1024))
     q, g, o = ctx.empty((T, 24, 256)), ctx.empty((T, 24, 256)), ctx.empty((T, 24, 256))
-    for i, (buf, n) in enumerate(((k, T * 1024), (v, T * 1024), (q, T * 6144), (g, T * 6144))):
-        ctx.fill_normal(buf, n, 0x51334200 + i)
+    for i, (buf, cnt) in enumerate(((k, n * 1024), (v, n * 1024), (q, T * 6144), (g, T * 6144))):
+        ctx.fill_normal(buf, cnt, 0x51334200 + i)
+    if base:
+        kv.write(3, seq, 0, base, k, v)
+    k_new, v_new = k.offset(base * 1024), v.offset(base * 1024)
+
+    def run():
+        kv.seq_truncate(seq, base)
+        kv.attn_prefill(3, seq, base, T, q, k_new, v_new, o, gate=g)
+
     for _ in range(2):
-        kv.seq_reset(seq)
-        kv.attn_prefill(3, seq, 0, T, q, k, v, o, gate=g)
+        run()
     ctx.sync()
-    ctx.kernel_timer_start("q38_attn_prefill_mfma", reps)
-    for _ in range(reps):
-        kv.seq_reset(seq)
-        kv.attn_prefill(3, seq, 0, T, q, k, v, o, gate=g)
-    k_ms, k_n = ctx.kernel_timer_stop()
+    timed = {}
+    for name in ("q38_attn_prefill_mfma", "q38_prefill_merge", "q38_kv_split_mfma"):
+        ctx.kernel_timer_start(name, reps)
+        for _ in range(reps):
+            run()
+        k_ms, k_n = ctx.kernel_timer_stop()
+        timed[name] = k_ms / k_n if k_n else 0.0
     kv.close()
     for b in (k, v, q, g, o):
         b.free()
-    ms = k_ms / max(k_n, 1)
-    tflops = PREFILL_FLOPS / (ms * 1e-3) / 1e12
-    return {"tokens": T, "kernel_ms": ms, "algorithmic_gflop": PREFILL_FLOPS / 1e9, "tflop_s": tflops,
+    ms = timed["q38_attn_prefill_mfma"] + timed["q38_prefill_merge"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"tokens": T, "prefix": base, "kernel_ms": ms, "merge_ms": timed["q38_prefill_merge"],
+            "kv_split_ms": timed["q38_kv_split_mfma"], "algorithmic_gflop": flops / 1e9, "tflop_s": tflops,
             "frac_bf16_peak": tflops / BF16_PEAK_TFLOPS,
             "mfma_tflop_s_executed": 3 * tflops,
             "note": "bf16x3 (hi*hi + hi*lo + lo*hi) MFMA products with f32 accumulation; "
                     "algorithmic flops count each product once"}
+
+
+def prefill_attention_sweep(pkg, ctx, cases=((0, 512), (0, 1024), (0, 2048), (0, 8192), (8192, 512))):
+    """Prefill attention at other (prefix, prompt) lengths (the 4096-token
+    prompt is its own entry): kernel (+ merge) and K/V split times,
+    algorithmic TFLOP/s."""
+    res = {}
+    for base, T in cases:
+        r = prefill_attention(pkg, ctx, 4 if T > 4096 else 10, T, base)
+        res[f"{base}+{T}"] = {k: r[k] for k in ("kernel_ms", "merge_ms", "kv_split_ms", "tflop_s", "frac_bf16_peak")}
+    return res
 
 
 def decode_context_sweep(pkg, ctx, contexts=(1024, 4096, 16384, 65536, 131072), steps: int = 48):
@@ -736,6 +761,8 @@ EXTRAS = {
     "gdn_prefill_4096": ("chunked Gated-DeltaNet prefill, 4096 tokens", lambda pkg, ctx: gdn_prefill(pkg, ctx, 5)),
     "linear_core_prefill_4096": ("linear_core over a 4096-token prompt (one layer)",
                                  lambda pkg, ctx: linear_core_prefill(pkg, ctx, 5)),
+    "prefill_attention_sweep": ("prefill attention at 512-8192-token prompts and 512 after 8192",
+                                lambda pkg, ctx: prefill_attention_sweep(pkg, ctx)),
     "decode_context_sweep": ("decode step at 1K-128K context (16 layers rotated)",
                              lambda pkg, ctx: decode_context_sweep(pkg, ctx)),
     "batched_decode_32": ("batched paged decode, 32 sequences, context ~U[1K, 32K]",

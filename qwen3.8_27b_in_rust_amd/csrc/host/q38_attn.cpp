@@ -98,6 +98,7 @@ struct q38_ctx {
     hipModule_t mod_prefill = nullptr;
     hipFunction_t f_prefill = nullptr;
     hipFunction_t f_kv_split = nullptr;
+    hipFunction_t f_prefill_merge = nullptr;
     hipModule_t mod_gdn_chunk = nullptr;
     hipFunction_t f_chunk_prep = nullptr;
     hipFunction_t f_chunk_scan = nullptr;
@@ -323,6 +324,7 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleLoad(&ctx->mod_prefill, p_prefill.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_prefill, ctx->mod_prefill, "q38_attn_prefill_mfma"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_kv_split, ctx->mod_prefill, "q38_kv_split_mfma"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_prefill_merge, ctx->mod_prefill, "q38_prefill_merge"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split, ctx->mod_decode, "q38_attn_decode_split"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_many, ctx->mod_decode, "q38_attn_decode_split_many"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_pre, ctx->mod_decode, "q38_attn_decode_split_pre"));
@@ -538,6 +540,7 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemv_q8k_q6k") f = ctx->f_gemv_q6k;
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
+    else if (name == "q38_prefill_merge") f = ctx->f_prefill_merge;
     else if (name == "q38_gdn_chunk_prep") f = ctx->f_chunk_prep;
     else if (name == "q38_gdn_chunk_scan") f = ctx->f_chunk_scan;
     else if (name == "q38_gdn_post") f = ctx->f_gdn_post;
@@ -1040,21 +1043,71 @@ namespace {
 /* Spread the 3 * n_qblocks (head pair, query block) jobs of one kv head over
  * Q38_PREFILL_BINS bins of at most Q38_PREFILL_JOBS_MAX jobs, a job weighing
  * the key blocks its workgroup streams: longest first onto the lightest bin,
- * then moves and swaps out of the heaviest bin while they lower it.  Writes
- * the table (0xFF past a bin's last job) and returns the jobs per bin. */
-int place_prefill_jobs(int base_pos, int n_tokens, int n_qblocks, uint8_t *table) {
+ * then moves and swaps out of the heaviest bin while they lower it.  When a
+ * job is longer than 1.35x the average bin's blocks (the last query blocks of a
+ * short prompt, or every block of a prompt after a long prefix), jobs are
+ * first cut into pieces of about a third of that share, of equal key ranges, each
+ * starting on a block every row of the job sees whole; the pieces write partials (one slot each) that
+ * q38_prefill_merge combines, and `splits` lists them.  Writes the table
+ * (code 0xFFFF past a bin's last job) and returns the jobs per bin. */
+int place_prefill_jobs(int base_pos, int n_tokens, int n_qblocks, q38_prefill_job *table,
+                       q38_prefill_split *splits, int *n_split, int *n_slots) {
+    constexpr int kBins = Q38_PREFILL_BINS, kMax = Q38_PREFILL_JOBS_MAX;
+    constexpr int kMinPiece = 8; /* key blocks: a piece's own cost (its Q, its partials) is ~1 */
     struct Job {
         int weight;
-        uint8_t code;
+        q38_prefill_job j;
     };
-    std::vector<Job> jobs;
+    long total = 0, longest = 0;
     for (int qb = 0; qb < n_qblocks; ++qb) {
         const int q_last = std::min((qb + 1) * Q38_PREFILL_QUERIES, n_tokens) - 1;
-        const int weight = (base_pos + q_last) / Q38_PREFILL_KEYS + 1;
-        for (int hp = 0; hp < Q38_PREFILL_HEAD_PAIRS; ++hp) jobs.push_back({weight, (uint8_t)(hp << 6 | qb)});
+        const long n_kb = (base_pos + q_last) / Q38_PREFILL_KEYS + 1;
+        total += Q38_PREFILL_HEAD_PAIRS * n_kb;
+        longest = std::max(longest, n_kb);
     }
+    const long avg = (total + kBins - 1) / kBins;
+    /* pieces of a third of a bin's share, so that the bins can be evened out;
+     * only when some job is longer than 1.35 shares: below that the pieces'
+     * own costs outweigh the balance (2048 tokens, longest job 1.28 shares:
+     * 0.224 ms cut against 0.198 ms whole; 1024 tokens after 9000, 48 jobs
+     * of 1.39 shares for 64 bins, are cut) */
+    long cap = longest * 20 > avg * 27 ? std::max<long>((avg + 2) / 3, kMinPiece) : longest;
+    std::vector<Job> jobs;
+    int slots = 0, ns = 0;
+retry:
+    jobs.clear();
+    slots = ns = 0;
+    for (int qb = 0; qb < n_qblocks; ++qb) {
+        const int q_last = std::min((qb + 1) * Q38_PREFILL_QUERIES, n_tokens) - 1;
+        const int n_kb = (base_pos + q_last) / Q38_PREFILL_KEYS + 1;
+        /* the last block every row of the job sees whole: keys up to the
+         * position of its first row */
+        const int first_pos = base_pos + qb * Q38_PREFILL_QUERIES;
+        const int seen = first_pos >= Q38_PREFILL_KEYS - 1 ? (first_pos - (Q38_PREFILL_KEYS - 1)) / Q38_PREFILL_KEYS
+                                                           : -1;
+        int np = n_kb > cap ? (int)((n_kb + cap - 1) / cap) : 1;
+        while (np > 1 && (long)(np - 1) * n_kb / np > seen) --np; /* the last piece's start */
+        for (int hp = 0; hp < Q38_PREFILL_HEAD_PAIRS; ++hp) {
+            const uint16_t code = (uint16_t)(hp << 6 | qb);
+            if (np == 1) {
+                jobs.push_back({n_kb + 1, {code, 0xFFFF, 0, (uint16_t)n_kb}});
+                continue;
+            }
+            splits[ns++] = {code, (uint16_t)slots, (uint16_t)np, 0};
+            for (int i = 0; i < np; ++i) {
+                const int kb0 = (int)((long)i * n_kb / np), kb1 = (int)((long)(i + 1) * n_kb / np);
+                jobs.push_back({kb1 - kb0 + 1, {code, (uint16_t)(slots + i), (uint16_t)kb0, (uint16_t)kb1}});
+            }
+            slots += np;
+        }
+    }
+    if ((int)jobs.size() > kBins * kMax) {
+        cap *= 2; /* more pieces than the table holds */
+        goto retry;
+    }
+    *n_split = ns;
+    *n_slots = slots;
     std::stable_sort(jobs.begin(), jobs.end(), [](const Job &x, const Job &y) { return x.weight > y.weight; });
-    constexpr int kBins = Q38_PREFILL_BINS, kMax = Q38_PREFILL_JOBS_MAX;
     std::vector<std::vector<Job>> bins(kBins);
     std::vector<long> load(kBins, 0);
     for (const Job &jb : jobs) {
@@ -1100,9 +1153,9 @@ int place_prefill_jobs(int base_pos, int n_tokens, int n_qblocks, uint8_t *table
     }
     int per = 1;
     for (const auto &b : bins) per = std::max(per, (int)b.size());
-    memset(table, 0xFF, (size_t)kBins * kMax);
+    for (int i = 0; i < kBins * kMax; ++i) table[i] = {0xFFFF, 0xFFFF, 0, 0};
     for (int b = 0; b < kBins; ++b)
-        for (int i = 0; i < (int)bins[b].size(); ++i) table[b * per + i] = bins[b][i].code;
+        for (int i = 0; i < (int)bins[b].size(); ++i) table[b * per + i] = bins[b][i].j;
     return per;
 }
 
@@ -1140,22 +1193,39 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
     a.n_kblocks = (int)((end - 1) / Q38_PREFILL_KEYS + 1);
     size_t n_wg = (size_t)a.n_qblocks * Q38_ATTN_KV_HEADS * Q38_PREFILL_HEAD_PAIRS;
     if (n_wg > 0x7FFFFFFFull) return fail("prompt too long");
+    q38_prefill_merge_args mg;
+    memset(&mg, 0, sizeof(mg));
     if (a.n_qblocks <= 64) {
         /* few jobs per CU: placed here so that every bin (one workgroup per CU)
          * gets the same number of key blocks, which the hardware's
          * longest-first order cannot do with 3 jobs per CU */
-        a.jobs_per_wg = place_prefill_jobs(base_pos, n_tokens, a.n_qblocks, a.jobs);
+        a.jobs_per_wg = place_prefill_jobs(base_pos, n_tokens, a.n_qblocks, a.jobs, mg.split, &mg.n_split, &a.n_slots);
+        if (a.jobs_per_wg < 0) return -1;
         n_wg = (size_t)Q38_ATTN_KV_HEADS * Q38_PREFILL_BINS;
     }
-    /* the workspace for the K/V block images before anything is changed */
-    if (ctx->ensure_work((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES)) return -1;
+    /* the workspace for the K/V block images and the pieces' partials, before
+     * anything is changed */
+    const size_t img_bytes = ((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES + 255) / 256 * 256;
+    const size_t part_rows = (size_t)Q38_ATTN_KV_HEADS * a.n_slots * Q38_PREFILL_QUERIES * 2;
+    if (ctx->ensure_work(img_bytes + part_rows * (Q38_ATTN_HEAD_DIM + 2) * sizeof(float))) return -1;
     a.images = ctx->work;
+    a.part_o = reinterpret_cast<float *>(static_cast<char *>(ctx->work) + img_bytes);
+    a.part_ml = a.part_o + part_rows * Q38_ATTN_HEAD_DIM;
     /* append the prompt's rows (reserves pages) */
     if (q38_kv_write(kv, layer, seq, base_pos, n_tokens, d_k, d_v)) return -1;
     /* the K/V of positions 0 .. base_pos+n_tokens-1 split once into bf16
      * hi/lo block images, then the attention kernel */
     if (ctx->launch(ctx->f_kv_split, a.n_kblocks, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
-    return ctx->launch(ctx->f_prefill, (unsigned)n_wg, 1, 1, 256, &a);
+    if (ctx->launch(ctx->f_prefill, (unsigned)n_wg, 1, 1, 256, &a)) return -1;
+    if (mg.n_split == 0) return 0;
+    mg.part_o = a.part_o;
+    mg.part_ml = a.part_ml;
+    mg.gate = d_gate;
+    mg.out = d_out;
+    mg.n_tokens = n_tokens;
+    mg.n_slots = a.n_slots;
+    return ctx->launch(ctx->f_prefill_merge, (unsigned)mg.n_split, Q38_ATTN_KV_HEADS, 2 * Q38_PREFILL_QUERIES / 4,
+                       256, &mg);
 }
 
 /* ---------------------------------------------------------------- DeltaNet */

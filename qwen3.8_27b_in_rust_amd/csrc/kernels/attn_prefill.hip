@@ -198,12 +198,17 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
     const int n_jobs = a.jobs_per_wg > 0 ? a.jobs_per_wg : 1;
     for (int job = 0; job < n_jobs; ++job) {
         int j, hp, qb;
+        int kb_begin = 0, kb_stop = -1; /* the job's key blocks (-1: up to the diagonal) */
+        int slot = -1;                  /* a piece's partial slot (-1: the whole job) */
         if (a.jobs_per_wg > 0) {
             j = (L & 7) >> 1;
-            const int code = a.jobs[(2 * (L >> 3) + (L & 1)) * a.jobs_per_wg + job];
-            if (code == 0xFF) break; /* the bin's jobs are done (the same for every wave) */
-            hp = code >> 6;
-            qb = code & 63;
+            const q38_prefill_job jb = a.jobs[(2 * (L >> 3) + (L & 1)) * a.jobs_per_wg + job];
+            if (jb.code == 0xFFFF) break; /* the bin's jobs are done (the same for every wave) */
+            hp = jb.code >> 6;
+            qb = jb.code & 63;
+            kb_begin = jb.kb0;
+            kb_stop = jb.kb1;
+            if (jb.slot != 0xFFFF) slot = jb.slot;
         } else {
             int c;
             if ((nq & 1) == 0) {
@@ -226,7 +231,9 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
         const int q0 = qb * kQ + kQW * (wave >> 1);      /* the wave's first query token */
         const int q_last = min(qb * kQ + kQ, a.n_tokens) - 1; /* last real query token of the block */
         const int kmax = a.base_pos + q_last;            /* last key position any row needs */
-        const int n_kb = kmax / kKB + 1;
+        /* a piece stops before the diagonal; its first block, like block 0,
+         * is seen whole by every row of the job (the host splits so) */
+        const int n_kb = kb_stop >= 0 ? kb_stop : kmax / kKB + 1;
         const bool active = q0 <= q_last;                /* the wave has real rows */
         const int pos_first = a.base_pos + q0;           /* the wave's first row's position */
         const int pos_last = a.base_pos + min(q0 + kQW - 1, q_last);
@@ -291,7 +298,7 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
                              : "memory");
             }
         };
-        fetch(0, 0);
+        fetch(kb_begin, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
 
@@ -299,9 +306,9 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
         constexpr int kMyPieces = (kPieces + kWaves - 1) / kWaves;
         static_assert(kMyPieces <= 16 + 3, "pieces fit the QK steps and the first PV steps");
 
-        int kb = 0;
+        int kb = kb_begin;
         while (kb < n_kb) {
-            const int buf = kb & 1;
+            const int buf = (kb - kb_begin) & 1;
             /* The next block's image is loaded a piece at a time between the
              * matrix instructions below: issued all at once, 75 KB per workgroup
              * queue behind the CU's memory path and stall every wave before its
@@ -434,8 +441,8 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
                 clear_o();
                 __syncthreads(); /* every wave has read the flag */
                 if (tid < 2) restart_flag[tid] = 0;
-                kb = 0;
-                fetch(0, 0);
+                kb = kb_begin;
+                fetch(kb_begin, 0);
                 __builtin_amdgcn_s_waitcnt(0);
                 __syncthreads();
                 continue;
@@ -449,6 +456,28 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
         {
             const q38_halves lh = q38_both_halves(l); /* both halves of the keys */
             l = lh.a + lh.b;
+        }
+        if (slot >= 0) {
+            /* a piece: O as it is, and each row's reference and weight sum
+             * (row col's, held by lane col), for q38_prefill_merge */
+            const size_t sl = (size_t)j * a.n_slots + slot;
+            const int hh = wave & 1;
+            const int r0 = kQW * (wave >> 1); /* the wave's first row in the job */
+            float *po = a.part_o + (sl * kQ * 2 + hh) * Q38_ATTN_HEAD_DIM;
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int r = r0 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    po[(size_t)r * 2 * Q38_ATTN_HEAD_DIM + 32 * n + col] = O[n][v];
+                }
+            }
+            if (h == 0) {
+                float *pml = a.part_ml + ((sl * kQ + r0 + col) * 2 + hh) * 2;
+                pml[0] = m;
+                pml[1] = l;
+            }
+            continue;
         }
         /* The inverse sums of this lane's 16 rows; then, per 32 output dims,
          * the 16 rows' gate factors (loads and sigmoids in one straight
@@ -493,4 +522,62 @@ extern "C" __global__ __launch_bounds__(kThreads, 1) void q38_attn_prefill_mfma(
             }
         }
     }
+}
+
+/* The pieces of split prefill jobs combined (grid (n_split, 4 kv heads, 32),
+ * 256 threads): per (row, head) of a split job, each piece's unnormalised O
+ * and weight sum rescaled from its own reference to the largest, summed,
+ * then normalised and gated as a whole job's rows are.  Up to 8 pieces' loads
+ * are issued at once. */
+extern "C" __global__ __launch_bounds__(256) void q38_prefill_merge(q38_prefill_merge_args a) {
+    constexpr int kBatch = 8;
+    const q38_prefill_split sp = a.split[blockIdx.x];
+    const int j = blockIdx.y;
+    const int pair = 4 * blockIdx.z + (threadIdx.x >> 6); /* (row, head) of the job */
+    const int r = pair >> 1, hh = pair & 1;
+    const int t = (sp.code & 63) * kQ + r;
+    if (t >= a.n_tokens) return;
+    const int d = 4 * (threadIdx.x & 63);
+    const int head = j * Q38_ATTN_GROUP + 2 * (sp.code >> 6) + hh;
+    const size_t out_off = ((size_t)t * Q38_ATTN_HEADS + head) * Q38_ATTN_HEAD_DIM + d;
+    const bool gated = a.gate != nullptr;
+    const f32x4 g = gated ? q38_ld4(a.gate + out_off) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const size_t slot0 = (size_t)j * a.n_slots + sp.slot0;
+    const int n = sp.n;
+    float M = -INFINITY, Lsum = 0.0f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+    for (int i0 = 0; i0 < n; i0 += kBatch) {
+        float m[kBatch], l[kBatch];
+        f32x4 o[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const bool in = i0 + k < n;
+            const size_t row = ((slot0 + (in ? i0 + k : i0)) * kQ + r) * 2 + hh; /* a piece known to exist */
+            m[k] = in ? a.part_ml[row * 2] : -INFINITY;
+            l[k] = a.part_ml[row * 2 + 1];
+            o[k] = q38_ld4(a.part_o + row * Q38_ATTN_HEAD_DIM + d);
+        }
+        float mx = M;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) mx = fmaxf(mx, m[k]);
+        const float f = q38_exp2(M - mx); /* 0 while M is -inf */
+        Lsum *= f;
+        O *= f;
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const float w = q38_exp2(m[k] - mx); /* 0 for absent pieces */
+            Lsum = __builtin_fmaf(w, l[k], Lsum);
+            O = q38_fma4(w, o[k], O);
+        }
+        M = mx;
+    }
+    const float inv = 1.0f / Lsum;
+    f32x4 res = O * inv;
+    if (gated) {
+        res.x *= q38_sigmoid(g.x);
+        res.y *= q38_sigmoid(g.y);
+        res.z *= q38_sigmoid(g.z);
+        res.w *= q38_sigmoid(g.w);
+    }
+    q38_st4(a.out + out_off, res);
 }

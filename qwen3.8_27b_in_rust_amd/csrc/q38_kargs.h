@@ -216,6 +216,23 @@ typedef struct {
 #define Q38_PREFILL_HEAD_PAIRS 3
 #define Q38_PREFILL_BINS 64     /* workgroups per kv head when the host places the jobs */
 #define Q38_PREFILL_JOBS_MAX 4  /* jobs per such workgroup */
+#define Q38_PREFILL_SPLITS_MAX (3 * 64) /* jobs split into pieces in one launch */
+/* One placed job: head pair << 6 | query block (0xFFFF: none), its key
+ * blocks [kb0, kb1), and the partial slot its piece writes (0xFFFF: the
+ * whole job, normalised and stored). */
+typedef struct {
+    uint16_t code;
+    uint16_t slot;
+    uint16_t kb0;
+    uint16_t kb1;
+} q38_prefill_job;
+/* A job split into n pieces written to partial slots slot0 .. slot0+n-1. */
+typedef struct {
+    uint16_t code;
+    uint16_t slot0;
+    uint16_t n;
+    uint16_t pad_;
+} q38_prefill_split;
 #define Q38_PREFILL_KROW 264  /* bf16 per K row in a block image (256 + 16 B pad) */
 #define Q38_PREFILL_VROW 40   /* bf16 per transposed V row (32 key slots + 16 B pad) */
 /* One K/V block of one kv head split into bf16 hi/lo, laid out exactly as
@@ -235,14 +252,31 @@ typedef struct {
     int32_t n_qblocks;
     int32_t n_kblocks;         /* blocks of keys 0 .. base_pos + n_tokens - 1 */
     /* 0: grid (12 * n_qblocks), one (kv head, head pair, query block) job per
-     * workgroup.  Else grid (4 * Q38_PREFILL_BINS): workgroup L serves kv head
-     * (L % 8) / 2 and runs the jobs of bin 2 (L / 8) + L % 2, job i of bin b at
-     * jobs[b * jobs_per_wg + i] = head pair << 6 | query block (0xFF: none);
+     * workgroup over all its key blocks.  Else grid (4 * Q38_PREFILL_BINS):
+     * workgroup L serves kv head (L % 8) / 2 and runs the jobs of bin
+     * 2 (L / 8) + L % 2, job i of bin b at jobs[b * jobs_per_wg + i];
      * n_qblocks <= 64. */
     int32_t jobs_per_wg;
-    int32_t pad_;
-    uint8_t jobs[Q38_PREFILL_BINS * Q38_PREFILL_JOBS_MAX];
+    int32_t n_slots;           /* partial slots per kv head (pieces of split jobs) */
+    float *part_o;             /* [4][n_slots][64 rows][2 heads][256] unnormalised O of a piece */
+    float *part_ml;            /* [4][n_slots][64][2][2]: its (reference, weight sum) per row */
+    q38_prefill_job jobs[Q38_PREFILL_BINS * Q38_PREFILL_JOBS_MAX];
 } q38_prefill_args;
+
+/* Combines the pieces of split prefill jobs: grid (n_split, 4 kv heads, 32),
+ * 256 threads; workgroup (g, j, y) forms rows/heads 4y .. 4y+3 of split job
+ * g of kv head j, a thread 4 output dims of one (row, head). */
+typedef struct {
+    const float *part_o;
+    const float *part_ml;
+    const float *gate;
+    float *out;
+    int32_t n_tokens;
+    int32_t n_slots;
+    int32_t n_split;
+    int32_t pad_;
+    q38_prefill_split split[Q38_PREFILL_SPLITS_MAX];
+} q38_prefill_merge_args;
 
 /* Weight projections.  Q8_K activations are planar: for T tokens of width
  * W (B = W/256 blocks each) int8 quants [T][W] | int16 group sums [T][B][16]

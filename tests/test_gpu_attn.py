@@ -487,40 +487,60 @@ def test_prefill_past_64_query_blocks(pkg, ctx, ref, margin):
     _check_rows(margin, _prefill_case(pkg, ctx, ref, 100, T, 990, rows=rows))
 
 
-def test_prefill_reference_restart(pkg, ctx, ref, margin):
+@pytest.mark.parametrize("base,T,step,gate,permute", [(0, 1024, 1, True, False), (3001, 700, 7, True, False),
+                                                     (9000, 200, 1, True, False), (0, 512, 1, False, True)])
+def test_prefill_split_jobs(pkg, ctx, ref, margin, base, T, step, gate, permute):
+    """Prompts whose longest jobs pass 1.1 times a workgroup's share of key
+    blocks (the last query blocks of a short prompt; every job after a long
+    prefix): the host cuts jobs into pieces of key blocks that write partials,
+    and q38_prefill_merge combines them.  1024 tokens from position 0 (36 of
+    48 jobs cut), 700 after a 3001-token prefix (the prompt starts inside a
+    key block), 200 after 9000 (every job in 16 pieces), 512 with permuted pages and
+    no gate; every row, or every 7th and the last."""
+    rows = sorted(set(range(0, T, step)) | {T - 1})
+    _check_rows(margin, _prefill_case(pkg, ctx, ref, base, T, 1100 + T, gate=gate, permute=permute, rows=rows))
+
+
+@pytest.mark.parametrize("base", [0, 2000])
+def test_prefill_reference_restart(pkg, ctx, ref, margin, base):
     """Keys far above the first block's scores: the prefill kernel keeps one
-    reference max per query taken from key block 0 and restarts a workgroup's
-    key loop when a later block passes it by more than 2^64.  Heads 0-5 query
-    one direction u; key 70 of kv head 0 scores 60 (natural units) and key 150
-    scores 130, so queries 70.. restart at block 2 and queries 150.. again at
-    block 4.  All rows against the restatement."""
+    reference max per query taken from its first key block and restarts a
+    workgroup's key loop when a later block passes it by more than 2^64.
+    Heads 0-5 query one direction u; key base+70 of kv head 0 scores 60
+    (natural units) and key base+150 scores 130, so queries 70.. restart and
+    queries 150.. again.  After a 2000-token prefix every job is cut into
+    pieces, so the restarts return to a piece's first block.  All rows
+    against the restatement."""
     from q38amd import synth
     T = 200
-    kv = pkg.KVCache(ctx, n_slots=17, max_pages=T // 16 + 4, max_seqs=1, max_tokens_per_seq=T)
+    n = base + T
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=n // 16 + 4, max_seqs=1, max_tokens_per_seq=n)
     try:
         seq = kv.seq_create()
         layer = 3
-        K = synth.normal(1001, T * 1024).reshape(T, 4, 256)
-        V = synth.normal(1002, T * 1024).reshape(T, 4, 256)
+        K = synth.normal(1001, n * 1024).reshape(n, 4, 256)
+        V = synth.normal(1002, n * 1024).reshape(n, 4, 256)
         Q = synth.normal(1003, T * 6144).reshape(T, 24, 256)
         u = synth.normal(1004, 256)
         Q[:, 0:6, :] = u
         un = u / np.linalg.norm(u)
-        K[70, 0] = (60.0 * 16.0 / np.linalg.norm(u)) * un
-        K[150, 0] = (130.0 * 16.0 / np.linalg.norm(u)) * un
+        K[base + 70, 0] = (60.0 * 16.0 / np.linalg.norm(u)) * un
+        K[base + 150, 0] = (130.0 * 16.0 / np.linalg.norm(u)) * un
         K, V, Q = K.astype(np.float32).reshape(-1), V.astype(np.float32).reshape(-1), Q.astype(np.float32).reshape(-1)
         d_k, d_v = ctx.array(K), ctx.array(V)
+        if base:
+            kv.write(layer, seq, 0, base, d_k, d_v)
         d_o = ctx.empty((T, 24, 256))
-        kv.attn_prefill(layer, seq, 0, T, ctx.array(Q), d_k, d_v, d_o)
+        kv.attn_prefill(layer, seq, base, T, ctx.array(Q), d_k.offset(base * 1024), d_v.offset(base * 1024), d_o)
         got = d_o.download()
         Kr, Vr = K.reshape(-1, 1024), V.reshape(-1, 1024)
         worst = (0.0, 0.0)
         for t in range(T):
-            want = ref.attn_heads(Q[t * 6144:(t + 1) * 6144], Kr[:t + 1], Vr[:t + 1])
+            want = ref.attn_heads(Q[t * 6144:(t + 1) * 6144], Kr[:base + t + 1], Vr[:base + t + 1])
             worst = tuple(max(a, b) for a, b in zip(worst, abs_rel(got[t], want)))
         # the planted keys dominate: head 0 of query 120 returns v_70, of query 190 v_150
-        assert np.max(np.abs(got[120, 0] - Vr[70, :256])) <= 1e-3
-        assert np.max(np.abs(got[190, 0] - Vr[150, :256])) <= 1e-3
+        assert np.max(np.abs(got[120, 0] - Vr[base + 70, :256])) <= 1e-3
+        assert np.max(np.abs(got[190, 0] - Vr[base + 150, :256])) <= 1e-3
     finally:
         kv.close()
     _check_rows(margin, worst)
