@@ -894,6 +894,9 @@ def main():
                    "page_tokens": 16, "layers_rotated": 16},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_source": "profiled, not measured in this run: profiles/attn_decode_split_32k_traffic.json "
+                                       "(rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this kernel on this workload, "
+                                       "scaled by the same counters on a plain copy)",
                      "kernel": "q38_attn_decode_split", "algorithmic_bytes_per_launch": SPLIT_BYTES},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -158,8 +158,12 @@ int q38_full_core(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids,
 
 /*
  * q38_full_core with no device allocation.  No counterpart in the
- * reference: it is for callers that cannot allocate -- code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc.  Arguments,
+ * reference: it is for callers that cannot allocate -- tight serving loops,
+ * harnesses that forbid hipMalloc.  It is not for HIP stream capture: an
+ * append that starts a new page uploads that page's id through a pinned
+ * staging ring (a stream-ordered copy, and a stream synchronisation when the
+ * ring wraps), and positions and page ids are launch arguments fixed at the
+ * call; q38_decode_graph_* is the replayable form.  Arguments,
  * results and errors are those of q38_full_core; the split-K partials live
  * in a fixed per-device scratch array of Q38_NOALLOC_SCRATCH_BYTES instead
  * of the context's growable workspace, so a call whose partials need more

@@ -66,7 +66,8 @@ int q38_gguf_upload(q38_ctx *ctx, const q38_gguf *g, void **d_base, size_t *byte
 /*
  * checkpoint_state / restore_target_state (src/model/ops.rs:1627-1647) on
  * the device: copy a sequence's recurrent state -- conv_state
- * [48][3][10240] and delta_state [48][48][128][128] f32, n_conv and
+ * [48][10240][3] (per layer, channel-major with the 3 taps of a channel
+ * adjacent) and delta_state [48][48][128][128] f32, n_conv and
  * n_delta floats (multiples of 4, 16-byte aligned) -- to the checkpoint and
  * back, ordered on the context's stream (no host round trip).  The position
  * the reference saves with it is the caller's scalar; the KV cache rolls

@@ -1090,13 +1090,13 @@ retry:
         for (int hp = 0; hp < Q38_PREFILL_HEAD_PAIRS; ++hp) {
             const uint16_t code = (uint16_t)(hp << 6 | qb);
             if (np == 1) {
-                jobs.push_back({n_kb + 1, {code, 0xFFFF, 0, (uint16_t)n_kb}});
+                jobs.push_back({n_kb + 1, {code, 0xFFFF, 0, n_kb}});
                 continue;
             }
             splits[ns++] = {code, (uint16_t)slots, (uint16_t)np, 0};
             for (int i = 0; i < np; ++i) {
                 const int kb0 = (int)((long)i * n_kb / np), kb1 = (int)((long)(i + 1) * n_kb / np);
-                jobs.push_back({kb1 - kb0 + 1, {code, (uint16_t)(slots + i), (uint16_t)kb0, (uint16_t)kb1}});
+                jobs.push_back({kb1 - kb0 + 1, {code, (uint16_t)(slots + i), kb0, kb1}});
             }
             slots += np;
         }
@@ -1161,6 +1161,12 @@ retry:
 
 }  // namespace
 
+/* kernel arguments travel by value; keep them within the 4 KiB a launch
+ * carries on every HIP runtime */
+static_assert(sizeof(q38_prefill_args) <= 4096, "prefill arguments exceed 4 KiB");
+static_assert(sizeof(q38_decode_args) <= 4096, "decode arguments exceed 4 KiB");
+static_assert(sizeof(q38_prefill_merge_args) <= 4096, "prefill merge arguments exceed 4 KiB");
+
 int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens, const float *d_q,
                      const float *d_k, const float *d_v, const float *d_gate, float *d_out) {
     if (kv == nullptr) return fail("kv is NULL");
@@ -1200,7 +1206,6 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
          * gets the same number of key blocks, which the hardware's
          * longest-first order cannot do with 3 jobs per CU */
         a.jobs_per_wg = place_prefill_jobs(base_pos, n_tokens, a.n_qblocks, a.jobs, mg.split, &mg.n_split, &a.n_slots);
-        if (a.jobs_per_wg < 0) return -1;
         n_wg = (size_t)Q38_ATTN_KV_HEADS * Q38_PREFILL_BINS;
     }
     /* the workspace for the K/V block images and the pieces' partials, before

@@ -219,12 +219,13 @@ typedef struct {
 #define Q38_PREFILL_SPLITS_MAX (3 * 64) /* jobs split into pieces in one launch */
 /* One placed job: head pair << 6 | query block (0xFFFF: none), its key
  * blocks [kb0, kb1), and the partial slot its piece writes (0xFFFF: the
- * whole job, normalised and stored). */
+ * whole job, normalised and stored).  Key-block indices are 32-bit: a
+ * sequence may hold up to 16,777,216 tokens, 524,288 blocks of 32 keys. */
 typedef struct {
     uint16_t code;
     uint16_t slot;
-    uint16_t kb0;
-    uint16_t kb1;
+    int32_t kb0;
+    int32_t kb1;
 } q38_prefill_job;
 /* A job split into n pieces written to partial slots slot0 .. slot0+n-1. */
 typedef struct {

@@ -1,6 +1,7 @@
 // Host-side check of the prefill job planner (place_prefill_jobs in
 // q38_attn.cpp, compiled into this program): for prompts of 1..4096 tokens
-// after prefixes of 0..131000, every (head pair, query block) job's key blocks
+// after prefixes of 0..16,773,120 (the longest sequence the cache accepts is
+// 16,777,216 tokens, so key-block indices pass 65535), every (head pair, query block) job's key blocks
 // are covered exactly once by its pieces, a piece starts on a block that
 // every row of its job sees whole, partial slots are unique and dense, the
 // split list matches the pieces, and no bin holds more than the table allows.
@@ -18,7 +19,8 @@ int q38_scratch_address(int, void **ptr) {
 #include <map>
 int main() {
     int cases = 0, worst_case_ratio_x100 = 0;
-    for (int base : {0, 1, 31, 32, 100, 1000, 3000, 3001, 9000, 50000, 131000}) {
+    for (int base : {0, 1, 31, 32, 100, 1000, 3000, 3001, 9000, 50000, 131000, 2097088, 2097120, 2100000,
+                     16773120}) {
         for (int T : {1, 2, 17, 63, 64, 65, 200, 512, 700, 1000, 1024, 1500, 2048, 3000, 4096}) {
             const int nq = (T + 63) / 64;
             q38_prefill_job table[Q38_PREFILL_BINS * Q38_PREFILL_JOBS_MAX];

@@ -490,7 +490,7 @@ def test_prefill_past_64_query_blocks(pkg, ctx, ref, margin):
 @pytest.mark.parametrize("base,T,step,gate,permute", [(0, 1024, 1, True, False), (3001, 700, 7, True, False),
                                                      (9000, 200, 1, True, False), (0, 512, 1, False, True)])
 def test_prefill_split_jobs(pkg, ctx, ref, margin, base, T, step, gate, permute):
-    """Prompts whose longest jobs pass 1.1 times a workgroup's share of key
+    """Prompts whose longest jobs pass 1.35 times a workgroup's share of key
     blocks (the last query blocks of a short prompt; every job after a long
     prefix): the host cuts jobs into pieces of key blocks that write partials,
     and q38_prefill_merge combines them.  1024 tokens from position 0 (36 of

@@ -1,6 +1,6 @@
 """The prefill job planner (host logic of q38_attn_prefill) checked on the
 CPU: tests/host/prefill_plan_check.cpp includes the library's source and
-walks prompts of 1..4096 tokens after prefixes of 0..131000 (coverage of
+walks prompts of 1..4096 tokens after prefixes of 0..16,773,120 (coverage of
 every job's key blocks, piece starts every row sees whole, dense unique
 partial slots, table bounds)."""
 import os
