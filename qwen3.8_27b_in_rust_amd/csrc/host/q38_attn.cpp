@@ -107,6 +107,8 @@ struct q38_ctx {
     hipFunction_t f_decode_split_many = nullptr; /* any number of splits */
     hipFunction_t f_decode_split_pre = nullptr; /* the same with full_core's pre step fused */
     hipFunction_t f_decode_split_pre_many = nullptr;
+    hipFunction_t f_decode_split_one = nullptr;     /* one sequence: arguments in one load round */
+    hipFunction_t f_decode_split_pre_one = nullptr;
     hipFunction_t f_decode_merge = nullptr;
     hipFunction_t f_kv_copy = nullptr;
     hipFunction_t f_attn_pre = nullptr;
@@ -328,6 +330,8 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split, ctx->mod_decode, "q38_attn_decode_split"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_many, ctx->mod_decode, "q38_attn_decode_split_many"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_pre, ctx->mod_decode, "q38_attn_decode_split_pre"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_one, ctx->mod_decode, "q38_attn_decode_split_one"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_pre_one, ctx->mod_decode, "q38_attn_decode_split_pre_one"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_split_pre_many, ctx->mod_decode,
                                  "q38_attn_decode_split_pre_many"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_decode_merge, ctx->mod_decode, "q38_attn_decode_merge"));
@@ -523,6 +527,8 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_attn_decode_split_many") f = ctx->f_decode_split_many;
     else if (name == "q38_attn_decode_split_pre") f = ctx->f_decode_split_pre;
     else if (name == "q38_attn_decode_split_pre_many") f = ctx->f_decode_split_pre_many;
+    else if (name == "q38_attn_decode_split_one") f = ctx->f_decode_split_one;
+    else if (name == "q38_attn_decode_split_pre_one") f = ctx->f_decode_split_pre_one;
     else if (name == "q38_attn_decode_merge") f = ctx->f_decode_merge;
     else if (name == "q38_kv_copy") f = ctx->f_kv_copy;
     else if (name == "q38_attn_pre") f = ctx->f_attn_pre;
@@ -819,14 +825,28 @@ struct decode_pre {
     const float *k_norm;
 };
 
-/* One decode launch (plus the merge) for n_seq <= Q38_MAX_BATCH sequences
- * whose pages are reserved; `work` holds plan.work_bytes. */
-int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const int32_t *positions,
-                 const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate,
-                 float *d_out, const decode_plan &plan, void *work, const decode_pre *pre = nullptr) {
+/* The arguments of one decode launch: the split kernel, its grid, and the
+ * merge that follows it when some sequence has more than one split. */
+struct decode_launch {
+    q38_decode_args a;
+    q38_merge_args m;
+    hipFunction_t f = nullptr;
+    unsigned grid_x = 0;
+    bool merge = false;
+};
+
+/* Arguments of one decode launch for n_seq <= Q38_MAX_BATCH sequences whose
+ * pages are reserved; `work` holds plan.work_bytes.  `arg_pages` chooses the
+ * split kernel that takes each split's first page ids in its arguments (at
+ * most Q38_HEAD_PAGE_SPLITS splits), else the one reading every id from the
+ * page table; -1 picks by the split count. */
+int build_decode(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                 const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate, float *d_out,
+                 const decode_plan &plan, void *work, const decode_pre *pre, int arg_pages_choice,
+                 decode_launch *L) {
     q38_ctx *ctx = kv->ctx;
     const int split_tokens = plan.split_tokens;
-    q38_decode_args a;
+    q38_decode_args &a = L->a;
     memset(&a, 0, sizeof(a));
     a.kpool = kv->kslot(slot);
     a.vpool = kv->vslot(slot);
@@ -860,8 +880,10 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
     /* up to 256 splits, each split's first two page ids ride in the launch
      * arguments (from the host mirror of the page table), so the kernel's
      * first row loads wait on no page-table load */
-    const bool arg_pages = total <= Q38_HEAD_PAGE_SPLITS;
+    const bool arg_pages = arg_pages_choice < 0 ? total <= Q38_HEAD_PAGE_SPLITS : arg_pages_choice > 0;
     if (arg_pages) {
+        if (total > Q38_HEAD_PAGE_SPLITS)
+            return fail("%d splits: at most %d carry their page ids in the arguments", total, Q38_HEAD_PAGE_SPLITS);
         for (int b = 0; b < n_seq; ++b) {
             const int32_t *row = &kv->page_table[(size_t)seq_ids[b] * kv->pt_stride];
             const int held = kv->seq_pages[seq_ids[b]];
@@ -874,27 +896,42 @@ int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const 
         }
     }
 
-    const bool any_multi = plan.work_bytes > 0;
-    if (any_multi) {
-        if (work == nullptr) return fail("decode workspace missing");
+    L->merge = plan.work_bytes > 0;
+    if (work != nullptr) {
         a.part_o = static_cast<float *>(work);
         a.part_ml = a.part_o + (size_t)total * Q38_ATTN_HEADS * Q38_ATTN_HEAD_DIM;
+    } else if (L->merge) {
+        return fail("decode workspace missing");
     }
-    hipFunction_t f = pre != nullptr ? (arg_pages ? ctx->f_decode_split_pre : ctx->f_decode_split_pre_many)
-                                     : (arg_pages ? ctx->f_decode_split : ctx->f_decode_split_many);
-    if (ctx->launch(f, total, Q38_ATTN_KV_HEADS, 1, ctx->decode_block, &a)) return -1;
-    if (any_multi) {
-        q38_merge_args m;
-        memset(&m, 0, sizeof(m));
-        m.part_o = a.part_o;
-        m.part_ml = a.part_ml;
-        m.gate = a.gate;
-        m.gate_head_stride = a.gate_head_stride;
-        m.out = d_out;
-        m.n_seq = n_seq;
-        memcpy(m.split_base, a.split_base, sizeof(m.split_base));
-        if (ctx->launch(ctx->f_decode_merge, n_seq, Q38_ATTN_HEADS, 4, 256, &m)) return -1;
-    }
+    const bool one = arg_pages && n_seq == 1;
+    L->f = pre != nullptr ? (one ? ctx->f_decode_split_pre_one
+                                 : arg_pages ? ctx->f_decode_split_pre : ctx->f_decode_split_pre_many)
+                          : (one ? ctx->f_decode_split_one : arg_pages ? ctx->f_decode_split : ctx->f_decode_split_many);
+    L->grid_x = (unsigned)total;
+    q38_merge_args &m = L->m;
+    memset(&m, 0, sizeof(m));
+    m.part_o = a.part_o;
+    m.part_ml = a.part_ml;
+    m.gate = a.gate;
+    m.gate_head_stride = a.gate_head_stride;
+    m.out = d_out;
+    m.n_seq = n_seq;
+    memcpy(m.split_base, a.split_base, sizeof(m.split_base));
+    return 0;
+}
+
+/* One decode launch (plus the merge) for n_seq <= Q38_MAX_BATCH sequences
+ * whose pages are reserved; `work` holds plan.work_bytes. */
+int decode_chunk(q38_kv *kv, int slot, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                 const float *d_q, const float *d_k_new, const float *d_v_new, const float *d_gate,
+                 float *d_out, const decode_plan &plan, void *work, const decode_pre *pre = nullptr) {
+    q38_ctx *ctx = kv->ctx;
+    decode_launch L;
+    if (build_decode(kv, slot, n_seq, seq_ids, positions, d_q, d_k_new, d_v_new, d_gate, d_out, plan,
+                     plan.work_bytes > 0 ? work : nullptr, pre, -1, &L))
+        return -1;
+    if (ctx->launch(L.f, L.grid_x, Q38_ATTN_KV_HEADS, 1, ctx->decode_block, &L.a)) return -1;
+    if (L.merge && ctx->launch(ctx->f_decode_merge, n_seq, Q38_ATTN_HEADS, 4, 256, &L.m)) return -1;
     return 0;
 }
 
@@ -1036,6 +1073,179 @@ int q38_full_core_noalloc(q38_kv *kv, int layer, int n_seq, const int32_t *seq_i
     const decode_pre pre{d_q_norm, d_k_norm};
     return decode_all(kv, layer, n_seq, seq_ids, positions, d_q_and_gate, d_key, d_value, nullptr, d_out, &pre,
                       kv->ctx->scratch, Q38_NOALLOC_SCRATCH_BYTES);
+}
+
+/* ----------------------------------------------------- replayed decode graph */
+
+/* A token's decode calls as one instantiated HIP graph: per call a split
+ * node and a merge node (the merge exits at once when every sequence has
+ * one split), in call order.  Launch arguments depend on the positions and
+ * are rewritten in place by q38_decode_graph_set_positions. */
+struct q38_decode_graph {
+    struct Call {
+        q38_decode_call c;
+        int slot = 0;
+        bool appends = false;
+        bool has_pre = false;
+        decode_pre pre{nullptr, nullptr};
+        hipGraphNode_t split_node = nullptr;
+        hipGraphNode_t merge_node = nullptr;
+        decode_launch L;
+    };
+    q38_kv *kv = nullptr;
+    int n_seq = 0;
+    int arg_pages = 0; /* the split kernel taking first page ids as arguments (batch 1) */
+    int32_t seq_ids[Q38_MAX_BATCH] = {0};
+    int32_t positions[Q38_MAX_BATCH] = {0};
+    std::vector<Call> calls;
+    void *work = nullptr;
+    size_t work_bytes = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    ~q38_decode_graph() {
+        if (exec != nullptr) (void)hipGraphExecDestroy(exec);
+        if (graph != nullptr) (void)hipGraphDestroy(graph);
+        if (work != nullptr) (void)hipFree(work);
+    }
+
+    /* Checks of positions for every call, with nothing changed; then the
+     * workspace (grown only between replays: the caller's stream is idle),
+     * the page reservations and each call's launch arguments. */
+    int prepare(const int32_t *pos) {
+        if (pos == nullptr) return fail("NULL positions");
+        for (const Call &k : calls) {
+            int slot = 0;
+            if (validate_decode(kv, k.c.layer, n_seq, seq_ids, pos, k.appends, &slot)) return -1;
+        }
+        decode_plan plan;
+        if (plan_decode(kv->ctx, n_seq, pos, &plan)) return -1;
+        if (arg_pages && plan.total_splits > Q38_HEAD_PAGE_SPLITS)
+            return fail("%d splits: this graph's split kernel takes at most %d", plan.total_splits,
+                        Q38_HEAD_PAGE_SPLITS);
+        const size_t need = (size_t)plan.total_splits * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2) * sizeof(float);
+        if (need > work_bytes) {
+            if (work != nullptr) {
+                Q38_HIP(hipStreamSynchronize(kv->ctx->stream));
+                Q38_HIP(hipFree(work));
+                work = nullptr;
+                work_bytes = 0;
+            }
+            const size_t want = std::max(need, (size_t)1 << 20);
+            Q38_HIP(hipMalloc(&work, want));
+            work_bytes = want;
+        }
+        bool any_append = false;
+        for (const Call &k : calls) any_append |= k.appends;
+        if (any_append)
+            for (int b = 0; b < n_seq; ++b)
+                if (kv->reserve(seq_ids[b], pos[b] + 1)) return -1;
+        for (Call &k : calls) {
+            if (build_decode(kv, k.slot, n_seq, seq_ids, pos, k.c.d_q, k.c.d_k_new, k.c.d_v_new,
+                             k.has_pre ? nullptr : k.c.d_gate, k.c.d_out, plan, work, k.has_pre ? &k.pre : nullptr,
+                             arg_pages, &k.L))
+                return -1;
+        }
+        memcpy(positions, pos, sizeof(int32_t) * n_seq);
+        return 0;
+    }
+
+    void node_params(Call &k, bool merge, hipKernelNodeParams *p, void **arg) {
+        *p = hipKernelNodeParams{};
+        if (!merge) {
+            *arg = &k.L.a;
+            p->func = reinterpret_cast<void *>(k.L.f);
+            p->gridDim = dim3(k.L.grid_x, Q38_ATTN_KV_HEADS, 1);
+            p->blockDim = dim3(kv->ctx->decode_block, 1, 1);
+        } else {
+            *arg = &k.L.m;
+            p->func = reinterpret_cast<void *>(kv->ctx->f_decode_merge);
+            p->gridDim = dim3(n_seq, Q38_ATTN_HEADS, 4);
+            p->blockDim = dim3(256, 1, 1);
+        }
+        p->kernelParams = arg;
+        p->sharedMemBytes = 0;
+        p->extra = nullptr;
+    }
+};
+
+int q38_decode_graph_create(q38_kv *kv, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                            int n_calls, const q38_decode_call *calls, q38_decode_graph **out) {
+    if (out == nullptr) return fail("NULL out");
+    *out = nullptr;
+    if (kv == nullptr) return fail("kv is NULL");
+    if (n_seq < 1 || n_seq > Q38_MAX_BATCH) return fail("n_seq %d outside 1..%d", n_seq, Q38_MAX_BATCH);
+    if (seq_ids == nullptr || positions == nullptr) return fail("NULL seq_ids/positions");
+    if (n_calls < 1 || calls == nullptr) return fail("no decode calls");
+    std::unique_ptr<q38_decode_graph> g(new q38_decode_graph());
+    g->kv = kv;
+    g->n_seq = n_seq;
+    memcpy(g->seq_ids, seq_ids, sizeof(int32_t) * n_seq);
+    for (int b = 0; b < n_seq; ++b)
+        for (int c = 0; c < b; ++c)
+            if (seq_ids[c] == seq_ids[b]) return fail("sequence %d appears twice", seq_ids[b]);
+    g->arg_pages = n_seq == 1 && kv->ctx->split_tokens == 0 ? 1 : 0;
+    g->calls.resize(n_calls);
+    for (int i = 0; i < n_calls; ++i) {
+        q38_decode_graph::Call &k = g->calls[i];
+        k.c = calls[i];
+        if (kv->slot_of(k.c.layer, &k.slot)) return -1;
+        if (k.c.d_q == nullptr || k.c.d_out == nullptr) return fail("call %d: NULL q/out", i);
+        if ((k.c.d_q_norm == nullptr) != (k.c.d_k_norm == nullptr))
+            return fail("call %d: d_q_norm and d_k_norm go together", i);
+        k.has_pre = k.c.d_q_norm != nullptr;
+        if (k.has_pre && (k.c.d_k_new == nullptr || k.c.d_v_new == nullptr))
+            return fail("call %d: full_core needs its key and value", i);
+        if ((k.c.d_k_new == nullptr) != (k.c.d_v_new == nullptr))
+            return fail("call %d: d_k_new and d_v_new go together", i);
+        k.appends = k.c.d_k_new != nullptr;
+        k.pre = decode_pre{k.c.d_q_norm, k.c.d_k_norm};
+    }
+    if (g->prepare(positions)) return -1;
+    Q38_HIP(hipGraphCreate(&g->graph, 0));
+    hipGraphNode_t prev = nullptr;
+    for (q38_decode_graph::Call &k : g->calls) {
+        hipKernelNodeParams p;
+        void *arg = nullptr;
+        g->node_params(k, false, &p, &arg);
+        Q38_HIP(hipGraphAddKernelNode(&k.split_node, g->graph, prev ? &prev : nullptr, prev ? 1 : 0, &p));
+        prev = k.split_node;
+        g->node_params(k, true, &p, &arg);
+        Q38_HIP(hipGraphAddKernelNode(&k.merge_node, g->graph, &prev, 1, &p));
+        prev = k.merge_node;
+    }
+    Q38_HIP(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0));
+    *out = g.release();
+    return 0;
+}
+
+int q38_decode_graph_set_positions(q38_decode_graph *g, const int32_t *positions) {
+    if (g == nullptr) return fail("graph is NULL");
+    /* a replay still running reads the arguments being replaced */
+    Q38_HIP(hipStreamSynchronize(g->kv->ctx->stream));
+    if (g->prepare(positions)) return -1;
+    for (q38_decode_graph::Call &k : g->calls) {
+        hipKernelNodeParams p;
+        void *arg = nullptr;
+        g->node_params(k, false, &p, &arg);
+        Q38_HIP(hipGraphExecKernelNodeSetParams(g->exec, k.split_node, &p));
+        g->node_params(k, true, &p, &arg);
+        Q38_HIP(hipGraphExecKernelNodeSetParams(g->exec, k.merge_node, &p));
+    }
+    return 0;
+}
+
+int q38_decode_graph_launch(q38_decode_graph *g) {
+    if (g == nullptr) return fail("graph is NULL");
+    Q38_HIP(hipGraphLaunch(g->exec, g->kv->ctx->stream));
+    return 0;
+}
+
+int q38_decode_graph_destroy(q38_decode_graph *g) {
+    if (g == nullptr) return 0;
+    Q38_HIP(hipStreamSynchronize(g->kv->ctx->stream));
+    delete g;
+    return 0;
 }
 
 namespace {

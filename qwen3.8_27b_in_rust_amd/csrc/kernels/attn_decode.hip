@@ -176,7 +176,10 @@ Q38_DEV void q38_norm_rope4_cs(f32x4 &x, f32x4 w, int lane, const float (*cs)[2]
 #define Q38_DECODE_MIN_WGS 1 /* workgroups per CU the register budget is sized for */
 #endif
 
-template <bool kPre, bool kArgPages>
+/* kOneSeq: a launch of one sequence (n_seq == 1, split g of that sequence),
+ * so every argument a workgroup needs sits at a fixed offset and is loaded
+ * in one round, before the first row loads. */
+template <bool kPre, bool kArgPages, bool kOneSeq = false>
 Q38_DEV void decode_split(const q38_decode_args &a) {
     constexpr int NW = Q38_DECODE_WAVES;
     __shared__ float red_o[NW][Q38_ATTN_GROUP][Q38_ATTN_HEAD_DIM];
@@ -187,11 +190,12 @@ Q38_DEV void decode_split(const q38_decode_args &a) {
     const int g = blockIdx.x;
     const int j = blockIdx.y;
     int b = 0;
-    while (b + 1 < a.n_seq && a.split_base[b + 1] <= g) ++b;
-    const int seq = a.seq[b];
-    const int pos = a.pos[b];
-    const int split = g - a.split_base[b];
-    const int nsplit = a.split_base[b + 1] - a.split_base[b];
+    if (!kOneSeq)
+        while (b + 1 < a.n_seq && a.split_base[b + 1] <= g) ++b;
+    const int seq = kOneSeq ? a.seq[0] : a.seq[b];
+    const int pos = kOneSeq ? a.pos[0] : a.pos[b];
+    const int split = kOneSeq ? g : g - a.split_base[b];
+    const int nsplit = kOneSeq ? a.total_splits : a.split_base[b + 1] - a.split_base[b];
     const int t_begin = split * a.split_tokens;
     const int t_end = min(pos + 1, t_begin + a.split_tokens);
 
@@ -430,6 +434,12 @@ extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WG
     decode_split<false, true>(a);
 }
 
+/* One sequence of at most Q38_HEAD_PAGE_SPLITS splits (batch-1 decode). */
+extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_one(
+    q38_decode_args a) {
+    decode_split<false, true, true>(a);
+}
+
 /* Any number of splits: every page id read from the page table. */
 extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_many(
     q38_decode_args a) {
@@ -442,6 +452,11 @@ extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WG
 extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_pre(
     q38_decode_args a) {
     decode_split<true, true>(a);
+}
+
+extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_pre_one(
+    q38_decode_args a) {
+    decode_split<true, true, true>(a);
 }
 
 extern "C" __global__ __launch_bounds__(64 * Q38_DECODE_WAVES, Q38_DECODE_MIN_WGS) void q38_attn_decode_split_pre_many(

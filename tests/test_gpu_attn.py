@@ -479,10 +479,12 @@ def test_prefill_4096_prompt(pkg, ctx, ref, margin):
 def test_prefill_past_64_query_blocks(pkg, ctx, ref, margin):
     """Prompts of more than 64 query blocks run one job per workgroup in the
     grid's own order (shorter ones on host-placed jobs): 4160 tokens after a
-    100-token prefix, rows of the first, last and ragged query blocks and
-    samples between."""
+    100-token prefix (65 query blocks).  All 24 heads of one row in every
+    64-query block (its row offset varies from block to block), plus the
+    first, last and ragged rows and samples between."""
     T = 4160
-    rows = sorted(set([0, 1, 63, 64, 2047, 4095, 4096, 4127, 4128, T - 1] +
+    per_block = [qb * 64 + (qb * 37) % 64 for qb in range((T + 63) // 64)]
+    rows = sorted(set([0, 1, 63, 64, 2047, 4095, 4096, 4127, 4128, T - 1] + [r for r in per_block if r < T] +
                       list(np.random.default_rng(11).integers(0, T, 12))))
     _check_rows(margin, _prefill_case(pkg, ctx, ref, 100, T, 990, rows=rows))
 
