@@ -14,6 +14,16 @@
  *   dot_q4_k_q8_k_scalar          src/kernel/tensor.rs:365-391
  *   dot_q5_k_q8_k_scalar          src/kernel/tensor.rs:393-428
  *   dot_q6_k_q8_k_scalar          src/kernel/tensor.rs:430-457
+ *   unpack_q3_scales              src/kernel/tensor.rs:34-44
+ *   dot_q3_k_q8_k_scalar          src/kernel/tensor.rs:335-363
+ *   dot_iq4_xs_q8_k               src/kernel/iq.rs:379-405 (KVALUES_IQ4NL,
+ *                                 src/kernel/iq_tables.rs:53-56)
+ *   dot_f32/f16/bf16/q8_0_scalar  src/kernel/tensor.rs:79-117 (the row dots
+ *                                 of tensor_gemv_f32 / tensor_gemm_f32,
+ *                                 tensor.rs:1095-1129, :1175-1215, for the
+ *                                 weights project() does not quantise
+ *                                 for, ops.rs:632-637), bf16_to_f32
+ *                                 src/kernel/quant.rs:49-51
  *   gemv_rows / gemm_rows         src/kernel/tensor.rs:954-1002 (every
  *                                 output element is one row dot, so the
  *                                 row split across threads does not change it)
@@ -246,11 +256,97 @@ static float dot_q6_k(const uint8_t *data, const q8k_view *q, int blocks) {
     return total;
 }
 
+/* unpack_q3_scales, tensor.rs:34-44: 16 signed 6-bit scales from 12 bytes */
+static void unpack_q3_scales(const uint8_t *packed, int8_t *scales) {
+    for (int index = 0; index < 16; ++index) {
+        const uint8_t low = index < 8 ? (uint8_t)(packed[index] & 15) : (uint8_t)(packed[index - 8] >> 4);
+        const uint8_t high = (uint8_t)((packed[8 + index % 4] >> (2 * (index / 4))) & 3);
+        scales[index] = (int8_t)((int32_t)(low | (high << 4)) - 32);
+    }
+}
+
+/* dot_q3_k_q8_k_scalar, tensor.rs:335-363.  Block: hmask[32] | qs[64] |
+ * scales[12] | d (f16), 110 bytes. */
+static float dot_q3_k(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *blk = data + (size_t)block * 110;
+        const uint8_t *high = blk;
+        const uint8_t *low = blk + 32;
+        int8_t scales[16];
+        unpack_q3_scales(blk + 96, scales);
+        const float d = q38r_f16_to_f32(read_u16(blk + 108)) * b->scale;
+        int32_t weighted = 0;
+        int group = 0;
+        for (int half = 0; half < 2; ++half) {
+            for (int field = 0; field < 4; ++field) {
+                const uint8_t high_bit = (uint8_t)(1u << group);
+                const int32_t scale0 = scales[group * 2];
+                const int32_t scale1 = scales[group * 2 + 1];
+                for (int lane = 0; lane < 32; ++lane) {
+#if Q38R_MUTANT == 19
+                    const int32_t qv = (int32_t)((low[half * 32 + lane] >> (field * 2)) & 3) -
+                                       ((high[lane] & high_bit) ? 4 : 0); /* planted: high-bit sense inverted */
+#else
+                    const int32_t qv = (int32_t)((low[half * 32 + lane] >> (field * 2)) & 3) -
+                                       ((high[lane] & high_bit) ? 0 : 4);
+#endif
+                    const int32_t scale = lane < 16 ? scale0 : scale1;
+                    weighted += scale * qv * b->quants[half * 128 + field * 32 + lane];
+                }
+                group += 1;
+            }
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
+/* KVALUES_IQ4NL (src/kernel/iq_tables.rs:53-56): ggml's published 16-entry
+ * code book of the IQ4_NL / IQ4_XS formats. */
+static const int8_t kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                         1,    13,   25,  38,  53,  69,  89,  113};
+
+/* dot_iq4_xs_q8_k, iq.rs:379-405.  Block: d (f16) | scales_h (u16) |
+ * scales_l[4] | qs[128], 136 bytes. */
+static float dot_iq4_xs(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 136;
+        const float d = q38r_f16_to_f32(read_u16(w)) * b->scale;
+        const uint16_t scale_high = read_u16(w + 2);
+        const uint8_t *scale_low = w + 4;
+        const uint8_t *quants = w + 8;
+        int32_t weighted = 0;
+        for (int group = 0; group < 8; ++group) {
+            const int32_t scale = (int32_t)((scale_low[group / 2] >> (4 * (group % 2))) & 15) |
+                                  (int32_t)((scale_high >> (2 * group)) & 3) << 4;
+            int32_t subtotal = 0;
+            for (int lane = 0; lane < 16; ++lane) {
+                const uint8_t packed = quants[group * 16 + lane];
+                subtotal += (int32_t)b->quants[group * 32 + lane] * kvalues_iq4nl[packed & 15];
+                subtotal += (int32_t)b->quants[group * 32 + lane + 16] * kvalues_iq4nl[packed >> 4];
+            }
+#if Q38R_MUTANT == 20
+            weighted += scale * subtotal; /* planted: the 32 offset dropped */
+#else
+            weighted += (scale - 32) * subtotal;
+#endif
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
 int q38r_quant_block_bytes(int ggml_type) {
     switch (ggml_type) {
+    case Q38R_GGML_Q3_K: return 110;
     case Q38R_GGML_Q4_K: return 144;
     case Q38R_GGML_Q5_K: return 176;
     case Q38R_GGML_Q6_K: return 210;
+    case Q38R_GGML_IQ4_XS: return 136;
     default: return 0;
     }
 }
@@ -272,6 +368,8 @@ float q38r_dot_q8_k(int ggml_type, const uint8_t *row, const void *planar, int n
     case Q38R_GGML_Q4_K: return dot_q4_k(row, view, blocks);
     case Q38R_GGML_Q5_K: return dot_q5_k(row, view, blocks);
     case Q38R_GGML_Q6_K: return dot_q6_k(row, view, blocks);
+    case Q38R_GGML_Q3_K: return dot_q3_k(row, view, blocks);
+    case Q38R_GGML_IQ4_XS: return dot_iq4_xs(row, view, blocks);
     default: return NAN;
     }
 }
@@ -312,6 +410,116 @@ int q38r_gemv_q8_k(int ggml_type, int rows, int width, const void *weights, cons
             created[i] = 1;
         else
             gemv_worker(&jobs[i]);
+    }
+    for (int i = 0; i < n_threads; ++i)
+        if (created[i]) pthread_join(th[i], NULL);
+    return 0;
+}
+
+/* ---------------------------------------------------------------- f32 input */
+
+static float read_f32(const uint8_t *p) {
+    float v;
+    memcpy(&v, p, sizeof(v));
+    return v;
+}
+
+/* bf16_to_f32, quant.rs:49-51 */
+static float bf16_to_f32(const uint8_t *p) {
+    const uint32_t bits = (uint32_t)read_u16(p) << 16;
+    float v;
+    memcpy(&v, &bits, sizeof(v));
+    return v;
+}
+
+/* Bytes of one block of `block_elems` weights of an f32-path type. */
+int q38r_f32_block(int ggml_type, int *block_elems) {
+    switch (ggml_type) {
+    case Q38R_GGML_F32: *block_elems = 1; return 4;
+    case Q38R_GGML_F16: *block_elems = 1; return 2;
+    case Q38R_GGML_BF16: *block_elems = 1; return 2;
+    case Q38R_GGML_Q8_0: *block_elems = 32; return 34;
+    default: *block_elems = 0; return 0;
+    }
+}
+
+/* dot_f32_scalar / dot_f16_scalar / dot_bf16_scalar / dot_q8_0_scalar,
+ * tensor.rs:79-117: one sequential fused multiply-add chain over the row
+ * (mul_add).  Q8_0: d * q rounded first, then the fused add. */
+float q38r_dot_f32_row(int ggml_type, const uint8_t *row, const float *input, int n) {
+    float total = 0.0f;
+    switch (ggml_type) {
+    case Q38R_GGML_F32:
+        for (int i = 0; i < n; ++i) total = fmaf(read_f32(row + (size_t)i * 4), input[i], total);
+        return total;
+    case Q38R_GGML_F16:
+        for (int i = 0; i < n; ++i) total = fmaf(q38r_f16_to_f32(read_u16(row + (size_t)i * 2)), input[i], total);
+        return total;
+    case Q38R_GGML_BF16:
+#if Q38R_MUTANT == 21
+        for (int i = 0; i < n; ++i) total = fmaf(bf16_to_f32(row + (size_t)(i ^ 1) * 2), input[i], total); /* planted */
+#else
+        for (int i = 0; i < n; ++i) total = fmaf(bf16_to_f32(row + (size_t)i * 2), input[i], total);
+#endif
+        return total;
+    case Q38R_GGML_Q8_0: {
+        int base = 0, block = 0;
+        while (base < n) {
+            const float d = q38r_f16_to_f32(read_u16(row + (size_t)block * 34));
+            for (int i = 0; i < 32; ++i) {
+                const int8_t q = (int8_t)row[(size_t)block * 34 + 2 + i];
+                total = fmaf(d * (float)q, input[base + i], total);
+            }
+            base += 32;
+            block += 1;
+        }
+        return total;
+    }
+    default:
+        return NAN;
+    }
+}
+
+typedef struct {
+    int type, rows, width, n_tokens, row0, row1;
+    size_t row_bytes;
+    const uint8_t *weights;
+    const float *input;
+    float *out;
+} gemv_f32_job;
+
+static void *gemv_f32_worker(void *arg) {
+    const gemv_f32_job *j = (const gemv_f32_job *)arg;
+    for (int row = j->row0; row < j->row1; ++row)
+        for (int t = 0; t < j->n_tokens; ++t)
+            j->out[(size_t)t * j->rows + row] = q38r_dot_f32_row(j->type, j->weights + (size_t)row * j->row_bytes,
+                                                                 j->input + (size_t)t * j->width, j->width);
+    return NULL;
+}
+
+/* tensor_gemv_f32 / tensor_gemm_f32 (tensor.rs:1095-1129, :1175-1215):
+ * out[t*rows + row] = dot_row(row, input token t); rows over threads. */
+int q38r_gemv_f32(int ggml_type, int rows, int width, const void *weights, const float *input, int n_tokens,
+                  float *out, int n_threads) {
+    int be = 0;
+    const int bb = q38r_f32_block(ggml_type, &be);
+    if (bb == 0 || width % be != 0 || rows < 0 || n_tokens < 0) return -1;
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > 64) n_threads = 64;
+    pthread_t th[64];
+    int created[64] = {0};
+    gemv_f32_job jobs[64];
+    const int per = (rows + n_threads - 1) / n_threads;
+    for (int i = 0; i < n_threads; ++i) {
+        const int row0 = i * per;
+        const int row1 = (i + 1) * per < rows ? (i + 1) * per : rows;
+        if (row0 >= row1) break;
+        jobs[i] = (gemv_f32_job){ggml_type, rows, width, n_tokens, row0, row1, (size_t)(width / be) * bb,
+                                 (const uint8_t *)weights, input, out};
+        if (n_threads > 1 && pthread_create(&th[i], NULL, gemv_f32_worker, &jobs[i]) == 0)
+            created[i] = 1;
+        else
+            gemv_f32_worker(&jobs[i]);
     }
     for (int i = 0; i < n_threads; ++i)
         if (created[i]) pthread_join(th[i], NULL);

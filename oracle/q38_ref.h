@@ -99,9 +99,15 @@ void q38r_linear_core(const float *conv_w, const float *dt, const float *a,
 
 /* ---- weight projections: src/kernel/quant.rs, src/kernel/tensor.rs ---- */
 #define Q38R_Q8K_BLOCK 256
+#define Q38R_GGML_F32 0
+#define Q38R_GGML_F16 1
+#define Q38R_GGML_Q8_0 8
+#define Q38R_GGML_Q3_K 11
 #define Q38R_GGML_Q4_K 12
 #define Q38R_GGML_Q5_K 13
 #define Q38R_GGML_Q6_K 14
+#define Q38R_GGML_IQ4_XS 23
+#define Q38R_GGML_BF16 30
 
 float q38r_f16_to_f32(uint16_t value);                                   /* quant.rs:22-47 */
 /* quantize_block, quant.rs:55-95: one 256-value block. */
@@ -112,13 +118,23 @@ void q38r_quantize_block(const float *values, float *scale, int8_t *quants, int1
 int q38r_quantize_q8_k(const float *input, int n_tokens, int width, void *planar);
 /* Bytes of one 256-weight block of a K-quant type (0 if unsupported). */
 int q38r_quant_block_bytes(int ggml_type);
-/* dot_q4/q5/q6_k_q8_k_scalar (tensor.rs:365-457): one weight row against
- * token `token` of a planar Q8_K buffer of n_tokens rows. */
+/* dot_q3/q4/q5/q6_k_q8_k_scalar (tensor.rs:335-457) and dot_iq4_xs_q8_k
+ * (iq.rs:379-405): one weight row against token `token` of a planar Q8_K
+ * buffer of n_tokens rows. */
 float q38r_dot_q8_k(int ggml_type, const uint8_t *row, const void *planar, int n_tokens, int width, int token);
 /* tensor_gemv_q8_k / tensor_gemm_q8_k (tensor.rs:1131-1173, :1217-1270):
  * out[t*rows + row] for every row and token; rows split over threads. */
 int q38r_gemv_q8_k(int ggml_type, int rows, int width, const void *weights, const void *planar, int n_tokens,
                    float *out, int n_threads);
+
+/* The f32-input path (tensor_gemv_f32 / tensor_gemm_f32, tensor.rs:1095-1129,
+ * :1175-1215) for F32, F16, BF16 and Q8_0 weights: bytes and weights of one
+ * block (0 if unsupported), one row dot (dot_*_scalar, tensor.rs:79-117),
+ * and out[t*rows + row] for n_tokens f32 input rows [T][width]. */
+int q38r_f32_block(int ggml_type, int *block_elems);
+float q38r_dot_f32_row(int ggml_type, const uint8_t *row, const float *input, int n);
+int q38r_gemv_f32(int ggml_type, int rows, int width, const void *weights, const float *input, int n_tokens,
+                  float *out, int n_threads);
 
 /* Layer slot maps, ops.rs:38-47. */
 int q38r_is_full_attention(int layer);

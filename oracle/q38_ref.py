@@ -68,6 +68,8 @@ def open_library(path: str):
         "q38r_quantize_q8_k": (c_int, [_F, c_int, c_int, ctypes.c_void_p]),
         "q38r_quant_block_bytes": (c_int, [c_int]),
         "q38r_gemv_q8_k": (c_int, [c_int, c_int, c_int, ctypes.c_void_p, ctypes.c_void_p, c_int, _F, c_int]),
+        "q38r_f32_block": (c_int, [c_int, ctypes.POINTER(c_int)]),
+        "q38r_gemv_f32": (c_int, [c_int, c_int, c_int, ctypes.c_void_p, _F, c_int, _F, c_int]),
         "q38r_is_full_attention": (c_int, [c_int]),
         "q38r_recurrent_index": (c_int, [c_int]),
         "q38r_available_cores": (c_int, []),
@@ -183,8 +185,11 @@ def linear_core(conv_w, dt, a, norm_w, conv_state, delta_state, qkv, z, beta, al
 
 
 # ------------------------------------------------------- weight projections
-GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 12, 13, 14
-QUANT_BLOCK_BYTES = {GGML_Q4_K: 144, GGML_Q5_K: 176, GGML_Q6_K: 210}
+GGML_Q3_K, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_IQ4_XS = 11, 12, 13, 14, 23
+QUANT_BLOCK_BYTES = {GGML_Q3_K: 110, GGML_Q4_K: 144, GGML_Q5_K: 176, GGML_Q6_K: 210, GGML_IQ4_XS: 136}
+# the f32-input path's weight types: (weights per block, bytes per block)
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
+F32_PATH_BLOCKS = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_BF16: (1, 2), GGML_Q8_0: (32, 34)}
 
 
 def q8k_bytes(n_tokens: int, width: int) -> int:
@@ -225,5 +230,21 @@ def gemv_q8_k(ggml_type: int, weights: np.ndarray, planar: np.ndarray, n_tokens:
     out = np.empty((n_tokens, rows), np.float32)
     p = np.ascontiguousarray(planar, np.uint8)
     if lib().q38r_gemv_q8_k(ggml_type, rows, width, w.ctypes.data, p.ctypes.data, n_tokens, _f(out), threads) != 0:
+        raise ValueError("unsupported type or width")
+    return out
+
+
+def gemv_f32(ggml_type: int, weights: np.ndarray, x: np.ndarray, threads: int = 1) -> np.ndarray:
+    """tensor_gemv_f32 / tensor_gemm_f32 (tensor.rs:1095-1129, :1175-1215):
+    out [T][rows] for weights [rows][row_bytes] of an F32/F16/BF16/Q8_0 type
+    and f32 input x [T][width]."""
+    w = np.ascontiguousarray(weights, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    T, W = x.shape
+    rows = w.shape[0]
+    out = np.empty((T, rows), np.float32)
+    if lib().q38r_gemv_f32(ggml_type, rows, W, w.ctypes.data, _f(x), T, _f(out), threads) != 0:
         raise ValueError("unsupported type or width")
     return out

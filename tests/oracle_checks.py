@@ -331,13 +331,47 @@ def _scale_min(s, j):
     return (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4), (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
 
 
+# ggml's published IQ4_NL / IQ4_XS code book
+_KVALUES_IQ4 = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int64)
+
+
+def _q3k_scales(sc12):
+    """The 16 6-bit Q3_K scales as ggml's dequantize_row_q3_K unpacks them:
+    four little-endian words, the high 2-bit pairs spread from the third."""
+    aux = np.frombuffer(np.asarray(sc12, np.uint8).tobytes(), np.uint32).astype(np.uint64)
+    k1, k2 = 0x03030303, 0x0F0F0F0F
+    tmp = aux[2]
+    words = [(aux[0] & k2) | (((tmp >> 0) & k1) << 4), (aux[1] & k2) | (((tmp >> 2) & k1) << 4),
+             ((aux[0] >> 4) & k2) | (((tmp >> 4) & k1) << 4), ((aux[1] >> 4) & k2) | (((tmp >> 6) & k1) << 4)]
+    return np.frombuffer(np.array(words, np.uint32).tobytes(), np.int8).astype(np.int64) - 32
+
+
 def _dequant_row(ty, row):
     """A weight row's values the way the decoded path reads them."""
     out = []
-    bb = {12: 144, 13: 176, 14: 210}[ty]
+    bb = {11: 110, 12: 144, 13: 176, 14: 210, 23: 136}[ty]
     for blk in np.asarray(row, np.uint8).reshape(-1, bb).astype(np.int64):
         w = np.zeros(256)
-        if ty in (12, 13):
+        if ty == 11:
+            hm, qs, d = blk[0:32], blk[32:96], _f16(blk[108], blk[109])
+            sc = _q3k_scales(blk[96:108].astype(np.uint8))
+            m, i = 0, 0
+            for n in range(2):
+                for shift in range(0, 8, 2):
+                    for part in range(2):
+                        lanes = np.arange(16 * part, 16 * part + 16)
+                        qv = ((qs[32 * n + lanes] >> shift) & 3) - np.where(hm[lanes] & (1 << m), 0, 4)
+                        w[128 * n + 32 * (shift // 2) + 16 * part + np.arange(16)] = d * sc[i] * qv
+                        i += 1
+                    m += 1
+        elif ty == 23:
+            d, sh, sl, qs = _f16(blk[0], blk[1]), int(blk[2]) | (int(blk[3]) << 8), blk[4:8], blk[8:136]
+            for ib in range(8):
+                ls = ((sl[ib // 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+                q = qs[16 * ib:16 * ib + 16]
+                w[32 * ib:32 * ib + 16] = d * (ls - 32) * _KVALUES_IQ4[q & 15]
+                w[32 * ib + 16:32 * ib + 32] = d * (ls - 32) * _KVALUES_IQ4[q >> 4]
+        elif ty in (12, 13):
             d, dmin = _f16(blk[0], blk[1]), _f16(blk[2], blk[3])
             s = blk[4:16]
             qs = blk[16:144] if ty == 12 else blk[48:176]
@@ -369,15 +403,19 @@ def _dequant_row(ty, row):
 def _random_kquant(ty, rows, width, seed):
     """Weight rows of random bytes with finite, moderate f16 scales."""
     rng = np.random.default_rng(seed)
-    bb = {12: 144, 13: 176, 14: 210}[ty]
+    bb = {11: 110, 12: 144, 13: 176, 14: 210, 23: 136}[ty]
     w = rng.integers(0, 256, (rows, width // 256, bb), dtype=np.uint8)
     f16 = lambda lo, hi, n: np.frombuffer(rng.uniform(lo, hi, n).astype(np.float16).tobytes(), np.uint8).reshape(n, 2)
     n = rows * (width // 256)
     if ty in (12, 13):
         w.reshape(n, bb)[:, 0:2] = f16(1e-3, 4e-2, n)
         w.reshape(n, bb)[:, 2:4] = f16(1e-3, 4e-2, n)
-    else:
+    elif ty == 14:
         w.reshape(n, bb)[:, 208:210] = f16(1e-3, 4e-2, n)
+    elif ty == 11:
+        w.reshape(n, bb)[:, 108:110] = f16(1e-3, 4e-2, n)
+    else:
+        w.reshape(n, bb)[:, 0:2] = f16(1e-4, 4e-3, n)
     return w.reshape(rows, -1)
 
 
@@ -418,7 +456,7 @@ def check_kquant_dots_against_dequantised_rows(ref, synth):
     x[1] = ((np.arange(W) * 7919) % 101) / np.float32(50.0) - np.float32(1.0)
     p = ref.quantize_q8_k(x)
     a = _q8k_dequant(p, T, W, ref).reshape(T, W)
-    for ty in (ref.GGML_Q4_K, ref.GGML_Q5_K, ref.GGML_Q6_K):
+    for ty in (ref.GGML_Q3_K, ref.GGML_Q4_K, ref.GGML_Q5_K, ref.GGML_Q6_K, ref.GGML_IQ4_XS):
         wb = _random_kquant(ty, 7, W, 0x51333872 + ty)
         got = ref.gemv_q8_k(ty, wb, p, T, W)
         for r in range(7):
@@ -435,10 +473,64 @@ def check_gemv_serial_equals_threaded(ref, synth):
     W = 512
     x = np.random.default_rng(0x51333873).standard_normal((2, W)).astype(np.float32)
     p = ref.quantize_q8_k(x)
-    for ty in (ref.GGML_Q4_K, ref.GGML_Q6_K):
+    for ty in (ref.GGML_Q3_K, ref.GGML_Q4_K, ref.GGML_Q6_K, ref.GGML_IQ4_XS):
         wb = _random_kquant(ty, 37, W, 0x51333874 + ty)
         if not np.array_equal(ref.gemv_q8_k(ty, wb, p, 2, W, threads=1), ref.gemv_q8_k(ty, wb, p, 2, W, threads=5)):
             return f"type {ty}: threaded GEMV differs from serial"
+    return None
+
+
+def _random_f32_path(ty, rows, width, seed):
+    """Weight rows of an F32/F16/BF16/Q8_0 type: finite values of ~N(0, 0.05)
+    (Q8_0: random quants, f16 scales 1e-4..1e-2), and their values decoded in
+    numpy (float16 / the bf16 high half / d * q) as float64."""
+    rng = np.random.default_rng(seed)
+    if ty == 0:
+        v = (rng.standard_normal((rows, width)) * 0.05).astype(np.float32)
+        return v.view(np.uint8).reshape(rows, -1), v.astype(np.float64)
+    if ty == 1:
+        v = (rng.standard_normal((rows, width)) * 0.05).astype(np.float16)
+        return v.view(np.uint8).reshape(rows, -1), v.astype(np.float64)
+    if ty == 30:
+        f = (rng.standard_normal((rows, width)) * 0.05).astype(np.float32)
+        hi = (f.view(np.uint32) >> 16).astype(np.uint16)
+        return hi.view(np.uint8).reshape(rows, -1), (hi.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    nb = width // 32
+    q = rng.integers(-128, 128, (rows, nb, 32)).astype(np.int8)
+    d = rng.uniform(1e-4, 1e-2, (rows, nb)).astype(np.float16)
+    blk = np.zeros((rows, nb, 34), np.uint8)
+    blk[:, :, 0:2] = d.view(np.uint8).reshape(rows, nb, 2)
+    blk[:, :, 2:] = q.view(np.uint8)
+    vals = (d.astype(np.float64)[:, :, None] * q.astype(np.float64)).reshape(rows, width)
+    return blk.reshape(rows, -1), vals
+
+
+def check_f32_path_dots(ref, synth):
+    """tensor_gemv_f32's row dots (F32, F16, BF16, Q8_0) against the float64
+    dot of the weights decoded independently in numpy: within 1e-5 of the
+    sum of |w x| (a sequential f32 chain of ~1000 products), over random
+    inputs and the reference's own activation pattern (tensor.rs:582-586);
+    one row also against the closed form of a one-hot input (the weight
+    itself, exactly)."""
+    W, T, R = 1024, 3, 9
+    rng = np.random.default_rng(0x51333875)
+    x = rng.standard_normal((T, W)).astype(np.float32)
+    x[1] = ((np.arange(W) * 7919) % 101) / np.float32(50.0) - np.float32(1.0)
+    x[2] = 0.0
+    x[2, 37] = 1.0
+    for ty in (ref.GGML_F32, ref.GGML_F16, ref.GGML_BF16, ref.GGML_Q8_0):
+        wb, wv = _random_f32_path(ty, R, W, 0x51333876 + ty)
+        got = ref.gemv_f32(ty, wb, x)
+        for r in range(R):
+            for t in range(2):
+                want = float(np.dot(wv[r], x[t].astype(np.float64)))
+                scale = float(np.dot(np.abs(wv[r]), np.abs(x[t].astype(np.float64))))
+                if abs(got[t, r] - want) > 1e-5 * scale:
+                    return f"type {ty} row {r} token {t}: {got[t, r]} vs {want} (scale {scale:.3e})"
+            if got[2, r] != np.float32(wv[r, 37]):
+                return f"type {ty} row {r}: one-hot input gives {got[2, r]}, not the weight {wv[r, 37]}"
+        if not np.array_equal(got, ref.gemv_f32(ty, wb, x, threads=4)):
+            return f"type {ty}: threaded f32 GEMV differs from serial"
     return None
 
 

@@ -28,6 +28,9 @@ MUTANTS = {
     16: "Q6_K third quarter with the wrong high bits",
     17: "Q5_K fifth bit not advanced per chunk",
     18: "Q8_K group sums over the wrong groups",
+    19: "Q3_K high bit read with the opposite sense",
+    20: "IQ4_XS group scale without its -32 offset",
+    21: "BF16 row dot reading neighbouring elements swapped",
 }
 
 
