@@ -306,14 +306,17 @@ int q38_q8k_bytes(int n_tokens, int width, size_t *bytes);
 int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, void *d_q8k);
 
 /* tensor_gemv_q8_k / tensor_gemm_q8_k (src/kernel/tensor.rs:1131-1173,
- * :1217-1270) for Q4_K (ggml type 12), Q5_K (13) and Q6_K (14) weights:
- * d_weights [rows][width/256 blocks] in the GGUF block layout (144, 176,
- * 210 bytes per block, 16-byte aligned base), d_q8k from
- * q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the reference's
- * batched form writes it).  width is at most 49152.  Each element equals the
- * reference's scalar dot_q*_k_q8_k (tensor.rs:365-457) bit for bit.  From 32
- * tokens (16 for matrices of 8192 rows or more) the integer dots run on the
- * int8 matrix unit; the result is the same bit for bit. */
+ * :1217-1270) for Q3_K (ggml type 11), Q4_K (12), Q5_K (13), Q6_K (14) and
+ * IQ4_XS (23) weights: d_weights [rows][width/256 blocks] in the GGUF block
+ * layout (110, 144, 176, 210, 136 bytes per block, 16-byte aligned base),
+ * d_q8k from q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
+ * reference's batched form writes it).  width is at most 49152.  Each
+ * element equals the reference's scalar dot_q*_k_q8_k (tensor.rs:335-457)
+ * or dot_iq4_xs_q8_k (src/kernel/iq.rs:379-405) bit for bit.  For Q4_K, Q5_K
+ * and Q6_K from 32 tokens (16 for matrices of 8192 rows or more) the
+ * integer dots run on the int8 matrix unit; the result is the same bit for
+ * bit.  Other weight types fail with -1 (the reference's f32 path below, or
+ * types outside this path). */
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
                   int n_tokens, float *d_out);
 
@@ -327,6 +330,20 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
  * launch are paid once. */
 int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
                         const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out);
+
+/* tensor_gemv_f32 / tensor_gemm_f32 (src/kernel/tensor.rs:1095-1129,
+ * :1175-1215): the projection path of weights project() does not quantise
+ * for (ops.rs:632-637), with f32 activations d_x [n_tokens][width]:
+ * F32 (ggml type 0), F16 (1), BF16 (30) or Q8_0 (8) weights d_weights
+ * [rows][row bytes] in the GGUF layout, d_out [n_tokens][rows].  width a
+ * multiple of 8 (Q8_0: of 64), d_weights 16-byte aligned (Q8_0: 4), d_x
+ * 16-byte aligned.  Every product w * x is the reference's (Q8_0: d * q
+ * rounded, then multiplied); the sums are reassociated (the reference's own
+ * x86 build reassociates them too), so each element lies within the
+ * rounding of an f32 sum of the reference's scalar dot_*_scalar
+ * (tensor.rs:79-117). */
+int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const float *d_x,
+                 int n_tokens, float *d_out);
 
 #ifdef __cplusplus
 }

@@ -95,6 +95,7 @@ _SIGNATURES = {
     "q38_q8k_bytes": (c_int, [c_int, c_int, POINTER(c_size_t)]),
     "q38_quantize_q8_k": (c_int, [_P, c_int, c_int, _P, _P]),
     "q38_gemv_q8_k": (c_int, [_P, c_int, c_int, c_int, _P, _P, c_int, _P]),
+    "q38_gemv_f32": (c_int, [_P, c_int, c_int, c_int, _P, _P, c_int, _P]),
     "q38_gemv_q8_k_multi": (c_int, [_P, c_int, c_int, _I32P, c_int, POINTER(c_void_p), _P, c_int,
                                     POINTER(c_void_p)]),
     "q38_attn_prefill": (c_int, [_P, c_int, c_int, c_int, c_int, _P, _P, _P, _P, _P]),
@@ -312,6 +313,10 @@ class Context:
 
     def quantize_q8_k(self, n_tokens, width, x, q8k):
         _check(lib().q38_quantize_q8_k(self.handle, n_tokens, width, _ptr(x), _ptr(q8k)), "q38_quantize_q8_k")
+
+    def gemv_f32(self, ggml_type, rows, width, weights, x, n_tokens, out):
+        _check(lib().q38_gemv_f32(self.handle, ggml_type, rows, width, _ptr(weights), _ptr(x), n_tokens, _ptr(out)),
+               "q38_gemv_f32")
 
     def gemv_q8_k(self, ggml_type, rows, width, weights, q8k, n_tokens, out):
         _check(lib().q38_gemv_q8_k(self.handle, ggml_type, rows, width, _ptr(weights), _ptr(q8k), n_tokens,

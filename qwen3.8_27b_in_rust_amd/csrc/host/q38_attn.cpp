@@ -121,6 +121,9 @@ struct q38_ctx {
     hipFunction_t f_gemv_q4k = nullptr;
     hipFunction_t f_gemv_q5k = nullptr;
     hipFunction_t f_gemv_q6k = nullptr;
+    hipFunction_t f_gemv_q3k = nullptr;
+    hipFunction_t f_gemv_iq4xs = nullptr;
+    hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
     hipFunction_t f_copy = nullptr;
@@ -135,7 +138,7 @@ struct q38_ctx {
     int clock_khz = 0;
     int lds_bytes = 0;
     int lds_per_cu = 0;
-    int gemv_occupancy[3] = {1, 1, 1}; /* Q4_K, Q5_K, Q6_K GEMV workgroups a CU holds (registers) */
+    int gemv_occupancy[5] = {1, 1, 1, 1, 1}; /* Q4_K, Q5_K, Q6_K, Q3_K, IQ4_XS GEMV workgroups a CU holds */
     char name[256] = {0};
     /* this device's copy of the fixed scratch array (q38_full_core_noalloc) */
     void *scratch = nullptr;
@@ -352,9 +355,16 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q4k, ctx->mod_proj, "q38_gemv_q8k_q4k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q5k, ctx->mod_proj, "q38_gemv_q8k_q5k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q6k, ctx->mod_proj, "q38_gemv_q8k_q6k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q3k, ctx->mod_proj, "q38_gemv_q8k_q3k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_iq4xs, ctx->mod_proj, "q38_gemv_q8k_iq4xs"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[0], ctx->mod_proj, "q38_gemv_f32_f32"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[1], ctx->mod_proj, "q38_gemv_f32_f16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[2], ctx->mod_proj, "q38_gemv_f32_bf16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[3], ctx->mod_proj, "q38_gemv_f32_q8_0"));
     {
-        const hipFunction_t gv[3] = {ctx->f_gemv_q4k, ctx->f_gemv_q5k, ctx->f_gemv_q6k};
-        for (int i = 0; i < 3; ++i) {
+        const hipFunction_t gv[5] = {ctx->f_gemv_q4k, ctx->f_gemv_q5k, ctx->f_gemv_q6k, ctx->f_gemv_q3k,
+                                     ctx->f_gemv_iq4xs};
+        for (int i = 0; i < 5; ++i) {
             int n = 0;
             Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, gv[i], 256, 0));
             ctx->gemv_occupancy[i] = std::max(1, n);
@@ -544,6 +554,12 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemv_q8k_q4k") f = ctx->f_gemv_q4k;
     else if (name == "q38_gemv_q8k_q5k") f = ctx->f_gemv_q5k;
     else if (name == "q38_gemv_q8k_q6k") f = ctx->f_gemv_q6k;
+    else if (name == "q38_gemv_q8k_q3k") f = ctx->f_gemv_q3k;
+    else if (name == "q38_gemv_q8k_iq4xs") f = ctx->f_gemv_iq4xs;
+    else if (name == "q38_gemv_f32_f32") f = ctx->f_gemv_f32[0];
+    else if (name == "q38_gemv_f32_f16") f = ctx->f_gemv_f32[1];
+    else if (name == "q38_gemv_f32_bf16") f = ctx->f_gemv_f32[2];
+    else if (name == "q38_gemv_f32_q8_0") f = ctx->f_gemv_f32[3];
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
     else if (name == "q38_prefill_merge") f = ctx->f_prefill_merge;
@@ -1639,10 +1655,18 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
                         const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out) {
     if (ctx == nullptr) return fail("ctx is NULL");
     hipFunction_t f = nullptr;
-    if (ggml_type == Q38_GGML_Q4_K) f = ctx->f_gemv_q4k;
-    else if (ggml_type == Q38_GGML_Q5_K) f = ctx->f_gemv_q5k;
-    else if (ggml_type == Q38_GGML_Q6_K) f = ctx->f_gemv_q6k;
-    else return fail("unsupported quant type %d (Q4_K 12, Q5_K 13, Q6_K 14)", ggml_type);
+    int ti_occ = 0; /* index into gemv_occupancy */
+    if (ggml_type == Q38_GGML_Q4_K) f = ctx->f_gemv_q4k, ti_occ = 0;
+    else if (ggml_type == Q38_GGML_Q5_K) f = ctx->f_gemv_q5k, ti_occ = 1;
+    else if (ggml_type == Q38_GGML_Q6_K) f = ctx->f_gemv_q6k, ti_occ = 2;
+    else if (ggml_type == Q38_GGML_Q3_K) f = ctx->f_gemv_q3k, ti_occ = 3;
+    else if (ggml_type == Q38_GGML_IQ4_XS) f = ctx->f_gemv_iq4xs, ti_occ = 4;
+    else
+        return fail("unsupported quant type %d (Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, IQ4_XS 23; F32, F16, BF16 "
+                    "and Q8_0 weights take q38_gemv_f32)",
+                    ggml_type);
+    /* the int8 matrix-unit form exists for Q4_K, Q5_K and Q6_K */
+    const bool has_gemm = ggml_type == Q38_GGML_Q4_K || ggml_type == Q38_GGML_Q5_K || ggml_type == Q38_GGML_Q6_K;
     if (n_mats < 1 || n_mats > Q38_GEMV_MAX_MATS) return fail("n_mats %d outside 1..%d", n_mats, Q38_GEMV_MAX_MATS);
     if (rows == nullptr || d_weights == nullptr || d_out == nullptr) return fail("NULL argument");
     if (n_tokens < 0) return fail("negative n_tokens");
@@ -1664,7 +1688,6 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
      * flight -- and with them its share of the bandwidth -- grow with the
      * workgroups it runs side by side */
     const int max_units = std::min(Q38_GEMV_UNITS_MAX, 4096 / tok_pass);
-    const int ti_occ = ggml_type == Q38_GGML_Q4_K ? 0 : ggml_type == Q38_GGML_Q5_K ? 1 : 2;
     const long tok_groups_all = ((long)n_tokens + tok_pass - 1) / tok_pass;
     int target_per_wg = max_units / blocks;
     {
@@ -1703,8 +1726,8 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
      * 5120 Q4_K at 16 tokens, 5120 x 17408 Q6_K at 32) */
     long min_rows = a.rows[0];
     for (int i = 1; i < kept; ++i) min_rows = std::min<long>(min_rows, a.rows[i]); /* non-empty matrices */
-    if (n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
-        (n_tokens >= Q38_GEMM_MIN_TOKENS && min_rows >= 64L * Q38_GEMM_ROWS)) {
+    if (has_gemm && (n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
+                     (n_tokens >= Q38_GEMM_MIN_TOKENS && min_rows >= 64L * Q38_GEMM_ROWS))) {
         const int ti = ggml_type == Q38_GGML_Q4_K ? 0 : ggml_type == Q38_GGML_Q5_K ? 1 : 2;
         const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
         if (tok_tiles > 65535) return fail("too many tokens");
@@ -1738,6 +1761,39 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
                   int n_tokens, float *d_out) {
     return q38_gemv_q8_k_multi(ctx, ggml_type, 1, &rows, width, &d_weights, d_q8k, n_tokens, &d_out);
+}
+
+int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const float *d_x,
+                 int n_tokens, float *d_out) {
+    if (ctx == nullptr) return fail("ctx is NULL");
+    int ti = -1, block = 1, block_bytes = 0;
+    if (ggml_type == Q38_GGML_F32) ti = 0, block_bytes = 4;
+    else if (ggml_type == Q38_GGML_F16) ti = 1, block_bytes = 2;
+    else if (ggml_type == Q38_GGML_BF16) ti = 2, block_bytes = 2;
+    else if (ggml_type == Q38_GGML_Q8_0) ti = 3, block = 32, block_bytes = 34;
+    else
+        return fail("unsupported weight type %d for the f32 path (F32 0, F16 1, BF16 30, Q8_0 8)", ggml_type);
+    if (rows < 0 || n_tokens < 0) return fail("negative rows or n_tokens");
+    const int wmul = ti == 3 ? 64 : 8;
+    if (width <= 0 || width % wmul != 0) return fail("width %d is not a positive multiple of %d", width, wmul);
+    if (rows == 0 || n_tokens == 0) return 0;
+    if (d_weights == nullptr || d_x == nullptr || d_out == nullptr) return fail("NULL argument");
+    if ((uintptr_t)d_weights % (ti == 3 ? 4 : 16) != 0)
+        return fail("d_weights must be %d-byte aligned", ti == 3 ? 4 : 16);
+    if ((uintptr_t)d_x % 16 != 0) return fail("d_x must be 16-byte aligned");
+    const long row_groups = ((long)rows + 3) / 4;
+    const long tok_groups = ((long)n_tokens + Q38_GEMV_TOKENS - 1) / Q38_GEMV_TOKENS;
+    if (row_groups > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
+    q38_gemv_f32_args a;
+    memset(&a, 0, sizeof(a));
+    a.weights = static_cast<const uint8_t *>(d_weights);
+    a.x = d_x;
+    a.out = d_out;
+    a.row_bytes = (int64_t)(width / block) * block_bytes;
+    a.rows = rows;
+    a.width = width;
+    a.n_tokens = n_tokens;
+    return ctx->launch(ctx->f_gemv_f32[ti], (unsigned)row_groups, (unsigned)tok_groups, 1, 256, &a);
 }
 
 }  /* extern "C" */

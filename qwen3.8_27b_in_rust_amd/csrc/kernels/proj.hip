@@ -8,6 +8,11 @@
  *   dot_q4_k_q8_k      src/kernel/tensor.rs:365-391
  *   dot_q5_k_q8_k      src/kernel/tensor.rs:393-428
  *   dot_q6_k_q8_k      src/kernel/tensor.rs:430-457
+ *   dot_q3_k_q8_k      src/kernel/tensor.rs:335-363 (unpack_q3_scales :34-44)
+ *   dot_iq4_xs_q8_k    src/kernel/iq.rs:379-405 (code book iq_tables.rs:53-56)
+ *   dot_f32/f16/bf16/q8_0 (f32 input), tensor.rs:79-117, through
+ *                      tensor_gemv_f32 / tensor_gemm_f32, tensor.rs:1095-1129,
+ *                      :1175-1215
  *   tensor_gemv_q8_k / tensor_gemm_q8_k, tensor.rs:1131-1173, :1217-1270:
  *                      out[token * rows + row] = one row dot per element
  *
@@ -73,6 +78,23 @@ template <int TYPE> struct KQuant;
 template <> struct KQuant<Q38_GGML_Q4_K> { static constexpr int bytes = 144, words = 36; };
 template <> struct KQuant<Q38_GGML_Q5_K> { static constexpr int bytes = 176, words = 44; };
 template <> struct KQuant<Q38_GGML_Q6_K> { static constexpr int bytes = 210, words = 52; };
+template <> struct KQuant<Q38_GGML_Q3_K> { static constexpr int bytes = 110, words = 27; };
+template <> struct KQuant<Q38_GGML_IQ4_XS> { static constexpr int bytes = 136, words = 34; };
+
+/* ggml's IQ4_NL / IQ4_XS code book as int8 bytes, 4 per word:
+ * -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113 */
+constexpr uint32_t kIq4Lut[4] = {0xBFAD9881u, 0xF6EADDCFu, 0x26190D01u, 0x71594535u};
+
+/* The code-book values of 4 nibbles (one per byte, 0..15) as 4 int8 bytes:
+ * v_perm_b32 picks byte n & 7 of the low or high half of the book, and
+ * bit 3 of each nibble chooses between the two. */
+Q38_DEV uint32_t q38_iq4_lookup(uint32_t nib) {
+    const uint32_t sel = nib & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4Lut[1], kIq4Lut[0], sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4Lut[3], kIq4Lut[2], sel);
+    const uint32_t mask = ((nib >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & mask) | (lo & ~mask);
+}
 
 /* One 256-weight block of one row (a "unit"), held by one lane. */
 template <int TYPE> struct Unit {
@@ -88,7 +110,48 @@ template <int TYPE> struct Unit {
  * place; the scale is its own halfword.  Every byte read lies in the block. */
 template <int TYPE>
 Q38_DEV void load_unit(const uint8_t *weights, size_t g, Unit<TYPE> &u) {
-    if (TYPE == Q38_GGML_Q6_K) {
+    if (TYPE == Q38_GGML_Q3_K) {
+        /* 110-byte blocks start 2-byte aligned: the 108 bytes before the
+         * scale are read as 27 dwords from the dword boundary at or below
+         * the start plus the halfword at 106, and shifted into place; the
+         * f16 scale is its own halfword.  Every byte read lies in the block
+         * or (the 2 bytes below an odd start) in the one before it. */
+        const size_t s = g * 110;
+        const uint32_t o = (uint32_t)(s & 3); /* 0 or 2 */
+        const uint32_t *base = reinterpret_cast<const uint32_t *>(weights + (s - o));
+        uint32_t win[28];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            u32x4 v;
+            __builtin_memcpy(&v, base + 4 * i, 16);
+            win[4 * i] = v.x;
+            win[4 * i + 1] = v.y;
+            win[4 * i + 2] = v.z;
+            win[4 * i + 3] = v.w;
+        }
+        win[24] = base[24];
+        win[25] = base[25];
+        win[26] = base[26];
+        win[27] = *reinterpret_cast<const uint16_t *>(weights + s + 106);
+        u.dh = *reinterpret_cast<const uint16_t *>(weights + s + 108);
+#pragma unroll
+        for (int j = 0; j < 27; ++j) u.w[j] = __builtin_amdgcn_alignbyte(win[j + 1], win[j], o);
+    } else if (TYPE == Q38_GGML_IQ4_XS) {
+        /* 136-byte blocks start 8-byte aligned */
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(weights + g * 136);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            u32x4 v;
+            __builtin_memcpy(&v, p + 4 * i, 16);
+            u.w[4 * i] = v.x;
+            u.w[4 * i + 1] = v.y;
+            u.w[4 * i + 2] = v.z;
+            u.w[4 * i + 3] = v.w;
+        }
+        u.w[32] = p[32];
+        u.w[33] = p[33];
+        u.dh = 0;
+    } else if (TYPE == Q38_GGML_Q6_K) {
         const size_t s = g * 210;
         const uint32_t o = (uint32_t)(s & 3); /* 0 or 2 */
         const uint32_t *base = reinterpret_cast<const uint32_t *>(weights + (s - o));
@@ -130,7 +193,28 @@ template <int TYPE> struct UnitScales {
 
 template <int TYPE>
 Q38_DEV void unit_scales(const Unit<TYPE> &u, UnitScales<TYPE> &s) {
-    if (TYPE == Q38_GGML_Q6_K) {
+    if (TYPE == Q38_GGML_Q3_K) {
+        /* unpack_q3_scales: low nibble from byte i (i < 8) or the high
+         * nibble of byte i - 8, high 2 bits from byte 8 + i % 4 at 2 (i / 4);
+         * the 12 scale bytes are block bytes 96..107, words 24..26 */
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int low = i < 8 ? q38_sbyte(u.w[24], u.w[25], u.w[26], i) & 15
+                                  : q38_sbyte(u.w[24], u.w[25], u.w[26], i - 8) >> 4;
+            const int high = (q38_sbyte(u.w[24], u.w[25], u.w[26], 8 + i % 4) >> (2 * (i / 4))) & 3;
+            s.sc[i] = (low | (high << 4)) - 32;
+        }
+        s.d = q38_f16(u.dh);
+        s.dmin = 0.0f;
+    } else if (TYPE == Q38_GGML_IQ4_XS) {
+        /* group g: low 4 bits from scales_l[g / 2] (nibble g % 2), high 2
+         * bits from scales_h at 2g; offset 32 */
+        const uint32_t sh = u.w[0] >> 16, sl = u.w[1];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s.sc[g] = (int)(((sl >> (4 * g)) & 15u) | (((sh >> (2 * g)) & 3u) << 4)) - 32;
+        s.d = q38_f16(u.w[0]);
+        s.dmin = 0.0f;
+    } else if (TYPE == Q38_GGML_Q6_K) {
 #pragma unroll
         for (int g = 0; g < 16; ++g) s.sc[g] = (int)(int8_t)((u.w[48 + g / 4] >> (8 * (g & 3))) & 255u);
         s.d = q38_f16(u.dh);
@@ -160,7 +244,45 @@ Q38_DEV float unit_term(const Unit<TYPE> &u, const UnitScales<TYPE> &s, const ui
         bsum[2 * k] = (int)(int16_t)(v & 0xffffu);
         bsum[2 * k + 1] = (int)(int16_t)(v >> 16);
     }
-    if (TYPE == Q38_GGML_Q6_K) {
+    if (TYPE == Q38_GGML_Q3_K) {
+        /* group s (16 values 16s..16s+15: half s / 8, field (s % 8) / 2,
+         * lanes 16 (s % 2)..+15): q = 2 low bits + 4 * high bit in 0..7 is
+         * the reference's qv + 4, so sum qv a = dot(q, a) - 4 * bsum[s] */
+        int weighted = 0;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const int half = g >> 3, field = (g >> 1) & 3, part = g & 1;
+            const u32x4 av = aq[g];
+            int dot = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t low = (u.w[8 + 8 * half + 4 * part + c] >> (2 * field)) & 0x03030303u;
+                const uint32_t hb = (u.w[4 * part + c] >> (4 * half + field)) & 0x01010101u;
+                dot = q38_sdot4(low | (hb << 2), av[c], dot);
+            }
+            weighted += s.sc[g] * (dot - 4 * bsum[g]);
+        }
+        const float d = s.d * a_scale;
+        return d * (float)weighted;
+    } else if (TYPE == Q38_GGML_IQ4_XS) {
+        /* group g: its 16 quant bytes hold values 32g..32g+15 in the low
+         * nibbles and 32g+16.. in the high ones */
+        int weighted = 0;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const u32x4 alo = aq[2 * g], ahi = aq[2 * g + 1];
+            int sub = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t x = u.w[2 + 4 * g + c];
+                sub = q38_sdot4(q38_iq4_lookup(x & 0x0F0F0F0Fu), alo[c], sub);
+                sub = q38_sdot4(q38_iq4_lookup((x >> 4) & 0x0F0F0F0Fu), ahi[c], sub);
+            }
+            weighted += s.sc[g] * sub;
+        }
+        const float d = s.d * a_scale;
+        return d * (float)weighted;
+    } else if (TYPE == Q38_GGML_Q6_K) {
         int dg[16];
 #pragma unroll
         for (int g = 0; g < 16; ++g) dg[g] = 0;
@@ -625,6 +747,137 @@ extern "C" __global__ __launch_bounds__(64) void q38_quantize_q8k(q38_quantize_a
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q4k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q5k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q5_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q6k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q6_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q3k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q3_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4xs(q38_gemv_args a) {
+    gemv_q8k<Q38_GGML_IQ4_XS>(a);
+}
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q4k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q5k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q5_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q6k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q6_K>(a); }
+
+/*
+ * Projections of f32 activations by F32, F16, BF16 or Q8_0 weights (the
+ * path project() takes for weights it does not quantise for, ops.rs:632-637:
+ * tensor_gemv_f32 / tensor_gemm_f32, tensor.rs:1095-1129, :1175-1215).
+ * grid (ceil(rows / 4), ceil(T / tok_pass)), 256 threads: one wave per
+ * weight row, the row read once per pass of up to 8 tokens.  A lane takes
+ * units of E consecutive weights (E = 8; Q8_0: one 32-weight block), units
+ * lane, lane + 64, ... of the row, decodes them to f32 exactly (f16 and bf16
+ * widen exactly; Q8_0 is d * q rounded once, the reference's product) and
+ * adds w * x into its partial sum with fused multiply-adds, unit after unit;
+ * the 64 partial sums are then added by a butterfly.  Every product is the
+ * reference's; the order of the additions is not (the reference runs one
+ * chain over the row on its scalar path and 8-lane partial sums on x86), so
+ * results agree within the rounding of a reassociated f32 sum.
+ */
+template <int TYPE> struct F32Unit;
+template <> struct F32Unit<Q38_GGML_F32> { static constexpr int E = 8, bytes = 32; };
+template <> struct F32Unit<Q38_GGML_F16> { static constexpr int E = 8, bytes = 16; };
+template <> struct F32Unit<Q38_GGML_BF16> { static constexpr int E = 8, bytes = 16; };
+template <> struct F32Unit<Q38_GGML_Q8_0> { static constexpr int E = 32, bytes = 34; };
+
+/* Unit u of a row starting at `row` (4-byte aligned): its E weights. */
+template <int TYPE>
+Q38_DEV void f32_unit(const uint8_t *row, int u, float (&w)[F32Unit<TYPE>::E]) {
+    if (TYPE == Q38_GGML_F32) {
+        u32x4 v0, v1;
+        __builtin_memcpy(&v0, row + (size_t)u * 32, 16);
+        __builtin_memcpy(&v1, row + (size_t)u * 32 + 16, 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[i] = __uint_as_float(v0[i]);
+            w[4 + i] = __uint_as_float(v1[i]);
+        }
+    } else if (TYPE == Q38_GGML_F16 || TYPE == Q38_GGML_BF16) {
+        u32x4 v;
+        __builtin_memcpy(&v, row + (size_t)u * 16, 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (TYPE == Q38_GGML_F16) {
+                w[2 * i] = q38_f16(v[i]);
+                w[2 * i + 1] = q38_f16(v[i] >> 16);
+            } else {
+                w[2 * i] = __uint_as_float(v[i] << 16);
+                w[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
+            }
+        }
+    } else {
+        /* a 34-byte block starts 2-byte aligned: 8 dwords from the dword
+         * boundary at or below it and the halfwords at 30 and 32, shifted
+         * into 9 words from the start (bytes 0-1 the f16 scale, 2-33 the
+         * quants); every byte read lies in this block or the one before */
+        const size_t s = (size_t)u * 34;
+        const uint32_t o = (uint32_t)((uintptr_t)(row + s) & 3); /* 0 or 2 for a 4-byte aligned matrix */
+        const uint32_t *base = reinterpret_cast<const uint32_t *>(row + (s - o));
+        uint32_t win[9];
+        u32x4 v0, v1;
+        __builtin_memcpy(&v0, base, 16);
+        __builtin_memcpy(&v1, base + 4, 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            win[i] = v0[i];
+            win[4 + i] = v1[i];
+        }
+        win[8] = *reinterpret_cast<const uint16_t *>(row + s + 30);
+        const uint32_t h32 = *reinterpret_cast<const uint16_t *>(row + s + 32);
+        uint32_t b[9];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[j] = __builtin_amdgcn_alignbyte(win[j + 1], win[j], o);
+        /* word 7 (bytes 28..31): the window's word 7 when o == 0; with
+         * o == 2 its upper half and the halfword at 30 */
+        b[8] = h32;
+        const float d = q38_f16(b[0]);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int byte = 2 + i;
+            const int q = (int)(int8_t)((b[byte >> 2] >> (8 * (byte & 3))) & 255u);
+            w[i] = d * (float)q;
+        }
+    }
+}
+
+template <int TYPE>
+Q38_DEV void gemv_f32(const q38_gemv_f32_args &a) {
+    constexpr int E = F32Unit<TYPE>::E;
+    constexpr int TP = Q38_GEMV_TOKENS;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.rows) return; /* whole waves only: no barrier follows */
+    const int tok0 = blockIdx.y * TP;
+    const int tp = min(TP, a.n_tokens - tok0);
+    const int units = a.width / E;
+    const uint8_t *wrow = a.weights + (size_t)row * a.row_bytes;
+    float acc[TP];
+#pragma unroll
+    for (int t = 0; t < TP; ++t) acc[t] = 0.0f;
+    for (int u = lane; u < units; u += 64) {
+        float w[E];
+        f32_unit<TYPE>(wrow, u, w);
+#pragma unroll
+        for (int t = 0; t < TP; ++t) {
+            if (t < tp) {
+                const float *x = a.x + (size_t)(tok0 + t) * a.width + (size_t)u * E;
+#pragma unroll
+                for (int i4 = 0; i4 < E; i4 += 4) {
+                    const f32x4 xv = q38_ld4(x + i4);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[t] = __builtin_fmaf(w[i4 + c], xv[c], acc[t]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TP; ++t) {
+        if (t < tp) {
+            float v = acc[t];
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+            if (lane == 0) a.out[(size_t)(tok0 + t) * a.rows + row] = v;
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_f32(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_F32>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_f16(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_F16>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_bf16(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_BF16>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_q8_0(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_Q8_0>(a); }

@@ -284,9 +284,15 @@ typedef struct {
  * | f32 scales [T][B] -- Q38_Q8K_BYTES(T, W) bytes. */
 #define Q38_Q8K_BLOCK 256
 #define Q38_Q8K_BYTES(T, W) ((size_t)(T) * ((W) / Q38_Q8K_BLOCK) * (Q38_Q8K_BLOCK + 32 + 4))
+#define Q38_GGML_F32 0
+#define Q38_GGML_F16 1
+#define Q38_GGML_Q8_0 8
+#define Q38_GGML_Q3_K 11
 #define Q38_GGML_Q4_K 12
 #define Q38_GGML_Q5_K 13
 #define Q38_GGML_Q6_K 14
+#define Q38_GGML_IQ4_XS 23
+#define Q38_GGML_BF16 30
 #define Q38_GEMV_TOKENS 8 /* most tokens one GEMV workgroup serves per pass over its weights */
 #define Q38_GEMV_MAX_BLOCKS 192 /* 256-wide blocks per row (width 49152): one token's blocks fit LDS */
 #define Q38_GEMV_UNITS_MAX 1024 /* (row, block) units per GEMV workgroup: four steps of 256 */
@@ -327,6 +333,19 @@ typedef struct {
     int32_t tok_pass;
     int32_t pad_;
 } q38_gemv_args;
+
+/* f32-input projections (F32, F16, BF16, Q8_0 weights): grid (ceil(rows /
+ * 4), ceil(T / Q38_GEMV_TOKENS)), 256 threads, one wave per row. */
+typedef struct {
+    const uint8_t *weights; /* [rows][row_bytes], 4-byte aligned (16 for F32/F16/BF16) */
+    const float *x;         /* [T][width], 16-byte aligned */
+    float *out;             /* [T][rows] */
+    int64_t row_bytes;
+    int32_t rows;
+    int32_t width;
+    int32_t n_tokens;
+    int32_t pad_;
+} q38_gemv_f32_args;
 
 /* Merge of split-K partials.  grid (n_seq, 24, 4). */
 typedef struct {

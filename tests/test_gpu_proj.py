@@ -1,17 +1,22 @@
-"""The weight projections on the GPU (q38_quantize_q8_k, q38_gemv_q8_k)
-against the oracle's restatement of quantize_q8_k (src/kernel/quant.rs:55-128)
-and of the scalar K-quant x Q8_K row dots (src/kernel/tensor.rs:365-457)
+"""The weight projections on the GPU (q38_quantize_q8_k, q38_gemv_q8_k,
+q38_gemv_f32) against the oracle's restatement of quantize_q8_k
+(src/kernel/quant.rs:55-128), of the scalar Q3_K..Q6_K x Q8_K row dots
+(src/kernel/tensor.rs:335-457) and the IQ4_XS one (src/kernel/iq.rs:379-405)
 driven per row as tensor_gemv_q8_k / tensor_gemm_q8_k do
-(tensor.rs:1131-1173, :1217-1270).  The integer parts and the f32 block terms
-follow the reference's operation order, so both are held bit-exact."""
+(tensor.rs:1131-1173, :1217-1270), and of the f32-input row dots of
+tensor_gemv_f32 (tensor.rs:79-117, :1095-1129).  The integer parts and the
+f32 block terms follow the reference's operation order, so the Q8_K path is
+held bit-exact; the f32 path's sums are reassociated and held within 1e-5
+of the sum of |w x|."""
 import numpy as np
 import pytest
-from oracle_checks import _random_kquant
+from oracle_checks import _random_f32_path, _random_kquant
 from parity import check_attn
 
 pytestmark = pytest.mark.gpu
 
-TYPES = {"Q4_K": 12, "Q5_K": 13, "Q6_K": 14}
+TYPES = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_XS": 23}
+F32_TYPES = {"F32": 0, "F16": 1, "BF16": 30, "Q8_0": 8}
 HIDDEN = 5120
 
 
@@ -73,11 +78,11 @@ def test_gemv_q8_k_subnormal_scales_and_widest_rows(ctx, ref, name):
         d_q = _quantize_on_device(ctx, x)
         wb = _random_kquant(ty, rows, W, 0x513338A9 + ty)
         blocks = wb.reshape(rows * (W // 256), -1)
-        off = 208 if ty == 14 else 0
+        off = {14: 208, 11: 108}.get(ty, 0)  # the block's f16 scale
         sub = np.array([0x0001, 0x03ff, 0x8200, 0x0000, 0x8000], np.uint16)
         for i in range(0, blocks.shape[0], 3):
             blocks[i, off:off + 2] = np.frombuffer(sub[i % 5].tobytes(), np.uint8)
-        if ty != 14:
+        if ty in (12, 13):  # dmin
             blocks[1::4, 2:4] = np.frombuffer(np.uint16(0x0155).tobytes(), np.uint8)
         d_w = ctx.array(wb, np.uint8)
         d_o = ctx.empty((T, rows))
@@ -149,6 +154,50 @@ def test_gemm_many_tokens_bit_exact(ctx, ref, name, rows, W, T):
     assert bad.size == 0, (bad.size, bad[:5], got.reshape(-1)[bad[:5]], want.reshape(-1)[bad[:5]])
 
 
+@pytest.mark.parametrize("name", sorted(F32_TYPES))
+@pytest.mark.parametrize("rows,W,T", [(48, HIDDEN, 1), (48, HIDDEN, 3), (257, 1024, 9), (5, 6144, 17),
+                                      (1031, 2048, 1)])
+def test_gemv_f32_path(ctx, ref, name, rows, W, T):
+    """tensor_gemv_f32 / tensor_gemm_f32 for the weight types project()
+    does not quantise for (the 48-row beta / alpha projections of a DeltaNet
+    layer and other shapes; several token passes): every element within
+    1e-5 of the sum of |w x| of the oracle's sequential chain, and of the
+    float64 dot of the weights decoded in numpy; a one-hot input row gives
+    each weight exactly."""
+    ty = F32_TYPES[name]
+    rng = np.random.default_rng(0x51333940 + ty + rows)
+    x = rng.standard_normal((T, W)).astype(np.float32)
+    if T > 1:
+        x[1] = ((np.arange(W) * 7919) % 101) / np.float32(50.0) - np.float32(1.0)  # tensor.rs:582-586
+        x[T - 1] = 0.0
+        x[T - 1, W - 3] = 1.0
+    wb, wv = _random_f32_path(ty, rows, W, 0x51333941 + ty + W)
+    d_o = ctx.empty((T, rows))
+    ctx.gemv_f32(ty, rows, W, ctx.array(wb, np.uint8), ctx.array(x), T, d_o)
+    got = d_o.download().astype(np.float64)
+    want = ref.gemv_f32(ty, wb, x, threads=16).astype(np.float64)
+    exact = x.astype(np.float64) @ wv.T
+    scale = np.abs(x.astype(np.float64)) @ np.abs(wv).T
+    assert np.all(np.abs(got - want) <= 1e-5 * scale + 1e-30), float(np.max(np.abs(got - want) / (scale + 1e-30)))
+    assert np.all(np.abs(got - exact) <= 1e-5 * scale + 1e-30)
+    if T > 1:
+        assert np.array_equal(got[T - 1], wv[:, W - 3].astype(np.float32).astype(np.float64))
+
+
+def test_gemv_f32_argument_checks(pkg, ctx):
+    w = ctx.empty((4096,), np.uint8)
+    x = ctx.empty((1024,))
+    o = ctx.empty((16,))
+    with pytest.raises(pkg.Q38Error, match="unsupported weight type"):
+        ctx.gemv_f32(12, 4, 256, w, x, 1, o)
+    with pytest.raises(pkg.Q38Error, match="multiple of 8"):
+        ctx.gemv_f32(0, 4, 100, w, x, 1, o)
+    with pytest.raises(pkg.Q38Error, match="multiple of 64"):
+        ctx.gemv_f32(8, 4, 96, w, x, 1, o)
+    with pytest.raises(pkg.Q38Error, match="aligned"):
+        ctx.gemv_f32(1, 4, 256, w.ptr + 2, x, 1, o)
+
+
 def test_projection_argument_checks(pkg, ctx):
     x = ctx.empty((300,))
     q = ctx.empty((4096,), np.uint8)
@@ -211,3 +260,82 @@ def test_projections_feed_full_core(pkg, ctx, ref, margin, synth):
         check_attn(margin, got, want)
     finally:
         kv.close()
+
+
+def test_linear_attention_chain(pkg, ctx, ref, margin, synth):
+    """The reference's linear_attention (ops.rs:744-804) on the device: the
+    layer input quantised once (quantize_input), the qkv (10240 rows, Q4_K)
+    and z (6144 rows, Q5_K) projections on the Q8_K path, beta and alpha
+    (48 rows each, BF16 and Q8_0) on the f32 path, linear_core, the
+    attention output quantised again and the ssm_out projection (5120 rows
+    of 6144, Q6_K).  Each stage against the oracle on the device's input to
+    that stage: the quantisations and Q8_K projections bit for bit, the f32
+    projections within 1e-5 of the sum of |w x|, linear_core's output within
+    1e-3 with its conv state bit-exact and its state within 1e-4 relative.
+    The whole chain against the oracle's own chain is recorded too: there
+    the ssm_out input is quantised from two linear_core outputs that differ
+    by up to ~1e-4, so a few of its int8 quants may differ by one step."""
+    H, V = HIDDEN, 6144
+    rng = np.random.default_rng(0x51333950)
+    x = (rng.standard_normal((1, H)) * 0.002).astype(np.float32)
+    w_qkv = _random_kquant(12, 10240, H, 0x51333951)
+    w_z = _random_kquant(13, V, H, 0x51333952)
+    w_b, _ = _random_f32_path(30, 48, H, 0x51333953)
+    w_a, _ = _random_f32_path(8, 48, H, 0x51333954)
+    w_out = _random_kquant(14, H, V, 0x51333955)
+    conv_w = synth.normal(0x51333956, 10240 * 4, sigma=0.5)
+    dt = synth.normal(0x51333957, 48)
+    a = -np.abs(synth.normal(0x51333958, 48))
+    norm = synth.normal(0x51333959, 128, sigma=0.1, mean=1.0)
+    conv0 = synth.normal(0x5133395A, 10240 * 3)
+    delta0 = synth.normal(0x5133395B, 48 * 128 * 128, sigma=0.02)
+
+    # the device chain
+    d_q8 = _quantize_on_device(ctx, x)
+    d_qkv, d_z = ctx.empty((1, 10240)), ctx.empty((1, V))
+    d_beta, d_alpha = ctx.empty((1, 48)), ctx.empty((1, 48))
+    ctx.gemv_q8_k(12, 10240, H, ctx.array(w_qkv, np.uint8), d_q8, 1, d_qkv)
+    ctx.gemv_q8_k(13, V, H, ctx.array(w_z, np.uint8), d_q8, 1, d_z)
+    d_x = ctx.array(x)
+    ctx.gemv_f32(30, 48, H, ctx.array(w_b, np.uint8), d_x, 1, d_beta)
+    ctx.gemv_f32(8, 48, H, ctx.array(w_a, np.uint8), d_x, 1, d_alpha)
+    got_proj = [d.download()[0] for d in (d_qkv, d_z, d_beta, d_alpha)]
+    d_conv, d_delta = ctx.array(conv0), ctx.array(delta0)
+    d_attn = ctx.empty((1, V))
+    ctx.linear_core(1, 1, *[ctx.array(v) for v in (conv_w, dt, a, norm)], d_conv, d_delta, d_qkv, d_z, d_beta,
+                    d_alpha, d_attn)
+    attn = d_attn.download()
+    d_q8o = ctx.empty((ctx.q8k_bytes(1, V),), np.uint8)
+    ctx.quantize_q8_k(1, V, d_attn, d_q8o)
+    d_out = ctx.empty((1, H))
+    ctx.gemv_q8_k(14, H, V, ctx.array(w_out, np.uint8), d_q8o, 1, d_out)
+    out = d_out.download()[0]
+
+    # stage by stage against the oracle
+    q8 = ref.quantize_q8_k(x)
+    assert np.array_equal(d_q8.download(), q8)
+    assert np.array_equal(got_proj[0], ref.gemv_q8_k(12, w_qkv, q8, 1, H)[0])
+    assert np.array_equal(got_proj[1], ref.gemv_q8_k(13, w_z, q8, 1, H)[0])
+    for got, ty, w in ((got_proj[2], 30, w_b), (got_proj[3], 8, w_a)):
+        _, wv = _random_f32_path(ty, 48, H, 0x51333953 if ty == 30 else 0x51333954)
+        want = ref.gemv_f32(ty, w, x)[0]
+        scale = np.abs(wv) @ np.abs(x[0].astype(np.float64))
+        assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * scale), ty
+    c_ref, s_ref = conv0.copy(), delta0.copy()
+    attn_ref = ref.linear_core(conv_w, dt, a, norm, c_ref, s_ref, *got_proj, threads=16)
+    margin("linear_core out max-abs (device projections)", float(np.max(np.abs(attn[0] - attn_ref))), 1e-3)
+    assert np.array_equal(d_conv.download(), c_ref)
+    from parity import check_state
+    check_state(margin, d_delta.download(), s_ref)
+    q8o = ref.quantize_q8_k(attn)
+    assert np.array_equal(d_q8o.download(), q8o)
+    assert np.array_equal(out, ref.gemv_q8_k(14, w_out, q8o, 1, V)[0])
+
+    # the oracle's chain on its own, end to end (recorded)
+    proj = [ref.gemv_q8_k(12, w_qkv, q8, 1, H)[0], ref.gemv_q8_k(13, w_z, q8, 1, H)[0],
+            ref.gemv_f32(30, w_b, x)[0], ref.gemv_f32(8, w_a, x)[0]]
+    c2, s2 = conv0.copy(), delta0.copy()
+    attn2 = ref.linear_core(conv_w, dt, a, norm, c2, s2, *proj, threads=16)
+    out2 = ref.gemv_q8_k(14, w_out, ref.quantize_q8_k(attn2.reshape(1, -1)), 1, V)[0]
+    rel = float(np.max(np.abs(out - out2)) / np.max(np.abs(out2)))
+    margin("chain end to end, ssm_out rel to max|out|", rel, 1e-2)
