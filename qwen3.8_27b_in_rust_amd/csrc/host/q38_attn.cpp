@@ -134,6 +134,7 @@ struct q38_ctx {
     int timer_used = 0;
     int cu_count = 0;
     int decode_block = 64 * Q38_DECODE_WAVES; /* threads of a decode workgroup (the kernel's launch bound) */
+    int gdn_decode_block = 512;               /* threads of a q38_gdn_decode workgroup (its launch bound) */
     int split_tokens = 0; /* context tokens per decode workgroup; 0: chosen per launch */
     int clock_khz = 0;
     int lds_bytes = 0;
@@ -345,6 +346,8 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gdn_step_rows, ctx->mod_gdn, "q38_gdn_step_rows"));
     Q38_HIP(hipFuncGetAttribute(&ctx->decode_block, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
                                 ctx->f_decode_split));
+    Q38_HIP(hipFuncGetAttribute(&ctx->gdn_decode_block, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK,
+                                ctx->f_gdn_decode));
     /* the decode kernel's reductions and its page-id array are sized for
      * exactly Q38_DECODE_WAVES waves */
     if (ctx->decode_block != 64 * Q38_DECODE_WAVES)
@@ -1567,7 +1570,7 @@ int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weig
         a.norm_w = w->d_norm;
         a.out = d_out;
         a.arrivals = ctx->arrivals;
-        return ctx->launch(ctx->f_gdn_decode, Q38_LIN_V_HEADS, n_seq, 1, 512, &a);
+        return ctx->launch(ctx->f_gdn_decode, Q38_LIN_V_HEADS, n_seq, 1, ctx->gdn_decode_block, &a);
     }
     if (((uintptr_t)d_conv_state | (uintptr_t)d_qkv | (uintptr_t)d_z | (uintptr_t)d_out) % 16 != 0)
         return fail("d_conv_state, d_qkv, d_z and d_out must be 16-byte aligned");

@@ -17,11 +17,12 @@
 #include "q38_device.h"
 
 /* One linear_core token (ops.rs:648-742) in ONE launch: grid (48 value
- * heads, n_seq), 512 threads.  The workgroup of value head vh (key head kh =
+ * heads, n_seq), Q38_GDN_DECODE_THREADS threads.  The workgroup of value head vh (key head kh =
  * vh % 16):
  *  1. issues the loads of its head's 128x128 state first (16 lanes per row,
- *     4 rows per 16-lane group, lane i holding columns 4i..4i+3 and
- *     64+4i..64+4i+3), so the state streams in while the prologue runs;
+ *     128 * 16 / threads rows per 16-lane group, lane i holding columns
+ *     4i..4i+3 and 64+4i..64+4i+3), so the state streams in while the
+ *     prologue runs;
  *  2. prologue (ops.rs:665-687): threads 0..383 take one channel each -- q
  *     and k of key head kh and v of value head vh -- conv1d over the 3-tap
  *     state and the raw input (separate multiplies and adds, left to right),
@@ -38,7 +39,16 @@
  * arrive writes the shifted q/k state and resets the counter to zero for the
  * next call.  No workgroup waits on another.  The arithmetic is that of
  * q38_gdn_pre followed by the recurrence, operation for operation. */
-extern "C" __global__ __launch_bounds__(512) void q38_gdn_decode(q38_gdn_decode_args a) {
+/* 1024 threads (2 state rows per 16-lane group): 4.77 us per layer back to
+ * back against 4.88 us with 512 (4 rows per group), the same results bit
+ * for bit */
+#ifndef Q38_GDN_DECODE_THREADS
+#define Q38_GDN_DECODE_THREADS 1024
+#endif
+extern "C" __global__ __launch_bounds__(Q38_GDN_DECODE_THREADS) void q38_gdn_decode(q38_gdn_decode_args a) {
+    /* state rows per 16-lane group */
+    constexpr int R = Q38_LIN_HEAD_DIM * 16 / Q38_GDN_DECODE_THREADS;
+    static_assert(R >= 1 && Q38_GDN_DECODE_THREADS >= 512, "at least 385 threads for the prologue");
     __shared__ __attribute__((aligned(16))) float xqkv[3][Q38_LIN_HEAD_DIM]; /* q, k (normed), v */
     __shared__ __attribute__((aligned(16))) float o_lds[Q38_LIN_HEAD_DIM];
     __shared__ double red[4];
@@ -50,7 +60,7 @@ extern "C" __global__ __launch_bounds__(512) void q38_gdn_decode(q38_gdn_decode_
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int grp = tid >> 4; /* 0..31: rows 4*grp .. 4*grp+3 */
+    const int grp = tid >> 4; /* rows R*grp .. R*grp+R-1 */
     const int li = tid & 15;
     const int d0 = 4 * li;
     const int d1 = 64 + 4 * li;
@@ -90,10 +100,10 @@ extern "C" __global__ __launch_bounds__(512) void q38_gdn_decode(q38_gdn_decode_
     /* then the state, in flight while the prologue computes (the memory
      * counter is in issue order, so these stay outstanding) */
     float *st = a.state + s * Q38_LIN_STATE_FLOATS + (size_t)vh * Q38_LIN_HEAD_DIM * Q38_LIN_HEAD_DIM;
-    f32x4 S0[4], S1[4];
+    f32x4 S0[R], S1[R];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * grp + r;
+    for (int r = 0; r < R; ++r) {
+        const int row = R * grp + r;
         S0[r] = q38_ld4_stream(st + row * Q38_LIN_HEAD_DIM + d0);
         S1[r] = q38_ld4_stream(st + row * Q38_LIN_HEAD_DIM + d1);
     }
@@ -139,12 +149,14 @@ extern "C" __global__ __launch_bounds__(512) void q38_gdn_decode(q38_gdn_decode_
     /* 3. the recurrence (ops.rs:698-714) */
     const f32x4 k0 = q38_ld4(&xqkv[1][d0]), k1 = q38_ld4(&xqkv[1][d1]);
     const f32x4 q0 = q38_ld4(&xqkv[0][d0]), q1 = q38_ld4(&xqkv[0][d1]);
-    const f32x4 v = q38_ld4(&xqkv[2][4 * grp]);
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = xqkv[2][R * grp + r];
     const float beta = gates[0];
     const float decay = expf(gates[1]);
-    float o[4];
+    float o[R];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < R; ++r) {
         S0[r] *= decay;
         S1[r] *= decay;
         float pred = q38_dot4(S0[r], k0, 0.0f);
@@ -157,13 +169,16 @@ extern "C" __global__ __launch_bounds__(512) void q38_gdn_decode(q38_gdn_decode_
         res = q38_dot4(S1[r], q1, res);
         res = q38_sum16(res);
         o[r] = res * query_scale;
-        const int row = 4 * grp + r;
+        const int row = R * grp + r;
         q38_st4_stream(st + row * Q38_LIN_HEAD_DIM + d0, S0[r]);
         q38_st4_stream(st + row * Q38_LIN_HEAD_DIM + d1, S1[r]);
     }
 
     /* 4. gated RMSNorm (ops.rs:735-740) */
-    if (li == 0) q38_st4(&o_lds[4 * grp], f32x4{o[0], o[1], o[2], o[3]});
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) o_lds[R * grp + r] = o[r];
+    }
     __syncthreads();
     if (tid < 64) {
         const float x0 = o_lds[tid];
