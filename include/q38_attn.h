@@ -181,46 +181,6 @@ int q38_full_core_noalloc(q38_kv *kv, int layer, int n_seq, const int32_t *seq_i
                           const float *d_q_and_gate, const float *d_key, const float *d_value,
                           float *d_out);
 
-/*
- * A token's decode calls recorded once as a HIP graph and replayed per token.
- * The reference runs full_core once per full-attention layer per token
- * (ops.rs:942-986 calling :813-940; the layer loop of ops.rs:1153-1172); a
- * serving loop that repeats the same calls every token records them here
- * and replays them, so the launches are prepared once.  Each call is the
- * q38_attn_decode form (d_q_norm NULL: q post-norm and post-RoPE, optional
- * append d_k_new/d_v_new, optional d_gate) or the q38_full_core form
- * (d_q_norm and d_k_norm set: d_q holds q|gate rows, d_k_new/d_v_new the
- * raw key and value, d_gate unused) of one full-attention layer, for the
- * same n_seq (1..64) distinct sequences; device buffers are fixed at
- * creation.  Results equal those of the plain calls in the same order.
- *
- * create: checks every call at `positions`, reserves the pages of appending
- * calls and instantiates the graph (nothing is launched).  set_positions:
- * waits for the context's stream (a replay in flight reads the arguments it
- * replaces), checks the calls at the new positions with nothing changed on
- * failure, reserves pages (their ids are uploaded on the stream, ahead of
- * the next replay) and rewrites every launch's arguments and grid.  launch:
- * one replay on the context's stream, at the positions last set.  The graph
- * owns its split-K workspace (grown by set_positions when a longer context
- * needs it); calls to set_positions and launch come from one thread.
- */
-typedef struct q38_decode_graph q38_decode_graph;
-typedef struct {
-    int32_t layer;
-    int32_t pad_;
-    const float *d_q;
-    const float *d_k_new;
-    const float *d_v_new;
-    const float *d_gate;
-    const float *d_q_norm;
-    const float *d_k_norm;
-    float *d_out;
-} q38_decode_call;
-int q38_decode_graph_create(q38_kv *kv, int n_seq, const int32_t *seq_ids, const int32_t *positions,
-                            int n_calls, const q38_decode_call *calls, q38_decode_graph **out);
-int q38_decode_graph_set_positions(q38_decode_graph *g, const int32_t *positions);
-int q38_decode_graph_launch(q38_decode_graph *g);
-int q38_decode_graph_destroy(q38_decode_graph *g);
 
 /* The q/k RMSNorm + RoPE prologue of full_core alone (ops.rs:832-856) for
  * n_tokens tokens at positions pos0, pos0+1, ...: writes d_q_out, d_gate_out
@@ -282,6 +242,67 @@ typedef struct {
 int q38_linear_core(q38_ctx *ctx, int n_seq, int n_tokens, const q38_linear_weights *w,
                     float *d_conv_state, float *d_delta_state, const float *d_qkv,
                     const float *d_z, const float *d_beta, const float *d_alpha, float *d_out);
+
+/* ---------------------------------------------------- replayed token graph */
+
+/*
+ * A token's work recorded once as a HIP graph and replayed per token.  The
+ * reference runs, per token and layer, full_core (ops.rs:942-986 calling
+ * :813-940) or linear_core (ops.rs:744-804 calling :648-742) with the
+ * projections around them; a serving loop repeats the same launches every
+ * token.  A graph is built in order from:
+ *  - decode calls (q38_decode_graph_add_decode): the q38_attn_decode form
+ *    (d_q_norm NULL: q post-norm and post-RoPE, optional append
+ *    d_k_new/d_v_new, optional d_gate) or the q38_full_core form (d_q_norm
+ *    and d_k_norm set: d_q holds q|gate rows, d_k_new/d_v_new the raw key
+ *    and value, d_gate unused) of one full-attention layer, for the graph's
+ *    n_seq (1..64) distinct sequences at the positions given at begin;
+ *  - one-token linear_core calls (q38_decode_graph_add_linear_core, the
+ *    arguments of q38_linear_core with n_tokens 1);
+ *  - graphs of the caller's own work (q38_decode_graph_add_graph: a
+ *    hipGraph_t, copied at the add), e.g. the projections and norms between
+ *    the cores, captured from the caller's stream;
+ * each step after the previous one.  Device buffers are fixed at the add.
+ * Results equal those of the plain calls in the same order, bit for bit.
+ *
+ * begin: checks the sequences, records the positions; add_decode checks the
+ * call at those positions and reserves the pages it appends to.  end:
+ * instantiates (nothing is launched).  set_positions: waits for the
+ * context's stream (a replay in flight reads the arguments it replaces),
+ * checks every decode call at the new positions with nothing changed on
+ * failure, reserves pages (their ids are uploaded on the stream, ahead of
+ * the next replay) and rewrites every decode launch's arguments and grid;
+ * the other steps do not depend on positions.  launch: one replay on the
+ * context's stream at the positions last set.  The graph owns its split-K
+ * workspace; no allocation, memset or host synchronisation is recorded in
+ * it.  q38_decode_graph_create is begin + one add_decode per call + end.
+ * Calls on one graph come from one thread.
+ */
+typedef struct q38_decode_graph q38_decode_graph;
+typedef struct {
+    int32_t layer;
+    int32_t pad_;
+    const float *d_q;
+    const float *d_k_new;
+    const float *d_v_new;
+    const float *d_gate;
+    const float *d_q_norm;
+    const float *d_k_norm;
+    float *d_out;
+} q38_decode_call;
+int q38_decode_graph_begin(q38_kv *kv, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                           q38_decode_graph **out);
+int q38_decode_graph_add_decode(q38_decode_graph *g, const q38_decode_call *call);
+int q38_decode_graph_add_linear_core(q38_decode_graph *g, int n_seq, const q38_linear_weights *w,
+                                     float *d_conv_state, float *d_delta_state, const float *d_qkv,
+                                     const float *d_z, const float *d_beta, const float *d_alpha, float *d_out);
+int q38_decode_graph_add_graph(q38_decode_graph *g, void *hip_graph);
+int q38_decode_graph_end(q38_decode_graph *g);
+int q38_decode_graph_create(q38_kv *kv, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                            int n_calls, const q38_decode_call *calls, q38_decode_graph **out);
+int q38_decode_graph_set_positions(q38_decode_graph *g, const int32_t *positions);
+int q38_decode_graph_launch(q38_decode_graph *g);
+int q38_decode_graph_destroy(q38_decode_graph *g);
 
 /* ------------------------------------------------------- weight projections */
 

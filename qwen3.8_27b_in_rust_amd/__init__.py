@@ -89,6 +89,11 @@ _SIGNATURES = {
     "q38_full_core_noalloc": (c_int, [_P, c_int, c_int, _I32P, _I32P, _P, _P, _P, _P, _P, _P]),
     "q38_attn_pre": (c_int, [_P, c_int, c_int, _P, _P, _P, _P, _P, _P, _P]),
     "q38_decode_graph_create": (c_int, [_P, c_int, _I32P, _I32P, c_int, POINTER(_DecodeCall), POINTER(c_void_p)]),
+    "q38_decode_graph_begin": (c_int, [_P, c_int, _I32P, _I32P, POINTER(c_void_p)]),
+    "q38_decode_graph_add_decode": (c_int, [_P, POINTER(_DecodeCall)]),
+    "q38_decode_graph_add_linear_core": (c_int, [_P, c_int, POINTER(_LinearWeights), _P, _P, _P, _P, _P, _P, _P]),
+    "q38_decode_graph_add_graph": (c_int, [_P, _P]),
+    "q38_decode_graph_end": (c_int, [_P]),
     "q38_decode_graph_set_positions": (c_int, [_P, _I32P]),
     "q38_decode_graph_launch": (c_int, [_P]),
     "q38_decode_graph_destroy": (c_int, [_P]),
@@ -412,10 +417,11 @@ class KVCache:
                                            _ptr(k_norm), _ptr(q_and_gate), _ptr(key), _ptr(value), _ptr(out)),
                "q38_full_core_noalloc")
 
-    def decode_graph(self, seq_ids, positions, calls):
-        """A DecodeGraph of `calls`: dicts with layer, q, out and optionally
+    def decode_graph(self, seq_ids, positions, calls=None):
+        """A DecodeGraph: `calls` are dicts with layer, q, out and optionally
         k_new, v_new, gate (the attn_decode form) or q_norm, k_norm with
-        q = q|gate rows and k_new/v_new the raw key/value (full_core)."""
+        q = q|gate rows and k_new/v_new the raw key/value (full_core); with
+        no calls, an open graph to fill with add_* and end()."""
         return DecodeGraph(self, seq_ids, positions, calls)
 
     def attn_prefill(self, layer, seq, base_pos, n_tokens, q, k, v, out, gate=None):
@@ -423,26 +429,52 @@ class KVCache:
                                       _ptr(gate), _ptr(out)), "q38_attn_prefill")
 
 
-class DecodeGraph:
-    """q38_decode_graph_*: a token's decode calls recorded once as a HIP graph."""
+def _decode_call(c: dict) -> _DecodeCall:
+    d = _DecodeCall()
+    d.layer = c["layer"]
+    d.d_q = _ptr(c["q"])
+    d.d_k_new = _ptr(c.get("k_new"))
+    d.d_v_new = _ptr(c.get("v_new"))
+    d.d_gate = _ptr(c.get("gate"))
+    d.d_q_norm = _ptr(c.get("q_norm"))
+    d.d_k_norm = _ptr(c.get("k_norm"))
+    d.d_out = _ptr(c["out"])
+    return d
 
-    def __init__(self, kv, seq_ids, positions, calls):
+
+class DecodeGraph:
+    """q38_decode_graph_*: a token's work recorded once as a HIP graph.  With
+    `calls`, the graph of those decode calls (q38_decode_graph_create);
+    without, an open graph to fill with add_* and close with end()."""
+
+    def __init__(self, kv, seq_ids, positions, calls=None):
         self.kv = kv
         self.n_seq = len(seq_ids)
-        arr = (_DecodeCall * len(calls))()
-        for i, c in enumerate(calls):
-            arr[i].layer = c["layer"]
-            arr[i].d_q = _ptr(c["q"])
-            arr[i].d_k_new = _ptr(c.get("k_new"))
-            arr[i].d_v_new = _ptr(c.get("v_new"))
-            arr[i].d_gate = _ptr(c.get("gate"))
-            arr[i].d_q_norm = _ptr(c.get("q_norm"))
-            arr[i].d_k_norm = _ptr(c.get("k_norm"))
-            arr[i].d_out = _ptr(c["out"])
         h = c_void_p()
-        _check(lib().q38_decode_graph_create(kv.handle, self.n_seq, _i32(seq_ids), _i32(positions), len(calls), arr,
-                                             ctypes.byref(h)), "q38_decode_graph_create")
+        if calls is not None:
+            arr = (_DecodeCall * len(calls))(*[_decode_call(c) for c in calls])
+            _check(lib().q38_decode_graph_create(kv.handle, self.n_seq, _i32(seq_ids), _i32(positions), len(calls),
+                                                 arr, ctypes.byref(h)), "q38_decode_graph_create")
+        else:
+            _check(lib().q38_decode_graph_begin(kv.handle, self.n_seq, _i32(seq_ids), _i32(positions),
+                                                ctypes.byref(h)), "q38_decode_graph_begin")
         self.handle = h.value
+
+    def add_decode(self, call: dict) -> None:
+        c = _decode_call(call)
+        _check(lib().q38_decode_graph_add_decode(self.handle, ctypes.byref(c)), "q38_decode_graph_add_decode")
+
+    def add_linear_core(self, n_seq, conv_w, dt, a, norm, conv_state, delta_state, qkv, z, beta, alpha, out):
+        w = _LinearWeights(_ptr(conv_w), _ptr(dt), _ptr(a), _ptr(norm))
+        _check(lib().q38_decode_graph_add_linear_core(self.handle, n_seq, ctypes.byref(w), _ptr(conv_state),
+                                                      _ptr(delta_state), _ptr(qkv), _ptr(z), _ptr(beta),
+                                                      _ptr(alpha), _ptr(out)), "q38_decode_graph_add_linear_core")
+
+    def add_graph(self, hip_graph: int) -> None:
+        _check(lib().q38_decode_graph_add_graph(self.handle, hip_graph), "q38_decode_graph_add_graph")
+
+    def end(self) -> None:
+        _check(lib().q38_decode_graph_end(self.handle), "q38_decode_graph_end")
 
     def set_positions(self, positions) -> None:
         _check(lib().q38_decode_graph_set_positions(self.handle, _i32(positions)), "q38_decode_graph_set_positions")

@@ -1094,12 +1094,15 @@ int q38_full_core_noalloc(q38_kv *kv, int layer, int n_seq, const int32_t *seq_i
                       kv->ctx->scratch, Q38_NOALLOC_SCRATCH_BYTES);
 }
 
-/* ----------------------------------------------------- replayed decode graph */
+/* ----------------------------------------------------- replayed token graph */
 
-/* A token's decode calls as one instantiated HIP graph: per call a split
- * node and a merge node (the merge exits at once when every sequence has
- * one split), in call order.  Launch arguments depend on the positions and
- * are rewritten in place by q38_decode_graph_set_positions. */
+/* A token's work as one instantiated HIP graph, in the order it was added:
+ * full-attention decode calls (a split node and a merge node each; the merge
+ * exits at once when every sequence has one split), one-token linear_core
+ * calls (one node each), and graphs of the caller's own work (one child node
+ * each, copied at the add).  Only the decode calls depend on the positions;
+ * their launch arguments and grids are rewritten in place by
+ * q38_decode_graph_set_positions. */
 struct q38_decode_graph {
     struct Call {
         q38_decode_call c;
@@ -1121,6 +1124,8 @@ struct q38_decode_graph {
     size_t work_bytes = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    hipGraphNode_t last = nullptr; /* the node the next step depends on */
+    int steps = 0;
 
     ~q38_decode_graph() {
         if (exec != nullptr) (void)hipGraphExecDestroy(exec);
@@ -1128,21 +1133,14 @@ struct q38_decode_graph {
         if (work != nullptr) (void)hipFree(work);
     }
 
-    /* Checks of positions for every call, with nothing changed; then the
-     * workspace (grown only between replays: the caller's stream is idle),
-     * the page reservations and each call's launch arguments. */
-    int prepare(const int32_t *pos) {
-        if (pos == nullptr) return fail("NULL positions");
-        for (const Call &k : calls) {
-            int slot = 0;
-            if (validate_decode(kv, k.c.layer, n_seq, seq_ids, pos, k.appends, &slot)) return -1;
-        }
-        decode_plan plan;
-        if (plan_decode(kv->ctx, n_seq, pos, &plan)) return -1;
-        if (arg_pages && plan.total_splits > Q38_HEAD_PAGE_SPLITS)
-            return fail("%d splits: this graph's split kernel takes at most %d", plan.total_splits,
+    /* The split-K workspace for `pos`, grown only while no replay runs
+     * (the caller's stream has been waited for). */
+    int ensure_work(const int32_t *pos, decode_plan *plan) {
+        if (plan_decode(kv->ctx, n_seq, pos, plan)) return -1;
+        if (arg_pages && plan->total_splits > Q38_HEAD_PAGE_SPLITS)
+            return fail("%d splits: this graph's split kernel takes at most %d", plan->total_splits,
                         Q38_HEAD_PAGE_SPLITS);
-        const size_t need = (size_t)plan.total_splits * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2) * sizeof(float);
+        const size_t need = (size_t)plan->total_splits * Q38_ATTN_HEADS * (Q38_ATTN_HEAD_DIM + 2) * sizeof(float);
         if (need > work_bytes) {
             if (work != nullptr) {
                 Q38_HIP(hipStreamSynchronize(kv->ctx->stream));
@@ -1154,19 +1152,34 @@ struct q38_decode_graph {
             Q38_HIP(hipMalloc(&work, want));
             work_bytes = want;
         }
+        return 0;
+    }
+
+    /* Checks of positions for every call, with nothing changed; then the
+     * workspace, the page reservations and each call's launch arguments. */
+    int prepare(const int32_t *pos) {
+        if (pos == nullptr) return fail("NULL positions");
+        for (const Call &k : calls) {
+            int slot = 0;
+            if (validate_decode(kv, k.c.layer, n_seq, seq_ids, pos, k.appends, &slot)) return -1;
+        }
+        decode_plan plan;
+        if (ensure_work(pos, &plan)) return -1;
         bool any_append = false;
         for (const Call &k : calls) any_append |= k.appends;
         if (any_append)
             for (int b = 0; b < n_seq; ++b)
                 if (kv->reserve(seq_ids[b], pos[b] + 1)) return -1;
-        for (Call &k : calls) {
-            if (build_decode(kv, k.slot, n_seq, seq_ids, pos, k.c.d_q, k.c.d_k_new, k.c.d_v_new,
-                             k.has_pre ? nullptr : k.c.d_gate, k.c.d_out, plan, work, k.has_pre ? &k.pre : nullptr,
-                             arg_pages, &k.L))
-                return -1;
-        }
+        for (Call &k : calls)
+            if (build(k, pos, plan)) return -1;
         memcpy(positions, pos, sizeof(int32_t) * n_seq);
         return 0;
+    }
+
+    int build(Call &k, const int32_t *pos, const decode_plan &plan) {
+        return build_decode(kv, k.slot, n_seq, seq_ids, pos, k.c.d_q, k.c.d_k_new, k.c.d_v_new,
+                            k.has_pre ? nullptr : k.c.d_gate, k.c.d_out, plan, work, k.has_pre ? &k.pre : nullptr,
+                            arg_pages, &k.L);
     }
 
     void node_params(Call &k, bool merge, hipKernelNodeParams *p, void **arg) {
@@ -1186,60 +1199,170 @@ struct q38_decode_graph {
         p->sharedMemBytes = 0;
         p->extra = nullptr;
     }
+
+    int open_for_steps() const {
+        if (exec != nullptr) return fail("the graph is already instantiated");
+        if (steps >= 4096) return fail("a token graph holds at most 4096 steps");
+        return 0;
+    }
+
+    int add_kernel(hipGraphNode_t *node, const hipKernelNodeParams &p) {
+        Q38_HIP(hipGraphAddKernelNode(node, graph, last ? &last : nullptr, last ? 1 : 0, &p));
+        last = *node;
+        ++steps;
+        return 0;
+    }
 };
 
-int q38_decode_graph_create(q38_kv *kv, int n_seq, const int32_t *seq_ids, const int32_t *positions,
-                            int n_calls, const q38_decode_call *calls, q38_decode_graph **out) {
+int q38_decode_graph_begin(q38_kv *kv, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                           q38_decode_graph **out) {
     if (out == nullptr) return fail("NULL out");
     *out = nullptr;
     if (kv == nullptr) return fail("kv is NULL");
     if (n_seq < 1 || n_seq > Q38_MAX_BATCH) return fail("n_seq %d outside 1..%d", n_seq, Q38_MAX_BATCH);
     if (seq_ids == nullptr || positions == nullptr) return fail("NULL seq_ids/positions");
-    if (n_calls < 1 || calls == nullptr) return fail("no decode calls");
+    for (int b = 0; b < n_seq; ++b) {
+        if (kv->check_seq(seq_ids[b])) return -1;
+        for (int c = 0; c < b; ++c)
+            if (seq_ids[c] == seq_ids[b]) return fail("sequence %d appears twice", seq_ids[b]);
+    }
     std::unique_ptr<q38_decode_graph> g(new q38_decode_graph());
     g->kv = kv;
     g->n_seq = n_seq;
     memcpy(g->seq_ids, seq_ids, sizeof(int32_t) * n_seq);
-    for (int b = 0; b < n_seq; ++b)
-        for (int c = 0; c < b; ++c)
-            if (seq_ids[c] == seq_ids[b]) return fail("sequence %d appears twice", seq_ids[b]);
+    memcpy(g->positions, positions, sizeof(int32_t) * n_seq);
     g->arg_pages = n_seq == 1 && kv->ctx->split_tokens == 0 ? 1 : 0;
-    g->calls.resize(n_calls);
-    for (int i = 0; i < n_calls; ++i) {
-        q38_decode_graph::Call &k = g->calls[i];
-        k.c = calls[i];
-        if (kv->slot_of(k.c.layer, &k.slot)) return -1;
-        if (k.c.d_q == nullptr || k.c.d_out == nullptr) return fail("call %d: NULL q/out", i);
-        if ((k.c.d_q_norm == nullptr) != (k.c.d_k_norm == nullptr))
-            return fail("call %d: d_q_norm and d_k_norm go together", i);
-        k.has_pre = k.c.d_q_norm != nullptr;
-        if (k.has_pre && (k.c.d_k_new == nullptr || k.c.d_v_new == nullptr))
-            return fail("call %d: full_core needs its key and value", i);
-        if ((k.c.d_k_new == nullptr) != (k.c.d_v_new == nullptr))
-            return fail("call %d: d_k_new and d_v_new go together", i);
-        k.appends = k.c.d_k_new != nullptr;
-        k.pre = decode_pre{k.c.d_q_norm, k.c.d_k_norm};
-    }
-    if (g->prepare(positions)) return -1;
     Q38_HIP(hipGraphCreate(&g->graph, 0));
-    hipGraphNode_t prev = nullptr;
-    for (q38_decode_graph::Call &k : g->calls) {
+    *out = g.release();
+    return 0;
+}
+
+int q38_decode_graph_add_decode(q38_decode_graph *g, const q38_decode_call *call) {
+    if (g == nullptr || call == nullptr) return fail("NULL argument");
+    if (g->open_for_steps()) return -1;
+    q38_decode_graph::Call k;
+    k.c = *call;
+    q38_kv *kv = g->kv;
+    if (kv->slot_of(k.c.layer, &k.slot)) return -1;
+    if (k.c.d_q == nullptr || k.c.d_out == nullptr) return fail("NULL q/out");
+    if ((k.c.d_q_norm == nullptr) != (k.c.d_k_norm == nullptr)) return fail("d_q_norm and d_k_norm go together");
+    k.has_pre = k.c.d_q_norm != nullptr;
+    if (k.has_pre && (k.c.d_k_new == nullptr || k.c.d_v_new == nullptr))
+        return fail("the full_core form needs its key and value");
+    if ((k.c.d_k_new == nullptr) != (k.c.d_v_new == nullptr)) return fail("d_k_new and d_v_new go together");
+    k.appends = k.c.d_k_new != nullptr;
+    k.pre = decode_pre{k.c.d_q_norm, k.c.d_k_norm};
+    int slot = 0;
+    if (validate_decode(kv, k.c.layer, g->n_seq, g->seq_ids, g->positions, k.appends, &slot)) return -1;
+    decode_plan plan;
+    if (g->ensure_work(g->positions, &plan)) return -1;
+    if (k.appends)
+        for (int b = 0; b < g->n_seq; ++b)
+            if (kv->reserve(g->seq_ids[b], g->positions[b] + 1)) return -1;
+    if (g->build(k, g->positions, plan)) return -1;
+    /* the workspace may have moved: every call's arguments name the current one */
+    for (q38_decode_graph::Call &o : g->calls) {
+        if (g->build(o, g->positions, plan)) return -1;
         hipKernelNodeParams p;
         void *arg = nullptr;
-        g->node_params(k, false, &p, &arg);
-        Q38_HIP(hipGraphAddKernelNode(&k.split_node, g->graph, prev ? &prev : nullptr, prev ? 1 : 0, &p));
-        prev = k.split_node;
-        g->node_params(k, true, &p, &arg);
-        Q38_HIP(hipGraphAddKernelNode(&k.merge_node, g->graph, &prev, 1, &p));
-        prev = k.merge_node;
+        g->node_params(o, false, &p, &arg);
+        Q38_HIP(hipGraphKernelNodeSetParams(o.split_node, &p));
+        g->node_params(o, true, &p, &arg);
+        Q38_HIP(hipGraphKernelNodeSetParams(o.merge_node, &p));
     }
+    g->calls.push_back(k);
+    q38_decode_graph::Call &kk = g->calls.back();
+    hipKernelNodeParams p;
+    void *arg = nullptr;
+    g->node_params(kk, false, &p, &arg);
+    if (g->add_kernel(&kk.split_node, p)) return -1;
+    g->node_params(kk, true, &p, &arg);
+    return g->add_kernel(&kk.merge_node, p);
+}
+
+int q38_decode_graph_add_linear_core(q38_decode_graph *g, int n_seq, const q38_linear_weights *w,
+                                     float *d_conv_state, float *d_delta_state, const float *d_qkv,
+                                     const float *d_z, const float *d_beta, const float *d_alpha, float *d_out) {
+    if (g == nullptr || w == nullptr) return fail("NULL argument");
+    if (g->open_for_steps()) return -1;
+    if (n_seq < 1 || n_seq > 65535) return fail("n_seq %d outside 1..65535", n_seq);
+    if (!w->d_conv_w || !w->d_dt || !w->d_a || !w->d_norm || !d_conv_state || !d_delta_state || !d_qkv || !d_z ||
+        !d_beta || !d_alpha || !d_out)
+        return fail("NULL argument");
+    q38_ctx *ctx = g->kv->ctx;
+    /* the arrival counters exist before any replay (no allocation or fill
+     * inside the graph; the kernel leaves them zero) */
+    if (ctx->ensure_arrivals(n_seq)) return -1;
+    q38_gdn_decode_args a;
+    memset(&a, 0, sizeof(a));
+    a.qkv_raw = d_qkv;
+    a.conv_w = w->d_conv_w;
+    a.conv_state = d_conv_state;
+    a.state = d_delta_state;
+    a.z = d_z;
+    a.beta_raw = d_beta;
+    a.alpha_raw = d_alpha;
+    a.dt = w->d_dt;
+    a.a = w->d_a;
+    a.norm_w = w->d_norm;
+    a.out = d_out;
+    a.arrivals = ctx->arrivals;
+    void *arg = &a;
+    hipKernelNodeParams p{};
+    p.func = reinterpret_cast<void *>(ctx->f_gdn_decode);
+    p.gridDim = dim3(Q38_LIN_V_HEADS, n_seq, 1);
+    p.blockDim = dim3(ctx->gdn_decode_block, 1, 1);
+    p.kernelParams = &arg;
+    p.sharedMemBytes = 0;
+    p.extra = nullptr;
+    hipGraphNode_t node = nullptr;
+    return g->add_kernel(&node, p);
+}
+
+int q38_decode_graph_add_graph(q38_decode_graph *g, void *hip_graph) {
+    if (g == nullptr || hip_graph == nullptr) return fail("NULL argument");
+    if (g->open_for_steps()) return -1;
+    hipGraphNode_t node = nullptr;
+    Q38_HIP(hipGraphAddChildGraphNode(&node, g->graph, g->last ? &g->last : nullptr, g->last ? 1 : 0,
+                                      static_cast<hipGraph_t>(hip_graph)));
+    g->last = node;
+    ++g->steps;
+    return 0;
+}
+
+int q38_decode_graph_end(q38_decode_graph *g) {
+    if (g == nullptr) return fail("graph is NULL");
+    if (g->exec != nullptr) return fail("the graph is already instantiated");
+    if (g->steps == 0) return fail("the graph has no steps");
     Q38_HIP(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0));
-    *out = g.release();
+    return 0;
+}
+
+int q38_decode_graph_create(q38_kv *kv, int n_seq, const int32_t *seq_ids, const int32_t *positions,
+                            int n_calls, const q38_decode_call *calls, q38_decode_graph **out) {
+    if (out == nullptr) return fail("NULL out");
+    *out = nullptr;
+    if (n_calls < 1 || calls == nullptr) return fail("no decode calls");
+    q38_decode_graph *g = nullptr;
+    if (q38_decode_graph_begin(kv, n_seq, seq_ids, positions, &g)) return -1;
+    for (int i = 0; i < n_calls; ++i) {
+        if (q38_decode_graph_add_decode(g, &calls[i])) {
+            const std::string why = g_last_error;
+            delete g;
+            return fail("call %d: %s", i, why.c_str());
+        }
+    }
+    if (q38_decode_graph_end(g)) {
+        delete g;
+        return -1;
+    }
+    *out = g;
     return 0;
 }
 
 int q38_decode_graph_set_positions(q38_decode_graph *g, const int32_t *positions) {
     if (g == nullptr) return fail("graph is NULL");
+    if (g->exec == nullptr) return fail("the graph is not instantiated (q38_decode_graph_end)");
     /* a replay still running reads the arguments being replaced */
     Q38_HIP(hipStreamSynchronize(g->kv->ctx->stream));
     if (g->prepare(positions)) return -1;
@@ -1256,6 +1379,7 @@ int q38_decode_graph_set_positions(q38_decode_graph *g, const int32_t *positions
 
 int q38_decode_graph_launch(q38_decode_graph *g) {
     if (g == nullptr) return fail("graph is NULL");
+    if (g->exec == nullptr) return fail("the graph is not instantiated (q38_decode_graph_end)");
     Q38_HIP(hipGraphLaunch(g->exec, g->kv->ctx->stream));
     return 0;
 }

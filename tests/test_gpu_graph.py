@@ -132,3 +132,122 @@ def test_graph_rejects_bad_positions_and_keeps_working(pkg, ctx, synth):
             assert np.array_equal(out_g.download(), out_p.download())
     finally:
         kv.close()
+
+
+def _linear_inputs(ctx, synth, seed):
+    return [ctx.array(synth.normal(seed + i, m)) for i, m in enumerate((10240, 6144, 48, 48))]
+
+
+def test_token_graph_interleaves_linear_core(pkg, ctx, synth):
+    """A token graph in the model's layer order -- three one-token
+    linear_core steps, then a full_core decode call, twice (DeltaNet layers
+    0-2 and 4-6, attention layers 3 and 7) -- replayed for three tokens with
+    positions advanced and new inputs written into the fixed buffers before
+    each replay, against the plain calls in the same order on a twin cache
+    and twin states: every output and the final states bit for bit."""
+    n_tok = 3000
+    kvs = [_cache(pkg, ctx, 1, n_tok, 0x7A00) for _ in range(2)]
+    try:
+        conv_w = ctx.array(synth.normal(0x7A10, 10240 * 4, sigma=0.5))
+        dt = ctx.array(synth.normal(0x7A11, 48))
+        a = ctx.array(-np.abs(synth.normal(0x7A12, 48)))
+        norm = ctx.array(synth.normal(0x7A13, 128, sigma=0.1, mean=1.0))
+        qn = ctx.array(synth.normal(0x7A14, 256, sigma=0.1, mean=1.0))
+        kn = ctx.array(synth.normal(0x7A15, 256, sigma=0.1, mean=1.0))
+        conv0 = synth.normal(0x7A16, 6 * 30720)
+        delta0 = synth.normal(0x7A17, 6 * 48 * 128 * 128, sigma=0.02)
+        conv = [ctx.array(conv0) for _ in range(2)]
+        delta = [ctx.array(delta0) for _ in range(2)]
+        lin_in = [_linear_inputs(ctx, synth, 0x7A20 + 8 * i) for i in range(6)]
+        att_in = {L: [ctx.array(synth.normal(0x7A60 + L, 12288)), ctx.array(synth.normal(0x7A70 + L, 1024)),
+                      ctx.array(synth.normal(0x7A80 + L, 1024))] for L in (3, 7)}
+        outs = [{k: ctx.empty((6144,)) for k in range(8)} for _ in range(2)]
+
+        kv_g, seqs_g, _ = kvs[0]
+        pos0 = 2990
+        graph = kv_g.decode_graph(seqs_g, [pos0])
+        for layer in range(8):
+            if layer in (3, 7):
+                q, key, val = att_in[layer]
+                graph.add_decode({"layer": layer, "q": q, "k_new": key, "v_new": val, "q_norm": qn, "k_norm": kn,
+                                  "out": outs[0][layer]})
+            else:
+                r = layer if layer < 3 else layer - 1
+                graph.add_linear_core(1, conv_w, dt, a, norm, conv[0].offset(r * 30720),
+                                      delta[0].offset(r * 48 * 128 * 128), *lin_in[r], outs[0][layer])
+        graph.end()
+        kv_p, seqs_p, _ = kvs[1]
+        with graph:
+            for t in range(3):
+                pos = pos0 + t
+                # this token's inputs, written into the buffers both paths read
+                for r in range(6):
+                    for i, buf in enumerate(lin_in[r]):
+                        buf.upload(synth.normal(0x7B00 + 100 * t + 8 * r + i, buf.shape[0]))
+                for L in (3, 7):
+                    for i, buf in enumerate(att_in[L]):
+                        buf.upload(synth.normal(0x7C00 + 100 * t + 4 * L + i, buf.shape[0]))
+                graph.set_positions([pos])
+                graph.launch()
+                for layer in range(8):
+                    if layer in (3, 7):
+                        q, key, val = att_in[layer]
+                        kv_p.full_core(layer, seqs_p, [pos], qn, kn, q, key, val, outs[1][layer])
+                    else:
+                        r = layer if layer < 3 else layer - 1
+                        ctx.linear_core(1, 1, conv_w, dt, a, norm, conv[1].offset(r * 30720),
+                                        delta[1].offset(r * 48 * 128 * 128), *lin_in[r], outs[1][layer])
+                for layer in range(8):
+                    got, want = outs[0][layer].download(), outs[1][layer].download()
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (t, layer)
+        assert np.array_equal(conv[0].download(), conv[1].download())
+        assert np.array_equal(delta[0].download().view(np.uint32), delta[1].download().view(np.uint32))
+    finally:
+        for kv, _, _ in kvs:
+            kv.close()
+
+
+def test_token_graph_with_a_captured_child_graph(pkg, ctx, synth):
+    """The caller's own work as a child step: a graph captured from the
+    context's stream (a device copy of layer 3's output into layer 7's query
+    buffer, a data dependency) sits between two decode calls; the replay
+    equals the plain sequence decode, copy, decode bit for bit."""
+    import ctypes
+    import os
+    hip = ctypes.CDLL(os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "libamdhip64.so"))
+    hip.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    n_tok = 2000
+    kv, seqs, _ = _cache(pkg, ctx, 1, n_tok, 0x7D00)
+    try:
+        q3 = ctx.array(synth.normal(0x7D10, 6144))
+        q7 = ctx.empty((24, 256))
+        o3, o7 = ctx.empty((24, 256)), ctx.empty((24, 256))
+        stream = ctx.stream()
+        ctx.sync()
+        child = ctypes.c_void_p()
+        assert hip.hipStreamBeginCapture(stream, 2) == 0  # relaxed capture mode
+        ctx.copy(q7, o3, 6144 * 4)
+        assert hip.hipStreamEndCapture(stream, ctypes.byref(child)) == 0
+        graph = kv.decode_graph(seqs, [1500])
+        graph.add_decode({"layer": 3, "q": q3, "out": o3})
+        graph.add_graph(child.value)
+        graph.add_decode({"layer": 7, "q": q7, "out": o7})
+        graph.end()
+        hip.hipGraphDestroy(child)
+        with graph:
+            graph.set_positions([1999])
+            graph.launch()
+            got3, got7 = o3.download(), o7.download()
+        ctx.sync()
+        o3.zero()
+        q7.zero()
+        kv.attn_decode(3, seqs, [1999], q3, o3)
+        ctx.copy(q7, o3, 6144 * 4)
+        kv.attn_decode(7, seqs, [1999], q7, o7)
+        assert np.array_equal(got3, o3.download())
+        assert np.array_equal(got7, o7.download())
+        assert np.abs(got7).max() > 0
+    finally:
+        kv.close()
