@@ -122,6 +122,19 @@ int q38_seq_capacity(q38_kv *kv, int seq, int *n_tokens);
  * ops.rs:858-866, for many tokens).  Reserves pages as needed. */
 int q38_kv_write(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, const float *d_k,
                  const float *d_v);
+/* Prefill's key/value block images (bf16 hi/lo copies of each 32-position
+ * block, laid out as the prefill kernel's tiles) are kept per (sequence,
+ * layer) between q38_attn_prefill calls, so a call converts only blocks it
+ * has not converted before: a prompt prefilled in pieces, or a few tokens
+ * verified after a long context, no longer re-converts the whole prefix.
+ * Every write at position p (appends, q38_kv_write, prefill) and every
+ * truncate, reset, free or q38_seq_set_pages drops the images from p's
+ * block on.  They take 74,752 bytes per block and kv head (~9.3 KB per
+ * token and layer).  enable = 0 frees them and converts every call whole;
+ * results are the same bit for bit.  On by default.  No counterpart in the
+ * reference (its prefill reads the f32 cache directly, ops.rs:1153-1172). */
+int q38_kv_set_prefill_cache(q38_kv *kv, int enable);
+
 /* Gather positions pos0..pos0+n_tokens-1 back into rows [n_tokens][1024]. */
 int q38_kv_read(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float *d_k, float *d_v);
 

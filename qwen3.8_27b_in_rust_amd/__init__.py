@@ -75,6 +75,7 @@ _SIGNATURES = {
     "q38_kv_create": (c_int, [_P, c_int, c_int, c_int, c_int, POINTER(c_void_p)]),
     "q38_kv_destroy": (c_int, [_P]),
     "q38_kv_free_pages": (c_int, [_P, POINTER(c_int)]),
+    "q38_kv_set_prefill_cache": (c_int, [_P, c_int]),
     "q38_seq_create": (c_int, [_P, POINTER(c_int)]),
     "q38_seq_free": (c_int, [_P, c_int]),
     "q38_seq_reset": (c_int, [_P, c_int]),
@@ -361,6 +362,9 @@ class KVCache:
         if self.handle:
             lib().q38_kv_destroy(self.handle)
             self.handle = None
+
+    def set_prefill_cache(self, enable: bool) -> None:
+        _check(lib().q38_kv_set_prefill_cache(self.handle, int(bool(enable))), "q38_kv_set_prefill_cache")
 
     def free_pages(self) -> int:
         n = c_int()

@@ -215,6 +215,41 @@ struct q38_kv {
     int32_t *staging = nullptr;
     size_t staging_len = 0;
     size_t staging_head = 0;
+    /* Prefill's bf16 hi/lo images of each (sequence, slot)'s 32-key blocks,
+     * [4 kv heads][cap] x Q38_PREFILL_IMAGE_BYTES, kept between calls:
+     * blocks [0, valid) are images of the keys and values now in the cache.
+     * Every write at position p cuts valid to p / 32. */
+    struct Images {
+        void *buf = nullptr;
+        int cap = 0;
+        int valid = 0;
+    };
+    std::vector<Images> images; /* [max_seqs][n_slots] */
+    bool image_cache = true;
+
+    Images &img(int seq, int slot) { return images[(size_t)seq * n_slots + slot]; }
+
+    /* positions >= pos of `seq` changed in `slot` (every slot when slot < 0) */
+    void images_from(int seq, int slot, long pos) {
+        const int b = (int)std::min<long>(std::max<long>(pos, 0) / Q38_PREFILL_KEYS, 1L << 30);
+        for (int s = slot < 0 ? 0 : slot; s < (slot < 0 ? n_slots : slot + 1); ++s) {
+            Images &im = img(seq, s);
+            im.valid = std::min(im.valid, b);
+        }
+    }
+
+    /* the sequence's image buffers released (no call may still read them) */
+    void images_free(int seq) {
+        bool any = false;
+        for (int s = 0; s < n_slots; ++s) any |= img(seq, s).buf != nullptr;
+        if (!any) return;
+        (void)hipStreamSynchronize(ctx->stream);
+        for (int s = 0; s < n_slots; ++s) {
+            Images &im = img(seq, s);
+            if (im.buf != nullptr) (void)hipFree(im.buf);
+            im = Images();
+        }
+    }
 
     size_t slot_floats() const { return (size_t)max_pages * Q38_PAGE_FLOATS; }
     float *kslot(int slot) const { return kpool + (size_t)slot * slot_floats(); }
@@ -261,6 +296,7 @@ struct q38_kv {
     }
 
     void release_from(int seq, int keep_pages) {
+        images_from(seq, -1, (long)keep_pages * Q38_PAGE_TOKENS);
         for (int p = seq_pages[seq] - 1; p >= keep_pages; --p) {
             free_pages.push_back(page_table[(size_t)seq * pt_stride + p]);
             page_table[(size_t)seq * pt_stride + p] = -1;
@@ -632,6 +668,7 @@ int q38_kv_create(q38_ctx *ctx, int n_slots, int max_pages, int max_seqs, int ma
     for (int p = 0; p < max_pages; ++p) kv->free_pages[p] = max_pages - 1 - p; /* pop gives 0,1,2.. */
     kv->seq_live.assign(max_seqs, 0);
     kv->seq_pages.assign(max_seqs, 0);
+    kv->images.assign((size_t)max_seqs * n_slots, q38_kv::Images());
     kv->staging_len = std::max<size_t>(1 << 16, (size_t)kv->pt_stride * 4);
     Q38_HIP(hipHostMalloc((void **)&kv->staging, kv->staging_len * sizeof(int32_t), hipHostMallocDefault));
     Q38_HIP(hipStreamSynchronize(ctx->stream));
@@ -642,11 +679,22 @@ int q38_kv_create(q38_ctx *ctx, int n_slots, int max_pages, int max_seqs, int ma
 int q38_kv_destroy(q38_kv *kv) {
     if (kv == nullptr) return 0;
     (void)hipStreamSynchronize(kv->ctx->stream);
+    for (q38_kv::Images &im : kv->images)
+        if (im.buf != nullptr) (void)hipFree(im.buf);
     (void)hipFree(kv->kpool);
     (void)hipFree(kv->vpool);
     (void)hipFree(kv->d_page_table);
     (void)hipHostFree(kv->staging);
     delete kv;
+    return 0;
+}
+
+int q38_kv_set_prefill_cache(q38_kv *kv, int enable) {
+    if (kv == nullptr) return fail("kv is NULL");
+    if (!enable) {
+        for (int s = 0; s < kv->max_seqs; ++s) kv->images_free(s);
+    }
+    kv->image_cache = enable != 0;
     return 0;
 }
 
@@ -673,6 +721,7 @@ int q38_seq_free(q38_kv *kv, int seq) {
     if (kv == nullptr) return fail("kv is NULL");
     if (kv->check_seq(seq)) return -1;
     kv->release_from(seq, 0);
+    kv->images_free(seq);
     kv->seq_live[seq] = 0;
     return 0;
 }
@@ -743,6 +792,7 @@ static int kv_copy(q38_kv *kv, int layer, int seq, int pos0, int n_tokens, float
     if (n_tokens == 0) return 0;
     if (to_pages) {
         if (kv->reserve(seq, pos0 + n_tokens)) return -1;
+        kv->images_from(seq, slot, pos0);
     } else if (pos0 + n_tokens > kv->seq_pages[seq] * Q38_PAGE_TOKENS) {
         return fail("positions %d..%d are not reserved", pos0, pos0 + n_tokens - 1);
     }
@@ -1018,8 +1068,10 @@ int decode_all(q38_kv *kv, int layer, int n_seq, const int32_t *seq_ids, const i
         work = ctx->work;
     }
     if (appends)
-        for (int b = 0; b < n_seq; ++b)
+        for (int b = 0; b < n_seq; ++b) {
             if (kv->reserve(seq_ids[b], positions[b] + 1)) return -1;
+            kv->images_from(seq_ids[b], slot, positions[b]);
+        }
     const size_t q_rows = pre != nullptr ? Q38_ATTN_QG_DIM : Q38_ATTN_Q_DIM;
     for (int b0 = 0; b0 < n_seq; b0 += Q38_MAX_BATCH) {
         const int n = std::min(Q38_MAX_BATCH, n_seq - b0);
@@ -1170,6 +1222,9 @@ struct q38_decode_graph {
         if (any_append)
             for (int b = 0; b < n_seq; ++b)
                 if (kv->reserve(seq_ids[b], pos[b] + 1)) return -1;
+        for (const Call &k : calls)
+            if (k.appends)
+                for (int b = 0; b < n_seq; ++b) kv->images_from(seq_ids[b], k.slot, pos[b]);
         for (Call &k : calls)
             if (build(k, pos, plan)) return -1;
         memcpy(positions, pos, sizeof(int32_t) * n_seq);
@@ -1257,8 +1312,10 @@ int q38_decode_graph_add_decode(q38_decode_graph *g, const q38_decode_call *call
     decode_plan plan;
     if (g->ensure_work(g->positions, &plan)) return -1;
     if (k.appends)
-        for (int b = 0; b < g->n_seq; ++b)
+        for (int b = 0; b < g->n_seq; ++b) {
             if (kv->reserve(g->seq_ids[b], g->positions[b] + 1)) return -1;
+            kv->images_from(g->seq_ids[b], k.slot, g->positions[b]);
+        }
     if (g->build(k, g->positions, plan)) return -1;
     /* the workspace may have moved: every call's arguments name the current one */
     for (q38_decode_graph::Call &o : g->calls) {
@@ -1561,19 +1618,53 @@ int q38_attn_prefill(q38_kv *kv, int layer, int seq, int base_pos, int n_tokens,
         a.jobs_per_wg = place_prefill_jobs(base_pos, n_tokens, a.n_qblocks, a.jobs, mg.split, &mg.n_split, &a.n_slots);
         n_wg = (size_t)Q38_ATTN_KV_HEADS * Q38_PREFILL_BINS;
     }
-    /* the workspace for the K/V block images and the pieces' partials, before
-     * anything is changed */
-    const size_t img_bytes = ((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES + 255) / 256 * 256;
+    /* the block images: the (sequence, slot)'s own buffer, kept between
+     * calls and grown to hold n_kblocks blocks (its valid images copied
+     * over); with the cache switched off, or no memory for it, the
+     * context's workspace, converted whole */
+    q38_kv::Images *im = kv->image_cache ? &kv->img(seq, slot) : nullptr;
+    if (im != nullptr && im->cap < a.n_kblocks) {
+        const long max_blocks = ((long)kv->pt_stride * Q38_PAGE_TOKENS + Q38_PREFILL_KEYS - 1) / Q38_PREFILL_KEYS;
+        const int cap = (int)std::min<long>(max_blocks, std::max<long>(a.n_kblocks, 2L * im->cap));
+        const size_t block_bytes = Q38_PREFILL_IMAGE_BYTES;
+        void *buf = nullptr;
+        if (hipMalloc(&buf, (size_t)Q38_ATTN_KV_HEADS * cap * block_bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            im = nullptr;
+        } else {
+            for (int j = 0; j < Q38_ATTN_KV_HEADS && im->valid > 0; ++j)
+                Q38_HIP(hipMemcpyAsync(static_cast<char *>(buf) + (size_t)j * cap * block_bytes,
+                                       static_cast<char *>(im->buf) + (size_t)j * im->cap * block_bytes,
+                                       (size_t)im->valid * block_bytes, hipMemcpyDeviceToDevice, ctx->stream));
+            if (im->buf != nullptr) {
+                Q38_HIP(hipStreamSynchronize(ctx->stream));
+                Q38_HIP(hipFree(im->buf));
+            }
+            im->buf = buf;
+            im->cap = cap;
+        }
+    }
+    /* the workspace for the pieces' partials (and the images without a
+     * cache), before anything is changed */
+    const size_t img_bytes =
+        im != nullptr ? 0 : ((size_t)Q38_ATTN_KV_HEADS * a.n_kblocks * Q38_PREFILL_IMAGE_BYTES + 255) / 256 * 256;
     const size_t part_rows = (size_t)Q38_ATTN_KV_HEADS * a.n_slots * Q38_PREFILL_QUERIES * 2;
     if (ctx->ensure_work(img_bytes + part_rows * (Q38_ATTN_HEAD_DIM + 2) * sizeof(float))) return -1;
-    a.images = ctx->work;
+    a.images = im != nullptr ? im->buf : ctx->work;
+    a.img_stride = im != nullptr ? im->cap : a.n_kblocks;
     a.part_o = reinterpret_cast<float *>(static_cast<char *>(ctx->work) + img_bytes);
     a.part_ml = a.part_o + part_rows * Q38_ATTN_HEAD_DIM;
-    /* append the prompt's rows (reserves pages) */
+    /* append the prompt's rows (reserves pages; the blocks from base_pos on
+     * are no longer valid images) */
     if (q38_kv_write(kv, layer, seq, base_pos, n_tokens, d_k, d_v)) return -1;
-    /* the K/V of positions 0 .. base_pos+n_tokens-1 split once into bf16
-     * hi/lo block images, then the attention kernel */
-    if (ctx->launch(ctx->f_kv_split, a.n_kblocks, Q38_ATTN_KV_HEADS, 1, 256, &a)) return -1;
+    /* the K/V blocks without a valid image split once into bf16 hi/lo
+     * images, then the attention kernel */
+    a.kb0 = im != nullptr ? std::min(im->valid, a.n_kblocks) : 0;
+    if (a.kb0 < a.n_kblocks &&
+        ctx->launch(ctx->f_kv_split, a.n_kblocks - a.kb0, Q38_ATTN_KV_HEADS, 1, 256, &a))
+        return -1;
+    /* the blocks every key of which is now in the cache stay valid */
+    if (im != nullptr) im->valid = (int)(end / Q38_PREFILL_KEYS);
     if (ctx->launch(ctx->f_prefill, (unsigned)n_wg, 1, 1, 256, &a)) return -1;
     if (mg.n_split == 0) return 0;
     mg.part_o = a.part_o;

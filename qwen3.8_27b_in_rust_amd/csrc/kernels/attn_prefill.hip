@@ -102,13 +102,14 @@ static_assert(sizeof(Tile) == Q38_PREFILL_IMAGE_BYTES, "tile and image agree");
 
 Q38_DEV const uint4 *image_of(const q38_prefill_args &a, int j, int kb) {
     return reinterpret_cast<const uint4 *>(static_cast<const char *>(a.images) +
-                                           ((size_t)j * a.n_kblocks + kb) * Q38_PREFILL_IMAGE_BYTES);
+                                           ((size_t)j * a.img_stride + kb) * Q38_PREFILL_IMAGE_BYTES);
 }
 
 }  // namespace
 
-/* Split K/V blocks 0 .. n_kblocks-1 of kv head blockIdx.y into bf16 hi/lo
- * block images (grid (n_kblocks, 4), 256 threads).  Keys past the prompt's
+/* Split K/V blocks kb0 .. n_kblocks-1 of kv head blockIdx.y into bf16 hi/lo
+ * block images (grid (n_kblocks - kb0, 4), 256 threads; blocks before kb0
+ * hold images of unchanged keys from earlier calls).  Keys past the prompt's
  * last position read that position (finite data; the causal mask gives them
  * weight 0 in every row that can see them).  The K part goes out row by row;
  * the transposed V part is assembled in LDS (a 4-byte write per key pair and
@@ -116,12 +117,12 @@ Q38_DEV const uint4 *image_of(const q38_prefill_args &a, int j, int kb) {
  * written with scattered small stores. */
 extern "C" __global__ __launch_bounds__(256) void q38_kv_split_mfma(q38_prefill_args a) {
     __shared__ __attribute__((aligned(16))) __bf16 vimg[2][Q38_ATTN_HEAD_DIM][kVRow];
-    const int kb = blockIdx.x;
+    const int kb = a.kb0 + blockIdx.x;
     const int j = blockIdx.y;
     const int tid = threadIdx.x;
     const int kmax = a.base_pos + a.n_tokens - 1;
     Tile *img = reinterpret_cast<Tile *>(static_cast<char *>(a.images) +
-                                         ((size_t)j * a.n_kblocks + kb) * Q38_PREFILL_IMAGE_BYTES);
+                                         ((size_t)j * a.img_stride + kb) * Q38_PREFILL_IMAGE_BYTES);
     /* the block's two page ids first, then every K and V row load of this
      * thread at once (one memory round trip each, where a copy loop would
      * wait for each page id and row in turn).  Keys past the last position

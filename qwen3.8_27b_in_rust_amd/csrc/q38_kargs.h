@@ -247,7 +247,7 @@ typedef struct {
     const float *q;            /* [n_tokens][24][256] for positions base_pos.. */
     const float *gate;         /* [n_tokens][24][256] or NULL */
     float *out;                /* [n_tokens][24][256] */
-    void *images;              /* [4 kv heads][n_kblocks] block images */
+    void *images;              /* [4 kv heads][img_stride] block images */
     int32_t base_pos;
     int32_t n_tokens;
     int32_t n_qblocks;
@@ -259,6 +259,8 @@ typedef struct {
      * n_qblocks <= 64. */
     int32_t jobs_per_wg;
     int32_t n_slots;           /* partial slots per kv head (pieces of split jobs) */
+    int32_t img_stride;        /* blocks per kv head in `images` (>= n_kblocks) */
+    int32_t kb0;               /* q38_kv_split_mfma converts blocks kb0 .. n_kblocks-1 */
     float *part_o;             /* [4][n_slots][64 rows][2 heads][256] unnormalised O of a piece */
     float *part_ml;            /* [4][n_slots][64][2][2]: its (reference, weight sum) per row */
     q38_prefill_job jobs[Q38_PREFILL_BINS * Q38_PREFILL_JOBS_MAX];
