@@ -340,13 +340,15 @@ int q38_q8k_bytes(int n_tokens, int width, size_t *bytes);
 int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, void *d_q8k);
 
 /* tensor_gemv_q8_k / tensor_gemm_q8_k (src/kernel/tensor.rs:1131-1173,
- * :1217-1270) for Q3_K (ggml type 11), Q4_K (12), Q5_K (13), Q6_K (14) and
- * IQ4_XS (23) weights: d_weights [rows][width/256 blocks] in the GGUF block
- * layout (110, 144, 176, 210, 136 bytes per block, 16-byte aligned base),
- * d_q8k from q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
+ * :1217-1270) for Q2_K (ggml type 10), Q3_K (11), Q4_K (12), Q5_K (13),
+ * Q6_K (14), IQ4_NL (20) and IQ4_XS (23) weights: d_weights [rows][width/256
+ * blocks] in the GGUF block layout (84, 110, 144, 176, 210, 8 x 18, 136
+ * bytes per 256 weights, 16-byte aligned base), d_q8k from
+ * q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
  * reference's batched form writes it).  width is at most 49152.  Each
- * element equals the reference's scalar dot_q*_k_q8_k (tensor.rs:335-457)
- * or dot_iq4_xs_q8_k (src/kernel/iq.rs:379-405) bit for bit.  For Q4_K, Q5_K
+ * element equals the reference's scalar dot_q*_k_q8_k (tensor.rs:301-457)
+ * or dot_iq4_nl_q8_k / dot_iq4_xs_q8_k (src/kernel/iq.rs:355-405) bit for
+ * bit.  For Q4_K, Q5_K
  * and Q6_K from 32 tokens (16 for matrices of 8192 rows or more) the
  * integer dots run on the int8 matrix unit; the result is the same bit for
  * bit.  Other weight types fail with -1 (the reference's f32 path below, or

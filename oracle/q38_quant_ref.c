@@ -14,8 +14,10 @@
  *   dot_q4_k_q8_k_scalar          src/kernel/tensor.rs:365-391
  *   dot_q5_k_q8_k_scalar          src/kernel/tensor.rs:393-428
  *   dot_q6_k_q8_k_scalar          src/kernel/tensor.rs:430-457
+ *   dot_q2_k_q8_k_scalar          src/kernel/tensor.rs:301-333
  *   unpack_q3_scales              src/kernel/tensor.rs:34-44
  *   dot_q3_k_q8_k_scalar          src/kernel/tensor.rs:335-363
+ *   dot_iq4_nl_q8_k               src/kernel/iq.rs:355-377 (iq4_nl_group :96-99)
  *   dot_iq4_xs_q8_k               src/kernel/iq.rs:379-405 (KVALUES_IQ4NL,
  *                                 src/kernel/iq_tables.rs:53-56)
  *   dot_f32/f16/bf16/q8_0_scalar  src/kernel/tensor.rs:79-117 (the row dots
@@ -256,6 +258,50 @@ static float dot_q6_k(const uint8_t *data, const q8k_view *q, int blocks) {
     return total;
 }
 
+/* KVALUES_IQ4NL (src/kernel/iq_tables.rs:53-56): ggml's published 16-entry
+ * code book of the IQ4_NL / IQ4_XS formats. */
+static const int8_t kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                         1,    13,   25,  38,  53,  69,  89,  113};
+
+/* dot_q2_k_q8_k_scalar, tensor.rs:301-333.  Block: scales[16] (low nibble
+ * scale, high nibble minimum) | qs[64] | d | dmin (f16), 84 bytes. */
+static float dot_q2_k(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *blk = data + (size_t)block * 84;
+        const uint8_t *scales = blk;
+        const uint8_t *quants = blk + 16;
+        const float d = q38r_f16_to_f32(read_u16(blk + 80)) * b->scale;
+        const float dmin = q38r_f16_to_f32(read_u16(blk + 82)) * b->scale;
+        int32_t weighted = 0, minimum = 0;
+        for (int half = 0; half < 2; ++half) {
+            for (int field = 0; field < 4; ++field) {
+                const int scale_index = half * 8 + field * 2;
+                const int32_t scale0 = scales[scale_index] & 15;
+                const int32_t scale1 = scales[scale_index + 1] & 15;
+                const int shift = field * 2;
+                int32_t dot0 = 0, dot1 = 0;
+                for (int lane = 0; lane < 16; ++lane) {
+                    dot0 += (int32_t)((quants[half * 32 + lane] >> shift) & 3) *
+                            b->quants[half * 128 + field * 32 + lane];
+                    dot1 += (int32_t)((quants[half * 32 + 16 + lane] >> shift) & 3) *
+                            b->quants[half * 128 + field * 32 + 16 + lane];
+                }
+                weighted += scale0 * dot0 + scale1 * dot1;
+#if Q38R_MUTANT == 22
+                minimum += (int32_t)(scales[scale_index] & 15) * b->sums[scale_index]; /* planted: wrong nibble */
+#else
+                minimum += (int32_t)(scales[scale_index] >> 4) * b->sums[scale_index];
+#endif
+                minimum += (int32_t)(scales[scale_index + 1] >> 4) * b->sums[scale_index + 1];
+            }
+        }
+        total += d * (float)weighted - dmin * (float)minimum;
+    }
+    return total;
+}
+
 /* unpack_q3_scales, tensor.rs:34-44: 16 signed 6-bit scales from 12 bytes */
 static void unpack_q3_scales(const uint8_t *packed, int8_t *scales) {
     for (int index = 0; index < 16; ++index) {
@@ -303,10 +349,33 @@ static float dot_q3_k(const uint8_t *data, const q8k_view *q, int blocks) {
     return total;
 }
 
-/* KVALUES_IQ4NL (src/kernel/iq_tables.rs:53-56): ggml's published 16-entry
- * code book of the IQ4_NL / IQ4_XS formats. */
-static const int8_t kvalues_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
-                                         1,    13,   25,  38,  53,  69,  89,  113};
+/* dot_iq4_nl_q8_k, iq.rs:355-377: eight 18-byte GGUF blocks (f16 d, 16
+ * bytes of nibbles) per 256 weights, each group's term added to the total
+ * on its own. */
+static float dot_iq4_nl(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 144;
+        for (int group = 0; group < 8; ++group) {
+            const uint8_t *packed = w + group * 18;
+            const float d = q38r_f16_to_f32(read_u16(packed)) * b->scale;
+            int32_t weighted = 0;
+            for (int lane = 0; lane < 16; ++lane) {
+                const uint8_t p = packed[2 + lane];
+#if Q38R_MUTANT == 23
+                weighted += (int32_t)b->quants[group * 32 + lane] * kvalues_iq4nl[p >> 4]; /* planted: halves swapped */
+                weighted += (int32_t)b->quants[group * 32 + lane + 16] * kvalues_iq4nl[p & 15];
+#else
+                weighted += (int32_t)b->quants[group * 32 + lane] * kvalues_iq4nl[p & 15];
+                weighted += (int32_t)b->quants[group * 32 + lane + 16] * kvalues_iq4nl[p >> 4];
+#endif
+            }
+            total += d * (float)weighted;
+        }
+    }
+    return total;
+}
 
 /* dot_iq4_xs_q8_k, iq.rs:379-405.  Block: d (f16) | scales_h (u16) |
  * scales_l[4] | qs[128], 136 bytes. */
@@ -342,7 +411,9 @@ static float dot_iq4_xs(const uint8_t *data, const q8k_view *q, int blocks) {
 
 int q38r_quant_block_bytes(int ggml_type) {
     switch (ggml_type) {
+    case Q38R_GGML_Q2_K: return 84;
     case Q38R_GGML_Q3_K: return 110;
+    case Q38R_GGML_IQ4_NL: return 144;
     case Q38R_GGML_Q4_K: return 144;
     case Q38R_GGML_Q5_K: return 176;
     case Q38R_GGML_Q6_K: return 210;
@@ -368,7 +439,9 @@ float q38r_dot_q8_k(int ggml_type, const uint8_t *row, const void *planar, int n
     case Q38R_GGML_Q4_K: return dot_q4_k(row, view, blocks);
     case Q38R_GGML_Q5_K: return dot_q5_k(row, view, blocks);
     case Q38R_GGML_Q6_K: return dot_q6_k(row, view, blocks);
+    case Q38R_GGML_Q2_K: return dot_q2_k(row, view, blocks);
     case Q38R_GGML_Q3_K: return dot_q3_k(row, view, blocks);
+    case Q38R_GGML_IQ4_NL: return dot_iq4_nl(row, view, blocks);
     case Q38R_GGML_IQ4_XS: return dot_iq4_xs(row, view, blocks);
     default: return NAN;
     }

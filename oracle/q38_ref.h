@@ -102,7 +102,9 @@ void q38r_linear_core(const float *conv_w, const float *dt, const float *a,
 #define Q38R_GGML_F32 0
 #define Q38R_GGML_F16 1
 #define Q38R_GGML_Q8_0 8
+#define Q38R_GGML_Q2_K 10
 #define Q38R_GGML_Q3_K 11
+#define Q38R_GGML_IQ4_NL 20
 #define Q38R_GGML_Q4_K 12
 #define Q38R_GGML_Q5_K 13
 #define Q38R_GGML_Q6_K 14
@@ -118,9 +120,9 @@ void q38r_quantize_block(const float *values, float *scale, int8_t *quants, int1
 int q38r_quantize_q8_k(const float *input, int n_tokens, int width, void *planar);
 /* Bytes of one 256-weight block of a K-quant type (0 if unsupported). */
 int q38r_quant_block_bytes(int ggml_type);
-/* dot_q3/q4/q5/q6_k_q8_k_scalar (tensor.rs:335-457) and dot_iq4_xs_q8_k
- * (iq.rs:379-405): one weight row against token `token` of a planar Q8_K
- * buffer of n_tokens rows. */
+/* dot_q2/q3/q4/q5/q6_k_q8_k_scalar (tensor.rs:301-457), dot_iq4_nl_q8_k and
+ * dot_iq4_xs_q8_k (iq.rs:355-405): one weight row against token `token` of
+ * a planar Q8_K buffer of n_tokens rows. */
 float q38r_dot_q8_k(int ggml_type, const uint8_t *row, const void *planar, int n_tokens, int width, int token);
 /* tensor_gemv_q8_k / tensor_gemm_q8_k (tensor.rs:1131-1173, :1217-1270):
  * out[t*rows + row] for every row and token; rows split over threads. */

@@ -123,6 +123,8 @@ struct q38_ctx {
     hipFunction_t f_gemv_q6k = nullptr;
     hipFunction_t f_gemv_q3k = nullptr;
     hipFunction_t f_gemv_iq4xs = nullptr;
+    hipFunction_t f_gemv_q2k = nullptr;
+    hipFunction_t f_gemv_iq4nl = nullptr;
     hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
@@ -139,7 +141,7 @@ struct q38_ctx {
     int clock_khz = 0;
     int lds_bytes = 0;
     int lds_per_cu = 0;
-    int gemv_occupancy[5] = {1, 1, 1, 1, 1}; /* Q4_K, Q5_K, Q6_K, Q3_K, IQ4_XS GEMV workgroups a CU holds */
+    int gemv_occupancy[7] = {1, 1, 1, 1, 1, 1, 1}; /* Q4_K Q5_K Q6_K Q3_K IQ4_XS Q2_K IQ4_NL: GEMV workgroups a CU holds */
     char name[256] = {0};
     /* this device's copy of the fixed scratch array (q38_full_core_noalloc) */
     void *scratch = nullptr;
@@ -396,14 +398,16 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q6k, ctx->mod_proj, "q38_gemv_q8k_q6k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q3k, ctx->mod_proj, "q38_gemv_q8k_q3k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_iq4xs, ctx->mod_proj, "q38_gemv_q8k_iq4xs"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q2k, ctx->mod_proj, "q38_gemv_q8k_q2k"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_iq4nl, ctx->mod_proj, "q38_gemv_q8k_iq4nl"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[0], ctx->mod_proj, "q38_gemv_f32_f32"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[1], ctx->mod_proj, "q38_gemv_f32_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[2], ctx->mod_proj, "q38_gemv_f32_bf16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[3], ctx->mod_proj, "q38_gemv_f32_q8_0"));
     {
-        const hipFunction_t gv[5] = {ctx->f_gemv_q4k, ctx->f_gemv_q5k, ctx->f_gemv_q6k, ctx->f_gemv_q3k,
-                                     ctx->f_gemv_iq4xs};
-        for (int i = 0; i < 5; ++i) {
+        const hipFunction_t gv[7] = {ctx->f_gemv_q4k, ctx->f_gemv_q5k, ctx->f_gemv_q6k, ctx->f_gemv_q3k,
+                                     ctx->f_gemv_iq4xs, ctx->f_gemv_q2k, ctx->f_gemv_iq4nl};
+        for (int i = 0; i < 7; ++i) {
             int n = 0;
             Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, gv[i], 256, 0));
             ctx->gemv_occupancy[i] = std::max(1, n);
@@ -595,6 +599,8 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemv_q8k_q6k") f = ctx->f_gemv_q6k;
     else if (name == "q38_gemv_q8k_q3k") f = ctx->f_gemv_q3k;
     else if (name == "q38_gemv_q8k_iq4xs") f = ctx->f_gemv_iq4xs;
+    else if (name == "q38_gemv_q8k_q2k") f = ctx->f_gemv_q2k;
+    else if (name == "q38_gemv_q8k_iq4nl") f = ctx->f_gemv_iq4nl;
     else if (name == "q38_gemv_f32_f32") f = ctx->f_gemv_f32[0];
     else if (name == "q38_gemv_f32_f16") f = ctx->f_gemv_f32[1];
     else if (name == "q38_gemv_f32_bf16") f = ctx->f_gemv_f32[2];
@@ -1879,10 +1885,14 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     else if (ggml_type == Q38_GGML_Q6_K) f = ctx->f_gemv_q6k, ti_occ = 2;
     else if (ggml_type == Q38_GGML_Q3_K) f = ctx->f_gemv_q3k, ti_occ = 3;
     else if (ggml_type == Q38_GGML_IQ4_XS) f = ctx->f_gemv_iq4xs, ti_occ = 4;
+    else if (ggml_type == Q38_GGML_Q2_K) f = ctx->f_gemv_q2k, ti_occ = 5;
+    else if (ggml_type == Q38_GGML_IQ4_NL) f = ctx->f_gemv_iq4nl, ti_occ = 6;
     else
-        return fail("unsupported quant type %d (Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, IQ4_XS 23; F32, F16, BF16 "
-                    "and Q8_0 weights take q38_gemv_f32)",
+        return fail("unsupported quant type %d (Q2_K 10, Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, IQ4_NL 20, IQ4_XS 23; "
+                    "F32, F16, BF16 and Q8_0 weights take q38_gemv_f32)",
                     ggml_type);
+    /* f32 terms per block in the row sums: IQ4_NL adds one per 32-weight group */
+    const int nt = ggml_type == Q38_GGML_IQ4_NL ? 8 : 1;
     /* the int8 matrix-unit form exists for Q4_K, Q5_K and Q6_K */
     const bool has_gemm = ggml_type == Q38_GGML_Q4_K || ggml_type == Q38_GGML_Q5_K || ggml_type == Q38_GGML_Q6_K;
     if (n_mats < 1 || n_mats > Q38_GEMV_MAX_MATS) return fail("n_mats %d outside 1..%d", n_mats, Q38_GEMV_MAX_MATS);
@@ -1905,13 +1915,13 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
      * keeps one 144-210 byte block in flight, so the bytes a CU has in
      * flight -- and with them its share of the bandwidth -- grow with the
      * workgroups it runs side by side */
-    const int max_units = std::min(Q38_GEMV_UNITS_MAX, 4096 / tok_pass);
+    const int max_units = std::min(Q38_GEMV_UNITS_MAX, 4096 / (tok_pass * nt));
     const long tok_groups_all = ((long)n_tokens + tok_pass - 1) / tok_pass;
     int target_per_wg = max_units / blocks;
     {
         long all_rows = 0;
         for (int i = 0; i < n_mats; ++i) all_rows += std::max(rows[i], 0);
-        const long lds_max = (long)tok_pass * blocks * Q38_GEMV_REC_BYTES + (long)tok_pass * max_units * 4;
+        const long lds_max = (long)tok_pass * blocks * Q38_GEMV_REC_BYTES + (long)tok_pass * max_units * 4 * nt;
         long occ = ctx->gemv_occupancy[ti_occ];
         if (ctx->lds_per_cu > 0) occ = std::max(1L, std::min(occ, ctx->lds_per_cu / lds_max));
         const long slots = std::max(1L, (long)ctx->cu_count * occ / std::max(1L, tok_groups_all));
@@ -1972,7 +1982,7 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     a.width = width;
     a.n_tokens = n_tokens;
     a.tok_pass = tok_pass;
-    const unsigned lds = (unsigned)(tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * max_per_wg * blocks * 4);
+    const unsigned lds = (unsigned)(tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * max_per_wg * blocks * 4 * nt);
     return ctx->launch(f, (unsigned)wgs, (unsigned)tok_groups, 1, 256, &a, lds);
 }
 

@@ -8,7 +8,9 @@
  *   dot_q4_k_q8_k      src/kernel/tensor.rs:365-391
  *   dot_q5_k_q8_k      src/kernel/tensor.rs:393-428
  *   dot_q6_k_q8_k      src/kernel/tensor.rs:430-457
+ *   dot_q2_k_q8_k      src/kernel/tensor.rs:301-333
  *   dot_q3_k_q8_k      src/kernel/tensor.rs:335-363 (unpack_q3_scales :34-44)
+ *   dot_iq4_nl_q8_k    src/kernel/iq.rs:355-377 (eight per-group terms per block)
  *   dot_iq4_xs_q8_k    src/kernel/iq.rs:379-405 (code book iq_tables.rs:53-56)
  *   dot_f32/f16/bf16/q8_0 (f32 input), tensor.rs:79-117, through
  *                      tensor_gemv_f32 / tensor_gemm_f32, tensor.rs:1095-1129,
@@ -80,6 +82,14 @@ template <> struct KQuant<Q38_GGML_Q5_K> { static constexpr int bytes = 176, wor
 template <> struct KQuant<Q38_GGML_Q6_K> { static constexpr int bytes = 210, words = 52; };
 template <> struct KQuant<Q38_GGML_Q3_K> { static constexpr int bytes = 110, words = 27; };
 template <> struct KQuant<Q38_GGML_IQ4_XS> { static constexpr int bytes = 136, words = 34; };
+template <> struct KQuant<Q38_GGML_Q2_K> { static constexpr int bytes = 84, words = 21; };
+template <> struct KQuant<Q38_GGML_IQ4_NL> { static constexpr int bytes = 144, words = 36; };
+
+/* f32 terms a block adds to its row's total, in order: one (d * weighted
+ * [- dmin * minimum]) for the K-quants and IQ4_XS, one per 32-weight group
+ * for IQ4_NL (its groups carry their own f16 scales) */
+template <int TYPE> struct BlockTerms { static constexpr int n = 1; };
+template <> struct BlockTerms<Q38_GGML_IQ4_NL> { static constexpr int n = 8; };
 
 /* ggml's IQ4_NL / IQ4_XS code book as int8 bytes, 4 per word:
  * -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113 */
@@ -136,6 +146,20 @@ Q38_DEV void load_unit(const uint8_t *weights, size_t g, Unit<TYPE> &u) {
         u.dh = *reinterpret_cast<const uint16_t *>(weights + s + 108);
 #pragma unroll
         for (int j = 0; j < 27; ++j) u.w[j] = __builtin_amdgcn_alignbyte(win[j + 1], win[j], o);
+    } else if (TYPE == Q38_GGML_Q2_K) {
+        /* 84-byte blocks start 4-byte aligned */
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(weights + g * 84);
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            u32x4 v;
+            __builtin_memcpy(&v, p + 4 * i, 16);
+            u.w[4 * i] = v.x;
+            u.w[4 * i + 1] = v.y;
+            u.w[4 * i + 2] = v.z;
+            u.w[4 * i + 3] = v.w;
+        }
+        u.w[20] = p[20];
+        u.dh = 0;
     } else if (TYPE == Q38_GGML_IQ4_XS) {
         /* 136-byte blocks start 8-byte aligned */
         const uint32_t *p = reinterpret_cast<const uint32_t *>(weights + g * 136);
@@ -188,6 +212,7 @@ Q38_DEV void load_unit(const uint8_t *weights, size_t g, Unit<TYPE> &u) {
 template <int TYPE> struct UnitScales {
     int sc[16];
     int mn[8];
+    float gd[8]; /* IQ4_NL: the groups' scales */
     float d, dmin;
 };
 
@@ -205,6 +230,18 @@ Q38_DEV void unit_scales(const Unit<TYPE> &u, UnitScales<TYPE> &s) {
             s.sc[i] = (low | (high << 4)) - 32;
         }
         s.d = q38_f16(u.dh);
+        s.dmin = 0.0f;
+    } else if (TYPE == Q38_GGML_Q2_K) {
+        /* the 16 scale bytes (low nibble scale, high nibble minimum) */
+#pragma unroll
+        for (int g = 0; g < 16; ++g) s.sc[g] = (int)((u.w[g >> 2] >> (8 * (g & 3))) & 255u);
+        s.d = q38_f16(u.w[20]);
+        s.dmin = q38_f16(u.w[20] >> 16);
+    } else if (TYPE == Q38_GGML_IQ4_NL) {
+        /* group g's f16 scale is the halfword at byte 18 g */
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s.gd[g] = q38_f16(u.w[(18 * g) >> 2] >> (8 * ((18 * g) & 3)));
+        s.d = 0.0f;
         s.dmin = 0.0f;
     } else if (TYPE == Q38_GGML_IQ4_XS) {
         /* group g: low 4 bits from scales_l[g / 2] (nibble g % 2), high 2
@@ -244,7 +281,26 @@ Q38_DEV float unit_term(const Unit<TYPE> &u, const UnitScales<TYPE> &s, const ui
         bsum[2 * k] = (int)(int16_t)(v & 0xffffu);
         bsum[2 * k + 1] = (int)(int16_t)(v >> 16);
     }
-    if (TYPE == Q38_GGML_Q3_K) {
+    if (TYPE == Q38_GGML_Q2_K) {
+        /* group s (16 values 16s..16s+15: half s / 8, field (s % 8) / 2,
+         * lanes 16 (s % 2)..+15): 2-bit quants times the low nibble of
+         * scale byte s, minus the high nibble times the group's sum */
+        int weighted = 0, minimum = 0;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const int half = g >> 3, field = (g >> 1) & 3, part = g & 1;
+            const u32x4 av = aq[g];
+            int dot = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                dot = q38_sdot4((u.w[4 + 8 * half + 4 * part + c] >> (2 * field)) & 0x03030303u, av[c], dot);
+            weighted += (s.sc[g] & 15) * dot;
+            minimum += (s.sc[g] >> 4) * bsum[g];
+        }
+        const float d = s.d * a_scale;
+        const float dmin = s.dmin * a_scale;
+        return d * (float)weighted - dmin * (float)minimum;
+    } else if (TYPE == Q38_GGML_Q3_K) {
         /* group s (16 values 16s..16s+15: half s / 8, field (s % 8) / 2,
          * lanes 16 (s % 2)..+15): q = 2 low bits + 4 * high bit in 0..7 is
          * the reference's qv + 4, so sum qv a = dot(q, a) - 4 * bsum[s] */
@@ -350,6 +406,29 @@ Q38_DEV float unit_term(const Unit<TYPE> &u, const UnitScales<TYPE> &s, const ui
     }
 }
 
+/* IQ4_NL's eight group terms of one unit against one token's activation
+ * block (dot_iq4_nl_q8_k's per-group update, iq.rs:363-374): group g's 16
+ * quant bytes start at byte 18 g + 2 (2 bytes off a dword for even g). */
+Q38_DEV void unit_terms_iq4nl(const Unit<Q38_GGML_IQ4_NL> &u, const UnitScales<Q38_GGML_IQ4_NL> &s,
+                              const uint8_t *rec, float a_scale, float *out) {
+    const u32x4 *aq = reinterpret_cast<const u32x4 *>(rec);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        const int base = (18 * g + 2) >> 2;
+        const uint32_t o = (uint32_t)((18 * g + 2) & 3);
+        const u32x4 alo = aq[2 * g], ahi = aq[2 * g + 1];
+        int sub = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t x = o ? __builtin_amdgcn_alignbyte(u.w[base + c + 1], u.w[base + c], o) : u.w[base + c];
+            sub = q38_sdot4(q38_iq4_lookup(x & 0x0F0F0F0Fu), alo[c], sub);
+            sub = q38_sdot4(q38_iq4_lookup((x >> 4) & 0x0F0F0F0Fu), ahi[c], sub);
+        }
+        const float d = s.gd[g] * a_scale;
+        out[g] = d * (float)sub;
+    }
+}
+
 /*
  * A workgroup owns rows [row0, row0 + R) of one of up to Q38_GEMV_MAX_MATS
  * matrices that read the same activations, and the tokens [tok0, tok0 + tp);
@@ -391,7 +470,8 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     uint8_t *recs = lds;                                                     /* [tp][B] x kRec */
     int16_t *lsums = reinterpret_cast<int16_t *>(lds + (size_t)nrec * kRec); /* [tp][B][16] */
     float *lscales = reinterpret_cast<float *>(lsums + (size_t)nrec * 16);   /* [tp][B] */
-    float *terms = lscales + nrec;                                           /* [tp][units] */
+    constexpr int NT = BlockTerms<TYPE>::n;
+    float *terms = lscales + nrec;                                           /* [tp][units][NT] */
     const size_t g0 = (size_t)row0 * B;
 
     Unit<TYPE> w[2];
@@ -444,7 +524,10 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
             const int b = u % B;
             for (int t = 0; t < tp; ++t) {
                 const int r = t * B + b;
-                terms[t * units + u] = unit_term<TYPE>(w[k & 1], s, recs + r * kRec, lsums + r * 16, lscales[r]);
+                if constexpr (NT == 1)
+                    terms[t * units + u] = unit_term<TYPE>(w[k & 1], s, recs + r * kRec, lsums + r * 16, lscales[r]);
+                else
+                    unit_terms_iq4nl(w[k & 1], s, recs + r * kRec, lscales[r], terms + ((size_t)t * units + u) * NT);
             }
         }
     }
@@ -452,9 +535,9 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
 
     for (int i = tid; i < tp * rows_here; i += 256) {
         const int t = i / rows_here, r = i - t * rows_here;
-        const float *tr = terms + t * units + r * B;
+        const float *tr = terms + ((size_t)t * units + r * B) * NT;
         float total = 0.0f;
-        for (int b = 0; b < B; ++b) total += tr[b];
+        for (int b = 0; b < B * NT; ++b) total += tr[b];
         out[(size_t)(tok0 + t) * rows + row0 + r] = total;
     }
 }
@@ -748,6 +831,10 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q4k(q38_gemv_args
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q5k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q5_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q6k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q6_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q3k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q3_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q2k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q2_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4nl(q38_gemv_args a) {
+    gemv_q8k<Q38_GGML_IQ4_NL>(a);
+}
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4xs(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ4_XS>(a);
 }

@@ -289,7 +289,9 @@ typedef struct {
 #define Q38_GGML_F32 0
 #define Q38_GGML_F16 1
 #define Q38_GGML_Q8_0 8
+#define Q38_GGML_Q2_K 10
 #define Q38_GGML_Q3_K 11
+#define Q38_GGML_IQ4_NL 20
 #define Q38_GGML_Q4_K 12
 #define Q38_GGML_Q5_K 13
 #define Q38_GGML_Q6_K 14

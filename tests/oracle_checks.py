@@ -349,10 +349,30 @@ def _q3k_scales(sc12):
 def _dequant_row(ty, row):
     """A weight row's values the way the decoded path reads them."""
     out = []
-    bb = {11: 110, 12: 144, 13: 176, 14: 210, 23: 136}[ty]
+    bb = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 144, 23: 136}[ty]
     for blk in np.asarray(row, np.uint8).reshape(-1, bb).astype(np.int64):
         w = np.zeros(256)
-        if ty == 11:
+        if ty == 10:
+            # ggml's dequantize_row_q2_K: per 128 values, four 2-bit shifts,
+            # each 32 values as two 16-value groups with scale d * (sc & 15)
+            # and minimum dmin * (sc >> 4)
+            sc, qs = blk[0:16], blk[16:80]
+            d, dmin = _f16(blk[80], blk[81]), _f16(blk[82], blk[83])
+            i = 0
+            for n in range(2):
+                for shift in range(0, 8, 2):
+                    for part in range(2):
+                        q = (qs[32 * n + 16 * part + np.arange(16)] >> shift) & 3
+                        w[128 * n + 32 * (shift // 2) + 16 * part + np.arange(16)] = \
+                            d * (sc[i] & 15) * q - dmin * (sc[i] >> 4)
+                        i += 1
+        elif ty == 20:
+            for g in range(8):
+                sub = blk[18 * g:18 * g + 18]
+                d, q = _f16(sub[0], sub[1]), sub[2:18]
+                w[32 * g:32 * g + 16] = d * _KVALUES_IQ4[q & 15]
+                w[32 * g + 16:32 * g + 32] = d * _KVALUES_IQ4[q >> 4]
+        elif ty == 11:
             hm, qs, d = blk[0:32], blk[32:96], _f16(blk[108], blk[109])
             sc = _q3k_scales(blk[96:108].astype(np.uint8))
             m, i = 0, 0
@@ -403,7 +423,7 @@ def _dequant_row(ty, row):
 def _random_kquant(ty, rows, width, seed):
     """Weight rows of random bytes with finite, moderate f16 scales."""
     rng = np.random.default_rng(seed)
-    bb = {11: 110, 12: 144, 13: 176, 14: 210, 23: 136}[ty]
+    bb = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 144, 23: 136}[ty]
     w = rng.integers(0, 256, (rows, width // 256, bb), dtype=np.uint8)
     f16 = lambda lo, hi, n: np.frombuffer(rng.uniform(lo, hi, n).astype(np.float16).tobytes(), np.uint8).reshape(n, 2)
     n = rows * (width // 256)
@@ -414,6 +434,12 @@ def _random_kquant(ty, rows, width, seed):
         w.reshape(n, bb)[:, 208:210] = f16(1e-3, 4e-2, n)
     elif ty == 11:
         w.reshape(n, bb)[:, 108:110] = f16(1e-3, 4e-2, n)
+    elif ty == 10:
+        w.reshape(n, bb)[:, 80:82] = f16(1e-3, 4e-2, n)
+        w.reshape(n, bb)[:, 82:84] = f16(1e-3, 4e-2, n)
+    elif ty == 20:
+        for g in range(8):
+            w.reshape(n, bb)[:, 18 * g:18 * g + 2] = f16(1e-4, 4e-3, n)
     else:
         w.reshape(n, bb)[:, 0:2] = f16(1e-4, 4e-3, n)
     return w.reshape(rows, -1)
@@ -456,7 +482,8 @@ def check_kquant_dots_against_dequantised_rows(ref, synth):
     x[1] = ((np.arange(W) * 7919) % 101) / np.float32(50.0) - np.float32(1.0)
     p = ref.quantize_q8_k(x)
     a = _q8k_dequant(p, T, W, ref).reshape(T, W)
-    for ty in (ref.GGML_Q3_K, ref.GGML_Q4_K, ref.GGML_Q5_K, ref.GGML_Q6_K, ref.GGML_IQ4_XS):
+    for ty in (ref.GGML_Q2_K, ref.GGML_Q3_K, ref.GGML_Q4_K, ref.GGML_Q5_K, ref.GGML_Q6_K, ref.GGML_IQ4_NL,
+               ref.GGML_IQ4_XS):
         wb = _random_kquant(ty, 7, W, 0x51333872 + ty)
         got = ref.gemv_q8_k(ty, wb, p, T, W)
         for r in range(7):
@@ -473,7 +500,7 @@ def check_gemv_serial_equals_threaded(ref, synth):
     W = 512
     x = np.random.default_rng(0x51333873).standard_normal((2, W)).astype(np.float32)
     p = ref.quantize_q8_k(x)
-    for ty in (ref.GGML_Q3_K, ref.GGML_Q4_K, ref.GGML_Q6_K, ref.GGML_IQ4_XS):
+    for ty in (ref.GGML_Q2_K, ref.GGML_Q3_K, ref.GGML_Q4_K, ref.GGML_Q6_K, ref.GGML_IQ4_NL, ref.GGML_IQ4_XS):
         wb = _random_kquant(ty, 37, W, 0x51333874 + ty)
         if not np.array_equal(ref.gemv_q8_k(ty, wb, p, 2, W, threads=1), ref.gemv_q8_k(ty, wb, p, 2, W, threads=5)):
             return f"type {ty}: threaded GEMV differs from serial"

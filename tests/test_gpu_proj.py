@@ -1,7 +1,7 @@
 """The weight projections on the GPU (q38_quantize_q8_k, q38_gemv_q8_k,
 q38_gemv_f32) against the oracle's restatement of quantize_q8_k
 (src/kernel/quant.rs:55-128), of the scalar Q3_K..Q6_K x Q8_K row dots
-(src/kernel/tensor.rs:335-457) and the IQ4_XS one (src/kernel/iq.rs:379-405)
+(src/kernel/tensor.rs:301-457) and the IQ4_NL / IQ4_XS ones (src/kernel/iq.rs:355-405)
 driven per row as tensor_gemv_q8_k / tensor_gemm_q8_k do
 (tensor.rs:1131-1173, :1217-1270), and of the f32-input row dots of
 tensor_gemv_f32 (tensor.rs:79-117, :1095-1129).  The integer parts and the
@@ -15,7 +15,7 @@ from parity import check_attn
 
 pytestmark = pytest.mark.gpu
 
-TYPES = {"Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_XS": 23}
+TYPES = {"Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23}
 F32_TYPES = {"F32": 0, "F16": 1, "BF16": 30, "Q8_0": 8}
 HIDDEN = 5120
 
@@ -78,7 +78,7 @@ def test_gemv_q8_k_subnormal_scales_and_widest_rows(ctx, ref, name):
         d_q = _quantize_on_device(ctx, x)
         wb = _random_kquant(ty, rows, W, 0x513338A9 + ty)
         blocks = wb.reshape(rows * (W // 256), -1)
-        off = {14: 208, 11: 108}.get(ty, 0)  # the block's f16 scale
+        off = {14: 208, 11: 108, 10: 80}.get(ty, 0)  # the block's (first) f16 scale
         sub = np.array([0x0001, 0x03ff, 0x8200, 0x0000, 0x8000], np.uint16)
         for i in range(0, blocks.shape[0], 3):
             blocks[i, off:off + 2] = np.frombuffer(sub[i % 5].tobytes(), np.uint8)

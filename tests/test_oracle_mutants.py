@@ -31,6 +31,8 @@ MUTANTS = {
     19: "Q3_K high bit read with the opposite sense",
     20: "IQ4_XS group scale without its -32 offset",
     21: "BF16 row dot reading neighbouring elements swapped",
+    22: "Q2_K minimum from the scale nibble",
+    23: "IQ4_NL low and high nibbles swapped",
 }
 
 
