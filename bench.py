@@ -889,7 +889,10 @@ def main():
     tpath = os.path.join(ROOT, "profiles", "attn_decode_split_32k_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            rec = json.load(f)
+        # a record of another kernel says nothing about this one
+        if rec.get("kernel") == DECODE_KERNEL:
+            traffic = rec.get("hbm_bytes_per_launch")
 
     extra = {
         "split_kernel_us": k_ms * 1e3,
