@@ -187,6 +187,8 @@ struct q38_ctx {
     int launch(hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned block, void *args,
                unsigned lds_bytes = 0) {
         void *params[] = {args};
+        /* the stamped form takes the grid in threads, a 32-bit count */
+        if ((uint64_t)gx * block > 0xFFFFFFFFull) return fail("grid of %u workgroups too large", gx);
         const bool timing = f == timed && timer_used + 2 <= (int)timer_events.size();
         if (timing) {
             /* start/stop timestamps taken by the dispatch itself */
@@ -1905,10 +1907,16 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     if (width / Q38_Q8K_BLOCK > Q38_GEMV_MAX_BLOCKS)
         return fail("width %d above %d", width, Q38_GEMV_MAX_BLOCKS * Q38_Q8K_BLOCK);
     if (n_tokens == 0) return 0;
-    /* tokens per pass: as many as Q38_GEMV_ACT_LDS holds (one at least), up to 8 */
+    /* tokens per pass: as many as Q38_GEMV_ACT_LDS holds (one at least), up
+     * to 8, spread evenly over the passes that takes (8 tokens at most 3 per
+     * pass: 3, 3, 2) */
     const int blocks = width / Q38_Q8K_BLOCK;
     int tok_pass = std::max(1, std::min(Q38_GEMV_TOKENS, Q38_GEMV_ACT_LDS / (blocks * Q38_GEMV_REC_BYTES)));
     tok_pass = std::min(tok_pass, n_tokens);
+    {
+        const int passes = (n_tokens + tok_pass - 1) / tok_pass;
+        tok_pass = (n_tokens + passes - 1) / passes;
+    }
     /* rows per workgroup: up to Q38_GEMV_UNITS_MAX units (four per lane), the
      * per-token terms in at most 16 KiB of LDS, and few enough rows that the
      * launch has about as many workgroups as the CUs hold at once: a lane
@@ -1975,15 +1983,19 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
         return 0;
     }
     const long tok_groups = ((long)n_tokens + tok_pass - 1) / tok_pass;
-    if (wgs > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
+    /* one pass: a workgroup per row group; several: the passes of a row
+     * group 8 workgroup ids apart (one XCD, dispatched together) */
+    const long grid = tok_groups == 1 ? wgs : (wgs + 7) / 8 * 8 * tok_groups;
+    if (grid > 0x7FFFFFFFL) return fail("too many rows or tokens");
     a.wg_begin[kept] = (int32_t)wgs;
     a.n_mats = kept;
     a.q8k = d_q8k;
     a.width = width;
     a.n_tokens = n_tokens;
     a.tok_pass = tok_pass;
+    a.tok_groups = (int32_t)tok_groups;
     const unsigned lds = (unsigned)(tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * max_per_wg * blocks * 4 * nt);
-    return ctx->launch(f, (unsigned)wgs, (unsigned)tok_groups, 1, 256, &a, lds);
+    return ctx->launch(f, (unsigned)grid, 1, 1, 256, &a, lds);
 }
 
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,

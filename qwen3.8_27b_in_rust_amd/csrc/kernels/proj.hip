@@ -444,6 +444,9 @@ Q38_DEV void unit_terms_iq4nl(const Unit<Q38_GGML_IQ4_NL> &u, const UnitScales<Q
  *   3. one lane per (row, token) adds the row's B terms in block order, the
  *      reference's `total += ...` sequence, and stores the result.
  * The host sizes R and tp (LDS: tp * B * Q38_GEMV_REC_BYTES + tp * R * B * 4).
+ * When the tokens take several passes, the passes of one row group are
+ * workgroups 8 ids apart: they start together on one XCD, and all but the
+ * first find the rows' weights in its L2 rather than in HBM.
  */
 template <int TYPE>
 Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
@@ -451,20 +454,28 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     const int tid = threadIdx.x;
     const int width = a.width;
     const int B = width / Q38_Q8K_BLOCK;
-    /* the matrix of this workgroup: matrices share the activations and
-     * take consecutive ranges of blockIdx.x */
+    /* (row group, token pass) of this workgroup */
+    int grp = (int)blockIdx.x, pass = 0;
+    if (a.tok_groups > 1) {
+        const int q = (int)(blockIdx.x >> 3);
+        pass = q % a.tok_groups;
+        grp = (q / a.tok_groups) * 8 + (int)(blockIdx.x & 7);
+        if (grp >= a.wg_begin[a.n_mats]) return; /* the grid's round-up to 8 row groups */
+    }
+    /* the matrix of this row group: matrices share the activations and
+     * take consecutive ranges of row groups */
     int mat = 0;
 #pragma unroll
-    for (int i = 1; i < Q38_GEMV_MAX_MATS; ++i) mat += (i < a.n_mats && (int)blockIdx.x >= a.wg_begin[i]) ? 1 : 0;
+    for (int i = 1; i < Q38_GEMV_MAX_MATS; ++i) mat += (i < a.n_mats && grp >= a.wg_begin[i]) ? 1 : 0;
     const uint8_t *weights = a.weights[mat];
     float *out = a.out[mat];
     const int rows = a.rows[mat];
     const int R = a.rows_per_wg[mat];
-    const int row0 = ((int)blockIdx.x - a.wg_begin[mat]) * R;
+    const int row0 = (grp - a.wg_begin[mat]) * R;
     const int rows_here = min(R, rows - row0);
     const int units = rows_here * B;
     const int steps = (units + 255) >> 8;
-    const int tok0 = blockIdx.y * a.tok_pass;
+    const int tok0 = pass * a.tok_pass;
     const int tp = min(a.tok_pass, a.n_tokens - tok0);
     const int nrec = a.tok_pass * B;
     uint8_t *recs = lds;                                                     /* [tp][B] x kRec */

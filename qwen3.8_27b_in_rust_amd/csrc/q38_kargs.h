@@ -301,7 +301,7 @@ typedef struct {
 #define Q38_GEMV_MAX_BLOCKS 192 /* 256-wide blocks per row (width 49152): one token's blocks fit LDS */
 #define Q38_GEMV_UNITS_MAX 1024 /* (row, block) units per GEMV workgroup: four steps of 256 */
 #define Q38_GEMV_REC_BYTES (272 + 32 + 4) /* LDS bytes of one staged Q8_K block: padded quants, sums, scale */
-#define Q38_GEMV_ACT_LDS (48 * 1024) /* LDS for staged activations when tokens > 1 */
+#define Q38_GEMV_ACT_LDS (64 * 1024) /* LDS for staged activations when tokens > 1 */
 
 /* quantize_q8_k: grid (B, T), 64 threads (one wave per block). */
 typedef struct {
@@ -312,11 +312,15 @@ typedef struct {
 } q38_quantize_args;
 
 /* K-quant x Q8_K GEMV / GEMM over up to Q38_GEMV_MAX_MATS matrices of one
- * type and width that read the same activations: grid (wg_begin[n_mats],
- * ceil(T / tok_pass)), 256 threads, one lane per (row, block) unit; matrix
- * i takes workgroups wg_begin[i] .. wg_begin[i+1]-1, rows_per_wg[i] * B <=
- * Q38_GEMV_UNITS_MAX; dynamic LDS tok_pass * B * Q38_GEMV_REC_BYTES +
- * tok_pass * max_i(rows_per_wg[i]) * B * 4 bytes. */
+ * type and width that read the same activations: G = wg_begin[n_mats] row
+ * groups times P = tok_groups = ceil(T / tok_pass) token passes, 256
+ * threads, one lane per (row, block) unit; matrix i takes row groups
+ * wg_begin[i] .. wg_begin[i+1]-1, rows_per_wg[i] * B <= Q38_GEMV_UNITS_MAX;
+ * dynamic LDS tok_pass * B * Q38_GEMV_REC_BYTES + tok_pass *
+ * max_i(rows_per_wg[i]) * B * 4 bytes.  One token pass (P == 1): grid (G).
+ * Several: grid (8 * P * ceil(G / 8)), workgroup L serving pass (L / 8) % P
+ * of row group 8 (L / (8 P)) + L % 8 (none past G), so the passes of a row
+ * group are dispatched together onto one XCD and share its L2. */
 #define Q38_GEMV_MAX_MATS 4
 /* From this many tokens (twice as many for matrices of under 8192 rows) the
  * projections run on the int8 matrix unit (q38_gemm_q8k_*: grid (ceil(rows /
@@ -335,7 +339,7 @@ typedef struct {
     int32_t width;
     int32_t n_tokens;
     int32_t tok_pass;
-    int32_t pad_;
+    int32_t tok_groups;
 } q38_gemv_args;
 
 /* f32-input projections (F32, F16, BF16, Q8_0 weights): grid (ceil(rows /

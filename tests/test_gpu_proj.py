@@ -51,11 +51,14 @@ def test_quantize_q8_k_bit_exact(ctx, ref, T, W):
 
 @pytest.mark.parametrize("name", sorted(TYPES))
 @pytest.mark.parametrize("rows,W,T", [(257, HIDDEN, 1), (61, 768, 3), (33, 1280, 9), (4, 256, 17),
-                                      (1100, 17408, 4), (700, 2304, 1)])
+                                      (1100, 17408, 4), (517, 17408, 8), (700, 2304, 1)])
 def test_gemv_q8_k_bit_exact(ctx, ref, name, rows, W, T):
     """Row counts that leave a partial last workgroup, several token passes
-    (9 and 17 tokens), a width whose token passes hold 2 tokens (17408), and
-    matrices small enough to get one row per workgroup."""
+    (9 and 17 tokens), a width whose token passes hold at most 3 tokens
+    (17408: 8 tokens as passes of 3, 3 and 2, the passes of a row group
+    numbered 8 workgroups apart over a row-group count that is not a
+    multiple of 8), and matrices small enough to get one row per
+    workgroup."""
     ty = TYPES[name]
     x = _activations(T, W, 0x51333890 + T)
     d_q = _quantize_on_device(ctx, x)
