@@ -620,8 +620,14 @@ def linear_core_prefill(pkg, ctx, reps: int):
 
 
 FFN_MATS = ((12, 17408, 5120, "gate"), (12, 17408, 5120, "up"), (14, 5120, 17408, "down"))
-QUANT_BLOCK_BYTES = {12: 144, 13: 176, 14: 210}
-GEMV_KERNELS = {12: "q38_gemv_q8k_q4k", 13: "q38_gemv_q8k_q5k", 14: "q38_gemv_q8k_q6k"}
+QUANT_BLOCK_BYTES = {12: 144, 13: 176, 14: 210, 10: 84, 11: 110, 20: 144, 23: 136, 16: 66, 17: 74, 22: 82, 18: 98,
+                     21: 110, 19: 50, 29: 56}
+GEMV_KERNELS = {12: "q38_gemv_q8k_q4k", 13: "q38_gemv_q8k_q5k", 14: "q38_gemv_q8k_q6k", 10: "q38_gemv_q8k_q2k",
+                11: "q38_gemv_q8k_q3k", 20: "q38_gemv_q8k_iq4nl", 23: "q38_gemv_q8k_iq4xs",
+                16: "q38_gemv_q8k_iq2xxs", 17: "q38_gemv_q8k_iq2xs", 22: "q38_gemv_q8k_iq2s",
+                18: "q38_gemv_q8k_iq3xxs", 21: "q38_gemv_q8k_iq3s", 19: "q38_gemv_q8k_iq1s", 29: "q38_gemv_q8k_iq1m"}
+FORMAT_NAMES = {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 10: "Q2_K", 11: "Q3_K", 20: "IQ4_NL", 23: "IQ4_XS", 16: "IQ2_XXS",
+                17: "IQ2_XS", 22: "IQ2_S", 18: "IQ3_XXS", 21: "IQ3_S", 19: "IQ1_S", 29: "IQ1_M"}
 
 
 def gemv_bytes(ty: int, rows: int, width: int, n_tokens: int) -> int:
@@ -712,6 +718,46 @@ def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
         a.free()
     for e in (e0, e1):
         ctx.destroy_event(e)
+    return res
+
+
+def weight_formats(pkg, ctx, reps: int):
+    """One token through a 17408 x 5120 matrix (the FFN gate's shape) in every
+    Q8_K weight format: q38_gemv_q8_k's kernel duration and bandwidth, the
+    weights rotated over copies totalling >= 512 MB (beyond the last-level
+    cache).  Weights are random bytes (timing only)."""
+    rows, width = 17408, 5120
+    x = ctx.empty((1, width))
+    ctx.fill_normal(x, width, 0x51335200)
+    q = ctx.empty((ctx.q8k_bytes(1, width),), np.uint8)
+    ctx.quantize_q8_k(1, width, x, q)
+    out = ctx.empty((1, rows))
+    res = {}
+    for ty in (10, 11, 12, 13, 14, 20, 23, 16, 17, 22, 18, 21, 19, 29):
+        nbytes = rows * (width // 256) * QUANT_BLOCK_BYTES[ty]
+        copies = -(-512 * 2**20 // nbytes)
+        ws = []
+        for c in range(copies):
+            w = ctx.empty((nbytes,), np.uint8)
+            ctx.fill_normal(w, nbytes // 4, 0x51335210 + 64 * ty + c)
+            ws.append(w)
+        for w in ws:
+            ctx.gemv_q8_k(ty, rows, width, w, q, 1, out)
+        ctx.sync()
+        ctx.kernel_timer_start(GEMV_KERNELS[ty], reps * copies)
+        for _ in range(reps):
+            for w in ws:
+                ctx.gemv_q8_k(ty, rows, width, w, q, 1, out)
+        k_ms, k_n = ctx.kernel_timer_stop()
+        us = k_ms * 1e3 / max(k_n, 1)
+        b = gemv_bytes(ty, rows, width, 1)
+        res[FORMAT_NAMES[ty]] = {"kernel_us": round(us, 2), "weight_mb": round(nbytes / 1e6, 1),
+                                 "gb_s": round(b / (us * 1e-6) / 1e9, 1),
+                                 "frac_hbm": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+        for w in ws:
+            w.free()
+    for a in (x, q, out):
+        a.free()
     return res
 
 
@@ -843,6 +889,8 @@ EXTRAS = {
                           lambda pkg, ctx: ffn_projections(pkg, ctx, 1, 20)),
     "ffn_projections_8": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 8 tokens",
                           lambda pkg, ctx: ffn_projections(pkg, ctx, 8, 20)),
+    "weight_formats_1": ("one token through a 17408x5120 matrix in each Q8_K weight format",
+                         lambda pkg, ctx: weight_formats(pkg, ctx, 3)),
 }
 
 

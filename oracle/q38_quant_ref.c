@@ -20,6 +20,19 @@
  *   dot_iq4_nl_q8_k               src/kernel/iq.rs:355-377 (iq4_nl_group :96-99)
  *   dot_iq4_xs_q8_k               src/kernel/iq.rs:379-405 (KVALUES_IQ4NL,
  *                                 src/kernel/iq_tables.rs:53-56)
+ *   dot_iq3_s_q8_k                src/kernel/iq.rs:407-446
+ *   dot_iq3_xxs_q8_k              src/kernel/iq.rs:448-482
+ *   dot_iq2_xxs_q8_k              src/kernel/iq.rs:484-512
+ *   dot_iq2_xs_q8_k               src/kernel/iq.rs:514-547
+ *   dot_iq2_s_q8_k                src/kernel/iq.rs:549-578
+ *   dot_iq1_s_q8_k                src/kernel/iq.rs:580-612 (the repacked
+ *                                 form, :733-762, does the same integer
+ *                                 and f32 operations)
+ *   dot_iq1_m_q8_k                src/kernel/iq.rs:614-667
+ *                                 (grid32/grid64/sign_of :80-93; the grids
+ *                                 are ggml's tables, q38_iq_grids.h;
+ *                                 KSIGNS_IQ2XS[i] = i | parity(i) << 7 and
+ *                                 KMASK_IQ2XS[j] = 1 << j are formed here)
  *   dot_f32/f16/bf16/q8_0_scalar  src/kernel/tensor.rs:79-117 (the row dots
  *                                 of tensor_gemv_f32 / tensor_gemm_f32,
  *                                 tensor.rs:1095-1129, :1175-1215, for the
@@ -38,6 +51,7 @@
  * int16 [T][B][16], scales f32 [T][B].
  */
 #include "q38_ref.h"
+#include "q38_iq_grids.h"
 
 #include <math.h>
 #include <pthread.h>
@@ -409,6 +423,280 @@ static float dot_iq4_xs(const uint8_t *data, const q8k_view *q, int blocks) {
     return total;
 }
 
+/* ---- IQ formats: lattice-grid codes (iq.rs:407-667) ---- */
+static const uint64_t iq2xxs_grid[256] = Q38_IQ2XXS_GRID;
+static const uint64_t iq2xs_grid[512] = Q38_IQ2XS_GRID;
+static const uint64_t iq2s_grid[1024] = Q38_IQ2S_GRID;
+static const uint32_t iq3xxs_grid[256] = Q38_IQ3XXS_GRID;
+static const uint32_t iq3s_grid[512] = Q38_IQ3S_GRID;
+static const uint64_t iq1s_grid[2048] = Q38_IQ1S_GRID;
+static const float iq1_delta = 0.125f; /* IQ1_DELTA, iq.rs:19 */
+
+static uint32_t read_u32(const uint8_t *p) {
+    return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+}
+/* KSIGNS_IQ2XS[i]: the 7 stored sign bits and an eighth that makes the count even */
+static uint8_t ksigns(uint32_t i) { return (uint8_t)(i | (uint32_t)(__builtin_popcount(i) & 1) << 7); }
+static int32_t sign_of(uint32_t mask, uint32_t bit) { return (mask & bit) ? -1 : 1; }
+static int32_t grid64_byte(uint64_t entry, int lane) { return (int32_t)((entry >> (8 * lane)) & 255); }
+static int32_t grid32_byte(uint32_t entry, int lane) { return (int32_t)((entry >> (8 * lane)) & 255); }
+
+/* dot_iq3_s_q8_k, iq.rs:407-446.  Block: d (f16) | qs[64] | qh[8] |
+ * signs[32] | scales[4], 110 bytes. */
+static float dot_iq3_s(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 110;
+        const float d = q38r_f16_to_f32(read_u16(w)) * b->scale;
+        const uint8_t *indices = w + 2, *high = w + 66, *signs = w + 74, *scales = w + 106;
+        int32_t weighted = 0;
+        for (int group = 0; group < 8; ++group) {
+            const uint8_t *code = indices + group * 8;
+            const uint32_t high_bits = high[group];
+            const uint8_t *group_signs = signs + group * 4;
+            const int32_t scale = 1 + 2 * (int32_t)((scales[group / 2] >> (4 * (group % 2))) & 15);
+            int32_t subtotal = 0;
+            for (int section = 0; section < 4; ++section) {
+                const uint32_t index0 = code[section * 2] | ((high_bits << (8 - 2 * section)) & 0x100);
+#if Q38R_MUTANT == 28
+                const uint32_t index1 = code[section * 2 + 1] | ((high_bits << (8 - 2 * section)) & 0x100); /* planted */
+#else
+                const uint32_t index1 = code[section * 2 + 1] | ((high_bits << (7 - 2 * section)) & 0x100);
+#endif
+                const uint32_t g0 = iq3s_grid[index0], g1 = iq3s_grid[index1];
+                for (int lane = 0; lane < 4; ++lane) {
+                    const int32_t sign0 = sign_of(group_signs[section], 1u << lane);
+                    const int32_t sign1 = sign_of(group_signs[section], 1u << (lane + 4));
+                    subtotal += (int32_t)b->quants[group * 32 + section * 8 + lane] * grid32_byte(g0, lane) * sign0;
+                    subtotal += (int32_t)b->quants[group * 32 + section * 8 + lane + 4] * grid32_byte(g1, lane) * sign1;
+                }
+            }
+            weighted += scale * subtotal;
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
+/* dot_iq3_xxs_q8_k, iq.rs:448-482.  Block: d (f16) | qs[64] | 8 u32 of
+ * 4 x 7 sign bits and a 4-bit scale, 98 bytes. */
+static float dot_iq3_xxs(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 98;
+#if Q38R_MUTANT == 27
+        const float d = q38r_f16_to_f32(read_u16(w)) * b->scale; /* planted: the 1/4 dropped */
+#else
+        const float d = 0.25f * q38r_f16_to_f32(read_u16(w)) * b->scale;
+#endif
+        const uint8_t *indices = w + 2, *metadata = w + 66;
+        int32_t weighted = 0;
+        for (int group = 0; group < 8; ++group) {
+            const uint32_t packed = read_u32(metadata + group * 4);
+            const int32_t scale = 1 + 2 * (int32_t)(packed >> 28);
+            const uint8_t *code = indices + group * 8;
+            int32_t subtotal = 0;
+            for (int section = 0; section < 4; ++section) {
+                const uint32_t g0 = iq3xxs_grid[code[section * 2]], g1 = iq3xxs_grid[code[section * 2 + 1]];
+                const uint8_t signs = ksigns((packed >> (7 * section)) & 127);
+                for (int lane = 0; lane < 4; ++lane) {
+                    const int32_t sign0 = sign_of(signs, 1u << lane);
+                    const int32_t sign1 = sign_of(signs, 1u << (lane + 4));
+                    subtotal += (int32_t)b->quants[group * 32 + section * 8 + lane] * grid32_byte(g0, lane) * sign0;
+                    subtotal += (int32_t)b->quants[group * 32 + section * 8 + lane + 4] * grid32_byte(g1, lane) * sign1;
+                }
+            }
+            weighted += scale * subtotal;
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
+/* dot_iq2_xxs_q8_k, iq.rs:484-512.  Block: d (f16) | 8 groups of 4 grid
+ * indices and a u32 of 4 x 7 sign bits and a 4-bit scale, 66 bytes. */
+static float dot_iq2_xxs(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 66;
+        const float d = iq1_delta * q38r_f16_to_f32(read_u16(w)) * b->scale;
+        const uint8_t *codes = w + 2;
+        int32_t weighted = 0;
+        for (int group = 0; group < 8; ++group) {
+            const uint8_t *code = codes + group * 8;
+            const uint32_t metadata = read_u32(code + 4);
+#if Q38R_MUTANT == 24
+            const int32_t scale = 1 + 2 * (int32_t)((metadata >> 24) & 15); /* planted: wrong nibble */
+#else
+            const int32_t scale = 1 + 2 * (int32_t)(metadata >> 28);
+#endif
+            int32_t subtotal = 0;
+            for (int section = 0; section < 4; ++section) {
+                const uint64_t grid = iq2xxs_grid[code[section]];
+                const uint8_t signs = ksigns((metadata >> (7 * section)) & 127);
+                for (int lane = 0; lane < 8; ++lane)
+                    subtotal += (int32_t)b->quants[group * 32 + section * 8 + lane] * grid64_byte(grid, lane) *
+                                sign_of(signs, 1u << lane);
+            }
+            weighted += scale * subtotal;
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
+/* dot_iq2_xs_q8_k, iq.rs:514-547.  Block: d (f16) | 32 u16 codes (9-bit
+ * grid index, 7 sign bits) | scales[8], 74 bytes. */
+static float dot_iq2_xs(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 74;
+        const float d = iq1_delta * q38r_f16_to_f32(read_u16(w)) * b->scale;
+        const uint8_t *codes = w + 2, *scales = w + 66;
+        int32_t weighted = 0;
+        for (int group = 0; group < 8; ++group) {
+            uint16_t code[4];
+            for (int section = 0; section < 4; ++section) code[section] = read_u16(codes + group * 8 + section * 2);
+#if Q38R_MUTANT == 25
+            const int32_t scale0 = 1 + 2 * (int32_t)(scales[group] >> 4); /* planted: nibbles swapped */
+            const int32_t scale1 = 1 + 2 * (int32_t)(scales[group] & 15);
+#else
+            const int32_t scale0 = 1 + 2 * (int32_t)(scales[group] & 15);
+            const int32_t scale1 = 1 + 2 * (int32_t)(scales[group] >> 4);
+#endif
+            int32_t subtotal[2] = {0, 0};
+            for (int section = 0; section < 4; ++section) {
+                const uint64_t grid = iq2xs_grid[code[section] & 511];
+                const uint8_t signs = ksigns(code[section] >> 9);
+                for (int lane = 0; lane < 8; ++lane)
+                    subtotal[section / 2] += (int32_t)b->quants[group * 32 + section * 8 + lane] *
+                                             grid64_byte(grid, lane) * sign_of(signs, 1u << lane);
+            }
+            weighted += scale0 * subtotal[0] + scale1 * subtotal[1];
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
+/* dot_iq2_s_q8_k, iq.rs:549-578.  Block: d (f16) | qs[32] | signs[32] |
+ * qh[8] | scales[8], 82 bytes. */
+static float dot_iq2_s(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 82;
+        const float d = iq1_delta * q38r_f16_to_f32(read_u16(w)) * b->scale;
+        const uint8_t *indices = w + 2, *signs = w + 34, *high = w + 66, *scales = w + 74;
+        int32_t weighted = 0;
+        for (int group = 0; group < 8; ++group) {
+            const int32_t scale0 = 1 + 2 * (int32_t)(scales[group] & 15);
+            const int32_t scale1 = 1 + 2 * (int32_t)(scales[group] >> 4);
+            int32_t subtotal[2] = {0, 0};
+            for (int lane = 0; lane < 32; ++lane) {
+                const int section = lane / 8;
+#if Q38R_MUTANT == 26
+                const uint32_t index = indices[group * 4 + section] |
+                                       (((uint32_t)high[group] << (2 + 2 * section)) & 0x300); /* planted */
+#else
+                const uint32_t index = indices[group * 4 + section] |
+                                       (((uint32_t)high[group] << (8 - 2 * section)) & 0x300);
+#endif
+                const uint64_t grid = iq2s_grid[index];
+                const int32_t sign = sign_of(signs[group * 4 + section], 1u << (lane % 8));
+                subtotal[section / 2] += (int32_t)b->quants[group * 32 + lane] * grid64_byte(grid, lane % 8) * sign;
+            }
+            weighted += scale0 * subtotal[0] + scale1 * subtotal[1];
+        }
+        total += d * (float)weighted;
+    }
+    return total;
+}
+
+/* dot_iq1_s_q8_k, iq.rs:580-612.  Block: d (f16) | qs[32] | qh u16[8]
+ * (3 index bits per section, a 3-bit scale, the delta's sign), 50 bytes;
+ * grid bytes are signed (-1, 0, 1). */
+static float dot_iq1_s(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 50;
+        const float d = q38r_f16_to_f32(read_u16(w)) * b->scale;
+        const uint8_t *indices = w + 2, *high = w + 34;
+        int32_t weighted = 0, correction = 0;
+        for (int group = 0; group < 8; ++group) {
+            const uint16_t packed = read_u16(high + group * 2);
+            const int32_t scale = 1 + 2 * (int32_t)((packed >> 12) & 7);
+#if Q38R_MUTANT == 29
+            const int32_t delta = (packed & 0x8000) ? 1 : -1; /* planted: delta sign flipped */
+#else
+            const int32_t delta = (packed & 0x8000) ? -1 : 1;
+#endif
+            int32_t subtotal = 0;
+            for (int section = 0; section < 4; ++section) {
+                const uint32_t index = indices[group * 4 + section] | (uint32_t)((packed >> (3 * section)) & 7) << 8;
+                const uint64_t grid = iq1s_grid[index];
+                for (int lane = 0; lane < 8; ++lane)
+                    subtotal += (int32_t)b->quants[group * 32 + section * 8 + lane] *
+                                (int32_t)(int8_t)grid64_byte(grid, lane);
+            }
+            weighted += scale * subtotal;
+            correction += scale * delta * ((int32_t)b->sums[group * 2] + (int32_t)b->sums[group * 2 + 1]);
+        }
+        total += d * ((float)weighted + iq1_delta * (float)correction);
+    }
+    return total;
+}
+
+/* dot_iq1_m_q8_k, iq.rs:614-667.  Block: qs[32] | qh[16] (3 index bits
+ * and a delta sign per section) | scales u16[4] (3-bit scales; the f16 d
+ * in their top nibbles), 56 bytes. */
+static float dot_iq1_m(const uint8_t *data, const q8k_view *q, int blocks) {
+    float total = 0.0f;
+    for (int block = 0; block < blocks; ++block) {
+        const q8k_view *b = &q[block];
+        const uint8_t *w = data + (size_t)block * 56;
+        const uint8_t *indices = w, *high = w + 32, *packed_scales = w + 48;
+        const uint16_t scale_bits = (uint16_t)((read_u16(packed_scales) >> 12) |
+                                               ((read_u16(packed_scales + 2) >> 8) & 0x00f0) |
+                                               ((read_u16(packed_scales + 4) >> 4) & 0x0f00) |
+                                               (read_u16(packed_scales + 6) & 0xf000));
+        const float d = q38r_f16_to_f32(scale_bits) * b->scale;
+        int32_t weighted = 0, correction = 0;
+        for (int group = 0; group < 8; ++group) {
+            int32_t dot[2] = {0, 0}, correction_dot[2] = {0, 0};
+            for (int section = 0; section < 4; ++section) {
+                const uint32_t group_high = high[group * 2 + section / 2];
+                const uint32_t index = indices[group * 4 + section] | ((group_high << (8 - 4 * (section % 2))) & 0x700);
+                const uint64_t grid = iq1s_grid[index];
+#if Q38R_MUTANT == 30
+                const uint32_t delta_bit = 0x08; /* planted: odd sections test the even sections' bit */
+#else
+                const uint32_t delta_bit = section % 2 == 1 ? 0x80 : 0x08;
+#endif
+                const int32_t delta = (group_high & delta_bit) ? -1 : 1;
+                for (int lane = 0; lane < 8; ++lane) {
+                    const int32_t a = b->quants[group * 32 + section * 8 + lane];
+                    dot[section / 2] += a * (int32_t)(int8_t)grid64_byte(grid, lane);
+                    correction_dot[section / 2] += a * delta;
+                }
+            }
+            const uint16_t scales = read_u16(packed_scales + (group / 2) * 2);
+            const int shift = 6 * (group % 2);
+            const int32_t scale0 = 1 + 2 * (int32_t)((scales >> shift) & 7);
+            const int32_t scale1 = 1 + 2 * (int32_t)((scales >> (shift + 3)) & 7);
+            weighted += scale0 * dot[0] + scale1 * dot[1];
+            correction += scale0 * correction_dot[0] + scale1 * correction_dot[1];
+        }
+        total += d * ((float)weighted + iq1_delta * (float)correction);
+    }
+    return total;
+}
+
 int q38r_quant_block_bytes(int ggml_type) {
     switch (ggml_type) {
     case Q38R_GGML_Q2_K: return 84;
@@ -418,6 +706,13 @@ int q38r_quant_block_bytes(int ggml_type) {
     case Q38R_GGML_Q5_K: return 176;
     case Q38R_GGML_Q6_K: return 210;
     case Q38R_GGML_IQ4_XS: return 136;
+    case Q38R_GGML_IQ2_XXS: return 66;
+    case Q38R_GGML_IQ2_XS: return 74;
+    case Q38R_GGML_IQ2_S: return 82;
+    case Q38R_GGML_IQ3_XXS: return 98;
+    case Q38R_GGML_IQ3_S: return 110;
+    case Q38R_GGML_IQ1_S: return 50;
+    case Q38R_GGML_IQ1_M: return 56;
     default: return 0;
     }
 }
@@ -443,6 +738,13 @@ float q38r_dot_q8_k(int ggml_type, const uint8_t *row, const void *planar, int n
     case Q38R_GGML_Q3_K: return dot_q3_k(row, view, blocks);
     case Q38R_GGML_IQ4_NL: return dot_iq4_nl(row, view, blocks);
     case Q38R_GGML_IQ4_XS: return dot_iq4_xs(row, view, blocks);
+    case Q38R_GGML_IQ2_XXS: return dot_iq2_xxs(row, view, blocks);
+    case Q38R_GGML_IQ2_XS: return dot_iq2_xs(row, view, blocks);
+    case Q38R_GGML_IQ2_S: return dot_iq2_s(row, view, blocks);
+    case Q38R_GGML_IQ3_XXS: return dot_iq3_xxs(row, view, blocks);
+    case Q38R_GGML_IQ3_S: return dot_iq3_s(row, view, blocks);
+    case Q38R_GGML_IQ1_S: return dot_iq1_s(row, view, blocks);
+    case Q38R_GGML_IQ1_M: return dot_iq1_m(row, view, blocks);
     default: return NAN;
     }
 }

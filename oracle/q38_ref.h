@@ -109,6 +109,13 @@ void q38r_linear_core(const float *conv_w, const float *dt, const float *a,
 #define Q38R_GGML_Q5_K 13
 #define Q38R_GGML_Q6_K 14
 #define Q38R_GGML_IQ4_XS 23
+#define Q38R_GGML_IQ2_XXS 16
+#define Q38R_GGML_IQ2_XS 17
+#define Q38R_GGML_IQ3_XXS 18
+#define Q38R_GGML_IQ1_S 19
+#define Q38R_GGML_IQ3_S 21
+#define Q38R_GGML_IQ2_S 22
+#define Q38R_GGML_IQ1_M 29
 #define Q38R_GGML_BF16 30
 
 float q38r_f16_to_f32(uint16_t value);                                   /* quant.rs:22-47 */

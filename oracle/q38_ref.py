@@ -187,8 +187,10 @@ def linear_core(conv_w, dt, a, norm_w, conv_state, delta_state, qkv, z, beta, al
 # ------------------------------------------------------- weight projections
 GGML_Q2_K, GGML_Q3_K, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 10, 11, 12, 13, 14
 GGML_IQ4_NL, GGML_IQ4_XS = 20, 23
+GGML_IQ2_XXS, GGML_IQ2_XS, GGML_IQ3_XXS, GGML_IQ1_S, GGML_IQ3_S, GGML_IQ2_S, GGML_IQ1_M = 16, 17, 18, 19, 21, 22, 29
 QUANT_BLOCK_BYTES = {GGML_Q2_K: 84, GGML_Q3_K: 110, GGML_Q4_K: 144, GGML_Q5_K: 176, GGML_Q6_K: 210,
-                     GGML_IQ4_NL: 144, GGML_IQ4_XS: 136}
+                     GGML_IQ4_NL: 144, GGML_IQ4_XS: 136, GGML_IQ2_XXS: 66, GGML_IQ2_XS: 74, GGML_IQ2_S: 82,
+                     GGML_IQ3_XXS: 98, GGML_IQ3_S: 110, GGML_IQ1_S: 50, GGML_IQ1_M: 56}
 # the f32-input path's weight types: (weights per block, bytes per block)
 GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
 F32_PATH_BLOCKS = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_BF16: (1, 2), GGML_Q8_0: (32, 34)}

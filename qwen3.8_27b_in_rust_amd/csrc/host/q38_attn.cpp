@@ -88,6 +88,26 @@ std::string library_dir() {
  * (ops.rs:38-41); their slot is layer/4 (ops.rs:858). */
 bool is_full_attention(int layer) { return layer >= 0 && ((layer + 1) % 4 == 0 || layer == 64); }
 
+/* The weight formats of the Q8_K GEMV (tensor_gemv_q8_k's types,
+ * tensor.rs:70-75): kernel, f32 terms per block in a row's sum, and the
+ * bytes of the lattice grid an IQ kernel copies into LDS. */
+struct GemvType {
+    int ggml_type;
+    const char *kernel;
+    int terms;
+    int grid_bytes;
+};
+constexpr GemvType kGemv[] = {
+    {Q38_GGML_Q4_K, "q38_gemv_q8k_q4k", 1, 0},        {Q38_GGML_Q5_K, "q38_gemv_q8k_q5k", 1, 0},
+    {Q38_GGML_Q6_K, "q38_gemv_q8k_q6k", 1, 0},        {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", 1, 0},
+    {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", 1, 0},    {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", 1, 0},
+    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", 8, 0},    {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", 1, 256 * 8},
+    {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", 1, 512 * 8}, {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", 1, 1024 * 8},
+    {Q38_GGML_IQ3_XXS, "q38_gemv_q8k_iq3xxs", 1, 256 * 4}, {Q38_GGML_IQ3_S, "q38_gemv_q8k_iq3s", 1, 512 * 4},
+    {Q38_GGML_IQ1_S, "q38_gemv_q8k_iq1s", 1, 2048 * 8}, {Q38_GGML_IQ1_M, "q38_gemv_q8k_iq1m", 1, 2048 * 8},
+};
+constexpr int kGemvTypes = (int)(sizeof(kGemv) / sizeof(kGemv[0]));
+
 }  // namespace
 
 struct q38_ctx {
@@ -118,13 +138,7 @@ struct q38_ctx {
     hipModule_t mod_proj = nullptr;
     hipFunction_t f_quantize_q8k = nullptr;
     hipFunction_t f_gemm[3] = {nullptr, nullptr, nullptr}; /* Q4_K, Q5_K, Q6_K on the matrix unit */
-    hipFunction_t f_gemv_q4k = nullptr;
-    hipFunction_t f_gemv_q5k = nullptr;
-    hipFunction_t f_gemv_q6k = nullptr;
-    hipFunction_t f_gemv_q3k = nullptr;
-    hipFunction_t f_gemv_iq4xs = nullptr;
-    hipFunction_t f_gemv_q2k = nullptr;
-    hipFunction_t f_gemv_iq4nl = nullptr;
+    hipFunction_t f_gemv_q8k[kGemvTypes] = {}; /* by kGemv index */
     hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
@@ -141,7 +155,7 @@ struct q38_ctx {
     int clock_khz = 0;
     int lds_bytes = 0;
     int lds_per_cu = 0;
-    int gemv_occupancy[7] = {1, 1, 1, 1, 1, 1, 1}; /* Q4_K Q5_K Q6_K Q3_K IQ4_XS Q2_K IQ4_NL: GEMV workgroups a CU holds */
+    int gemv_occupancy[kGemvTypes] = {}; /* by kGemv index: GEMV workgroups a CU holds */
     char name[256] = {0};
     /* this device's copy of the fixed scratch array (q38_full_core_noalloc) */
     void *scratch = nullptr;
@@ -395,25 +409,16 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     const std::string p_proj = dir + "/proj.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_proj, p_proj.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_quantize_q8k, ctx->mod_proj, "q38_quantize_q8k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q4k, ctx->mod_proj, "q38_gemv_q8k_q4k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q5k, ctx->mod_proj, "q38_gemv_q8k_q5k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q6k, ctx->mod_proj, "q38_gemv_q8k_q6k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q3k, ctx->mod_proj, "q38_gemv_q8k_q3k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_iq4xs, ctx->mod_proj, "q38_gemv_q8k_iq4xs"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q2k, ctx->mod_proj, "q38_gemv_q8k_q2k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_iq4nl, ctx->mod_proj, "q38_gemv_q8k_iq4nl"));
+    for (int i = 0; i < kGemvTypes; ++i)
+        Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q8k[i], ctx->mod_proj, kGemv[i].kernel));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[0], ctx->mod_proj, "q38_gemv_f32_f32"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[1], ctx->mod_proj, "q38_gemv_f32_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[2], ctx->mod_proj, "q38_gemv_f32_bf16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[3], ctx->mod_proj, "q38_gemv_f32_q8_0"));
-    {
-        const hipFunction_t gv[7] = {ctx->f_gemv_q4k, ctx->f_gemv_q5k, ctx->f_gemv_q6k, ctx->f_gemv_q3k,
-                                     ctx->f_gemv_iq4xs, ctx->f_gemv_q2k, ctx->f_gemv_iq4nl};
-        for (int i = 0; i < 7; ++i) {
-            int n = 0;
-            Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, gv[i], 256, 0));
-            ctx->gemv_occupancy[i] = std::max(1, n);
-        }
+    for (int i = 0; i < kGemvTypes; ++i) {
+        int n = 0;
+        Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, ctx->f_gemv_q8k[i], 256, 0));
+        ctx->gemv_occupancy[i] = std::max(1, n);
     }
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[0], ctx->mod_proj, "q38_gemm_q8k_q4k"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[1], ctx->mod_proj, "q38_gemm_q8k_q5k"));
@@ -596,13 +601,6 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemm_q8k_q4k") f = ctx->f_gemm[0];
     else if (name == "q38_gemm_q8k_q5k") f = ctx->f_gemm[1];
     else if (name == "q38_gemm_q8k_q6k") f = ctx->f_gemm[2];
-    else if (name == "q38_gemv_q8k_q4k") f = ctx->f_gemv_q4k;
-    else if (name == "q38_gemv_q8k_q5k") f = ctx->f_gemv_q5k;
-    else if (name == "q38_gemv_q8k_q6k") f = ctx->f_gemv_q6k;
-    else if (name == "q38_gemv_q8k_q3k") f = ctx->f_gemv_q3k;
-    else if (name == "q38_gemv_q8k_iq4xs") f = ctx->f_gemv_iq4xs;
-    else if (name == "q38_gemv_q8k_q2k") f = ctx->f_gemv_q2k;
-    else if (name == "q38_gemv_q8k_iq4nl") f = ctx->f_gemv_iq4nl;
     else if (name == "q38_gemv_f32_f32") f = ctx->f_gemv_f32[0];
     else if (name == "q38_gemv_f32_f16") f = ctx->f_gemv_f32[1];
     else if (name == "q38_gemv_f32_bf16") f = ctx->f_gemv_f32[2];
@@ -613,7 +611,11 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gdn_chunk_prep") f = ctx->f_chunk_prep;
     else if (name == "q38_gdn_chunk_scan") f = ctx->f_chunk_scan;
     else if (name == "q38_gdn_post") f = ctx->f_gdn_post;
-    else return fail("unknown kernel %s", kernel_name);
+    else {
+        for (int i = 0; i < kGemvTypes; ++i)
+            if (name == kGemv[i].kernel) f = ctx->f_gemv_q8k[i];
+        if (f == nullptr) return fail("unknown kernel %s", kernel_name);
+    }
     while ((int)ctx->timer_events.size() < 2 * max_launches) {
         hipEvent_t e;
         Q38_HIP(hipEventCreate(&e));
@@ -1880,21 +1882,19 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
 int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
                         const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out) {
     if (ctx == nullptr) return fail("ctx is NULL");
-    hipFunction_t f = nullptr;
-    int ti_occ = 0; /* index into gemv_occupancy */
-    if (ggml_type == Q38_GGML_Q4_K) f = ctx->f_gemv_q4k, ti_occ = 0;
-    else if (ggml_type == Q38_GGML_Q5_K) f = ctx->f_gemv_q5k, ti_occ = 1;
-    else if (ggml_type == Q38_GGML_Q6_K) f = ctx->f_gemv_q6k, ti_occ = 2;
-    else if (ggml_type == Q38_GGML_Q3_K) f = ctx->f_gemv_q3k, ti_occ = 3;
-    else if (ggml_type == Q38_GGML_IQ4_XS) f = ctx->f_gemv_iq4xs, ti_occ = 4;
-    else if (ggml_type == Q38_GGML_Q2_K) f = ctx->f_gemv_q2k, ti_occ = 5;
-    else if (ggml_type == Q38_GGML_IQ4_NL) f = ctx->f_gemv_iq4nl, ti_occ = 6;
-    else
-        return fail("unsupported quant type %d (Q2_K 10, Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, IQ4_NL 20, IQ4_XS 23; "
+    int ti_occ = -1; /* kGemv index */
+    for (int i = 0; i < kGemvTypes; ++i)
+        if (kGemv[i].ggml_type == ggml_type) ti_occ = i;
+    if (ti_occ < 0)
+        return fail("unsupported quant type %d (Q2_K 10, Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, IQ2_XXS 16, IQ2_XS 17, "
+                    "IQ3_XXS 18, IQ1_S 19, IQ4_NL 20, IQ3_S 21, IQ2_S 22, IQ4_XS 23, IQ1_M 29; "
                     "F32, F16, BF16 and Q8_0 weights take q38_gemv_f32)",
                     ggml_type);
-    /* f32 terms per block in the row sums: IQ4_NL adds one per 32-weight group */
-    const int nt = ggml_type == Q38_GGML_IQ4_NL ? 8 : 1;
+    const hipFunction_t f = ctx->f_gemv_q8k[ti_occ];
+    /* f32 terms per block in the row sums (IQ4_NL adds one per 32-weight
+     * group) and the LDS copy of an IQ format's lattice grid */
+    const int nt = kGemv[ti_occ].terms;
+    const int grid_lds = kGemv[ti_occ].grid_bytes;
     /* the int8 matrix-unit form exists for Q4_K, Q5_K and Q6_K */
     const bool has_gemm = ggml_type == Q38_GGML_Q4_K || ggml_type == Q38_GGML_Q5_K || ggml_type == Q38_GGML_Q6_K;
     if (n_mats < 1 || n_mats > Q38_GEMV_MAX_MATS) return fail("n_mats %d outside 1..%d", n_mats, Q38_GEMV_MAX_MATS);
@@ -1929,7 +1929,8 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     {
         long all_rows = 0;
         for (int i = 0; i < n_mats; ++i) all_rows += std::max(rows[i], 0);
-        const long lds_max = (long)tok_pass * blocks * Q38_GEMV_REC_BYTES + (long)tok_pass * max_units * 4 * nt;
+        const long lds_max =
+            grid_lds + (long)tok_pass * blocks * Q38_GEMV_REC_BYTES + (long)tok_pass * max_units * 4 * nt;
         long occ = ctx->gemv_occupancy[ti_occ];
         if (ctx->lds_per_cu > 0) occ = std::max(1L, std::min(occ, ctx->lds_per_cu / lds_max));
         const long slots = std::max(1L, (long)ctx->cu_count * occ / std::max(1L, tok_groups_all));
@@ -1994,7 +1995,8 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     a.n_tokens = n_tokens;
     a.tok_pass = tok_pass;
     a.tok_groups = (int32_t)tok_groups;
-    const unsigned lds = (unsigned)(tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * max_per_wg * blocks * 4 * nt);
+    const unsigned lds =
+        (unsigned)(grid_lds + tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * max_per_wg * blocks * 4 * nt);
     return ctx->launch(f, (unsigned)grid, 1, 1, 256, &a, lds);
 }
 

@@ -12,6 +12,9 @@
  *   dot_q3_k_q8_k      src/kernel/tensor.rs:335-363 (unpack_q3_scales :34-44)
  *   dot_iq4_nl_q8_k    src/kernel/iq.rs:355-377 (eight per-group terms per block)
  *   dot_iq4_xs_q8_k    src/kernel/iq.rs:379-405 (code book iq_tables.rs:53-56)
+ *   dot_iq2_xxs/_iq2_xs/_iq2_s/_iq3_xxs/_iq3_s/_iq1_s/_iq1_m_q8_k
+ *                      src/kernel/iq.rs:407-667 (lattice grids: ggml's
+ *                      tables, q38_iq_grids.h, copied into LDS)
  *   dot_f32/f16/bf16/q8_0 (f32 input), tensor.rs:79-117, through
  *                      tensor_gemv_f32 / tensor_gemm_f32, tensor.rs:1095-1129,
  *                      :1175-1215
@@ -37,6 +40,7 @@
  * 8 tokens reuse the weights a lane holds (the batched form's token loop).
  */
 #include "q38_device.h"
+#include "../q38_iq_grids.h"
 
 namespace {
 
@@ -84,6 +88,57 @@ template <> struct KQuant<Q38_GGML_Q3_K> { static constexpr int bytes = 110, wor
 template <> struct KQuant<Q38_GGML_IQ4_XS> { static constexpr int bytes = 136, words = 34; };
 template <> struct KQuant<Q38_GGML_Q2_K> { static constexpr int bytes = 84, words = 21; };
 template <> struct KQuant<Q38_GGML_IQ4_NL> { static constexpr int bytes = 144, words = 36; };
+template <> struct KQuant<Q38_GGML_IQ2_XXS> { static constexpr int bytes = 66, words = 17; };
+template <> struct KQuant<Q38_GGML_IQ2_XS> { static constexpr int bytes = 74, words = 19; };
+template <> struct KQuant<Q38_GGML_IQ2_S> { static constexpr int bytes = 82, words = 21; };
+template <> struct KQuant<Q38_GGML_IQ3_XXS> { static constexpr int bytes = 98, words = 25; };
+template <> struct KQuant<Q38_GGML_IQ3_S> { static constexpr int bytes = 110, words = 28; };
+template <> struct KQuant<Q38_GGML_IQ1_S> { static constexpr int bytes = 50, words = 13; };
+template <> struct KQuant<Q38_GGML_IQ1_M> { static constexpr int bytes = 56, words = 14; };
+
+/* The IQ lattice grids (format data) and the bytes a workgroup copies into
+ * LDS: 8-byte entries (IQ2, IQ1: 8 weights) or 4-byte ones (IQ3: 4). */
+__device__ __attribute__((aligned(16))) const uint64_t kIq2xxsGrid[256] = Q38_IQ2XXS_GRID;
+__device__ __attribute__((aligned(16))) const uint64_t kIq2xsGrid[512] = Q38_IQ2XS_GRID;
+__device__ __attribute__((aligned(16))) const uint64_t kIq2sGrid[1024] = Q38_IQ2S_GRID;
+__device__ __attribute__((aligned(16))) const uint32_t kIq3xxsGrid[256] = Q38_IQ3XXS_GRID;
+__device__ __attribute__((aligned(16))) const uint32_t kIq3sGrid[512] = Q38_IQ3S_GRID;
+__device__ __attribute__((aligned(16))) const uint64_t kIq1sGrid[2048] = Q38_IQ1S_GRID;
+template <int TYPE> struct IqGrid { static constexpr int bytes = 0; };
+template <> struct IqGrid<Q38_GGML_IQ2_XXS> { static constexpr int bytes = sizeof(kIq2xxsGrid); };
+template <> struct IqGrid<Q38_GGML_IQ2_XS> { static constexpr int bytes = sizeof(kIq2xsGrid); };
+template <> struct IqGrid<Q38_GGML_IQ2_S> { static constexpr int bytes = sizeof(kIq2sGrid); };
+template <> struct IqGrid<Q38_GGML_IQ3_XXS> { static constexpr int bytes = sizeof(kIq3xxsGrid); };
+template <> struct IqGrid<Q38_GGML_IQ3_S> { static constexpr int bytes = sizeof(kIq3sGrid); };
+template <> struct IqGrid<Q38_GGML_IQ1_S> { static constexpr int bytes = sizeof(kIq1sGrid); };
+template <> struct IqGrid<Q38_GGML_IQ1_M> { static constexpr int bytes = sizeof(kIq1sGrid); };
+template <int TYPE> Q38_DEV const void *iq_grid_table() {
+    if (TYPE == Q38_GGML_IQ2_XXS) return kIq2xxsGrid;
+    if (TYPE == Q38_GGML_IQ2_XS) return kIq2xsGrid;
+    if (TYPE == Q38_GGML_IQ2_S) return kIq2sGrid;
+    if (TYPE == Q38_GGML_IQ3_XXS) return kIq3xxsGrid;
+    if (TYPE == Q38_GGML_IQ3_S) return kIq3sGrid;
+    return kIq1sGrid;
+}
+
+/* Bytes of a block held as little-endian words from its start (the indices
+ * are constants once the loops over groups and sections are unrolled). */
+Q38_DEV uint32_t wbyte(const uint32_t *w, int b) { return (w[b >> 2] >> (8 * (b & 3))) & 255u; }
+Q38_DEV uint32_t whalf(const uint32_t *w, int b) { return (w[b >> 2] >> (8 * (b & 3))) & 0xffffu; } /* b even */
+Q38_DEV uint32_t wword(const uint32_t *w, int b) {                                                  /* b even */
+    return (b & 3) ? (w[b >> 2] >> 16) | (w[(b >> 2) + 1] << 16) : w[b >> 2];
+}
+
+/* ksigns_iq2xs[i]: the 7 stored sign bits and an eighth that makes the
+ * count of minus signs even */
+Q38_DEV uint32_t iq_ksigns(uint32_t i) { return i | ((uint32_t)(__builtin_popcount(i) & 1) << 7); }
+
+/* The 4 grid bytes of x (each 1..127) negated where bit j of m (j < 4) is
+ * set: (x ^ 0xFF) + 1 per byte, no carry since no byte is 0. */
+Q38_DEV uint32_t iq_signed4(uint32_t x, uint32_t m) {
+    const uint32_t t = ((m & 15u) * 0x00204081u) & 0x01010101u;
+    return (x ^ (t * 0xFFu)) + t;
+}
 
 /* f32 terms a block adds to its row's total, in order: one (d * weighted
  * [- dmin * minimum]) for the K-quants and IQ4_XS, one per 32-weight group
@@ -118,9 +173,63 @@ template <int TYPE> struct Unit {
  * read as 52 dwords from the dword boundary at or below the start (16-byte
  * reads need dword alignment only) plus the halfword at 206, and shifted into
  * place; the scale is its own halfword.  Every byte read lies in the block. */
+/* IQ blocks of S bytes, S = 2 (mod 4), start 2-byte aligned: the block as
+ * (S + 2) / 4 words from its start.  (S - 2) / 4 whole words are read from
+ * the dword boundary at or below the start, then the block's last bytes --
+ * the halfword that ends it when the start is dword aligned, else the
+ * dword that ends it -- and the window is shifted into place.  Every byte
+ * read lies in the block or, for a start 2 bytes past a dword boundary, in
+ * the 2 bytes before it (block 0 starts dword aligned). */
+template <int S>
+Q38_DEV void load_block_2aligned(const uint8_t *weights, size_t g, uint32_t *w) {
+    constexpr int n = (S - 2) / 4;
+    const size_t s = g * S;
+    const uint32_t o = (uint32_t)(s & 3); /* 0 or 2 */
+    const uint32_t *base = reinterpret_cast<const uint32_t *>(weights + (s - o));
+    uint32_t win[n + 2];
+#pragma unroll
+    for (int i = 0; i < n / 4; ++i) {
+        u32x4 v;
+        __builtin_memcpy(&v, base + 4 * i, 16);
+        win[4 * i] = v.x;
+        win[4 * i + 1] = v.y;
+        win[4 * i + 2] = v.z;
+        win[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = (n / 4) * 4; i < n; ++i) win[i] = base[i];
+    const uint32_t tail_dword = base[o ? n : n - 1]; /* o == 0: an inner word, not used */
+    const uint32_t tail_half = *reinterpret_cast<const uint16_t *>(weights + s + S - 2);
+    win[n] = o ? tail_dword : tail_half;
+    win[n + 1] = 0;
+#pragma unroll
+    for (int j = 0; j <= n; ++j) w[j] = __builtin_amdgcn_alignbyte(win[j + 1], win[j], o);
+}
+
 template <int TYPE>
 Q38_DEV void load_unit(const uint8_t *weights, size_t g, Unit<TYPE> &u) {
-    if (TYPE == Q38_GGML_Q3_K) {
+    if constexpr (TYPE == Q38_GGML_IQ2_XXS || TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S ||
+                  TYPE == Q38_GGML_IQ3_XXS || TYPE == Q38_GGML_IQ3_S || TYPE == Q38_GGML_IQ1_S) {
+        static_assert(KQuant<TYPE>::bytes % 4 == 2 && KQuant<TYPE>::words == (KQuant<TYPE>::bytes + 2) / 4,
+                      "a 2-byte aligned IQ block");
+        load_block_2aligned<KQuant<TYPE>::bytes>(weights, g, u.w);
+        u.dh = 0;
+    } else if constexpr (TYPE == Q38_GGML_IQ1_M) {
+        /* 56-byte blocks start 8-byte aligned */
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(weights + g * KQuant<TYPE>::bytes);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            u32x4 v;
+            __builtin_memcpy(&v, p + 4 * i, 16);
+            u.w[4 * i] = v.x;
+            u.w[4 * i + 1] = v.y;
+            u.w[4 * i + 2] = v.z;
+            u.w[4 * i + 3] = v.w;
+        }
+        u.w[12] = p[12];
+        u.w[13] = p[13];
+        u.dh = 0;
+    } else if (TYPE == Q38_GGML_Q3_K) {
         /* 110-byte blocks start 2-byte aligned: the 108 bytes before the
          * scale are read as 27 dwords from the dword boundary at or below
          * the start plus the halfword at 106, and shifted into place; the
@@ -218,7 +327,58 @@ template <int TYPE> struct UnitScales {
 
 template <int TYPE>
 Q38_DEV void unit_scales(const Unit<TYPE> &u, UnitScales<TYPE> &s) {
-    if (TYPE == Q38_GGML_Q3_K) {
+    s.dmin = 0.0f;
+    if constexpr (TYPE == Q38_GGML_IQ2_XXS) {
+        /* group g: 4 grid indices at 2 + 8g, then a word of 4 x 7 sign bits
+         * and the scale in bits 28-31; d = IQ1_DELTA * d (iq.rs:489) */
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s.sc[g] = 1 + 2 * (int)(wword(u.w, 6 + 8 * g) >> 28);
+        s.d = 0.125f * q38_f16(u.w[0]);
+    } else if constexpr (TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S) {
+        /* one scale byte per group (sections 0-1: low nibble, 2-3: high) */
+        constexpr int at = TYPE == Q38_GGML_IQ2_XS ? 66 : 74;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const uint32_t b = wbyte(u.w, at + g);
+            s.sc[2 * g] = 1 + 2 * (int)(b & 15u);
+            s.sc[2 * g + 1] = 1 + 2 * (int)(b >> 4);
+        }
+        s.d = 0.125f * q38_f16(u.w[0]);
+    } else if constexpr (TYPE == Q38_GGML_IQ3_XXS) {
+        /* group g's word at 66 + 4g: 4 x 7 sign bits, the scale in 28-31;
+         * d = 0.25 * d (iq.rs:453) */
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s.sc[g] = 1 + 2 * (int)(wword(u.w, 66 + 4 * g) >> 28);
+        s.d = 0.25f * q38_f16(u.w[0]);
+    } else if constexpr (TYPE == Q38_GGML_IQ3_S) {
+        /* group g: nibble g % 2 of scale byte 106 + g / 2 */
+#pragma unroll
+        for (int g = 0; g < 8; ++g) s.sc[g] = 1 + 2 * (int)((wbyte(u.w, 106 + g / 2) >> (4 * (g % 2))) & 15u);
+        s.d = q38_f16(u.w[0]);
+    } else if constexpr (TYPE == Q38_GGML_IQ1_S) {
+        /* group g's halfword at 34 + 2g: 3 index bits per section, the
+         * scale in bits 12-14, the delta's sign in bit 15 */
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const uint32_t qh = whalf(u.w, 34 + 2 * g);
+            s.sc[g] = 1 + 2 * (int)((qh >> 12) & 7u);
+            s.mn[g] = (qh & 0x8000u) ? -1 : 1;
+        }
+        s.d = q38_f16(u.w[0]);
+    } else if constexpr (TYPE == Q38_GGML_IQ1_M) {
+        /* 3-bit scales in the halfwords at 48..55 (group g: halfword g / 2,
+         * bits 6 (g % 2) .. +5); d is their four top nibbles */
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const uint32_t sc = whalf(u.w, 48 + 2 * (g / 2));
+            const int shift = 6 * (g % 2);
+            s.sc[2 * g] = 1 + 2 * (int)((sc >> shift) & 7u);
+            s.sc[2 * g + 1] = 1 + 2 * (int)((sc >> (shift + 3)) & 7u);
+        }
+        const uint32_t bits = (whalf(u.w, 48) >> 12) | ((whalf(u.w, 50) >> 8) & 0x00f0u) |
+                              ((whalf(u.w, 52) >> 4) & 0x0f00u) | (whalf(u.w, 54) & 0xf000u);
+        s.d = q38_f16(bits);
+    } else if (TYPE == Q38_GGML_Q3_K) {
         /* unpack_q3_scales: low nibble from byte i (i < 8) or the high
          * nibble of byte i - 8, high 2 bits from byte 8 + i % 4 at 2 (i / 4);
          * the 12 scale bytes are block bytes 96..107, words 24..26 */
@@ -271,8 +431,95 @@ Q38_DEV void unit_scales(const Unit<TYPE> &u, UnitScales<TYPE> &s) {
  * minimum (Q6_K: d * weighted). */
 template <int TYPE>
 Q38_DEV float unit_term(const Unit<TYPE> &u, const UnitScales<TYPE> &s, const uint8_t *rec, const int16_t *gsums,
-                        float a_scale) {
+                        float a_scale, const uint8_t *grid) {
     const u32x4 *aq = reinterpret_cast<const u32x4 *>(rec);
+    /* 4 activations 4j .. 4j+3 */
+    auto a4 = [&](int j) { return aq[j >> 2][j & 3]; };
+    auto grid8 = [&](uint32_t idx) { return *reinterpret_cast<const uint2 *>(grid + 8 * idx); };
+    auto grid4 = [&](uint32_t idx) { return *reinterpret_cast<const uint32_t *>(grid + 4 * idx); };
+    if constexpr (TYPE == Q38_GGML_IQ2_XXS || TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S ||
+                  TYPE == Q38_GGML_IQ3_XXS || TYPE == Q38_GGML_IQ3_S) {
+        /* dot_iq2_xxs / _iq2_xs / _iq2_s / _iq3_xxs / _iq3_s_q8_k (iq.rs:407-578):
+         * section s of group g is values 32g + 8s .. +7, grid bytes with
+         * the section's 8 signs against the activations; the scale weights
+         * a group (IQ2_XS, IQ2_S: a pair of sections) */
+        int weighted = 0;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            int sub[2] = {0, 0};
+#pragma unroll
+            for (int sec = 0; sec < 4; ++sec) {
+                uint32_t lo, hi, signs;
+                if constexpr (TYPE == Q38_GGML_IQ2_XXS) {
+                    const uint2 e = grid8(wbyte(u.w, 2 + 8 * g + sec));
+                    lo = e.x, hi = e.y;
+                    signs = iq_ksigns((wword(u.w, 6 + 8 * g) >> (7 * sec)) & 127u);
+                } else if constexpr (TYPE == Q38_GGML_IQ2_XS) {
+                    const uint32_t code = whalf(u.w, 2 + 8 * g + 2 * sec);
+                    const uint2 e = grid8(code & 511u);
+                    lo = e.x, hi = e.y;
+                    signs = iq_ksigns(code >> 9);
+                } else if constexpr (TYPE == Q38_GGML_IQ2_S) {
+                    const uint32_t idx = wbyte(u.w, 2 + 4 * g + sec) | ((wbyte(u.w, 66 + g) << (8 - 2 * sec)) & 0x300u);
+                    const uint2 e = grid8(idx);
+                    lo = e.x, hi = e.y;
+                    signs = wbyte(u.w, 34 + 4 * g + sec);
+                } else if constexpr (TYPE == Q38_GGML_IQ3_XXS) {
+                    lo = grid4(wbyte(u.w, 2 + 8 * g + 2 * sec));
+                    hi = grid4(wbyte(u.w, 3 + 8 * g + 2 * sec));
+                    signs = iq_ksigns((wword(u.w, 66 + 4 * g) >> (7 * sec)) & 127u);
+                } else {
+                    const uint32_t qh = wbyte(u.w, 66 + g);
+                    lo = grid4(wbyte(u.w, 2 + 8 * g + 2 * sec) | ((qh << (8 - 2 * sec)) & 0x100u));
+                    hi = grid4(wbyte(u.w, 3 + 8 * g + 2 * sec) | ((qh << (7 - 2 * sec)) & 0x100u));
+                    signs = wbyte(u.w, 74 + 4 * g + sec);
+                }
+                int t = q38_sdot4(iq_signed4(lo, signs), a4(8 * g + 2 * sec), 0);
+                t = q38_sdot4(iq_signed4(hi, signs >> 4), a4(8 * g + 2 * sec + 1), t);
+                sub[sec / 2] += t;
+            }
+            if constexpr (TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S)
+                weighted += s.sc[2 * g] * sub[0] + s.sc[2 * g + 1] * sub[1];
+            else
+                weighted += s.sc[g] * (sub[0] + sub[1]);
+        }
+        return s.d * a_scale * (float)weighted;
+    }
+    if constexpr (TYPE == Q38_GGML_IQ1_S || TYPE == Q38_GGML_IQ1_M) {
+        /* dot_iq1_s_q8_k / dot_iq1_m_q8_k (iq.rs:580-667): signed grid bytes
+         * (-1, 0, 1) plus a delta of +-1/8 per group (IQ1_S, through the
+         * activations' group sums) or per section (IQ1_M) */
+        int weighted = 0, correction = 0;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            int dot[2] = {0, 0}, cdot[2] = {0, 0};
+#pragma unroll
+            for (int sec = 0; sec < 4; ++sec) {
+                uint32_t idx;
+                int delta = 1;
+                if constexpr (TYPE == Q38_GGML_IQ1_S) {
+                    idx = wbyte(u.w, 2 + 4 * g + sec) | (((whalf(u.w, 34 + 2 * g) >> (3 * sec)) & 7u) << 8);
+                } else {
+                    const uint32_t hb = wbyte(u.w, 32 + 2 * g + sec / 2);
+                    idx = wbyte(u.w, 4 * g + sec) | ((hb << (sec % 2 ? 4 : 8)) & 0x700u);
+                    delta = (hb & (sec % 2 ? 0x80u : 0x08u)) ? -1 : 1;
+                }
+                const uint2 e = grid8(idx);
+                const uint32_t a0 = a4(8 * g + 2 * sec), a1 = a4(8 * g + 2 * sec + 1);
+                dot[sec / 2] += q38_sdot4(e.y, a1, q38_sdot4(e.x, a0, 0));
+                if constexpr (TYPE == Q38_GGML_IQ1_M)
+                    cdot[sec / 2] += delta * q38_sdot4(0x01010101u, a1, q38_sdot4(0x01010101u, a0, 0));
+            }
+            if constexpr (TYPE == Q38_GGML_IQ1_S) {
+                weighted += s.sc[g] * (dot[0] + dot[1]);
+                correction += s.sc[g] * s.mn[g] * ((int)gsums[2 * g] + (int)gsums[2 * g + 1]);
+            } else {
+                weighted += s.sc[2 * g] * dot[0] + s.sc[2 * g + 1] * dot[1];
+                correction += s.sc[2 * g] * cdot[0] + s.sc[2 * g + 1] * cdot[1];
+            }
+        }
+        return s.d * a_scale * ((float)weighted + 0.125f * (float)correction);
+    }
     const u32x4 bs4[2] = {reinterpret_cast<const u32x4 *>(gsums)[0], reinterpret_cast<const u32x4 *>(gsums)[1]};
     int bsum[16];
 #pragma unroll
@@ -478,8 +725,15 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     const int tok0 = pass * a.tok_pass;
     const int tp = min(a.tok_pass, a.n_tokens - tok0);
     const int nrec = a.tok_pass * B;
-    uint8_t *recs = lds;                                                     /* [tp][B] x kRec */
-    int16_t *lsums = reinterpret_cast<int16_t *>(lds + (size_t)nrec * kRec); /* [tp][B][16] */
+    /* an IQ format's lattice grid first, then the staged activations */
+    constexpr int kGridBytes = IqGrid<TYPE>::bytes;
+    uint8_t *grid = lds;
+    if (kGridBytes > 0) {
+        const u32x4 *src = static_cast<const u32x4 *>(iq_grid_table<TYPE>());
+        for (int i = tid; i < kGridBytes / 16; i += 256) reinterpret_cast<u32x4 *>(grid)[i] = src[i];
+    }
+    uint8_t *recs = lds + kGridBytes;                                        /* [tp][B] x kRec */
+    int16_t *lsums = reinterpret_cast<int16_t *>(recs + (size_t)nrec * kRec); /* [tp][B][16] */
     float *lscales = reinterpret_cast<float *>(lsums + (size_t)nrec * 16);   /* [tp][B] */
     constexpr int NT = BlockTerms<TYPE>::n;
     float *terms = lscales + nrec;                                           /* [tp][units][NT] */
@@ -536,7 +790,8 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
             for (int t = 0; t < tp; ++t) {
                 const int r = t * B + b;
                 if constexpr (NT == 1)
-                    terms[t * units + u] = unit_term<TYPE>(w[k & 1], s, recs + r * kRec, lsums + r * 16, lscales[r]);
+                    terms[t * units + u] =
+                        unit_term<TYPE>(w[k & 1], s, recs + r * kRec, lsums + r * 16, lscales[r], grid);
                 else
                     unit_terms_iq4nl(w[k & 1], s, recs + r * kRec, lscales[r], terms + ((size_t)t * units + u) * NT);
             }
@@ -846,6 +1101,17 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q2k(q38_gemv_args
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4nl(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ4_NL>(a);
 }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq2xxs(q38_gemv_args a) {
+    gemv_q8k<Q38_GGML_IQ2_XXS>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq2xs(q38_gemv_args a) { gemv_q8k<Q38_GGML_IQ2_XS>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq2s(q38_gemv_args a) { gemv_q8k<Q38_GGML_IQ2_S>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq3xxs(q38_gemv_args a) {
+    gemv_q8k<Q38_GGML_IQ3_XXS>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq3s(q38_gemv_args a) { gemv_q8k<Q38_GGML_IQ3_S>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq1s(q38_gemv_args a) { gemv_q8k<Q38_GGML_IQ1_S>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq1m(q38_gemv_args a) { gemv_q8k<Q38_GGML_IQ1_M>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4xs(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ4_XS>(a);
 }

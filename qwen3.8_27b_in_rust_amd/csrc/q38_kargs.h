@@ -296,6 +296,13 @@ typedef struct {
 #define Q38_GGML_Q5_K 13
 #define Q38_GGML_Q6_K 14
 #define Q38_GGML_IQ4_XS 23
+#define Q38_GGML_IQ2_XXS 16
+#define Q38_GGML_IQ2_XS 17
+#define Q38_GGML_IQ3_XXS 18
+#define Q38_GGML_IQ1_S 19
+#define Q38_GGML_IQ3_S 21
+#define Q38_GGML_IQ2_S 22
+#define Q38_GGML_IQ1_M 29
 #define Q38_GGML_BF16 30
 #define Q38_GEMV_TOKENS 8 /* most tokens one GEMV workgroup serves per pass over its weights */
 #define Q38_GEMV_MAX_BLOCKS 192 /* 256-wide blocks per row (width 49152): one token's blocks fit LDS */

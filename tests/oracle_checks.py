@@ -325,6 +325,10 @@ def _f16(b0, b1):
     return np.frombuffer(np.array([b0, b1], np.uint8).tobytes(), np.float16)[0].astype(np.float64)
 
 
+def _f16_bits(h):
+    return np.array([h], np.uint16).view(np.float16)[0].astype(np.float64)
+
+
 def _scale_min(s, j):
     if j < 4:
         return s[j] & 63, s[j + 4] & 63
@@ -333,6 +337,32 @@ def _scale_min(s, j):
 
 # ggml's published IQ4_NL / IQ4_XS code book
 _KVALUES_IQ4 = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int64)
+
+
+_GRIDS_H = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "qwen3.8_27b_in_rust_amd",
+                        "csrc", "q38_iq_grids.h")
+_GRID_BYTES = {"Q38_IQ2XXS_GRID": 8, "Q38_IQ2XS_GRID": 8, "Q38_IQ2S_GRID": 8, "Q38_IQ3XXS_GRID": 4,
+               "Q38_IQ3S_GRID": 4, "Q38_IQ1S_GRID": 8}
+
+
+def _iq_grids():
+    """The IQ lattice grids of q38_iq_grids.h as byte arrays [entries][4 or 8]."""
+    import re
+    text = open(_GRIDS_H).read()
+    out = {}
+    for name, nb in _GRID_BYTES.items():
+        body = re.search(r"#define %s \{(.*?)\}" % name, text, re.S).group(1)
+        vals = np.array([int(v, 16) for v in re.findall(r"0x[0-9a-f]+", body)], np.uint64)
+        out[name] = np.frombuffer(vals.astype("<u8").tobytes(), np.uint8).reshape(-1, 8)[:, :nb].astype(np.int64)
+    return out
+
+
+def _ksign_mask(i):
+    """ggml's ksigns_iq2xs entry i as 8 signs: the 7 stored bits and an eighth
+    that makes the number of minus signs even."""
+    bits = [(i >> j) & 1 for j in range(7)]
+    bits.append(sum(bits) & 1)
+    return np.where(np.array(bits) == 1, -1, 1)
 
 
 def _q3k_scales(sc12):
@@ -346,13 +376,87 @@ def _q3k_scales(sc12):
     return np.frombuffer(np.array(words, np.uint32).tobytes(), np.int8).astype(np.int64) - 32
 
 
+_BLOCK_BYTES = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 144, 23: 136, 16: 66, 17: 74, 22: 82, 18: 98,
+                21: 110, 19: 50, 29: 56}
+
+
+def _dequant_iq(ty, blk, grids):
+    """ggml's dequantize_row_iq2_xxs / _iq2_xs / _iq2_s / _iq3_xxs / _iq3_s /
+    _iq1_s / _iq1_m for one 256-value block (float64)."""
+    w = np.zeros(256)
+    u16 = lambda o: int(blk[o]) | (int(blk[o + 1]) << 8)
+    u32 = lambda o: u16(o) | (u16(o + 2) << 16)
+    if ty == 29:  # IQ1_M: qs[32] | qh[16] | scales u16[4], d in their top nibbles
+        sc = [u16(48 + 2 * k) for k in range(4)]
+        d = _f16_bits((sc[0] >> 12) | ((sc[1] >> 8) & 0x00F0) | ((sc[2] >> 4) & 0x0F00) | (sc[3] & 0xF000))
+    else:
+        d = _f16(blk[0], blk[1])
+    for ib in range(8):
+        y = w[32 * ib:32 * ib + 32]
+        if ty == 16:  # IQ2_XXS
+            aux = u32(2 + 8 * ib + 4)
+            db = d * (0.5 + (aux >> 28)) * 0.25
+            for l in range(4):
+                y[8 * l:8 * l + 8] = db * grids["Q38_IQ2XXS_GRID"][blk[2 + 8 * ib + l]] * _ksign_mask((aux >> (7 * l)) & 127)
+        elif ty == 17:  # IQ2_XS
+            sc = blk[66 + ib]
+            for l in range(4):
+                q = u16(2 + 8 * ib + 2 * l)
+                db = d * (0.5 + ((sc >> (4 * (l // 2))) & 15)) * 0.25
+                y[8 * l:8 * l + 8] = db * grids["Q38_IQ2XS_GRID"][q & 511] * _ksign_mask(q >> 9)
+        elif ty == 22:  # IQ2_S: qs[32] | signs[32] | qh[8] | scales[8]
+            sc, qh = blk[74 + ib], blk[66 + ib]
+            for l in range(4):
+                db = d * (0.5 + ((sc >> (4 * (l // 2))) & 15)) * 0.25
+                idx = blk[2 + 4 * ib + l] | ((qh << (8 - 2 * l)) & 0x300)
+                signs = np.where((blk[34 + 4 * ib + l] >> np.arange(8)) & 1, -1, 1)
+                y[8 * l:8 * l + 8] = db * grids["Q38_IQ2S_GRID"][idx] * signs
+        elif ty == 18:  # IQ3_XXS: qs[64] | scales-and-signs u32[8]
+            aux = u32(66 + 4 * ib)
+            db = d * (0.5 + (aux >> 28)) * 0.5
+            for l in range(4):
+                s8 = _ksign_mask((aux >> (7 * l)) & 127)
+                y[8 * l:8 * l + 4] = db * grids["Q38_IQ3XXS_GRID"][blk[2 + 8 * ib + 2 * l]] * s8[:4]
+                y[8 * l + 4:8 * l + 8] = db * grids["Q38_IQ3XXS_GRID"][blk[2 + 8 * ib + 2 * l + 1]] * s8[4:]
+        elif ty == 21:  # IQ3_S: qs[64] | qh[8] | signs[32] | scales[4]
+            db = d * (1 + 2 * ((blk[106 + ib // 2] >> (4 * (ib % 2))) & 15))
+            qh = blk[66 + ib]
+            for l in range(4):
+                signs = np.where((blk[74 + 4 * ib + l] >> np.arange(8)) & 1, -1, 1)
+                g1 = grids["Q38_IQ3S_GRID"][blk[2 + 8 * ib + 2 * l] | ((qh << (8 - 2 * l)) & 256)]
+                g2 = grids["Q38_IQ3S_GRID"][blk[2 + 8 * ib + 2 * l + 1] | ((qh << (7 - 2 * l)) & 256)]
+                y[8 * l:8 * l + 4] = db * g1 * signs[:4]
+                y[8 * l + 4:8 * l + 8] = db * g2 * signs[4:]
+        elif ty == 19:  # IQ1_S: qs[32] | qh u16[8]
+            qh = u16(34 + 2 * ib)
+            dl = d * (2 * ((qh >> 12) & 7) + 1)
+            delta = -0.125 if qh & 0x8000 else 0.125
+            for l in range(4):
+                g = grids["Q38_IQ1S_GRID"][blk[2 + 4 * ib + l] | (((qh >> (3 * l)) & 7) << 8)]
+                y[8 * l:8 * l + 8] = dl * (np.where(g > 127, g - 256, g) + delta)
+        else:  # IQ1_M
+            sc = u16(48 + 2 * (ib // 2))
+            dl = [d * (2 * ((sc >> (6 * (ib % 2) + 3 * h)) & 7) + 1) for h in range(2)]
+            qh = [blk[32 + 2 * ib], blk[32 + 2 * ib + 1]]
+            for l in range(4):
+                hb = qh[l // 2]
+                idx = blk[4 * ib + l] | ((hb << (8 if l % 2 == 0 else 4)) & 0x700)
+                delta = -0.125 if hb & (0x08 if l % 2 == 0 else 0x80) else 0.125
+                g = grids["Q38_IQ1S_GRID"][idx]
+                y[8 * l:8 * l + 8] = dl[l // 2] * (np.where(g > 127, g - 256, g) + delta)
+    return w
+
+
 def _dequant_row(ty, row):
     """A weight row's values the way the decoded path reads them."""
     out = []
-    bb = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 144, 23: 136}[ty]
+    bb = _BLOCK_BYTES[ty]
+    grids = _iq_grids() if ty in (16, 17, 18, 19, 21, 22, 29) else None
     for blk in np.asarray(row, np.uint8).reshape(-1, bb).astype(np.int64):
         w = np.zeros(256)
-        if ty == 10:
+        if grids is not None:
+            w = _dequant_iq(ty, blk, grids)
+        elif ty == 10:
             # ggml's dequantize_row_q2_K: per 128 values, four 2-bit shifts,
             # each 32 values as two 16-value groups with scale d * (sc & 15)
             # and minimum dmin * (sc >> 4)
@@ -423,7 +527,7 @@ def _dequant_row(ty, row):
 def _random_kquant(ty, rows, width, seed):
     """Weight rows of random bytes with finite, moderate f16 scales."""
     rng = np.random.default_rng(seed)
-    bb = {10: 84, 11: 110, 12: 144, 13: 176, 14: 210, 20: 144, 23: 136}[ty]
+    bb = _BLOCK_BYTES[ty]
     w = rng.integers(0, 256, (rows, width // 256, bb), dtype=np.uint8)
     f16 = lambda lo, hi, n: np.frombuffer(rng.uniform(lo, hi, n).astype(np.float16).tobytes(), np.uint8).reshape(n, 2)
     n = rows * (width // 256)
@@ -440,6 +544,13 @@ def _random_kquant(ty, rows, width, seed):
     elif ty == 20:
         for g in range(8):
             w.reshape(n, bb)[:, 18 * g:18 * g + 2] = f16(1e-4, 4e-3, n)
+    elif ty == 29:
+        # IQ1_M: the f16 d is the top nibbles of the four scale halfwords
+        h = np.frombuffer(f16(1e-3, 4e-2, n).tobytes(), np.uint16)
+        blk = w.reshape(n, bb)
+        for k in range(4):
+            nib = ((h >> (4 * k)) & 15).astype(np.uint8)
+            blk[:, 49 + 2 * k] = (blk[:, 49 + 2 * k] & 0x0F) | (nib << 4)
     else:
         w.reshape(n, bb)[:, 0:2] = f16(1e-4, 4e-3, n)
     return w.reshape(rows, -1)
@@ -483,7 +594,8 @@ def check_kquant_dots_against_dequantised_rows(ref, synth):
     p = ref.quantize_q8_k(x)
     a = _q8k_dequant(p, T, W, ref).reshape(T, W)
     for ty in (ref.GGML_Q2_K, ref.GGML_Q3_K, ref.GGML_Q4_K, ref.GGML_Q5_K, ref.GGML_Q6_K, ref.GGML_IQ4_NL,
-               ref.GGML_IQ4_XS):
+               ref.GGML_IQ4_XS, ref.GGML_IQ2_XXS, ref.GGML_IQ2_XS, ref.GGML_IQ2_S, ref.GGML_IQ3_XXS, ref.GGML_IQ3_S,
+               ref.GGML_IQ1_S, ref.GGML_IQ1_M):
         wb = _random_kquant(ty, 7, W, 0x51333872 + ty)
         got = ref.gemv_q8_k(ty, wb, p, T, W)
         for r in range(7):

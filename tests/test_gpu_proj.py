@@ -1,7 +1,8 @@
 """The weight projections on the GPU (q38_quantize_q8_k, q38_gemv_q8_k,
 q38_gemv_f32) against the oracle's restatement of quantize_q8_k
-(src/kernel/quant.rs:55-128), of the scalar Q3_K..Q6_K x Q8_K row dots
-(src/kernel/tensor.rs:301-457) and the IQ4_NL / IQ4_XS ones (src/kernel/iq.rs:355-405)
+(src/kernel/quant.rs:55-128), of the scalar Q2_K..Q6_K x Q8_K row dots
+(src/kernel/tensor.rs:301-457) and the IQ ones -- IQ4_NL, IQ4_XS, IQ3_S,
+IQ3_XXS, IQ2_XXS, IQ2_XS, IQ2_S, IQ1_S, IQ1_M (src/kernel/iq.rs:355-667)
 driven per row as tensor_gemv_q8_k / tensor_gemm_q8_k do
 (tensor.rs:1131-1173, :1217-1270), and of the f32-input row dots of
 tensor_gemv_f32 (tensor.rs:79-117, :1095-1129).  The integer parts and the
@@ -15,7 +16,8 @@ from parity import check_attn
 
 pytestmark = pytest.mark.gpu
 
-TYPES = {"Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23}
+TYPES = {"Q2_K": 10, "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_NL": 20, "IQ4_XS": 23,
+         "IQ2_XXS": 16, "IQ2_XS": 17, "IQ2_S": 22, "IQ3_XXS": 18, "IQ3_S": 21, "IQ1_S": 19, "IQ1_M": 29}
 F32_TYPES = {"F32": 0, "F16": 1, "BF16": 30, "Q8_0": 8}
 HIDDEN = 5120
 
@@ -84,7 +86,12 @@ def test_gemv_q8_k_subnormal_scales_and_widest_rows(ctx, ref, name):
         off = {14: 208, 11: 108, 10: 80}.get(ty, 0)  # the block's (first) f16 scale
         sub = np.array([0x0001, 0x03ff, 0x8200, 0x0000, 0x8000], np.uint16)
         for i in range(0, blocks.shape[0], 3):
-            blocks[i, off:off + 2] = np.frombuffer(sub[i % 5].tobytes(), np.uint8)
+            if ty == 29:  # IQ1_M: the f16 is the top nibbles of the halfwords at 48, 50, 52, 54
+                for k in range(4):
+                    nib = (int(sub[i % 5]) >> (4 * k)) & 15
+                    blocks[i, 49 + 2 * k] = (blocks[i, 49 + 2 * k] & 0x0F) | (nib << 4)
+            else:
+                blocks[i, off:off + 2] = np.frombuffer(sub[i % 5].tobytes(), np.uint8)
         if ty in (12, 13):  # dmin
             blocks[1::4, 2:4] = np.frombuffer(np.uint16(0x0155).tobytes(), np.uint8)
         d_w = ctx.array(wb, np.uint8)

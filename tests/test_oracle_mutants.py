@@ -33,6 +33,13 @@ MUTANTS = {
     21: "BF16 row dot reading neighbouring elements swapped",
     22: "Q2_K minimum from the scale nibble",
     23: "IQ4_NL low and high nibbles swapped",
+    24: "IQ2_XXS group scale from the wrong nibble",
+    25: "IQ2_XS the two scale nibbles of a group swapped",
+    26: "IQ2_S high index bits of section s taken from the wrong pair",
+    27: "IQ3_XXS without the 1/4 in d",
+    28: "IQ3_S second index's high bit taken from the first index's bit",
+    29: "IQ1_S delta sign flipped",
+    30: "IQ1_M odd sections test the even sections' delta bit",
 }
 
 
@@ -40,7 +47,7 @@ MUTANTS = {
 def test_mutant_is_rejected(mutant, ref, synth, tmp_path):
     so = tmp_path / f"libq38ref_m{mutant}.so"
     subprocess.run(["gcc", "-O2", "-mfma", "-ffp-contract=off", "-fPIC", "-shared", f"-DQ38R_MUTANT={mutant}",
-                    "-o", str(so), os.path.join(ROOT, "oracle", "q38_ref.c"),
+                    "-I", os.path.join(ROOT, "qwen3.8_27b_in_rust_amd", "csrc"), "-o", str(so), os.path.join(ROOT, "oracle", "q38_ref.c"),
                     os.path.join(ROOT, "oracle", "q38_quant_ref.c"), "-lm", "-lpthread"], check=True)
     prev = ref.use_library(str(so))
     try:
