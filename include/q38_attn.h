@@ -340,15 +340,16 @@ int q38_q8k_bytes(int n_tokens, int width, size_t *bytes);
 int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, void *d_q8k);
 
 /* tensor_gemv_q8_k / tensor_gemm_q8_k (src/kernel/tensor.rs:1131-1173,
- * :1217-1270) for Q2_K (ggml type 10), Q3_K (11), Q4_K (12), Q5_K (13),
- * Q6_K (14), IQ4_NL (20) and IQ4_XS (23) weights: d_weights [rows][width/256
- * blocks] in the GGUF block layout (84, 110, 144, 176, 210, 8 x 18, 136
- * bytes per 256 weights, 16-byte aligned base), d_q8k from
- * q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
+ * :1217-1270) for every weight type the reference projects on this path:
+ * Q2_K (ggml type 10), Q3_K (11), Q4_K (12), Q5_K (13), Q6_K (14), IQ2_XXS
+ * (16), IQ2_XS (17), IQ3_XXS (18), IQ1_S (19), IQ4_NL (20), IQ3_S (21),
+ * IQ2_S (22), IQ4_XS (23) and IQ1_M (29): d_weights [rows][width/256
+ * blocks] in the GGUF block layout (84, 110, 144, 176, 210, 66, 74, 98, 50,
+ * 8 x 18, 110, 82, 136, 56 bytes per 256 weights, 16-byte aligned base),
+ * d_q8k from q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
  * reference's batched form writes it).  width is at most 49152.  Each
  * element equals the reference's scalar dot_q*_k_q8_k (tensor.rs:301-457)
- * or dot_iq4_nl_q8_k / dot_iq4_xs_q8_k (src/kernel/iq.rs:355-405) bit for
- * bit.  For Q4_K, Q5_K
+ * or dot_iq*_q8_k (src/kernel/iq.rs:355-667) bit for bit.  For Q4_K, Q5_K
  * and Q6_K from 32 tokens (16 for matrices of 8192 rows or more) the
  * integer dots run on the int8 matrix unit; the result is the same bit for
  * bit.  Other weight types fail with -1 (the reference's f32 path below, or
