@@ -27,8 +27,10 @@ prompt (with its conv/L2/gates and gated-norm kernels), prefill attention at
 context, batched paged decode,
 the launch floor, one-token linear_core over 48 layers, the 64-layer full
 stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
-the Q4_K/Q6_K FFN projections for 1 and 8 tokens, and the recurrent-state
-checkpoint, each rotating over enough buffers to defeat the cache.
+the Q4_K/Q6_K FFN projections for 1 and 8 tokens and for prompts, one token
+and a 4096-token prompt through one matrix in every weight format, and the
+recurrent-state checkpoint, each rotating over enough buffers to defeat the
+cache where the weights are streamed.
 """
 from __future__ import annotations
 
@@ -761,6 +763,39 @@ def weight_formats(pkg, ctx, reps: int):
     return res
 
 
+def weight_formats_prompt(pkg, ctx, n_tokens: int, reps: int):
+    """A prompt of n_tokens tokens through a 17408 x 5120 matrix in every Q8_K
+    weight format: the int8 matrix-unit form (IQ4_NL: 8-token GEMV passes),
+    kernel duration and useful int8 operations per second.  Weights are random
+    bytes (timing only)."""
+    rows, width = 17408, 5120
+    x = ctx.empty((n_tokens, width))
+    ctx.fill_normal(x, n_tokens * width, 0x51335300)
+    q = ctx.empty((ctx.q8k_bytes(n_tokens, width),), np.uint8)
+    ctx.quantize_q8_k(n_tokens, width, x, q)
+    out = ctx.empty((n_tokens, rows))
+    res = {}
+    for ty in (12, 13, 14, 10, 11, 23, 20, 16, 17, 22, 18, 21, 19, 29):
+        nbytes = rows * (width // 256) * QUANT_BLOCK_BYTES[ty]
+        w = ctx.empty((nbytes,), np.uint8)
+        ctx.fill_normal(w, nbytes // 4, 0x51335310 + ty)
+        ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
+        ctx.sync()
+        kern = GEMV_KERNELS[ty] if ty == 20 else GEMV_KERNELS[ty].replace("gemv", "gemm")
+        ctx.kernel_timer_start(kern, reps)
+        for _ in range(reps):
+            ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
+        k_ms, k_n = ctx.kernel_timer_stop()
+        ms = k_ms / max(k_n, 1)
+        tops = 2.0 * rows * width * n_tokens / (ms * 1e-3) / 1e12
+        res[FORMAT_NAMES[ty]] = {"kernel": kern, "ms": round(ms, 3), "int8_tops": round(tops, 1),
+                                 "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+        w.free()
+    for a in (x, q, out):
+        a.free()
+    return res
+
+
 INT8_PEAK_TOPS = 5000.0
 GEMM_KERNELS = {12: "q38_gemm_q8k_q4k", 13: "q38_gemm_q8k_q5k", 14: "q38_gemm_q8k_q6k"}
 
@@ -891,6 +926,8 @@ EXTRAS = {
                           lambda pkg, ctx: ffn_projections(pkg, ctx, 8, 20)),
     "weight_formats_1": ("one token through a 17408x5120 matrix in each Q8_K weight format",
                          lambda pkg, ctx: weight_formats(pkg, ctx, 3)),
+    "weight_formats_prompt_4096": ("a 4096-token prompt through a 17408x5120 matrix in each Q8_K weight format",
+                                   lambda pkg, ctx: weight_formats_prompt(pkg, ctx, 4096, 2)),
 }
 
 

@@ -89,22 +89,33 @@ std::string library_dir() {
 bool is_full_attention(int layer) { return layer >= 0 && ((layer + 1) % 4 == 0 || layer == 64); }
 
 /* The weight formats of the Q8_K GEMV (tensor_gemv_q8_k's types,
- * tensor.rs:70-75): kernel, f32 terms per block in a row's sum, and the
- * bytes of the lattice grid an IQ kernel copies into LDS. */
+ * tensor.rs:70-75): the GEMV kernel, its many-token form on the int8
+ * matrix unit (none for IQ4_NL, whose eight per-group f32 terms per block
+ * would be read out of the matrix unit group by group: prompts run as
+ * 8-token GEMV passes), f32 terms per block in a row's sum, and the bytes of
+ * the lattice grid an IQ kernel copies into LDS. */
 struct GemvType {
     int ggml_type;
     const char *kernel;
+    const char *gemm_kernel;
     int terms;
     int grid_bytes;
 };
 constexpr GemvType kGemv[] = {
-    {Q38_GGML_Q4_K, "q38_gemv_q8k_q4k", 1, 0},        {Q38_GGML_Q5_K, "q38_gemv_q8k_q5k", 1, 0},
-    {Q38_GGML_Q6_K, "q38_gemv_q8k_q6k", 1, 0},        {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", 1, 0},
-    {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", 1, 0},    {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", 1, 0},
-    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", 8, 0},    {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", 1, 256 * 8},
-    {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", 1, 512 * 8}, {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", 1, 1024 * 8},
-    {Q38_GGML_IQ3_XXS, "q38_gemv_q8k_iq3xxs", 1, 256 * 4}, {Q38_GGML_IQ3_S, "q38_gemv_q8k_iq3s", 1, 512 * 4},
-    {Q38_GGML_IQ1_S, "q38_gemv_q8k_iq1s", 1, 2048 * 8}, {Q38_GGML_IQ1_M, "q38_gemv_q8k_iq1m", 1, 2048 * 8},
+    {Q38_GGML_Q4_K, "q38_gemv_q8k_q4k", "q38_gemm_q8k_q4k", 1, 0},
+    {Q38_GGML_Q5_K, "q38_gemv_q8k_q5k", "q38_gemm_q8k_q5k", 1, 0},
+    {Q38_GGML_Q6_K, "q38_gemv_q8k_q6k", "q38_gemm_q8k_q6k", 1, 0},
+    {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", "q38_gemm_q8k_q3k", 1, 0},
+    {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", "q38_gemm_q8k_iq4xs", 1, 0},
+    {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", "q38_gemm_q8k_q2k", 1, 0},
+    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", nullptr, 8, 0},
+    {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", "q38_gemm_q8k_iq2xxs", 1, 256 * 8},
+    {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", "q38_gemm_q8k_iq2xs", 1, 512 * 8},
+    {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", "q38_gemm_q8k_iq2s", 1, 1024 * 8},
+    {Q38_GGML_IQ3_XXS, "q38_gemv_q8k_iq3xxs", "q38_gemm_q8k_iq3xxs", 1, 256 * 4},
+    {Q38_GGML_IQ3_S, "q38_gemv_q8k_iq3s", "q38_gemm_q8k_iq3s", 1, 512 * 4},
+    {Q38_GGML_IQ1_S, "q38_gemv_q8k_iq1s", "q38_gemm_q8k_iq1s", 1, 2048 * 8},
+    {Q38_GGML_IQ1_M, "q38_gemv_q8k_iq1m", "q38_gemm_q8k_iq1m", 1, 2048 * 8},
 };
 constexpr int kGemvTypes = (int)(sizeof(kGemv) / sizeof(kGemv[0]));
 
@@ -137,7 +148,7 @@ struct q38_ctx {
     hipFunction_t f_gdn_step_rows = nullptr;
     hipModule_t mod_proj = nullptr;
     hipFunction_t f_quantize_q8k = nullptr;
-    hipFunction_t f_gemm[3] = {nullptr, nullptr, nullptr}; /* Q4_K, Q5_K, Q6_K on the matrix unit */
+    hipFunction_t f_gemm[kGemvTypes] = {}; /* by kGemv index: the int8 matrix-unit form */
     hipFunction_t f_gemv_q8k[kGemvTypes] = {}; /* by kGemv index */
     hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
     hipModule_t mod_synth = nullptr;
@@ -420,9 +431,9 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
         Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, ctx->f_gemv_q8k[i], 256, 0));
         ctx->gemv_occupancy[i] = std::max(1, n);
     }
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[0], ctx->mod_proj, "q38_gemm_q8k_q4k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[1], ctx->mod_proj, "q38_gemm_q8k_q5k"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[2], ctx->mod_proj, "q38_gemm_q8k_q6k"));
+    for (int i = 0; i < kGemvTypes; ++i)
+        if (kGemv[i].gemm_kernel != nullptr)
+            Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[i], ctx->mod_proj, kGemv[i].gemm_kernel));
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
@@ -598,9 +609,6 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_copy_f32") f = ctx->f_copy;
     else if (name == "q38_noop") f = ctx->f_noop;
     else if (name == "q38_quantize_q8k") f = ctx->f_quantize_q8k;
-    else if (name == "q38_gemm_q8k_q4k") f = ctx->f_gemm[0];
-    else if (name == "q38_gemm_q8k_q5k") f = ctx->f_gemm[1];
-    else if (name == "q38_gemm_q8k_q6k") f = ctx->f_gemm[2];
     else if (name == "q38_gemv_f32_f32") f = ctx->f_gemv_f32[0];
     else if (name == "q38_gemv_f32_f16") f = ctx->f_gemv_f32[1];
     else if (name == "q38_gemv_f32_bf16") f = ctx->f_gemv_f32[2];
@@ -612,8 +620,10 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gdn_chunk_scan") f = ctx->f_chunk_scan;
     else if (name == "q38_gdn_post") f = ctx->f_gdn_post;
     else {
-        for (int i = 0; i < kGemvTypes; ++i)
+        for (int i = 0; i < kGemvTypes; ++i) {
             if (name == kGemv[i].kernel) f = ctx->f_gemv_q8k[i];
+            if (kGemv[i].gemm_kernel != nullptr && name == kGemv[i].gemm_kernel) f = ctx->f_gemm[i];
+        }
         if (f == nullptr) return fail("unknown kernel %s", kernel_name);
     }
     while ((int)ctx->timer_events.size() < 2 * max_launches) {
@@ -1895,8 +1905,8 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
      * group) and the LDS copy of an IQ format's lattice grid */
     const int nt = kGemv[ti_occ].terms;
     const int grid_lds = kGemv[ti_occ].grid_bytes;
-    /* the int8 matrix-unit form exists for Q4_K, Q5_K and Q6_K */
-    const bool has_gemm = ggml_type == Q38_GGML_Q4_K || ggml_type == Q38_GGML_Q5_K || ggml_type == Q38_GGML_Q6_K;
+    /* the int8 matrix-unit form (every format but IQ4_NL) */
+    const bool has_gemm = ctx->f_gemm[ti_occ] != nullptr;
     if (n_mats < 1 || n_mats > Q38_GEMV_MAX_MATS) return fail("n_mats %d outside 1..%d", n_mats, Q38_GEMV_MAX_MATS);
     if (rows == nullptr || d_weights == nullptr || d_out == nullptr) return fail("NULL argument");
     if (n_tokens < 0) return fail("negative n_tokens");
@@ -1965,7 +1975,7 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     for (int i = 1; i < kept; ++i) min_rows = std::min<long>(min_rows, a.rows[i]); /* non-empty matrices */
     if (has_gemm && (n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
                      (n_tokens >= Q38_GEMM_MIN_TOKENS && min_rows >= 64L * Q38_GEMM_ROWS))) {
-        const int ti = ggml_type == Q38_GGML_Q4_K ? 0 : ggml_type == Q38_GGML_Q5_K ? 1 : 2;
+        const int ti = ti_occ;
         const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
         if (tok_tiles > 65535) return fail("too many tokens");
         for (int i = 0; i < kept; ++i) {

@@ -825,7 +825,14 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
  *    planes w = 128 hi + lo (hi signed, lo in 0..127); two MFMAs per step
  *    accumulate over the block and weighted = 128 C_hi + C_lo;
  *  - Q4_K / Q5_K's minimum term sum_j m_j bsum_j is a third MFMA, of the
- *    activations against m_j splatted over its sub-block (sum_i m_j(i) a_i).
+ *    activations against m_j splatted over its sub-block (sum_i m_j(i) a_i);
+ *  - the other formats take the same form (gemm_step_bytes): Q3_K w = sc
+ *    (q - 4) and Q2_K w = sc q per 16-value group with Q2_K's minimum as the
+ *    third MFMA; IQ4_XS the code book's values biased by 128; the lattice
+ *    formats their grid bytes (from LDS) with signs, biased by 64 (IQ2, IQ3)
+ *    or 1 (IQ1), IQ1's delta correction as the third MFMA against scale x
+ *    delta.  IQ4_NL, whose eight groups each end in their own f32 term, has
+ *    no matrix-unit form (read out group by group it spills registers).
  * Every integer is exact; the f32 block term and the row total follow the
  * reference's operation order, so the result equals q38_gemv_q8_k's (and
  * the reference's) bit for bit.
@@ -866,11 +873,151 @@ Q38_DEV void split_weights(uint32_t q, int sc, short off, uint32_t &hi, uint32_t
     lo = le | (lo_ << 8);
 }
 
+/* Formats whose block term has a second integer sum over the activations:
+ * a minimum (Q2_K, Q4_K, Q5_K) or the IQ1 delta correction. */
+template <int TYPE> constexpr bool kGemmSecond =
+    TYPE == Q38_GGML_Q2_K || TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K || TYPE == Q38_GGML_IQ1_S ||
+    TYPE == Q38_GGML_IQ1_M;
+
+/* Grid bytes g (1..62) with their signs (bit j of m set: byte j negative),
+ * biased by 64: every byte 64 +- g, no carry or borrow between bytes. */
+Q38_DEV uint32_t iq_biased4(uint32_t g, uint32_t m) {
+    const uint32_t t = ((m & 15u) * 0x00204081u) & 0x01010101u;
+    const uint32_t neg = t * 0xFFu;
+    return (0x40404040u + (g & ~neg)) - (g & neg);
+}
+
+/* The lane's 16 weights of k step st (values 32 st + 16 h .. + 15 of the
+ * block) for the formats beyond Q4_K..Q6_K, as unsigned bytes q with the
+ * scale sc and offset off of w = sc (q - off), and (kGemmSecond) the bytes
+ * the activations meet in the second sum.  h picks between values computed
+ * for both halves, so no register index depends on the lane. */
+template <int TYPE>
+Q38_DEV void gemm_step_bytes(const Unit<TYPE> &u, const UnitScales<TYPE> &s, int st, int h, const uint8_t *grid,
+                             uint32_t (&q)[4], int &sc, short &off, uint32_t (&second)[4]) {
+    auto sel = [&](uint32_t a0, uint32_t a1) { return h ? a1 : a0; };
+    auto grid8 = [&](uint32_t idx) { return *reinterpret_cast<const uint2 *>(grid + 8 * idx); };
+    auto grid4 = [&](uint32_t idx) { return *reinterpret_cast<const uint32_t *>(grid + 4 * idx); };
+#pragma unroll
+    for (int j = 0; j < 4; ++j) second[j] = 0;
+    if constexpr (TYPE == Q38_GGML_Q3_K || TYPE == Q38_GGML_Q2_K) {
+        /* the step is 2 bits at shift 2 (st % 4) of the quant bytes of half
+         * st / 4, one 16-value group (2 st + h) per lane half; Q3_K adds the
+         * high bit from hmask bit st (value q + 4 hbit - 4) */
+        const int n = st >> 2, sh = 2 * (st & 3);
+        const int sg = h ? s.sc[2 * st + 1] : s.sc[2 * st]; /* group 2 st + h */
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (TYPE == Q38_GGML_Q3_K) {
+                const uint32_t qs = sel(u.w[8 + 8 * n + j], u.w[12 + 8 * n + j]);
+                const uint32_t hm = sel(u.w[j], u.w[4 + j]);
+                q[j] = ((qs >> sh) & 0x03030303u) | (((hm >> st) & 0x01010101u) << 2);
+            } else {
+                const uint32_t qs = sel(u.w[4 + 8 * n + j], u.w[8 + 8 * n + j]);
+                q[j] = (qs >> sh) & 0x03030303u;
+                second[j] = (uint32_t)(sg >> 4) * 0x01010101u;
+            }
+        }
+        sc = TYPE == Q38_GGML_Q3_K ? sg : (sg & 15);
+        off = TYPE == Q38_GGML_Q3_K ? (short)4 : (short)0;
+    } else if constexpr (TYPE == Q38_GGML_IQ4_XS) {
+        /* group st's 16 quant bytes: low nibbles are values 0..15, high
+         * nibbles 16..31; the code book's int8 values biased by 128 */
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t b = u.w[2 + 4 * st + j];
+            q[j] = q38_iq4_lookup(sel(b, b >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u;
+        }
+        sc = s.sc[st];
+        off = 128;
+    } else if constexpr (TYPE == Q38_GGML_IQ1_S || TYPE == Q38_GGML_IQ1_M) {
+        /* sections 2h and 2h + 1 of group st: signed grid bytes (-1, 0, 1)
+         * biased by 1; the second sum's bytes are scale x delta */
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            uint32_t idx0, idx1;
+            int d0 = 1, d1 = 1;
+            if constexpr (TYPE == Q38_GGML_IQ1_S) {
+                const uint32_t qh = whalf(u.w, 34 + 2 * st);
+                idx0 = wbyte(u.w, 2 + 4 * st + k) | (((qh >> (3 * k)) & 7u) << 8);
+                idx1 = wbyte(u.w, 2 + 4 * st + 2 + k) | (((qh >> (3 * (2 + k))) & 7u) << 8);
+            } else {
+                const uint32_t hb0 = wbyte(u.w, 32 + 2 * st), hb1 = wbyte(u.w, 33 + 2 * st);
+                idx0 = wbyte(u.w, 4 * st + k) | ((hb0 << (k ? 4 : 8)) & 0x700u);
+                idx1 = wbyte(u.w, 4 * st + 2 + k) | ((hb1 << (k ? 4 : 8)) & 0x700u);
+                d0 = (hb0 & (k ? 0x80u : 0x08u)) ? -1 : 1;
+                d1 = (hb1 & (k ? 0x80u : 0x08u)) ? -1 : 1;
+            }
+            const uint2 e = grid8(sel(idx0, idx1));
+            q[2 * k] = ((e.x ^ 0x80808080u) + 0x01010101u) ^ 0x80808080u;
+            q[2 * k + 1] = ((e.y ^ 0x80808080u) + 0x01010101u) ^ 0x80808080u;
+            const int scale = TYPE == Q38_GGML_IQ1_S ? s.sc[st] : (h ? s.sc[2 * st + 1] : s.sc[2 * st]);
+            const int delta = TYPE == Q38_GGML_IQ1_S ? s.mn[st] : (h ? d1 : d0);
+            const uint32_t m = (uint32_t)(uint8_t)(int8_t)(scale * delta) * 0x01010101u;
+            second[2 * k] = m;
+            second[2 * k + 1] = m;
+        }
+        sc = TYPE == Q38_GGML_IQ1_S ? s.sc[st] : (h ? s.sc[2 * st + 1] : s.sc[2 * st]);
+        off = 1;
+    } else {
+        /* IQ2 / IQ3: sections 2h and 2h + 1 of group st, grid bytes with
+         * their signs, biased by 64 */
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int sa = k, sb = 2 + k; /* the section for h = 0 and for h = 1 */
+            uint32_t lo, hi;
+            if constexpr (TYPE == Q38_GGML_IQ2_XXS) {
+                const uint32_t meta = wword(u.w, 6 + 8 * st);
+                const uint2 e = grid8(sel(wbyte(u.w, 2 + 8 * st + sa), wbyte(u.w, 2 + 8 * st + sb)));
+                const uint32_t sg = iq_ksigns(sel((meta >> (7 * sa)) & 127u, (meta >> (7 * sb)) & 127u));
+                lo = iq_biased4(e.x, sg), hi = iq_biased4(e.y, sg >> 4);
+            } else if constexpr (TYPE == Q38_GGML_IQ2_XS) {
+                const uint32_t code = sel(whalf(u.w, 2 + 8 * st + 2 * sa), whalf(u.w, 2 + 8 * st + 2 * sb));
+                const uint2 e = grid8(code & 511u);
+                const uint32_t sg = iq_ksigns(code >> 9);
+                lo = iq_biased4(e.x, sg), hi = iq_biased4(e.y, sg >> 4);
+            } else if constexpr (TYPE == Q38_GGML_IQ2_S) {
+                const uint32_t qh = wbyte(u.w, 66 + st);
+                const uint32_t i0 = wbyte(u.w, 2 + 4 * st + sa) | ((qh << (8 - 2 * sa)) & 0x300u);
+                const uint32_t i1 = wbyte(u.w, 2 + 4 * st + sb) | ((qh << (8 - 2 * sb)) & 0x300u);
+                const uint2 e = grid8(sel(i0, i1));
+                const uint32_t sg = sel(wbyte(u.w, 34 + 4 * st + sa), wbyte(u.w, 34 + 4 * st + sb));
+                lo = iq_biased4(e.x, sg), hi = iq_biased4(e.y, sg >> 4);
+            } else if constexpr (TYPE == Q38_GGML_IQ3_XXS) {
+                const uint32_t meta = wword(u.w, 66 + 4 * st);
+                const uint32_t g0 = grid4(sel(wbyte(u.w, 2 + 8 * st + 2 * sa), wbyte(u.w, 2 + 8 * st + 2 * sb)));
+                const uint32_t g1 = grid4(sel(wbyte(u.w, 3 + 8 * st + 2 * sa), wbyte(u.w, 3 + 8 * st + 2 * sb)));
+                const uint32_t sg = iq_ksigns(sel((meta >> (7 * sa)) & 127u, (meta >> (7 * sb)) & 127u));
+                lo = iq_biased4(g0, sg), hi = iq_biased4(g1, sg >> 4);
+            } else {
+                const uint32_t qh = wbyte(u.w, 66 + st);
+                const uint32_t a0 = wbyte(u.w, 2 + 8 * st + 2 * sa) | ((qh << (8 - 2 * sa)) & 0x100u);
+                const uint32_t a1 = wbyte(u.w, 3 + 8 * st + 2 * sa) | ((qh << (7 - 2 * sa)) & 0x100u);
+                const uint32_t b0 = wbyte(u.w, 2 + 8 * st + 2 * sb) | ((qh << (8 - 2 * sb)) & 0x100u);
+                const uint32_t b1 = wbyte(u.w, 3 + 8 * st + 2 * sb) | ((qh << (7 - 2 * sb)) & 0x100u);
+                const uint32_t sg = sel(wbyte(u.w, 74 + 4 * st + sa), wbyte(u.w, 74 + 4 * st + sb));
+                lo = iq_biased4(grid4(sel(a0, b0)), sg), hi = iq_biased4(grid4(sel(a1, b1)), sg >> 4);
+            }
+            q[2 * k] = lo;
+            q[2 * k + 1] = hi;
+        }
+        sc = (TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S) ? (h ? s.sc[2 * st + 1] : s.sc[2 * st]) : s.sc[st];
+        off = 64;
+    }
+}
+
 template <int TYPE>
 Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
     __shared__ __align__(16) int8_t act[2][kGemmTokens][kActRow];
     __shared__ float ascale[2][kGemmTokens];
+    /* an IQ format's lattice grid (the others keep 16 unused bytes) */
+    constexpr int kGridBytes = IqGrid<TYPE>::bytes;
+    __shared__ __align__(16) uint8_t grid[kGridBytes > 0 ? kGridBytes : 16];
     const int tid = threadIdx.x;
+    if constexpr (kGridBytes > 0) {
+        const u32x4 *src = static_cast<const u32x4 *>(iq_grid_table<TYPE>());
+        for (int i = tid; i < kGridBytes / 16; i += 256) reinterpret_cast<u32x4 *>(grid)[i] = src[i];
+    }
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5;
@@ -943,39 +1090,51 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
         for (int tt = 0; tt < kGemmTiles; ++tt) lsum[tt] = i32x16{};
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
-            i32x4 bh, bl;
-            int sc;
-            if (TYPE == Q38_GGML_Q6_K) sc = h ? s.sc[2 * st + 1] : s.sc[2 * st];
-            else sc = s.sc[st];
+            i32x4 bh, bl, bm;
+            if constexpr (TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K || TYPE == Q38_GGML_Q6_K) {
+                int sc;
+                if (TYPE == Q38_GGML_Q6_K) sc = h ? s.sc[2 * st + 1] : s.sc[2 * st];
+                else sc = s.sc[st];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t q;
-                if (TYPE == Q38_GGML_Q6_K) {
-                    const int hf = st >> 2, kq = st & 3;
-                    const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
-                    const uint32_t qh = word(32 + 8 * hf + j);
-                    q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
-                } else {
-                    const int c = st >> 1, nib = st & 1;
-                    const uint32_t qs = TYPE == Q38_GGML_Q4_K ? word(4 + 8 * c + j) : word(12 + 8 * c + j);
-                    q = (qs >> (4 * nib)) & 0x0F0F0F0Fu;
-                    if (TYPE == Q38_GGML_Q5_K) q |= ((word(4 + j) >> st) & 0x01010101u) << 4;
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t q;
+                    if (TYPE == Q38_GGML_Q6_K) {
+                        const int hf = st >> 2, kq = st & 3;
+                        const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
+                        const uint32_t qh = word(32 + 8 * hf + j);
+                        q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
+                    } else {
+                        const int c = st >> 1, nib = st & 1;
+                        const uint32_t qs = TYPE == Q38_GGML_Q4_K ? word(4 + 8 * c + j) : word(12 + 8 * c + j);
+                        q = (qs >> (4 * nib)) & 0x0F0F0F0Fu;
+                        if (TYPE == Q38_GGML_Q5_K) q |= ((word(4 + j) >> st) & 0x01010101u) << 4;
+                    }
+                    uint32_t hi, lo;
+                    split_weights(q, sc, TYPE == Q38_GGML_Q6_K ? (short)32 : (short)0, hi, lo);
+                    bh[j] = (int)hi;
+                    bl[j] = (int)lo;
+                    bm[j] = s.mn[st] * 0x01010101;
                 }
-                uint32_t hi, lo;
-                split_weights(q, sc, TYPE == Q38_GGML_Q6_K ? (short)32 : (short)0, hi, lo);
-                bh[j] = (int)hi;
-                bl[j] = (int)lo;
+            } else {
+                uint32_t q[4], second[4];
+                int sc;
+                short off;
+                gemm_step_bytes<TYPE>(u, s, st, h, grid, q, sc, off, second);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t hi, lo;
+                    split_weights(q[j], sc, off, hi, lo);
+                    bh[j] = (int)hi;
+                    bl[j] = (int)lo;
+                    bm[j] = (int)second[j];
+                }
             }
 #pragma unroll
             for (int tt = 0; tt < kGemmTiles; ++tt) {
                 const i32x4 A = *reinterpret_cast<const i32x4 *>(arow[tt] + 32 * st);
                 wsum[tt] = mfma_i8(A, bh, wsum[tt]);
                 lsum[tt] = mfma_i8(A, bl, lsum[tt]);
-                if (TYPE != Q38_GGML_Q6_K) {
-                    const int m4 = s.mn[st] * 0x01010101;
-                    const i32x4 bm = {m4, m4, m4, m4};
-                    msum[tt] = mfma_i8(A, bm, msum[tt]);
-                }
+                if constexpr (kGemmSecond<TYPE>) msum[tt] = mfma_i8(A, bm, msum[tt]);
             }
         }
 #pragma unroll
@@ -990,11 +1149,13 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
                 const float as = ascale[buf][tok];
                 const float d = s.d * as;
                 float term;
-                if (TYPE == Q38_GGML_Q6_K) {
-                    term = d * (float)wsum[tt][e];
-                } else {
+                if constexpr (TYPE == Q38_GGML_Q2_K || TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K) {
                     const float dmin = s.dmin * as;
                     term = d * (float)wsum[tt][e] - dmin * (float)msum[tt][e];
+                } else if constexpr (TYPE == Q38_GGML_IQ1_S || TYPE == Q38_GGML_IQ1_M) {
+                    term = d * ((float)wsum[tt][e] + 0.125f * (float)msum[tt][e]);
+                } else {
+                    term = d * (float)wsum[tt][e];
                 }
                 /* a step past the last block repeats it and adds nothing */
                 total[tt][e] = real ? total[tt][e] + term : total[tt][e];
@@ -1126,6 +1287,20 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4xs(q38_gemv_ar
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q4k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q5k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q5_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q6k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q6_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q2k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q2_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q3k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q3_K>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq4xs(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ4_XS>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2xxs(q38_gemv_args a) {
+    gemm_q8k<Q38_GGML_IQ2_XXS>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2xs(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ2_XS>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2s(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ2_S>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq3xxs(q38_gemv_args a) {
+    gemm_q8k<Q38_GGML_IQ3_XXS>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq3s(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ3_S>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq1s(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ1_S>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq1m(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ1_M>(a); }
 
 /*
  * Projections of f32 activations by F32, F16, BF16 or Q8_0 weights (the
