@@ -482,6 +482,11 @@ Q38_DEV float unit_term(const Unit<TYPE> &u, const UnitScales<TYPE> &s, const ui
                 weighted += s.sc[2 * g] * sub[0] + s.sc[2 * g + 1] * sub[1];
             else
                 weighted += s.sc[g] * (sub[0] + sub[1]);
+            /* IQ2: one group's grid loads at a time (215-226 registers, two
+             * waves per SIMD); scheduled freely the unrolled groups' loads
+             * need 260 registers, and capped at 256 they spill (6% slower) */
+            if constexpr (TYPE == Q38_GGML_IQ2_XXS || TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S)
+                __builtin_amdgcn_sched_barrier(0);
         }
         return s.d * a_scale * (float)weighted;
     }
@@ -1262,19 +1267,11 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q2k(q38_gemv_args
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4nl(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ4_NL>(a);
 }
-/* The IQ2 kernels are held to two waves per SIMD (256 registers, a few
- * bytes spilled): left alone they take 260 and run one wave per SIMD, 1.55x
- * slower on a 17408 x 5120 matrix (23.4 against 14.9 us for IQ2_XXS). */
-#define Q38_IQ2_OCCUPANCY __attribute__((amdgpu_waves_per_eu(2)))
-extern "C" __global__ __launch_bounds__(256) Q38_IQ2_OCCUPANCY void q38_gemv_q8k_iq2xxs(q38_gemv_args a) {
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq2xxs(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ2_XXS>(a);
 }
-extern "C" __global__ __launch_bounds__(256) Q38_IQ2_OCCUPANCY void q38_gemv_q8k_iq2xs(q38_gemv_args a) {
-    gemv_q8k<Q38_GGML_IQ2_XS>(a);
-}
-extern "C" __global__ __launch_bounds__(256) Q38_IQ2_OCCUPANCY void q38_gemv_q8k_iq2s(q38_gemv_args a) {
-    gemv_q8k<Q38_GGML_IQ2_S>(a);
-}
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq2xs(q38_gemv_args a) { gemv_q8k<Q38_GGML_IQ2_XS>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq2s(q38_gemv_args a) { gemv_q8k<Q38_GGML_IQ2_S>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq3xxs(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ3_XXS>(a);
 }
