@@ -638,6 +638,51 @@ def gemv_bytes(ty: int, rows: int, width: int, n_tokens: int) -> int:
     return rows * (width // 256) * QUANT_BLOCK_BYTES[ty] + n_tokens * (width // 256) * 292 + n_tokens * rows * 4
 
 
+def _graph_replay_us(ctx, work, reps: int):
+    """Capture work() from the context's stream into a HIP graph, replay it
+    reps times and return the microseconds per replay (None when the HIP
+    runtime's graph calls are not available)."""
+    import ctypes
+    try:
+        hip = ctypes.CDLL(os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "libamdhip64.so"))
+    except OSError:
+        return None
+    hip.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipGraphExecDestroy.argtypes = [ctypes.c_void_p]
+    hip.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    stream = ctx.stream()
+    ctx.sync()
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipStreamBeginCapture(stream, 2) != 0:  # relaxed capture mode
+        return None
+    work()
+    if hip.hipStreamEndCapture(stream, ctypes.byref(graph)) != 0:
+        return None
+    try:
+        if hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) != 0:
+            return None
+        hip.hipGraphLaunch(exe, stream)  # untimed first replay
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for _ in range(reps):
+            hip.hipGraphLaunch(exe, stream)
+        ctx.record(e1)
+        us = ctx.elapsed_ms(e0, e1) * 1e3 / reps
+        ctx.sync()
+        for e in (e0, e1):
+            ctx.destroy_event(e)
+        return us
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)
+
+
 def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
     """The FFN projections of `layers` layers (gate and up 17408x5120 Q4_K,
     down 5120x17408 Q6_K; 173 MB a layer, 693 MB for 4, beyond the 256 MB
@@ -694,6 +739,12 @@ def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
     fused_us = ctx.elapsed_ms(e0, e1) * 1e3 / reps
     res["fused_gate_up_sweep_us"] = fused_us
     res["fused_gate_up_sweep_gb_s"] = total_bytes / (fused_us * 1e-6) / 1e9
+    # the same sweep captured from the context's stream into one HIP graph and
+    # replayed, as a token graph replays a layer's projections
+    g_us = _graph_replay_us(ctx, sweep_fused, reps)
+    if g_us is not None:
+        res["fused_gate_up_sweep_graph_us"] = g_us
+        res["fused_gate_up_sweep_graph_gb_s"] = total_bytes / (g_us * 1e-6) / 1e9
     ctx.kernel_timer_start(GEMV_KERNELS[12], reps * layers)
     for _ in range(reps):
         sweep_fused()
