@@ -1933,7 +1933,12 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
      * keeps one 144-210 byte block in flight, so the bytes a CU has in
      * flight -- and with them its share of the bandwidth -- grow with the
      * workgroups it runs side by side */
-    const int max_units = std::min(Q38_GEMV_UNITS_MAX, 4096 / (tok_pass * nt));
+    /* f32 terms a workgroup keeps in LDS: 16 KiB, or for IQ4_NL's eight
+     * terms per block with several tokens 96 KiB (with at most 64 KiB of
+     * staged activations, the 160 KiB of a CU), so that a workgroup still
+     * holds a few rows (64 units would be 3 rows of a 5120-wide matrix) */
+    const int term_floats = (nt > 1 && tok_pass > 1) ? 24576 : 4096;
+    const int max_units = std::min(Q38_GEMV_UNITS_MAX, term_floats / (tok_pass * nt));
     const long tok_groups_all = ((long)n_tokens + tok_pass - 1) / tok_pass;
     int target_per_wg = max_units / blocks;
     {
