@@ -816,8 +816,8 @@ def weight_formats(pkg, ctx, reps: int):
 
 def weight_formats_prompt(pkg, ctx, n_tokens: int, reps: int):
     """A prompt of n_tokens tokens through a 17408 x 5120 matrix in every Q8_K
-    weight format: the int8 matrix-unit form (IQ4_NL: 8-token GEMV passes),
-    kernel duration and useful int8 operations per second.  Weights are random
+    weight format on the int8 matrix unit: kernel duration and useful int8
+    operations per second.  Weights are random
     bytes (timing only)."""
     rows, width = 17408, 5120
     x = ctx.empty((n_tokens, width))
@@ -832,12 +832,14 @@ def weight_formats_prompt(pkg, ctx, n_tokens: int, reps: int):
         ctx.fill_normal(w, nbytes // 4, 0x51335310 + ty)
         ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
         ctx.sync()
-        kern = GEMV_KERNELS[ty] if ty == 20 else GEMV_KERNELS[ty].replace("gemv", "gemm")
+        kern = GEMV_KERNELS[ty].replace("gemv", "gemm")
         ctx.kernel_timer_start(kern, reps)
         for _ in range(reps):
             ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
         k_ms, k_n = ctx.kernel_timer_stop()
-        ms = k_ms / max(k_n, 1)
+        if k_n == 0:
+            raise RuntimeError(f"{kern} was not launched")
+        ms = k_ms / k_n
         tops = 2.0 * rows * width * n_tokens / (ms * 1e-3) / 1e12
         res[FORMAT_NAMES[ty]] = {"kernel": kern, "ms": round(ms, 3), "int8_tops": round(tops, 1),
                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}

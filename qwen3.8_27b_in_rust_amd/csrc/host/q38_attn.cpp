@@ -90,10 +90,8 @@ bool is_full_attention(int layer) { return layer >= 0 && ((layer + 1) % 4 == 0 |
 
 /* The weight formats of the Q8_K GEMV (tensor_gemv_q8_k's types,
  * tensor.rs:70-75): the GEMV kernel, its many-token form on the int8
- * matrix unit (none for IQ4_NL, whose eight per-group f32 terms per block
- * would be read out of the matrix unit group by group: prompts run as
- * 8-token GEMV passes), f32 terms per block in a row's sum, and the bytes of
- * the lattice grid an IQ kernel copies into LDS. */
+ * matrix unit, f32 terms per block in a row's sum, and the bytes of the
+ * lattice grid an IQ kernel copies into LDS. */
 struct GemvType {
     int ggml_type;
     const char *kernel;
@@ -108,7 +106,7 @@ constexpr GemvType kGemv[] = {
     {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", "q38_gemm_q8k_q3k", 1, 0},
     {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", "q38_gemm_q8k_iq4xs", 1, 0},
     {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", "q38_gemm_q8k_q2k", 1, 0},
-    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", nullptr, 8, 0},
+    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", "q38_gemm_q8k_iq4nl", 8, 0},
     {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", "q38_gemm_q8k_iq2xxs", 1, 256 * 8},
     {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", "q38_gemm_q8k_iq2xs", 1, 512 * 8},
     {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", "q38_gemm_q8k_iq2s", 1, 1024 * 8},
@@ -1905,7 +1903,7 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
      * group) and the LDS copy of an IQ format's lattice grid */
     const int nt = kGemv[ti_occ].terms;
     const int grid_lds = kGemv[ti_occ].grid_bytes;
-    /* the int8 matrix-unit form (every format but IQ4_NL) */
+    /* the int8 matrix-unit form */
     const bool has_gemm = ctx->f_gemm[ti_occ] != nullptr;
     if (n_mats < 1 || n_mats > Q38_GEMV_MAX_MATS) return fail("n_mats %d outside 1..%d", n_mats, Q38_GEMV_MAX_MATS);
     if (rows == nullptr || d_weights == nullptr || d_out == nullptr) return fail("NULL argument");

@@ -836,8 +836,9 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
  *    third MFMA; IQ4_XS the code book's values biased by 128; the lattice
  *    formats their grid bytes (from LDS) with signs, biased by 64 (IQ2, IQ3)
  *    or 1 (IQ1), IQ1's delta correction as the third MFMA against scale x
- *    delta.  IQ4_NL, whose eight groups each end in their own f32 term, has
- *    no matrix-unit form (read out group by group it spills registers).
+ *    delta.  IQ4_NL, whose eight groups each end in their own f32 term,
+ *    has a kernel of its own (q38_gemm_q8k_iq4nl): in this one, read out
+ *    group by group, it spills registers.
  * Every integer is exact; the f32 block term and the row total follow the
  * reference's operation order, so the result equals q38_gemv_q8_k's (and
  * the reference's) bit for bit.
@@ -1204,6 +1205,82 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
 }
 
 }  // namespace
+
+/* IQ4_NL prompts on the int8 matrix unit (tensor_gemm_q8_k's IQ4_NL rows,
+ * dot_iq4_nl_q8_k, iq.rs:355-377): 128 rows x 64 tokens per workgroup as in
+ * gemm_q8k.  Per block and 32-token tile each 32-value group is one product
+ * of the code book's int8 values with the activations, read out at once
+ * into its f32 term (the group's f16 scale times the activation scale,
+ * times the integer sum), added in group order.  Weights and activations
+ * are loaded block by block without prefetch: at 144 registers several
+ * workgroups share a CU and cover each other's loads. */
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq4nl(q38_gemv_args a) {
+    __shared__ __align__(16) int8_t act[kGemmTokens][kActRow];
+    __shared__ float ascale[kGemmTokens];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const int width = a.width;
+    const int B = width / Q38_Q8K_BLOCK;
+    const int rows = a.rows[0];
+    const int row = blockIdx.x * kGemmRows + wave * 32 + (lane & 31);
+    const int rowc = min(row, rows - 1);
+    const int t0 = blockIdx.y * kGemmTokens;
+    const int T = a.n_tokens;
+    const int8_t *quants = static_cast<const int8_t *>(a.q8k);
+    const int16_t *sums = reinterpret_cast<const int16_t *>(quants + (size_t)T * width);
+    const float *scales = reinterpret_cast<const float *>(sums + (size_t)T * B * 16);
+    float total[kGemmTiles][16];
+#pragma unroll
+    for (int tt = 0; tt < kGemmTiles; ++tt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) total[tt][e] = 0.0f;
+    for (int b = 0; b < B; ++b) {
+        Unit<Q38_GGML_IQ4_NL> u;
+        load_unit<Q38_GGML_IQ4_NL>(a.weights[0], (size_t)rowc * B + b, u);
+#pragma unroll
+        for (int i = 0; i < kStagePieces; ++i) {
+            const int p = tid + 256 * i, t = min(t0 + (p >> 4), T - 1), c = p & 15;
+            *reinterpret_cast<u32x4 *>(&act[p >> 4][c * 16]) =
+                *reinterpret_cast<const u32x4 *>(quants + (size_t)t * width + b * 256 + c * 16);
+        }
+        if (tid < kGemmTokens) ascale[tid] = scales[(size_t)min(t0 + tid, T - 1) * B + b];
+        __syncthreads();
+        float gd[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) gd[g] = q38_f16(whalf(u.w, 18 * g));
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt) {
+            const int8_t *arow = &act[32 * tt + (lane & 31)][16 * h];
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                i32x4 bq;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t w = wword(u.w, 18 * g + 2 + 4 * j);
+                    bq[j] = (int)q38_iq4_lookup((h ? w >> 4 : w) & 0x0F0F0F0Fu);
+                }
+                const i32x16 acc = mfma_i8(*reinterpret_cast<const i32x4 *>(arow + 32 * g), bq, i32x16{});
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float as = ascale[32 * tt + 8 * (e >> 2) + 4 * h + (e & 3)];
+                    total[tt][e] = total[tt][e] + (gd[g] * as) * (float)acc[e];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (row < rows) {
+#pragma unroll
+        for (int tt = 0; tt < kGemmTiles; ++tt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int tok = t0 + 32 * tt + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (tok < T) a.out[0][(size_t)tok * rows + row] = total[tt][e];
+            }
+    }
+}
 
 extern "C" __global__ __launch_bounds__(64) void q38_quantize_q8k(q38_quantize_args a) {
     const int b = blockIdx.x;
