@@ -349,10 +349,9 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
  * d_q8k from q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
  * reference's batched form writes it).  width is at most 49152.  Each
  * element equals the reference's scalar dot_q*_k_q8_k (tensor.rs:301-457)
- * or dot_iq*_q8_k (src/kernel/iq.rs:355-667) bit for bit.  For every type
- * but IQ4_NL, from 32 tokens (16 for matrices of 8192 rows or more) the
- * integer dots run on the int8 matrix unit; the result is the same bit for
- * bit.  Other weight types fail with -1 (the reference's f32 path below, or
+ * or dot_iq*_q8_k (src/kernel/iq.rs:355-667) bit for bit.  For every type,
+ * from 32 tokens (16 for matrices of 8192 rows or more) the integer dots
+ * run on the int8 matrix unit; the result is the same bit for bit.  Other weight types fail with -1 (the reference's f32 path below, or
  * types outside this path). */
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
                   int n_tokens, float *d_out);

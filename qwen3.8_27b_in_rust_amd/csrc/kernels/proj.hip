@@ -819,16 +819,21 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
  * dot products on the int8 matrix unit (v_mfma_i32_32x32x32_i8, exact).
  * A workgroup of 4 waves owns 128 rows x 64 tokens; wave w owns rows
  * 128 bx + 32 w .. + 31 (lane l: row l % 32, k half l / 32 of each 32-value
- * step) and both 32-token tiles (the weights it unpacks serve both).  The activations are the MFMA's first
- * operand (tokens x k, from LDS, the next block's copied in while this one
- * is computed), the weights its second (k x rows, unpacked in registers from
- * the lane's own copy of its row's block), so every lane's accumulator
- * column is its own row: element 4J+i of a tile is token 8J + 4(l/32) + i.
- *  - the sub-block scale goes into the weights: w = sc q (Q4_K, Q5_K: a k
- *    step is one 32-value sub-block) or w = sc (q - 32) (Q6_K: a k step holds
- *    two 16-value groups, one per lane half), |w| <= 4096, split into byte
- *    planes w = 128 hi + lo (hi signed, lo in 0..127); two MFMAs per step
- *    accumulate over the block and weighted = 128 C_hi + C_lo;
+ * step) and both 32-token tiles.  The activations are the MFMA's first
+ * operand (tokens x k, from LDS), the weights its second (k x rows, unpacked
+ * in registers from the lane's own copy of its row's block), so every
+ * lane's accumulator column is its own row: element 4J+i of a tile is token
+ * 8J + 4(l/32) + i.  A block's weights and activations are loaded, then
+ * computed, without prefetch: at 160-220 registers (accumulators in
+ * ordinary VGPRs, the file built with -amdgpu-mfma-vgpr-form) two or three
+ * workgroups share a CU and cover each other's loads, where a prefetching
+ * form held 300-400 registers and one.
+ *  - the sub-block scale goes into the weights, split into two byte planes
+ *    accumulated over the block: Q4_K w = sc q with sc = 8 sh + sl, planes
+ *    q sh and q sl (packed 16-bit products, weighted = 8 C_hi + C_lo);
+ *    Q5_K w = sc q and Q6_K w = sc (q - 32) (a k step holds two 16-value
+ *    groups, one per lane half), |w| <= 4096, planes w = 128 hi + lo (hi
+ *    signed, lo in 0..127, weighted = 128 C_hi + C_lo);
  *  - Q4_K / Q5_K's minimum term sum_j m_j bsum_j is a third MFMA, of the
  *    activations against m_j splatted over its sub-block (sum_i m_j(i) a_i);
  *  - the other formats take the same form (gemm_step_bytes): Q3_K w = sc
@@ -837,8 +842,7 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
  *    formats their grid bytes (from LDS) with signs, biased by 64 (IQ2, IQ3)
  *    or 1 (IQ1), IQ1's delta correction as the third MFMA against scale x
  *    delta.  IQ4_NL, whose eight groups each end in their own f32 term,
- *    has a kernel of its own (q38_gemm_q8k_iq4nl): in this one, read out
- *    group by group, it spills registers.
+ *    has a kernel of its own (q38_gemm_q8k_iq4nl).
  * Every integer is exact; the f32 block term and the row total follow the
  * reference's operation order, so the result equals q38_gemv_q8_k's (and
  * the reference's) bit for bit.
@@ -846,13 +850,8 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-/* LDS writes complete, then a workgroup barrier; vector-memory loads in
- * flight stay in flight (gfx9 s_waitcnt: vmcnt 63, expcnt 7, lgkmcnt 0) */
-Q38_DEV void lds_barrier_bare() {
-    __builtin_amdgcn_s_waitcnt((15 | (3 << 14)) | (7 << 4) | (0 << 8));
-    __builtin_amdgcn_s_barrier();
-}
 typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 constexpr int kGemmRows = 128;
 constexpr int kGemmTokens = Q38_GEMM_TOKENS; /* tiles of 32 */
 constexpr int kGemmTiles = kGemmTokens / 32;
@@ -893,15 +892,26 @@ Q38_DEV uint32_t iq_biased4(uint32_t g, uint32_t m) {
     return (0x40404040u + (g & ~neg)) - (g & neg);
 }
 
+/* 0 for the lane half h = 0, all ones for h = 1, hidden from the optimizer:
+ * a choice between two register values made with it stays a bit select and
+ * never becomes an index into a register array (which would place the array
+ * in scratch memory) */
+Q38_DEV uint32_t lane_half_mask(int h) {
+    uint32_t m = 0u - (uint32_t)h;
+    asm volatile("" : "+v"(m));
+    return m;
+}
+
 /* The lane's 16 weights of k step st (values 32 st + 16 h .. + 15 of the
  * block) for the formats beyond Q4_K..Q6_K, as unsigned bytes q with the
  * scale sc and offset off of w = sc (q - off), and (kGemmSecond) the bytes
- * the activations meet in the second sum.  h picks between values computed
- * for both halves, so no register index depends on the lane. */
+ * the activations meet in the second sum.  hm (lane_half_mask) picks between
+ * values computed for both halves, so no register index depends on the lane. */
 template <int TYPE>
-Q38_DEV void gemm_step_bytes(const Unit<TYPE> &u, const UnitScales<TYPE> &s, int st, int h, const uint8_t *grid,
+Q38_DEV void gemm_step_bytes(const Unit<TYPE> &u, const UnitScales<TYPE> &s, int st, uint32_t hm, const uint8_t *grid,
                              uint32_t (&q)[4], int &sc, short &off, uint32_t (&second)[4]) {
-    auto sel = [&](uint32_t a0, uint32_t a1) { return h ? a1 : a0; };
+    auto sel = [&](uint32_t a0, uint32_t a1) { return (a0 & ~hm) | (a1 & hm); };
+    auto seli = [&](int a0, int a1) { return (int)sel((uint32_t)a0, (uint32_t)a1); };
     auto grid8 = [&](uint32_t idx) { return *reinterpret_cast<const uint2 *>(grid + 8 * idx); };
     auto grid4 = [&](uint32_t idx) { return *reinterpret_cast<const uint32_t *>(grid + 4 * idx); };
 #pragma unroll
@@ -911,7 +921,7 @@ Q38_DEV void gemm_step_bytes(const Unit<TYPE> &u, const UnitScales<TYPE> &s, int
          * st / 4, one 16-value group (2 st + h) per lane half; Q3_K adds the
          * high bit from hmask bit st (value q + 4 hbit - 4) */
         const int n = st >> 2, sh = 2 * (st & 3);
-        const int sg = h ? s.sc[2 * st + 1] : s.sc[2 * st]; /* group 2 st + h */
+        const int sg = seli(s.sc[2 * st], s.sc[2 * st + 1]); /* group 2 st + h */
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             if constexpr (TYPE == Q38_GGML_Q3_K) {
@@ -957,13 +967,13 @@ Q38_DEV void gemm_step_bytes(const Unit<TYPE> &u, const UnitScales<TYPE> &s, int
             const uint2 e = grid8(sel(idx0, idx1));
             q[2 * k] = ((e.x ^ 0x80808080u) + 0x01010101u) ^ 0x80808080u;
             q[2 * k + 1] = ((e.y ^ 0x80808080u) + 0x01010101u) ^ 0x80808080u;
-            const int scale = TYPE == Q38_GGML_IQ1_S ? s.sc[st] : (h ? s.sc[2 * st + 1] : s.sc[2 * st]);
-            const int delta = TYPE == Q38_GGML_IQ1_S ? s.mn[st] : (h ? d1 : d0);
+            const int scale = TYPE == Q38_GGML_IQ1_S ? s.sc[st] : seli(s.sc[2 * st], s.sc[2 * st + 1]);
+            const int delta = TYPE == Q38_GGML_IQ1_S ? s.mn[st] : seli(d0, d1);
             const uint32_t m = (uint32_t)(uint8_t)(int8_t)(scale * delta) * 0x01010101u;
             second[2 * k] = m;
             second[2 * k + 1] = m;
         }
-        sc = TYPE == Q38_GGML_IQ1_S ? s.sc[st] : (h ? s.sc[2 * st + 1] : s.sc[2 * st]);
+        sc = TYPE == Q38_GGML_IQ1_S ? s.sc[st] : seli(s.sc[2 * st], s.sc[2 * st + 1]);
         off = 1;
     } else {
         /* IQ2 / IQ3: sections 2h and 2h + 1 of group st, grid bytes with
@@ -1007,15 +1017,15 @@ Q38_DEV void gemm_step_bytes(const Unit<TYPE> &u, const UnitScales<TYPE> &s, int
             q[2 * k] = lo;
             q[2 * k + 1] = hi;
         }
-        sc = (TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S) ? (h ? s.sc[2 * st + 1] : s.sc[2 * st]) : s.sc[st];
+        sc = (TYPE == Q38_GGML_IQ2_XS || TYPE == Q38_GGML_IQ2_S) ? seli(s.sc[2 * st], s.sc[2 * st + 1]) : s.sc[st];
         off = 64;
     }
 }
 
 template <int TYPE>
 Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
-    __shared__ __align__(16) int8_t act[2][kGemmTokens][kActRow];
-    __shared__ float ascale[2][kGemmTokens];
+    __shared__ __align__(16) int8_t act[kGemmTokens][kActRow];
+    __shared__ float ascale[kGemmTokens];
     /* an IQ format's lattice grid (the others keep 16 unused bytes) */
     constexpr int kGridBytes = IqGrid<TYPE>::bytes;
     __shared__ __align__(16) uint8_t grid[kGridBytes > 0 ? kGridBytes : 16];
@@ -1027,6 +1037,7 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5;
+    const uint32_t hm = lane_half_mask(h);
     const int width = a.width;
     const int B = width / Q38_Q8K_BLOCK;
     const int rows = a.rows[0];
@@ -1038,159 +1049,107 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
     const int16_t *sums = reinterpret_cast<const int16_t *>(quants + (size_t)T * width);
     const float *scales = reinterpret_cast<const float *>(sums + (size_t)T * B * 16);
 
-    /* a block's activations: thread p copies pieces p, p + 256, ... (16
-     * bytes of token p / 16, block b); tokens past the prompt are zeros */
-    u32x4 stage[kStagePieces];
-    float stage_scale = 0.0f;
-    /* tokens past the prompt read the last token (no branch around a load,
-     * so the loop's wait counts stay exact); they only feed their own
-     * outputs, which are not stored */
-    auto fetch = [&](int b) {
-#pragma unroll
-        for (int i = 0; i < kStagePieces; ++i) {
-            const int p = tid + 256 * i, t = min(t0 + (p >> 4), T - 1), c = p & 15;
-            stage[i] = *reinterpret_cast<const u32x4 *>(quants + (size_t)t * width + b * 256 + c * 16);
-        }
-        stage_scale = scales[(size_t)min(t0 + (tid & (kGemmTokens - 1)), T - 1) * B + b]; /* threads < kGemmTokens */
-    };
-    auto put = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < kStagePieces; ++i) {
-            const int p = tid + 256 * i, t = p >> 4, c = p & 15;
-            *reinterpret_cast<u32x4 *>(&act[buf][t][c * 16]) = stage[i];
-        }
-        if (tid < kGemmTokens) ascale[buf][tid] = stage_scale;
-    };
-
     float total[kGemmTiles][16];
 #pragma unroll
     for (int tt = 0; tt < kGemmTiles; ++tt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) total[tt][e] = 0.0f;
 
-    /* the compute of one block from LDS buffer buf and weights u */
-    auto compute = [&](const Unit<TYPE> &u, int buf, bool real) {
+    for (int b = 0; b < B; ++b) {
+        Unit<TYPE> u;
+        load_unit<TYPE>(a.weights[0], (size_t)rowc * B + b, u);
+#pragma unroll
+        for (int i = 0; i < kStagePieces; ++i) {
+            const int p = tid + 256 * i, t = min(t0 + (p >> 4), T - 1), c = p & 15;
+            *reinterpret_cast<u32x4 *>(&act[p >> 4][c * 16]) =
+                *reinterpret_cast<const u32x4 *>(quants + (size_t)t * width + b * 256 + c * 16);
+        }
+        if (tid < kGemmTokens) ascale[tid] = scales[(size_t)min(t0 + tid, T - 1) * B + b];
+        __syncthreads();
         UnitScales<TYPE> s;
         unit_scales<TYPE>(u, s);
-        /* word k + 4 h of the block: both candidates are fixed registers and
-         * the lane half selects (an index that depends on the lane would put
-         * the block in scratch memory) */
-        auto word = [&](int k) { return h ? u.w[k + 4] : u.w[k]; };
-        const int8_t *arow[kGemmTiles];
-#pragma unroll
-        for (int tt = 0; tt < kGemmTiles; ++tt) arow[tt] = &act[buf][32 * tt + (lane & 31)][16 * h];
-        /* the block's integer sums per tile: weighted, and minimum (Q4_K, Q5_K) */
-        i32x16 wsum[kGemmTiles], msum[kGemmTiles];
+        auto word = [&](int k) { return (u.w[k] & ~hm) | (u.w[k + 4] & hm); };
 #pragma unroll
         for (int tt = 0; tt < kGemmTiles; ++tt) {
-            wsum[tt] = i32x16{};
-            msum[tt] = i32x16{};
-        }
-        /* two byte planes of the scaled weights per k step (values 32 st +
-         * 16 h .. + 15 of the block): w = sc q (Q4_K, Q5_K: the step is one
-         * 32-value sub-block) or w = sc (q - 32) (Q6_K: group 2 st + h);
-         * weighted = 128 C_hi + C_lo.  Q4_K / Q5_K's minimum is a third
-         * product, the activations against m splatted over the sub-block. */
-        i32x16 lsum[kGemmTiles];
+            const int8_t *arow = &act[32 * tt + (lane & 31)][16 * h];
+            i32x16 wsum = i32x16{}, lsum = i32x16{}, msum = i32x16{};
 #pragma unroll
-        for (int tt = 0; tt < kGemmTiles; ++tt) lsum[tt] = i32x16{};
+            for (int st = 0; st < 8; ++st) {
+                i32x4 bh, bl, bm;
+                if constexpr (TYPE == Q38_GGML_Q4_K) {
+                    /* w = sc q with sc = 8 sh + sl: the planes q sh and q sl
+                     * (at most 15 x 7 = 105 per byte) are packed 16-bit
+                     * products of the quant bytes, no carry between bytes */
+                    const unsigned short sh = (unsigned short)(s.sc[st] >> 3), sl = (unsigned short)(s.sc[st] & 7);
+                    const u16x2 SH = {sh, sh}, SL = {sl, sl};
+                    const int c = st >> 1, nib = st & 1;
 #pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            i32x4 bh, bl, bm;
-            if constexpr (TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K || TYPE == Q38_GGML_Q6_K) {
-                int sc;
-                if (TYPE == Q38_GGML_Q6_K) sc = h ? s.sc[2 * st + 1] : s.sc[2 * st];
-                else sc = s.sc[st];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t q;
-                    if (TYPE == Q38_GGML_Q6_K) {
-                        const int hf = st >> 2, kq = st & 3;
-                        const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
-                        const uint32_t qh = word(32 + 8 * hf + j);
-                        q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
-                    } else {
-                        const int c = st >> 1, nib = st & 1;
-                        const uint32_t qs = TYPE == Q38_GGML_Q4_K ? word(4 + 8 * c + j) : word(12 + 8 * c + j);
-                        q = (qs >> (4 * nib)) & 0x0F0F0F0Fu;
-                        if (TYPE == Q38_GGML_Q5_K) q |= ((word(4 + j) >> st) & 0x01010101u) << 4;
+                    for (int j = 0; j < 4; ++j) {
+                        const u16x2 q = __builtin_bit_cast(u16x2, (word(4 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu);
+                        bh[j] = __builtin_bit_cast(int, q * SH);
+                        bl[j] = __builtin_bit_cast(int, q * SL);
+                        bm[j] = s.mn[st] * 0x01010101;
                     }
-                    uint32_t hi, lo;
-                    split_weights(q, sc, TYPE == Q38_GGML_Q6_K ? (short)32 : (short)0, hi, lo);
-                    bh[j] = (int)hi;
-                    bl[j] = (int)lo;
-                    bm[j] = s.mn[st] * 0x01010101;
+                } else if constexpr (TYPE == Q38_GGML_Q5_K || TYPE == Q38_GGML_Q6_K) {
+                    int sc;
+                    if (TYPE == Q38_GGML_Q6_K) sc = (int)(((uint32_t)s.sc[2 * st] & ~hm) | ((uint32_t)s.sc[2 * st + 1] & hm));
+                    else sc = s.sc[st];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t q;
+                        if (TYPE == Q38_GGML_Q6_K) {
+                            const int hf = st >> 2, kq = st & 3;
+                            const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
+                            const uint32_t qh = word(32 + 8 * hf + j);
+                            q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
+                        } else {
+                            const int c = st >> 1, nib = st & 1;
+                            q = (word(12 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu;
+                            q |= ((word(4 + j) >> st) & 0x01010101u) << 4;
+                        }
+                        uint32_t hi, lo;
+                        split_weights(q, sc, TYPE == Q38_GGML_Q6_K ? (short)32 : (short)0, hi, lo);
+                        bh[j] = (int)hi;
+                        bl[j] = (int)lo;
+                        bm[j] = s.mn[st] * 0x01010101;
+                    }
+                } else {
+                    uint32_t q[4], second[4];
+                    int sc;
+                    short off;
+                    gemm_step_bytes<TYPE>(u, s, st, hm, grid, q, sc, off, second);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        uint32_t hi, lo;
+                        split_weights(q[j], sc, off, hi, lo);
+                        bh[j] = (int)hi;
+                        bl[j] = (int)lo;
+                        bm[j] = (int)second[j];
+                    }
                 }
-            } else {
-                uint32_t q[4], second[4];
-                int sc;
-                short off;
-                gemm_step_bytes<TYPE>(u, s, st, h, grid, q, sc, off, second);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t hi, lo;
-                    split_weights(q[j], sc, off, hi, lo);
-                    bh[j] = (int)hi;
-                    bl[j] = (int)lo;
-                    bm[j] = (int)second[j];
-                }
+                const i32x4 A = *reinterpret_cast<const i32x4 *>(arow + 32 * st);
+                wsum = mfma_i8(A, bh, wsum);
+                lsum = mfma_i8(A, bl, lsum);
+                if constexpr (kGemmSecond<TYPE>) msum = mfma_i8(A, bm, msum);
             }
-#pragma unroll
-            for (int tt = 0; tt < kGemmTiles; ++tt) {
-                const i32x4 A = *reinterpret_cast<const i32x4 *>(arow[tt] + 32 * st);
-                wsum[tt] = mfma_i8(A, bh, wsum[tt]);
-                lsum[tt] = mfma_i8(A, bl, lsum[tt]);
-                if constexpr (kGemmSecond<TYPE>) msum[tt] = mfma_i8(A, bm, msum[tt]);
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < kGemmTiles; ++tt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) wsum[tt][e] = wsum[tt][e] * 128 + lsum[tt][e];
-#pragma unroll
-        for (int tt = 0; tt < kGemmTiles; ++tt) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int tok = 32 * tt + 8 * (e >> 2) + 4 * h + (e & 3);
-                const float as = ascale[buf][tok];
+                const int ws = wsum[e] * (TYPE == Q38_GGML_Q4_K ? 8 : 128) + lsum[e];
+                const float as = ascale[32 * tt + 8 * (e >> 2) + 4 * h + (e & 3)];
                 const float d = s.d * as;
                 float term;
                 if constexpr (TYPE == Q38_GGML_Q2_K || TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K) {
                     const float dmin = s.dmin * as;
-                    term = d * (float)wsum[tt][e] - dmin * (float)msum[tt][e];
+                    term = d * (float)ws - dmin * (float)msum[e];
                 } else if constexpr (TYPE == Q38_GGML_IQ1_S || TYPE == Q38_GGML_IQ1_M) {
-                    term = d * ((float)wsum[tt][e] + 0.125f * (float)msum[tt][e]);
+                    term = d * ((float)ws + 0.125f * (float)msum[e]);
                 } else {
-                    term = d * (float)wsum[tt][e];
+                    term = d * (float)ws;
                 }
-                /* a step past the last block repeats it and adds nothing */
-                total[tt][e] = real ? total[tt][e] + term : total[tt][e];
+                total[tt][e] = total[tt][e] + term;
             }
         }
-    };
-
-    /* Weights and activations one block ahead: weights in the other of two
-     * register sets (the loop is unrolled by two), activations through the
-     * other LDS buffer.  The barriers are bare (LDS writes only): a fence
-     * would also wait for the weights in flight.  Every step issues the same
-     * loads and the same compute (no branch in the loop, so the wait counts
-     * stay exact); a step past the last block repeats it and adds nothing. */
-    Unit<TYPE> w[2];
-    fetch(0);
-    load_unit<TYPE>(a.weights[0], (size_t)rowc * B, w[0]);
-    put(0);
-    lds_barrier_bare();
-    auto step = [&](int b, Unit<TYPE> &cur, Unit<TYPE> &ahead) {
-        fetch(min(b + 1, B - 1));
-        load_unit<TYPE>(a.weights[0], (size_t)rowc * B + min(b + 1, B - 1), ahead);
-        __builtin_amdgcn_sched_barrier(0); /* the loads issue before the compute */
-        compute(cur, b & 1, b < B);
-        put((b + 1) & 1);
-        lds_barrier_bare();
-    };
-    for (int b = 0; b < B; b += 2) {
-        step(b, w[0], w[1]);
-        step(b + 1, w[1], w[0]);
+        __syncthreads();
     }
 
     if (row < rows) {
