@@ -892,6 +892,41 @@ Q38_DEV uint32_t iq_biased4(uint32_t g, uint32_t m) {
     return (0x40404040u + (g & ~neg)) - (g & neg);
 }
 
+/* Q4_K and Q5_K in the matrix-unit form: a lane reads only its half of the
+ * block (load_unit_half) */
+template <int TYPE> constexpr bool kGemmHalfUnit = TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K;
+
+/* The words of a Q4_K / Q5_K block that lane half h uses in the matrix-unit
+ * form, at the positions where the h = 0 lanes find theirs: the 16-byte
+ * header (d, dmin, the 12 scale bytes) in words 0-3; Q5_K's high bits of
+ * values 16 h .. + 15 of every sub-block (bytes 16 + 16 h ..) in words 4-7;
+ * of each 32-byte quant chunk c the 16 bytes 16 h .. + 15 in words
+ * q0 + 8 c .. + 3 (q0 = 4 for Q4_K, 12 for Q5_K).  Blocks start 16-byte
+ * aligned; every load is 16 bytes inside the block. */
+template <int TYPE>
+Q38_DEV void load_unit_half(const uint8_t *weights, size_t g, int h, Unit<TYPE> &u) {
+    const uint8_t *blk = weights + g * KQuant<TYPE>::bytes;
+    auto put = [&](int at, const u32x4 v) {
+        u.w[at] = v.x;
+        u.w[at + 1] = v.y;
+        u.w[at + 2] = v.z;
+        u.w[at + 3] = v.w;
+    };
+    put(0, *reinterpret_cast<const u32x4 *>(blk));
+    constexpr int q0 = TYPE == Q38_GGML_Q5_K ? 12 : 4;
+    if constexpr (TYPE == Q38_GGML_Q5_K) put(4, *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * h));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) put(q0 + 8 * c, *reinterpret_cast<const u32x4 *>(blk + 4 * q0 + 32 * c + 16 * h));
+#pragma unroll
+    for (int i = 0; i < KQuant<TYPE>::words; ++i)
+        if (i >= q0 && ((i - q0) & 7) >= 4) u.w[i] = 0; /* the other half's words: not read */
+    if constexpr (TYPE == Q38_GGML_Q5_K) {
+#pragma unroll
+        for (int i = 8; i < 12; ++i) u.w[i] = 0;
+    }
+    u.dh = 0;
+}
+
 /* 0 for the lane half h = 0, all ones for h = 1, hidden from the optimizer:
  * a choice between two register values made with it stays a bit select and
  * never becomes an index into a register array (which would place the array
@@ -1022,6 +1057,39 @@ Q38_DEV void gemm_step_bytes(const Unit<TYPE> &u, const UnitScales<TYPE> &s, int
     }
 }
 
+/* Byte planes of the scaled weights, one MFMA each: the formats whose
+ * scaled weights fit a signed byte take one (fold_weights), Q5_K three,
+ * the others two. */
+template <int TYPE> constexpr int kGemmPlanes =
+    (TYPE == Q38_GGML_Q2_K || TYPE == Q38_GGML_Q3_K || TYPE == Q38_GGML_IQ1_S || TYPE == Q38_GGML_IQ1_M) ? 1
+    : TYPE == Q38_GGML_Q5_K                                                                           ? 3
+                                                                                                      : 2;
+
+/* The one-plane formats' scaled weights as signed bytes, from
+ * gemm_step_bytes' unsigned q and scale sc:
+ *  - Q2_K w = sc q (sc <= 15, q <= 3: at most 45);
+ *  - Q3_K the negated -w = sc (4 - q) (sc in -32..31, q in 0..7: -128..124;
+ *    the block sum is negated back), as 16-bit products of the even and
+ *    odd bytes whose low bytes are kept;
+ *  - IQ1 w = sc (q - 1) (q in 0..2, sc <= 15) as sc q + 128 - sc per byte
+ *    (113..158, no carry) with the top bit flipped. */
+template <int TYPE>
+Q38_DEV uint32_t fold_weights(uint32_t q, int sc) {
+    if constexpr (TYPE == Q38_GGML_Q2_K) {
+        const u16x2 S = {(unsigned short)sc, (unsigned short)sc};
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * S);
+    } else if constexpr (TYPE == Q38_GGML_Q3_K) {
+        const s16x2 S = {(short)sc, (short)sc}, four = {4, 4};
+        const s16x2 e = (four - __builtin_bit_cast(s16x2, q & 0x00FF00FFu)) * S;
+        const s16x2 o = (four - __builtin_bit_cast(s16x2, (q >> 8) & 0x00FF00FFu)) * S;
+        return (__builtin_bit_cast(uint32_t, e) & 0x00FF00FFu) | ((__builtin_bit_cast(uint32_t, o) & 0x00FF00FFu) << 8);
+    } else {
+        const u16x2 S = {(unsigned short)sc, (unsigned short)sc};
+        const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * S);
+        return (p + (uint32_t)(128 - sc) * 0x01010101u) ^ 0x80808080u;
+    }
+}
+
 template <int TYPE>
 Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
     __shared__ __align__(16) int8_t act[kGemmTokens][kActRow];
@@ -1057,7 +1125,8 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
 
     for (int b = 0; b < B; ++b) {
         Unit<TYPE> u;
-        load_unit<TYPE>(a.weights[0], (size_t)rowc * B + b, u);
+        if constexpr (kGemmHalfUnit<TYPE>) load_unit_half<TYPE>(a.weights[0], (size_t)rowc * B + b, h, u);
+        else load_unit<TYPE>(a.weights[0], (size_t)rowc * B + b, u);
 #pragma unroll
         for (int i = 0; i < kStagePieces; ++i) {
             const int p = tid + 256 * i, t = min(t0 + (p >> 4), T - 1), c = p & 15;
@@ -1068,14 +1137,14 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
         __syncthreads();
         UnitScales<TYPE> s;
         unit_scales<TYPE>(u, s);
-        auto word = [&](int k) { return (u.w[k] & ~hm) | (u.w[k + 4] & hm); };
+        auto word = [&](int k) { return kGemmHalfUnit<TYPE> ? u.w[k] : (u.w[k] & ~hm) | (u.w[k + 4] & hm); };
 #pragma unroll
         for (int tt = 0; tt < kGemmTiles; ++tt) {
             const int8_t *arow = &act[32 * tt + (lane & 31)][16 * h];
-            i32x16 wsum = i32x16{}, lsum = i32x16{}, msum = i32x16{};
+            i32x16 wsum = i32x16{}, lsum = i32x16{}, xsum = i32x16{}, msum = i32x16{};
 #pragma unroll
             for (int st = 0; st < 8; ++st) {
-                i32x4 bh, bl, bm;
+                i32x4 bh, bl, bx, bm;
                 if constexpr (TYPE == Q38_GGML_Q4_K) {
                     /* w = sc q with sc = 8 sh + sl: the planes q sh and q sl
                      * (at most 15 x 7 = 105 per byte) are packed 16-bit
@@ -1090,28 +1159,35 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
                         bl[j] = __builtin_bit_cast(int, q * SL);
                         bm[j] = s.mn[st] * 0x01010101;
                     }
-                } else if constexpr (TYPE == Q38_GGML_Q5_K || TYPE == Q38_GGML_Q6_K) {
-                    int sc;
-                    if (TYPE == Q38_GGML_Q6_K) sc = (int)(((uint32_t)s.sc[2 * st] & ~hm) | ((uint32_t)s.sc[2 * st + 1] & hm));
-                    else sc = s.sc[st];
+                } else if constexpr (TYPE == Q38_GGML_Q5_K) {
+                    /* w = sc q, q <= 31: three planes of sc = 16 s2 + 4 s1 +
+                     * s0 (each at most 3, q s <= 93 per byte) */
+                    const unsigned short s2 = (unsigned short)(s.sc[st] >> 4), s1 = (unsigned short)((s.sc[st] >> 2) & 3),
+                                         s0 = (unsigned short)(s.sc[st] & 3);
+                    const u16x2 S2 = {s2, s2}, S1 = {s1, s1}, S0 = {s0, s0};
+                    const int c = st >> 1, nib = st & 1;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        uint32_t q;
-                        if (TYPE == Q38_GGML_Q6_K) {
-                            const int hf = st >> 2, kq = st & 3;
-                            const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
-                            const uint32_t qh = word(32 + 8 * hf + j);
-                            q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
-                        } else {
-                            const int c = st >> 1, nib = st & 1;
-                            q = (word(12 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu;
-                            q |= ((word(4 + j) >> st) & 0x01010101u) << 4;
-                        }
+                        const uint32_t qv = ((word(12 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu) |
+                                            (((word(4 + j) >> st) & 0x01010101u) << 4);
+                        const u16x2 q = __builtin_bit_cast(u16x2, qv);
+                        bh[j] = __builtin_bit_cast(int, q * S2);
+                        bl[j] = __builtin_bit_cast(int, q * S1);
+                        bx[j] = __builtin_bit_cast(int, q * S0);
+                        bm[j] = s.mn[st] * 0x01010101;
+                    }
+                } else if constexpr (TYPE == Q38_GGML_Q6_K) {
+                    const int sc = (int)(((uint32_t)s.sc[2 * st] & ~hm) | ((uint32_t)s.sc[2 * st + 1] & hm));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int hf = st >> 2, kq = st & 3;
+                        const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
+                        const uint32_t qh = word(32 + 8 * hf + j);
+                        const uint32_t q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
                         uint32_t hi, lo;
-                        split_weights(q, sc, TYPE == Q38_GGML_Q6_K ? (short)32 : (short)0, hi, lo);
+                        split_weights(q, sc, (short)32, hi, lo);
                         bh[j] = (int)hi;
                         bl[j] = (int)lo;
-                        bm[j] = s.mn[st] * 0x01010101;
                     }
                 } else {
                     uint32_t q[4], second[4];
@@ -1120,21 +1196,32 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
                     gemm_step_bytes<TYPE>(u, s, st, hm, grid, q, sc, off, second);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        uint32_t hi, lo;
-                        split_weights(q[j], sc, off, hi, lo);
-                        bh[j] = (int)hi;
-                        bl[j] = (int)lo;
+                        if constexpr (kGemmPlanes<TYPE> == 1) {
+                            bh[j] = (int)fold_weights<TYPE>(q[j], sc);
+                        } else {
+                            uint32_t hi, lo;
+                            split_weights(q[j], sc, off, hi, lo);
+                            bh[j] = (int)hi;
+                            bl[j] = (int)lo;
+                        }
                         bm[j] = (int)second[j];
                     }
                 }
                 const i32x4 A = *reinterpret_cast<const i32x4 *>(arow + 32 * st);
                 wsum = mfma_i8(A, bh, wsum);
-                lsum = mfma_i8(A, bl, lsum);
+                if constexpr (kGemmPlanes<TYPE> >= 2) lsum = mfma_i8(A, bl, lsum);
+                if constexpr (kGemmPlanes<TYPE> >= 3) xsum = mfma_i8(A, bx, xsum);
                 if constexpr (kGemmSecond<TYPE>) msum = mfma_i8(A, bm, msum);
             }
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int ws = wsum[e] * (TYPE == Q38_GGML_Q4_K ? 8 : 128) + lsum[e];
+                /* the weighted sum from its planes */
+                int ws;
+                if constexpr (TYPE == Q38_GGML_Q4_K) ws = wsum[e] * 8 + lsum[e];
+                else if constexpr (TYPE == Q38_GGML_Q5_K) ws = wsum[e] * 16 + lsum[e] * 4 + xsum[e];
+                else if constexpr (TYPE == Q38_GGML_Q3_K) ws = -wsum[e];
+                else if constexpr (kGemmPlanes<TYPE> == 1) ws = wsum[e];
+                else ws = wsum[e] * 128 + lsum[e];
                 const float as = ascale[32 * tt + 8 * (e >> 2) + 4 * h + (e & 3)];
                 const float d = s.d * as;
                 float term;
