@@ -862,20 +862,18 @@ Q38_DEV i32x16 mfma_i8(i32x4 a, i32x4 b, i32x16 c) { return __builtin_amdgcn_mfm
 
 /* Four weights w = sc * (q - off) (q the unpacked bytes, |w| <= 4096) split
  * into byte planes w = 128 hi + lo, hi signed, lo in 0..127; the arithmetic
- * runs on packed 16-bit lanes (even and odd bytes). */
+ * runs on packed 16-bit lanes (even and odd bytes, w = q sc - off sc in one
+ * multiply-add), and a byte permute gathers each plane's low bytes. */
 Q38_DEV void split_weights(uint32_t q, int sc, short off, uint32_t &hi, uint32_t &lo) {
     const s16x2 s2 = {(short)sc, (short)sc};
-    const s16x2 o2 = {off, off};
-    const s16x2 e = __builtin_bit_cast(s16x2, q & 0x00FF00FFu) - o2;
-    const s16x2 o = __builtin_bit_cast(s16x2, (q >> 8) & 0x00FF00FFu) - o2;
-    const s16x2 ve = e * s2, vo = o * s2;
+    const short c = (short)(-off * sc);
+    const s16x2 c2 = {c, c};
+    const s16x2 ve = __builtin_bit_cast(s16x2, q & 0x00FF00FFu) * s2 + c2;
+    const s16x2 vo = __builtin_bit_cast(s16x2, (q >> 8) & 0x00FF00FFu) * s2 + c2;
     const s16x2 sh = {7, 7};
-    const uint32_t he = __builtin_bit_cast(uint32_t, ve >> sh) & 0x00FF00FFu;
-    const uint32_t ho = __builtin_bit_cast(uint32_t, vo >> sh) & 0x00FF00FFu;
-    const uint32_t le = __builtin_bit_cast(uint32_t, ve) & 0x007F007Fu;
-    const uint32_t lo_ = __builtin_bit_cast(uint32_t, vo) & 0x007F007Fu;
-    hi = he | (ho << 8);
-    lo = le | (lo_ << 8);
+    /* bytes 0 and 2 of the even lanes, interleaved with those of the odd */
+    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, vo >> sh), __builtin_bit_cast(uint32_t, ve >> sh), 0x06020400u);
+    lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, vo), __builtin_bit_cast(uint32_t, ve), 0x06020400u) & 0x7F7F7F7Fu;
 }
 
 /* Formats whose block term has a second integer sum over the activations:
@@ -892,9 +890,24 @@ Q38_DEV uint32_t iq_biased4(uint32_t g, uint32_t m) {
     return (0x40404040u + (g & ~neg)) - (g & neg);
 }
 
-/* Q4_K and Q5_K in the matrix-unit form: a lane reads only its half of the
- * block (load_unit_half) */
-template <int TYPE> constexpr bool kGemmHalfUnit = TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K;
+/* Q4_K, Q5_K and Q6_K in the matrix-unit form: a lane reads only its half
+ * of the block (load_unit_half) */
+template <int TYPE> constexpr bool kGemmHalfUnit =
+    TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K || TYPE == Q38_GGML_Q6_K;
+
+/* 16 bytes at offset r (a multiple of 4) of a block that starts 2 bytes
+ * past a dword boundary (o = 2) or on one (o = 0): the dwords from the
+ * boundary at or below, shifted into place.  The fifth dword is read only
+ * where it lies in the block: at_end (the 16 bytes end 2 bytes before the
+ * block does) reads it only for o = 2. */
+Q38_DEV u32x4 load16_2aligned(const uint8_t *blk, uint32_t o, int r, bool at_end) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(blk + r - o);
+    u32x4 v;
+    __builtin_memcpy(&v, p, 16);
+    const uint32_t t = at_end ? p[o ? 4 : 3] : p[4];
+    return u32x4{__builtin_amdgcn_alignbyte(v.y, v.x, o), __builtin_amdgcn_alignbyte(v.z, v.y, o),
+                 __builtin_amdgcn_alignbyte(v.w, v.z, o), __builtin_amdgcn_alignbyte(t, v.w, o)};
+}
 
 /* The words of a Q4_K / Q5_K block that lane half h uses in the matrix-unit
  * form, at the positions where the h = 0 lanes find theirs: the 16-byte
@@ -903,6 +916,12 @@ template <int TYPE> constexpr bool kGemmHalfUnit = TYPE == Q38_GGML_Q4_K || TYPE
  * of each 32-byte quant chunk c the 16 bytes 16 h .. + 15 in words
  * q0 + 8 c .. + 3 (q0 = 4 for Q4_K, 12 for Q5_K).  Blocks start 16-byte
  * aligned; every load is 16 bytes inside the block. */
+/* Q6_K blocks (210 bytes, 2-byte aligned; load16_2aligned): of each
+ * 32-byte piece of ql (bytes 0-127) and qh (128-191) the 16 bytes 16 h ..
+ * + 15 in words 8 p .. + 3 (piece p), the 16 scale bytes in words 48-51
+ * and the f16 scale as dh.  Every byte read lies in the block or, for a
+ * start 2 bytes past a dword boundary, in the 2 bytes before it (block 0
+ * starts dword aligned). */
 template <int TYPE>
 Q38_DEV void load_unit_half(const uint8_t *weights, size_t g, int h, Unit<TYPE> &u) {
     const uint8_t *blk = weights + g * KQuant<TYPE>::bytes;
@@ -912,6 +931,16 @@ Q38_DEV void load_unit_half(const uint8_t *weights, size_t g, int h, Unit<TYPE> 
         u.w[at + 2] = v.z;
         u.w[at + 3] = v.w;
     };
+    if constexpr (TYPE == Q38_GGML_Q6_K) {
+        const uint32_t o = (uint32_t)((g * 210) & 3); /* 0 or 2 */
+#pragma unroll
+        for (int i = 0; i < 52; ++i) u.w[i] = 0; /* the other half's words: not read */
+#pragma unroll
+        for (int p = 0; p < 6; ++p) put(8 * p, load16_2aligned(blk, o, 32 * p + 16 * h, false));
+        put(48, load16_2aligned(blk, o, 192, true));
+        u.dh = *reinterpret_cast<const uint16_t *>(blk + 208);
+        return;
+    }
     put(0, *reinterpret_cast<const u32x4 *>(blk));
     constexpr int q0 = TYPE == Q38_GGML_Q5_K ? 12 : 4;
     if constexpr (TYPE == Q38_GGML_Q5_K) put(4, *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * h));
@@ -1404,18 +1433,23 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq1m(q38_gemv_arg
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4xs(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ4_XS>(a);
 }
+/* Q6_K, IQ4_XS, IQ2_S and IQ3_XXS are held to 168 registers (three
+ * workgroups per CU; Q6_K and IQ4_XS spill 6 dwords): 4096-token prompts
+ * through 17408 x 5120 ran 3-10% faster than at 169-178 registers and two. */
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q4k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q5k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q5_K>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q6k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q6_K>(a); }
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_q6k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q6_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q2k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q2_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q3k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q3_K>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq4xs(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ4_XS>(a); }
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_iq4xs(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ4_XS>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2xxs(q38_gemv_args a) {
     gemm_q8k<Q38_GGML_IQ2_XXS>(a);
 }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2xs(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ2_XS>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2s(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ2_S>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq3xxs(q38_gemv_args a) {
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_iq2s(q38_gemv_args a) {
+    gemm_q8k<Q38_GGML_IQ2_S>(a);
+}
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_iq3xxs(q38_gemv_args a) {
     gemm_q8k<Q38_GGML_IQ3_XXS>(a);
 }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq3s(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ3_S>(a); }
