@@ -832,14 +832,7 @@ def weight_formats_prompt(pkg, ctx, n_tokens: int, reps: int):
         ctx.fill_normal(w, nbytes // 4, 0x51335310 + ty)
         ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
         ctx.sync()
-        kern = GEMV_KERNELS[ty].replace("gemv", "gemm")
-        ctx.kernel_timer_start(kern, reps)
-        for _ in range(reps):
-            ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
-        k_ms, k_n = ctx.kernel_timer_stop()
-        if k_n == 0:
-            raise RuntimeError(f"{kern} was not launched")
-        ms = k_ms / k_n
+        kern, ms = _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps)
         tops = 2.0 * rows * width * n_tokens / (ms * 1e-3) / 1e12
         res[FORMAT_NAMES[ty]] = {"kernel": kern, "ms": round(ms, 3), "int8_tops": round(tops, 1),
                                  "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
@@ -850,7 +843,22 @@ def weight_formats_prompt(pkg, ctx, n_tokens: int, reps: int):
 
 
 INT8_PEAK_TOPS = 5000.0
-GEMM_KERNELS = {12: "q38_gemm_q8k_q4k", 13: "q38_gemm_q8k_q5k", 14: "q38_gemm_q8k_q6k"}
+
+
+def _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps):
+    """Kernel time per call of one projection and the kernel that ran it:
+    the split-block matrix-unit form, the 128 x 64 one or the GEMV, as the
+    library chose for the shape."""
+    gemv = GEMV_KERNELS[ty]
+    kernels = (gemv.replace("q38_gemv_q8k_", "q38_gemm_ks_q8k_"), gemv.replace("gemv", "gemm"), gemv)
+    for kern in kernels if ty != 20 else kernels[1:]:  # IQ4_NL has no split-block form
+        ctx.kernel_timer_start(kern, reps * 64)
+        for _ in range(reps):
+            ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
+        k_ms, k_n = ctx.kernel_timer_stop()
+        if k_n > 0:
+            return kern, k_ms / reps
+    raise RuntimeError(f"no projection kernel of type {ty} was launched")
 
 
 def prompt_projections(pkg, ctx, n_tokens: int, reps: int):
@@ -871,12 +879,7 @@ def prompt_projections(pkg, ctx, n_tokens: int, reps: int):
         out = ctx.empty((n_tokens, rows))
         ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
         ctx.sync()
-        kern = GEMM_KERNELS[ty] if n_tokens >= 16 else GEMV_KERNELS[ty]
-        ctx.kernel_timer_start(kern, reps * 64)
-        for _ in range(reps):
-            ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
-        k_ms, k_n = ctx.kernel_timer_stop()
-        ms = k_ms / max(k_n, 1) * (k_n / reps if reps else 1)
+        kern, ms = _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps)
         ops = 2.0 * rows * width * n_tokens
         res[label] = {"kernel": kern, "ms": ms, "int8_tops": ops / (ms * 1e-3) / 1e12,
                       "frac_int8_peak": ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}

@@ -90,32 +90,38 @@ bool is_full_attention(int layer) { return layer >= 0 && ((layer + 1) % 4 == 0 |
 
 /* The weight formats of the Q8_K GEMV (tensor_gemv_q8_k's types,
  * tensor.rs:70-75): the GEMV kernel, its many-token form on the int8
- * matrix unit, f32 terms per block in a row's sum, and the bytes of the
+ * matrix unit and that form with a row's blocks split over the waves (for
+ * small grids), f32 terms per block in a row's sum, and the bytes of the
  * lattice grid an IQ kernel copies into LDS. */
 struct GemvType {
     int ggml_type;
     const char *kernel;
     const char *gemm_kernel;
+    const char *gemm_ks_kernel;
     int terms;
     int grid_bytes;
 };
 constexpr GemvType kGemv[] = {
-    {Q38_GGML_Q4_K, "q38_gemv_q8k_q4k", "q38_gemm_q8k_q4k", 1, 0},
-    {Q38_GGML_Q5_K, "q38_gemv_q8k_q5k", "q38_gemm_q8k_q5k", 1, 0},
-    {Q38_GGML_Q6_K, "q38_gemv_q8k_q6k", "q38_gemm_q8k_q6k", 1, 0},
-    {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", "q38_gemm_q8k_q3k", 1, 0},
-    {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", "q38_gemm_q8k_iq4xs", 1, 0},
-    {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", "q38_gemm_q8k_q2k", 1, 0},
-    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", "q38_gemm_q8k_iq4nl", 8, 0},
-    {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", "q38_gemm_q8k_iq2xxs", 1, 256 * 8},
-    {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", "q38_gemm_q8k_iq2xs", 1, 512 * 8},
-    {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", "q38_gemm_q8k_iq2s", 1, 1024 * 8},
-    {Q38_GGML_IQ3_XXS, "q38_gemv_q8k_iq3xxs", "q38_gemm_q8k_iq3xxs", 1, 256 * 4},
-    {Q38_GGML_IQ3_S, "q38_gemv_q8k_iq3s", "q38_gemm_q8k_iq3s", 1, 512 * 4},
-    {Q38_GGML_IQ1_S, "q38_gemv_q8k_iq1s", "q38_gemm_q8k_iq1s", 1, 2048 * 8},
-    {Q38_GGML_IQ1_M, "q38_gemv_q8k_iq1m", "q38_gemm_q8k_iq1m", 1, 2048 * 8},
+    {Q38_GGML_Q4_K, "q38_gemv_q8k_q4k", "q38_gemm_q8k_q4k", "q38_gemm_ks_q8k_q4k", 1, 0},
+    {Q38_GGML_Q5_K, "q38_gemv_q8k_q5k", "q38_gemm_q8k_q5k", "q38_gemm_ks_q8k_q5k", 1, 0},
+    {Q38_GGML_Q6_K, "q38_gemv_q8k_q6k", "q38_gemm_q8k_q6k", "q38_gemm_ks_q8k_q6k", 1, 0},
+    {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", "q38_gemm_q8k_q3k", "q38_gemm_ks_q8k_q3k", 1, 0},
+    {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", "q38_gemm_q8k_iq4xs", "q38_gemm_ks_q8k_iq4xs", 1, 0},
+    {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", "q38_gemm_q8k_q2k", "q38_gemm_ks_q8k_q2k", 1, 0},
+    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", "q38_gemm_q8k_iq4nl", nullptr, 8, 0},
+    {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", "q38_gemm_q8k_iq2xxs", "q38_gemm_ks_q8k_iq2xxs", 1, 256 * 8},
+    {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", "q38_gemm_q8k_iq2xs", "q38_gemm_ks_q8k_iq2xs", 1, 512 * 8},
+    {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", "q38_gemm_q8k_iq2s", "q38_gemm_ks_q8k_iq2s", 1, 1024 * 8},
+    {Q38_GGML_IQ3_XXS, "q38_gemv_q8k_iq3xxs", "q38_gemm_q8k_iq3xxs", "q38_gemm_ks_q8k_iq3xxs", 1, 256 * 4},
+    {Q38_GGML_IQ3_S, "q38_gemv_q8k_iq3s", "q38_gemm_q8k_iq3s", "q38_gemm_ks_q8k_iq3s", 1, 512 * 4},
+    {Q38_GGML_IQ1_S, "q38_gemv_q8k_iq1s", "q38_gemm_q8k_iq1s", "q38_gemm_ks_q8k_iq1s", 1, 2048 * 8},
+    {Q38_GGML_IQ1_M, "q38_gemv_q8k_iq1m", "q38_gemm_q8k_iq1m", "q38_gemm_ks_q8k_iq1m", 1, 2048 * 8},
 };
 constexpr int kGemvTypes = (int)(sizeof(kGemv) / sizeof(kGemv[0]));
+/* The split-block GEMM's grid: at least this many workgroups (fewer: the
+ * GEMV), at most this many per CU (more: the 128 x 64 tiles) */
+constexpr long kGemmKsMinTiles = 64;
+constexpr long kGemmKsMaxPerCu = 5;
 
 }  // namespace
 
@@ -146,7 +152,8 @@ struct q38_ctx {
     hipFunction_t f_gdn_step_rows = nullptr;
     hipModule_t mod_proj = nullptr;
     hipFunction_t f_quantize_q8k = nullptr;
-    hipFunction_t f_gemm[kGemvTypes] = {}; /* by kGemv index: the int8 matrix-unit form */
+    hipFunction_t f_gemm[kGemvTypes] = {};    /* by kGemv index: the int8 matrix-unit form */
+    hipFunction_t f_gemm_ks[kGemvTypes] = {}; /* and its split-block form */
     hipFunction_t f_gemv_q8k[kGemvTypes] = {}; /* by kGemv index */
     hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
     hipModule_t mod_synth = nullptr;
@@ -429,9 +436,12 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
         Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, ctx->f_gemv_q8k[i], 256, 0));
         ctx->gemv_occupancy[i] = std::max(1, n);
     }
-    for (int i = 0; i < kGemvTypes; ++i)
+    for (int i = 0; i < kGemvTypes; ++i) {
         if (kGemv[i].gemm_kernel != nullptr)
             Q38_HIP(hipModuleGetFunction(&ctx->f_gemm[i], ctx->mod_proj, kGemv[i].gemm_kernel));
+        if (kGemv[i].gemm_ks_kernel != nullptr)
+            Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_ks[i], ctx->mod_proj, kGemv[i].gemm_ks_kernel));
+    }
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
     Q38_HIP(hipModuleGetFunction(&ctx->f_fill_normal, ctx->mod_synth, "q38_fill_normal"));
@@ -621,6 +631,7 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
         for (int i = 0; i < kGemvTypes; ++i) {
             if (name == kGemv[i].kernel) f = ctx->f_gemv_q8k[i];
             if (kGemv[i].gemm_kernel != nullptr && name == kGemv[i].gemm_kernel) f = ctx->f_gemm[i];
+            if (kGemv[i].gemm_ks_kernel != nullptr && name == kGemv[i].gemm_ks_kernel) f = ctx->f_gemm_ks[i];
         }
         if (f == nullptr) return fail("unknown kernel %s", kernel_name);
     }
@@ -1915,9 +1926,69 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     if (width / Q38_Q8K_BLOCK > Q38_GEMV_MAX_BLOCKS)
         return fail("width %d above %d", width, Q38_GEMV_MAX_BLOCKS * Q38_Q8K_BLOCK);
     if (n_tokens == 0) return 0;
-    /* tokens per pass: as many as Q38_GEMV_ACT_LDS holds (one at least), up
-     * to 8, spread evenly over the passes that takes (8 tokens at most 3 per
-     * pass: 3, 3, 2) */
+    int n_nonempty = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        if (rows[i] == 0) continue; /* nothing to compute for an empty matrix */
+        if (d_weights[i] == nullptr || d_out[i] == nullptr) return fail("NULL weights or output (matrix %d)", i);
+        if ((uintptr_t)d_weights[i] % 16 != 0) return fail("d_weights[%d] must be 16-byte aligned", i);
+        ++n_nonempty;
+    }
+    if (n_nonempty == 0) return 0;
+    if (d_q8k == nullptr || (uintptr_t)d_q8k % 16 != 0) return fail("d_q8k is NULL or not 16-byte aligned");
+    if (((long)n_tokens + Q38_GEMM_KS_TOKENS - 1) / Q38_GEMM_KS_TOKENS > 65535) return fail("too many tokens");
+
+    /* Many tokens: the int8 matrix-unit forms, one launch per matrix.  The
+     * split-block form (32 rows x 32 tokens per workgroup) from
+     * Q38_GEMM_MIN_TOKENS tokens on where its grid has at least
+     * kGemmKsMinTiles workgroups (on fewer, e.g. 1024 x 5120 below 64
+     * tokens, the GEMV is faster), while it has at most kGemmKsMaxPerCu
+     * workgroups per CU; beyond that the 128 x 64 tiles (measured on the
+     * FFN, q|gate and k matrices, 4-512 tokens).  IQ4_NL, which has only
+     * the 128 x 64 form, takes it from 32 tokens (16 for 8192+ rows). */
+    const int ti = ti_occ;
+    const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
+    const long ks_tok_tiles = ((long)n_tokens + Q38_GEMM_KS_TOKENS - 1) / Q38_GEMM_KS_TOKENS;
+    bool on_gemv[Q38_GEMV_MAX_MATS] = {};
+    for (int i = 0; i < n_mats; ++i) {
+        if (rows[i] == 0) continue;
+        const long row_tiles = ((long)rows[i] + Q38_GEMM_ROWS - 1) / Q38_GEMM_ROWS;
+        const long ks_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS * ks_tok_tiles;
+        bool ks = false, big = false;
+        if (ctx->f_gemm_ks[ti] != nullptr) {
+            if (n_tokens >= Q38_GEMM_MIN_TOKENS && ks_tiles >= kGemmKsMinTiles) {
+                ks = ks_tiles <= kGemmKsMaxPerCu * (long)ctx->cu_count;
+                big = !ks;
+            }
+        } else if (has_gemm) {
+            big = n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
+                  (n_tokens >= Q38_GEMM_MIN_TOKENS && rows[i] >= 64L * Q38_GEMM_ROWS);
+        }
+        if (!ks && !big) {
+            on_gemv[i] = true;
+            continue;
+        }
+        q38_gemv_args g;
+        memset(&g, 0, sizeof(g));
+        g.weights[0] = static_cast<const uint8_t *>(d_weights[i]);
+        g.out[0] = d_out[i];
+        g.rows[0] = rows[i];
+        g.n_mats = 1;
+        g.q8k = d_q8k;
+        g.width = width;
+        g.n_tokens = n_tokens;
+        if (ks) {
+            const long ks_row_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS;
+            if (ctx->launch(ctx->f_gemm_ks[ti], (unsigned)ks_row_tiles, (unsigned)ks_tok_tiles, 1,
+                            64 * Q38_GEMM_KS_WAVES, &g))
+                return -1;
+        } else if (ctx->launch(ctx->f_gemm[ti], (unsigned)row_tiles, (unsigned)tok_tiles, 1, 256, &g)) {
+            return -1;
+        }
+    }
+
+    /* The GEMV over the other matrices, in one launch.  Tokens per pass: as
+     * many as Q38_GEMV_ACT_LDS holds (one at least), up to 8, spread evenly
+     * over the passes that takes (8 tokens at most 3 per pass: 3, 3, 2) */
     const int blocks = width / Q38_Q8K_BLOCK;
     int tok_pass = std::max(1, std::min(Q38_GEMV_TOKENS, Q38_GEMV_ACT_LDS / (blocks * Q38_GEMV_REC_BYTES)));
     tok_pass = std::min(tok_pass, n_tokens);
@@ -1941,7 +2012,8 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     int target_per_wg = max_units / blocks;
     {
         long all_rows = 0;
-        for (int i = 0; i < n_mats; ++i) all_rows += std::max(rows[i], 0);
+        for (int i = 0; i < n_mats; ++i)
+            if (on_gemv[i]) all_rows += rows[i];
         const long lds_max =
             grid_lds + (long)tok_pass * blocks * Q38_GEMV_REC_BYTES + (long)tok_pass * max_units * 4 * nt;
         long occ = ctx->gemv_occupancy[ti_occ];
@@ -1955,9 +2027,7 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     int max_per_wg = 1;
     int kept = 0;
     for (int i = 0; i < n_mats; ++i) {
-        if (rows[i] == 0) continue; /* nothing to compute for an empty matrix */
-        if (d_weights[i] == nullptr || d_out[i] == nullptr) return fail("NULL weights or output (matrix %d)", i);
-        if ((uintptr_t)d_weights[i] % 16 != 0) return fail("d_weights[%d] must be 16-byte aligned", i);
+        if (!on_gemv[i]) continue;
         const int per_wg = target_per_wg;
         a.weights[kept] = static_cast<const uint8_t *>(d_weights[i]);
         a.out[kept] = d_out[i];
@@ -1969,33 +2039,6 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
         ++kept;
     }
     if (kept == 0) return 0;
-    if (d_q8k == nullptr || (uintptr_t)d_q8k % 16 != 0) return fail("d_q8k is NULL or not 16-byte aligned");
-    /* many tokens: the int8 matrix-unit form, one launch per matrix, 128
-     * rows x 64 tokens per workgroup; from 16 tokens on when a matrix has
-     * rows for 64+ workgroups, else from 32 (measured crossovers: 17408 x
-     * 5120 Q4_K at 16 tokens, 5120 x 17408 Q6_K at 32) */
-    long min_rows = a.rows[0];
-    for (int i = 1; i < kept; ++i) min_rows = std::min<long>(min_rows, a.rows[i]); /* non-empty matrices */
-    if (has_gemm && (n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
-                     (n_tokens >= Q38_GEMM_MIN_TOKENS && min_rows >= 64L * Q38_GEMM_ROWS))) {
-        const int ti = ti_occ;
-        const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
-        if (tok_tiles > 65535) return fail("too many tokens");
-        for (int i = 0; i < kept; ++i) {
-            q38_gemv_args g;
-            memset(&g, 0, sizeof(g));
-            g.weights[0] = a.weights[i];
-            g.out[0] = a.out[i];
-            g.rows[0] = a.rows[i];
-            g.n_mats = 1;
-            g.q8k = d_q8k;
-            g.width = width;
-            g.n_tokens = n_tokens;
-            const long row_tiles = ((long)a.rows[i] + Q38_GEMM_ROWS - 1) / Q38_GEMM_ROWS;
-            if (ctx->launch(ctx->f_gemm[ti], (unsigned)row_tiles, (unsigned)tok_tiles, 1, 256, &g)) return -1;
-        }
-        return 0;
-    }
     const long tok_groups = ((long)n_tokens + tok_pass - 1) / tok_pass;
     /* one pass: a workgroup per row group; several: the passes of a row
      * group 8 workgroup ids apart (one XCD, dispatched together) */

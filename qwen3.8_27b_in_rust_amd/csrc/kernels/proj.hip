@@ -1119,6 +1119,112 @@ Q38_DEV uint32_t fold_weights(uint32_t q, int sc) {
     }
 }
 
+/* One block's f32 terms for a tile of 32 tokens x 32 rows (the lane's 16
+ * outputs: row l % 32, tokens 8J + 4(l/32) + i for element 4J + i): the
+ * integer sums on the matrix unit, then the reference's f32 block term.
+ * A_of(st) gives the lane's 16 activations of k step st (token l % 32,
+ * values 32 st + 16 h .. + 15), as_of(e) the activation scale of element e;
+ * sink(e, term) takes element e's term. */
+template <int TYPE, typename AOf, typename AsOf, typename Sink>
+Q38_DEV void gemm_tile_terms(const Unit<TYPE> &u, const UnitScales<TYPE> &s, uint32_t hm, const uint8_t *grid,
+                             AOf A_of, AsOf as_of, Sink sink) {
+    auto word = [&](int k) { return kGemmHalfUnit<TYPE> ? u.w[k] : (u.w[k] & ~hm) | (u.w[k + 4] & hm); };
+    i32x16 wsum = i32x16{}, lsum = i32x16{}, xsum = i32x16{}, msum = i32x16{};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+        i32x4 bh, bl, bx, bm;
+        if constexpr (TYPE == Q38_GGML_Q4_K) {
+            /* w = sc q with sc = 8 sh + sl: the planes q sh and q sl
+             * (at most 15 x 7 = 105 per byte) are packed 16-bit
+             * products of the quant bytes, no carry between bytes */
+            const unsigned short sh = (unsigned short)(s.sc[st] >> 3), sl = (unsigned short)(s.sc[st] & 7);
+            const u16x2 SH = {sh, sh}, SL = {sl, sl};
+            const int c = st >> 1, nib = st & 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u16x2 q = __builtin_bit_cast(u16x2, (word(4 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu);
+                bh[j] = __builtin_bit_cast(int, q * SH);
+                bl[j] = __builtin_bit_cast(int, q * SL);
+                bm[j] = s.mn[st] * 0x01010101;
+            }
+        } else if constexpr (TYPE == Q38_GGML_Q5_K) {
+            /* w = sc q, q <= 31: three planes of sc = 16 s2 + 4 s1 +
+             * s0 (each at most 3, q s <= 93 per byte) */
+            const unsigned short s2 = (unsigned short)(s.sc[st] >> 4), s1 = (unsigned short)((s.sc[st] >> 2) & 3),
+                                 s0 = (unsigned short)(s.sc[st] & 3);
+            const u16x2 S2 = {s2, s2}, S1 = {s1, s1}, S0 = {s0, s0};
+            const int c = st >> 1, nib = st & 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t qv = ((word(12 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu) |
+                                    (((word(4 + j) >> st) & 0x01010101u) << 4);
+                const u16x2 q = __builtin_bit_cast(u16x2, qv);
+                bh[j] = __builtin_bit_cast(int, q * S2);
+                bl[j] = __builtin_bit_cast(int, q * S1);
+                bx[j] = __builtin_bit_cast(int, q * S0);
+                bm[j] = s.mn[st] * 0x01010101;
+            }
+        } else if constexpr (TYPE == Q38_GGML_Q6_K) {
+            const int sc = (int)(((uint32_t)s.sc[2 * st] & ~hm) | ((uint32_t)s.sc[2 * st + 1] & hm));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int hf = st >> 2, kq = st & 3;
+                const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
+                const uint32_t qh = word(32 + 8 * hf + j);
+                const uint32_t q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
+                uint32_t hi, lo;
+                split_weights(q, sc, (short)32, hi, lo);
+                bh[j] = (int)hi;
+                bl[j] = (int)lo;
+            }
+        } else {
+            uint32_t q[4], second[4];
+            int sc;
+            short off;
+            gemm_step_bytes<TYPE>(u, s, st, hm, grid, q, sc, off, second);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (kGemmPlanes<TYPE> == 1) {
+                    bh[j] = (int)fold_weights<TYPE>(q[j], sc);
+                } else {
+                    uint32_t hi, lo;
+                    split_weights(q[j], sc, off, hi, lo);
+                    bh[j] = (int)hi;
+                    bl[j] = (int)lo;
+                }
+                bm[j] = (int)second[j];
+            }
+        }
+        const i32x4 A = A_of(st);
+        wsum = mfma_i8(A, bh, wsum);
+        if constexpr (kGemmPlanes<TYPE> >= 2) lsum = mfma_i8(A, bl, lsum);
+        if constexpr (kGemmPlanes<TYPE> >= 3) xsum = mfma_i8(A, bx, xsum);
+        if constexpr (kGemmSecond<TYPE>) msum = mfma_i8(A, bm, msum);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        /* the weighted sum from its planes */
+        int ws;
+        if constexpr (TYPE == Q38_GGML_Q4_K) ws = wsum[e] * 8 + lsum[e];
+        else if constexpr (TYPE == Q38_GGML_Q5_K) ws = wsum[e] * 16 + lsum[e] * 4 + xsum[e];
+        else if constexpr (TYPE == Q38_GGML_Q3_K) ws = -wsum[e];
+        else if constexpr (kGemmPlanes<TYPE> == 1) ws = wsum[e];
+        else ws = wsum[e] * 128 + lsum[e];
+        const float as = as_of(e);
+        const float d = s.d * as;
+        float term;
+        if constexpr (TYPE == Q38_GGML_Q2_K || TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K) {
+            const float dmin = s.dmin * as;
+            term = d * (float)ws - dmin * (float)msum[e];
+        } else if constexpr (TYPE == Q38_GGML_IQ1_S || TYPE == Q38_GGML_IQ1_M) {
+            term = d * ((float)ws + 0.125f * (float)msum[e]);
+        } else {
+            term = d * (float)ws;
+        }
+        sink(e, term);
+    }
+}
+
 template <int TYPE>
 Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
     __shared__ __align__(16) int8_t act[kGemmTokens][kActRow];
@@ -1166,104 +1272,13 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
         __syncthreads();
         UnitScales<TYPE> s;
         unit_scales<TYPE>(u, s);
-        auto word = [&](int k) { return kGemmHalfUnit<TYPE> ? u.w[k] : (u.w[k] & ~hm) | (u.w[k + 4] & hm); };
 #pragma unroll
         for (int tt = 0; tt < kGemmTiles; ++tt) {
             const int8_t *arow = &act[32 * tt + (lane & 31)][16 * h];
-            i32x16 wsum = i32x16{}, lsum = i32x16{}, xsum = i32x16{}, msum = i32x16{};
-#pragma unroll
-            for (int st = 0; st < 8; ++st) {
-                i32x4 bh, bl, bx, bm;
-                if constexpr (TYPE == Q38_GGML_Q4_K) {
-                    /* w = sc q with sc = 8 sh + sl: the planes q sh and q sl
-                     * (at most 15 x 7 = 105 per byte) are packed 16-bit
-                     * products of the quant bytes, no carry between bytes */
-                    const unsigned short sh = (unsigned short)(s.sc[st] >> 3), sl = (unsigned short)(s.sc[st] & 7);
-                    const u16x2 SH = {sh, sh}, SL = {sl, sl};
-                    const int c = st >> 1, nib = st & 1;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const u16x2 q = __builtin_bit_cast(u16x2, (word(4 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu);
-                        bh[j] = __builtin_bit_cast(int, q * SH);
-                        bl[j] = __builtin_bit_cast(int, q * SL);
-                        bm[j] = s.mn[st] * 0x01010101;
-                    }
-                } else if constexpr (TYPE == Q38_GGML_Q5_K) {
-                    /* w = sc q, q <= 31: three planes of sc = 16 s2 + 4 s1 +
-                     * s0 (each at most 3, q s <= 93 per byte) */
-                    const unsigned short s2 = (unsigned short)(s.sc[st] >> 4), s1 = (unsigned short)((s.sc[st] >> 2) & 3),
-                                         s0 = (unsigned short)(s.sc[st] & 3);
-                    const u16x2 S2 = {s2, s2}, S1 = {s1, s1}, S0 = {s0, s0};
-                    const int c = st >> 1, nib = st & 1;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t qv = ((word(12 + 8 * c + j) >> (4 * nib)) & 0x0F0F0F0Fu) |
-                                            (((word(4 + j) >> st) & 0x01010101u) << 4);
-                        const u16x2 q = __builtin_bit_cast(u16x2, qv);
-                        bh[j] = __builtin_bit_cast(int, q * S2);
-                        bl[j] = __builtin_bit_cast(int, q * S1);
-                        bx[j] = __builtin_bit_cast(int, q * S0);
-                        bm[j] = s.mn[st] * 0x01010101;
-                    }
-                } else if constexpr (TYPE == Q38_GGML_Q6_K) {
-                    const int sc = (int)(((uint32_t)s.sc[2 * st] & ~hm) | ((uint32_t)s.sc[2 * st + 1] & hm));
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int hf = st >> 2, kq = st & 3;
-                        const uint32_t ql = word(16 * hf + 8 * (kq & 1) + j);
-                        const uint32_t qh = word(32 + 8 * hf + j);
-                        const uint32_t q = ((ql >> (4 * (kq >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kq)) & 0x03030303u) << 4);
-                        uint32_t hi, lo;
-                        split_weights(q, sc, (short)32, hi, lo);
-                        bh[j] = (int)hi;
-                        bl[j] = (int)lo;
-                    }
-                } else {
-                    uint32_t q[4], second[4];
-                    int sc;
-                    short off;
-                    gemm_step_bytes<TYPE>(u, s, st, hm, grid, q, sc, off, second);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        if constexpr (kGemmPlanes<TYPE> == 1) {
-                            bh[j] = (int)fold_weights<TYPE>(q[j], sc);
-                        } else {
-                            uint32_t hi, lo;
-                            split_weights(q[j], sc, off, hi, lo);
-                            bh[j] = (int)hi;
-                            bl[j] = (int)lo;
-                        }
-                        bm[j] = (int)second[j];
-                    }
-                }
-                const i32x4 A = *reinterpret_cast<const i32x4 *>(arow + 32 * st);
-                wsum = mfma_i8(A, bh, wsum);
-                if constexpr (kGemmPlanes<TYPE> >= 2) lsum = mfma_i8(A, bl, lsum);
-                if constexpr (kGemmPlanes<TYPE> >= 3) xsum = mfma_i8(A, bx, xsum);
-                if constexpr (kGemmSecond<TYPE>) msum = mfma_i8(A, bm, msum);
-            }
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                /* the weighted sum from its planes */
-                int ws;
-                if constexpr (TYPE == Q38_GGML_Q4_K) ws = wsum[e] * 8 + lsum[e];
-                else if constexpr (TYPE == Q38_GGML_Q5_K) ws = wsum[e] * 16 + lsum[e] * 4 + xsum[e];
-                else if constexpr (TYPE == Q38_GGML_Q3_K) ws = -wsum[e];
-                else if constexpr (kGemmPlanes<TYPE> == 1) ws = wsum[e];
-                else ws = wsum[e] * 128 + lsum[e];
-                const float as = ascale[32 * tt + 8 * (e >> 2) + 4 * h + (e & 3)];
-                const float d = s.d * as;
-                float term;
-                if constexpr (TYPE == Q38_GGML_Q2_K || TYPE == Q38_GGML_Q4_K || TYPE == Q38_GGML_Q5_K) {
-                    const float dmin = s.dmin * as;
-                    term = d * (float)ws - dmin * (float)msum[e];
-                } else if constexpr (TYPE == Q38_GGML_IQ1_S || TYPE == Q38_GGML_IQ1_M) {
-                    term = d * ((float)ws + 0.125f * (float)msum[e]);
-                } else {
-                    term = d * (float)ws;
-                }
-                total[tt][e] = total[tt][e] + term;
-            }
+            gemm_tile_terms<TYPE>(
+                u, s, hm, grid, [&](int st) { return *reinterpret_cast<const i32x4 *>(arow + 32 * st); },
+                [&](int e) { return ascale[32 * tt + 8 * (e >> 2) + 4 * h + (e & 3)]; },
+                [&](int e, float term) { total[tt][e] = total[tt][e] + term; });
         }
         __syncthreads();
     }
@@ -1276,6 +1291,92 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
                 const int tok = t0 + 32 * tt + 8 * (e >> 2) + 4 * h + (e & 3);
                 if (tok < T) a.out[0][(size_t)tok * rows + row] = total[tt][e];
             }
+    }
+}
+
+
+/* The matrix-unit form with the blocks of a row split over the waves, for
+ * grids that the 128-row x 64-token tiles would leave small (few rows or
+ * few tokens): a workgroup of Q38_GEMM_KS_WAVES waves owns 32 rows x 32
+ * tokens, and wave w takes blocks w, w + W, w + 2W, ... (W waves).  Each
+ * block's f32 terms are the ones gemm_q8k forms (gemm_tile_terms); a round
+ * of W blocks leaves them in LDS, and the workgroup adds them to the row
+ * totals in block order, so every output is the reference's sum bit for
+ * bit.  The activations are read straight from the Q8_K rows (tokens past
+ * the prompt read the last one; their outputs are not stored). */
+template <int TYPE>
+Q38_DEV void gemm_ks_q8k(const q38_gemv_args &a) {
+    constexpr int W = Q38_GEMM_KS_WAVES;
+    constexpr int kThreads = 64 * W;
+    /* two rounds' terms: [round & 1][wave][element][lane] */
+    __shared__ float terms[2][W][16][64];
+    constexpr int kGridBytes = IqGrid<TYPE>::bytes;
+    __shared__ __align__(16) uint8_t grid[kGridBytes > 0 ? kGridBytes : 16];
+    const int tid = threadIdx.x;
+    if constexpr (kGridBytes > 0) {
+        const u32x4 *src = static_cast<const u32x4 *>(iq_grid_table<TYPE>());
+        for (int i = tid; i < kGridBytes / 16; i += kThreads) reinterpret_cast<u32x4 *>(grid)[i] = src[i];
+        __syncthreads();
+    }
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const uint32_t hm = lane_half_mask(h);
+    const int width = a.width;
+    const int B = width / Q38_Q8K_BLOCK;
+    const int rows = a.rows[0];
+    const int row0 = blockIdx.x * Q38_GEMM_KS_ROWS;
+    const int rowc = min(row0 + (lane & 31), rows - 1);
+    const int t0 = blockIdx.y * Q38_GEMM_KS_TOKENS;
+    const int T = a.n_tokens;
+    const int8_t *quants = static_cast<const int8_t *>(a.q8k);
+    const int16_t *sums = reinterpret_cast<const int16_t *>(quants + (size_t)T * width);
+    const float *scales = reinterpret_cast<const float *>(sums + (size_t)T * B * 16);
+    /* the lane's activation row (token t0 + l % 32) and its elements' tokens */
+    const int8_t *arow = quants + (size_t)min(t0 + (lane & 31), T - 1) * width + 16 * h;
+    int etok[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) etok[e] = min(t0 + 8 * (e >> 2) + 4 * h + (e & 3), T - 1);
+
+    /* the 1024 outputs of the tile: thread i adds up elements i, i + 64 W, ... */
+    constexpr int kOwn = 1024 / kThreads;
+    float total[kOwn];
+#pragma unroll
+    for (int k = 0; k < kOwn; ++k) total[k] = 0.0f;
+    const int rounds = (B + W - 1) / W;
+    for (int r = 0; r < rounds; ++r) {
+        const int buf = r & 1;
+        const int b = r * W + wave;
+        if (b < B) {
+            Unit<TYPE> u;
+            if constexpr (kGemmHalfUnit<TYPE>) load_unit_half<TYPE>(a.weights[0], (size_t)rowc * B + b, h, u);
+            else load_unit<TYPE>(a.weights[0], (size_t)rowc * B + b, u);
+            i32x4 A[8];
+#pragma unroll
+            for (int st = 0; st < 8; ++st) A[st] = *reinterpret_cast<const i32x4 *>(arow + b * 256 + 32 * st);
+            float as[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) as[e] = scales[(size_t)etok[e] * B + b];
+            UnitScales<TYPE> s;
+            unit_scales<TYPE>(u, s);
+            gemm_tile_terms<TYPE>(
+                u, s, hm, grid, [&](int st) { return A[st]; }, [&](int e) { return as[e]; },
+                [&](int e, float term) { terms[buf][wave][e][lane] = term; });
+        }
+        __syncthreads();
+        /* this round's blocks r W .. r W + W - 1 in order (those that exist) */
+        const int nw = min(W, B - r * W);
+#pragma unroll
+        for (int k = 0; k < kOwn; ++k) {
+            const int idx = tid + kThreads * k;
+            for (int w = 0; w < nw; ++w) total[k] = total[k] + terms[buf][w][idx >> 6][idx & 63];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kOwn; ++k) {
+        const int idx = tid + kThreads * k, e = idx >> 6, l = idx & 63;
+        const int tok = t0 + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3), row = row0 + (l & 31);
+        if (tok < T && row < rows) a.out[0][(size_t)tok * rows + row] = total[k];
     }
 }
 
@@ -1433,9 +1534,9 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq1m(q38_gemv_arg
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4xs(q38_gemv_args a) {
     gemv_q8k<Q38_GGML_IQ4_XS>(a);
 }
-/* Q6_K, IQ4_XS, IQ2_S and IQ3_XXS are held to 168 registers (three
- * workgroups per CU; Q6_K and IQ4_XS spill 6 dwords): 4096-token prompts
- * through 17408 x 5120 ran 3-10% faster than at 169-178 registers and two. */
+/* Q6_K, IQ4_XS, IQ2_XS, IQ2_S and IQ3_XXS are held to 168 registers (three
+ * workgroups per CU; a few dwords spill): 4096-token prompts through
+ * 17408 x 5120 ran 3-10% faster than at 169-178 registers and two. */
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q4k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q4_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q5k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q5_K>(a); }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_q6k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q6_K>(a); }
@@ -1445,7 +1546,7 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2xxs(q38_gemv_args a) {
     gemm_q8k<Q38_GGML_IQ2_XXS>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq2xs(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ2_XS>(a); }
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_iq2xs(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ2_XS>(a); }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_iq2s(q38_gemv_args a) {
     gemm_q8k<Q38_GGML_IQ2_S>(a);
 }
@@ -1455,6 +1556,24 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq3s(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ3_S>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq1s(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ1_S>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq1m(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ1_M>(a); }
+#define Q38_GEMM_KS(name, T)                                                                                      \
+    extern "C" __global__ __launch_bounds__(64 * Q38_GEMM_KS_WAVES) void q38_gemm_ks_q8k_##name(q38_gemv_args a) { \
+        gemm_ks_q8k<T>(a);                                                                                        \
+    }
+Q38_GEMM_KS(q4k, Q38_GGML_Q4_K)
+Q38_GEMM_KS(q5k, Q38_GGML_Q5_K)
+Q38_GEMM_KS(q6k, Q38_GGML_Q6_K)
+Q38_GEMM_KS(q2k, Q38_GGML_Q2_K)
+Q38_GEMM_KS(q3k, Q38_GGML_Q3_K)
+Q38_GEMM_KS(iq4xs, Q38_GGML_IQ4_XS)
+Q38_GEMM_KS(iq2xxs, Q38_GGML_IQ2_XXS)
+Q38_GEMM_KS(iq2xs, Q38_GGML_IQ2_XS)
+Q38_GEMM_KS(iq2s, Q38_GGML_IQ2_S)
+Q38_GEMM_KS(iq3xxs, Q38_GGML_IQ3_XXS)
+Q38_GEMM_KS(iq3s, Q38_GGML_IQ3_S)
+Q38_GEMM_KS(iq1s, Q38_GGML_IQ1_S)
+Q38_GEMM_KS(iq1m, Q38_GGML_IQ1_M)
+#undef Q38_GEMM_KS
 
 /*
  * Projections of f32 activations by F32, F16, BF16 or Q8_0 weights (the

@@ -335,6 +335,13 @@ typedef struct {
 #define Q38_GEMM_MIN_TOKENS 16
 #define Q38_GEMM_ROWS 128
 #define Q38_GEMM_TOKENS 64
+/* Where that grid holds few workgroups (few rows or tokens), the blocks of a
+ * row are split over the waves instead (q38_gemm_ks_q8k_*: grid (ceil(rows /
+ * 32), ceil(T / 32)), Q38_GEMM_KS_WAVES waves of 64 threads, the same
+ * arguments with one matrix). */
+#define Q38_GEMM_KS_ROWS 32
+#define Q38_GEMM_KS_TOKENS 32
+#define Q38_GEMM_KS_WAVES 8
 typedef struct {
     const uint8_t *weights[Q38_GEMV_MAX_MATS]; /* [rows][B * block_bytes], 16-byte aligned */
     float *out[Q38_GEMV_MAX_MATS];             /* [T][rows] */

@@ -117,12 +117,13 @@ def test_gemv_q8_k_model_shapes(ctx, ref, name):
 
 
 @pytest.mark.parametrize("name", sorted(TYPES))
-@pytest.mark.parametrize("T", [1, 3, 9])
+@pytest.mark.parametrize("T", [1, 3, 9, 40])
 def test_gemv_multi_equals_single(ctx, ref, name, T):
     """Several matrices on one input in one launch (q|gate, k, v of a layer
     are 12288, 1024, 1024 rows; here smaller, with an empty matrix and a
     one-row one): every output bit for bit as the single-matrix launch and
-    the oracle."""
+    the oracle.  At 40 tokens the 1500-row matrix takes the matrix unit and
+    the small ones the GEMV, in one call."""
     ty = TYPES[name]
     W = 1280
     x = _activations(T, W, 0x513338E0 + T)
@@ -145,12 +146,16 @@ def test_gemv_multi_equals_single(ctx, ref, name, T):
 
 
 @pytest.mark.parametrize("name", sorted(TYPES))
-@pytest.mark.parametrize("rows,W,T", [(130, 1280, 32), (33, 256, 65), (300, HIDDEN, 130), (129, 2304, 64),
-                                      (8200, 256, 16)])
+@pytest.mark.parametrize("rows,W,T", [(130, 1280, 32), (2050, 256, 33), (1100, 1280, 65), (700, HIDDEN, 130),
+                                      (2100, 2304, 64), (8200, 256, 16), (4100, 768, 1000)])
 def test_gemm_many_tokens_bit_exact(ctx, ref, name, rows, W, T):
-    """The matrix-unit form (32 tokens and more, 16 for 8192+ rows): partial
-    row and token tiles, one and several 64-token tiles, bit for bit against
-    the oracle."""
+    """The matrix-unit forms from 16 tokens on, bit for bit against the
+    oracle, with partial row and token tiles.  The split-block form (32 rows
+    x 32 tokens per workgroup, a row's blocks over 8 waves) where its grid
+    has 64 to 1280 workgroups: 1, 5, 9 and 20 blocks, so the last round of
+    8 is partial; 4100 x 1000 (4128 such workgroups) takes the 128-row x
+    64-token tiles, as IQ4_NL does from 32 tokens (16 for 8192+ rows);
+    130 x 1280 (5 workgroups) stays on the GEMV."""
     ty = TYPES[name]
     x = _activations(T, W, 0x513338F0 + T + W)
     d_q = _quantize_on_device(ctx, x)
