@@ -349,10 +349,12 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
  * d_q8k from q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
  * reference's batched form writes it).  width is at most 49152.  Each
  * element equals the reference's scalar dot_q*_k_q8_k (tensor.rs:301-457)
- * or dot_iq*_q8_k (src/kernel/iq.rs:355-667) bit for bit.  For every type,
- * from 32 tokens (16 for matrices of 8192 rows or more) the integer dots
- * run on the int8 matrix unit; the result is the same bit for bit.  Other weight types fail with -1 (the reference's f32 path below, or
- * types outside this path). */
+ * or dot_iq*_q8_k (src/kernel/iq.rs:355-667) bit for bit.  From 16 tokens
+ * on, where the matrix has rows for 64+ tiles of 32 rows x 32 tokens, the
+ * integer dots run on the int8 matrix unit (IQ4_NL: from 32 tokens, 16 for
+ * 8192+ rows); the result is the same bit for bit.  Other weight types
+ * fail with -1 (the reference's f32 path below, or types outside this
+ * path). */
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,
                   int n_tokens, float *d_out);
 
@@ -362,8 +364,9 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
  * to 4 matrices of one type and width, matrix i with rows[i] rows at
  * d_weights[i], its output at d_out[i] [n_tokens][rows[i]], in one launch.
  * Each output equals q38_gemv_q8_k's for that matrix bit for bit; the
- * launch streams the matrices back to back, so the start and end of a
- * launch are paid once. */
+ * matrices that stay on the GEMV stream back to back in one launch, so the
+ * start and end of a launch are paid once (those on the matrix unit take a
+ * launch each). */
 int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
                         const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out);
 
