@@ -329,9 +329,10 @@ typedef struct {
  * of row group 8 (L / (8 P)) + L % 8 (none past G), so the passes of a row
  * group are dispatched together onto one XCD and share its L2. */
 #define Q38_GEMV_MAX_MATS 4
-/* From this many tokens (twice as many for matrices of under 8192 rows) the
- * projections run on the int8 matrix unit (q38_gemm_q8k_*: grid (ceil(rows /
- * 128), ceil(T / 64)), 256 threads, the same arguments with one matrix). */
+/* From this many tokens the projections may run on the int8 matrix unit
+ * (q38_gemm_q8k_*: grid (ceil(rows / 128), ceil(T / 64)), 256 threads, the
+ * same arguments with one matrix; IQ4_NL from twice as many for matrices
+ * of under 8192 rows). */
 #define Q38_GEMM_MIN_TOKENS 16
 #define Q38_GEMM_ROWS 128
 #define Q38_GEMM_TOKENS 64
