@@ -1297,16 +1297,16 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
 
 /* The matrix-unit form with the blocks of a row split over the waves, for
  * grids that the 128-row x 64-token tiles would leave small (few rows or
- * few tokens): a workgroup of Q38_GEMM_KS_WAVES waves owns 32 rows x 32
- * tokens, and wave w takes blocks w, w + W, w + 2W, ... (W waves).  Each
+ * few tokens): a workgroup of W waves (Q38_GEMM_KS_WAVES, or
+ * Q38_GEMM_KS_WAVES_WIDE where the grid has at most a workgroup per CU)
+ * owns 32 rows x 32 tokens, and wave w takes blocks w, w + W, w + 2W, ...  Each
  * block's f32 terms are the ones gemm_q8k forms (gemm_tile_terms); a round
  * of W blocks leaves them in LDS, and the workgroup adds them to the row
  * totals in block order, so every output is the reference's sum bit for
  * bit.  The activations are read straight from the Q8_K rows (tokens past
  * the prompt read the last one; their outputs are not stored). */
-template <int TYPE>
+template <int TYPE, int W>
 Q38_DEV void gemm_ks_q8k(const q38_gemv_args &a) {
-    constexpr int W = Q38_GEMM_KS_WAVES;
     constexpr int kThreads = 64 * W;
     /* two rounds' terms: [round & 1][wave][element][lane] */
     __shared__ float terms[2][W][16][64];
@@ -1558,7 +1558,11 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq1s(q38_gemv_arg
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq1m(q38_gemv_args a) { gemm_q8k<Q38_GGML_IQ1_M>(a); }
 #define Q38_GEMM_KS(name, T)                                                                                      \
     extern "C" __global__ __launch_bounds__(64 * Q38_GEMM_KS_WAVES) void q38_gemm_ks_q8k_##name(q38_gemv_args a) { \
-        gemm_ks_q8k<T>(a);                                                                                        \
+        gemm_ks_q8k<T, Q38_GEMM_KS_WAVES>(a);                                                                     \
+    }                                                                                                             \
+    extern "C" __global__ __launch_bounds__(64 * Q38_GEMM_KS_WAVES_WIDE) void q38_gemm_ks16_q8k_##name(          \
+        q38_gemv_args a) {                                                                                        \
+        gemm_ks_q8k<T, Q38_GEMM_KS_WAVES_WIDE>(a);                                                                \
     }
 Q38_GEMM_KS(q4k, Q38_GGML_Q4_K)
 Q38_GEMM_KS(q5k, Q38_GGML_Q5_K)

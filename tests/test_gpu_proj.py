@@ -147,15 +147,17 @@ def test_gemv_multi_equals_single(ctx, ref, name, T):
 
 @pytest.mark.parametrize("name", sorted(TYPES))
 @pytest.mark.parametrize("rows,W,T", [(130, 1280, 32), (2050, 256, 33), (1100, 1280, 65), (700, HIDDEN, 130),
-                                      (2100, 2304, 64), (8200, 256, 16), (4100, 768, 1000)])
+                                      (2100, 2304, 64), (8200, 256, 16), (4200, 2304, 40), (4100, 768, 1000)])
 def test_gemm_many_tokens_bit_exact(ctx, ref, name, rows, W, T):
     """The matrix-unit forms from 16 tokens on, bit for bit against the
     oracle, with partial row and token tiles.  The split-block form (32 rows
-    x 32 tokens per workgroup, a row's blocks over 8 waves) where its grid
-    has 64 to 1280 workgroups: 1, 5, 9 and 20 blocks, so the last round of
-    8 is partial; 4100 x 1000 (4128 such workgroups) takes the 128-row x
-    64-token tiles, as IQ4_NL does from 32 tokens (16 for 8192+ rows);
-    130 x 1280 (5 workgroups) stays on the GEMV."""
+    x 32 tokens per workgroup, a row's blocks split over the waves) where
+    its grid has 64 to 1280 workgroups: on 16 waves up to 256 workgroups
+    (1, 5, 9 and 20 blocks, so the last round is partial), on 8 beyond
+    (8200 x 16 with 1 block, 4200 x 40 with 9); 4100 x 1000 (4128 such
+    workgroups) takes the 128-row x 64-token tiles, as IQ4_NL does from 32
+    tokens (16 for 8192+ rows); 130 x 1280 (5 workgroups) stays on the
+    GEMV."""
     ty = TYPES[name]
     x = _activations(T, W, 0x513338F0 + T + W)
     d_q = _quantize_on_device(ctx, x)
