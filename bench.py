@@ -27,7 +27,8 @@ prompt (with its conv/L2/gates and gated-norm kernels), prefill attention at
 context, batched paged decode,
 the launch floor, one-token linear_core over 48 layers, the 64-layer full
 stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
-the Q4_K/Q6_K FFN projections for 1 and 8 tokens and for prompts, one token
+the Q4_K/Q6_K FFN projections for 1 and 8 tokens and for prompts, a decode
+layer's projection chain with the input quantised apart or inside the GEMV, one token
 and a 4096-token prompt through one matrix in every weight format, and the
 recurrent-state checkpoint, each rotating over enough buffers to defeat the
 cache where the weights are streamed.
@@ -683,6 +684,72 @@ def _graph_replay_us(ctx, work, reps: int):
         hip.hipGraphDestroy(graph)
 
 
+def layer_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
+    """The projections of `layers` attention-layer decode steps in order, each
+    input quantised then projected (ops.rs:617-639): x -> q|gate 12288, k
+    1024, v 1024 rows; the attention output (6144) -> o 5120 rows; x -> gate
+    and up 17408 rows; the FFN activation (17408) -> down 5120 rows (Q4_K,
+    the down projection Q6_K; 232 MB a layer, 929 MB for 4).  Two forms of
+    the same chain, bit-identical outputs: q38_quantize_q8_k then
+    q38_gemv_q8_k_multi per input (8 launches a layer), and
+    q38_quantize_project_q8_k (4 launches a layer); microseconds per layer,
+    as plain launches and replayed from a captured HIP graph."""
+    mats = []
+    for li in range(layers):
+        lm = []
+        for ty, rows_list, width in ((12, [12288, 1024, 1024], 5120), (12, [5120], 6144), (12, [17408, 17408], 5120),
+                                     (14, [5120], 17408)):
+            ws = []
+            for mi, rows in enumerate(rows_list):
+                nbytes = rows * (width // 256) * QUANT_BLOCK_BYTES[ty]
+                w = ctx.empty((nbytes,), np.uint8)
+                ctx.fill_normal(w, nbytes // 4, 0x51335400 + 16 * li + 4 * mi + ty)
+                ws.append(w)
+            lm.append((ty, rows_list, width, ws))
+        mats.append(lm)
+    xs = {}
+    for width in (5120, 6144, 17408):
+        x = ctx.empty((n_tokens, width))
+        ctx.fill_normal(x, n_tokens * width, 0x51335500 + width)
+        xs[width] = (x, ctx.empty((ctx.q8k_bytes(n_tokens, width),), np.uint8))
+    outs = [ctx.empty((n_tokens, 17408)) for _ in range(3)]
+
+    def chain(fused):
+        for lm in mats:
+            for ty, rows_list, width, ws in lm:
+                x, q = xs[width]
+                o = outs[:len(rows_list)]
+                if fused:
+                    ctx.quantize_project_q8_k(ty, rows_list, width, ws, x, n_tokens, q, o)
+                else:
+                    ctx.quantize_q8_k(n_tokens, width, x, q)
+                    ctx.gemv_q8_k_multi(ty, rows_list, width, ws, q, n_tokens, o)
+
+    res = {"tokens": n_tokens, "layers": layers}
+    e0, e1 = ctx.event(), ctx.event()
+    for label, fused in (("separate", False), ("fused", True)):
+        chain(fused)
+        ctx.sync()
+        ctx.record(e0)
+        for _ in range(reps):
+            chain(fused)
+        ctx.record(e1)
+        res[f"{label}_us_per_layer"] = ctx.elapsed_ms(e0, e1) * 1e3 / (reps * layers)
+        g_us = _graph_replay_us(ctx, lambda: chain(fused), reps)
+        if g_us is not None:
+            res[f"{label}_graph_us_per_layer"] = g_us / layers
+    for lm in mats:
+        for _, _, _, ws in lm:
+            for w in ws:
+                w.free()
+    for x, q in xs.values():
+        x.free()
+        q.free()
+    for o in outs:
+        o.free()
+    return res
+
+
 def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
     """The FFN projections of `layers` layers (gate and up 17408x5120 Q4_K,
     down 5120x17408 Q6_K; 173 MB a layer, 693 MB for 4, beyond the 256 MB
@@ -977,6 +1044,9 @@ EXTRAS = {
                               lambda pkg, ctx: prompt_projections(pkg, ctx, 64, 5)),
     "prompt_projections_4096": ("FFN projections of one layer for a 4096-token prompt",
                                 lambda pkg, ctx: prompt_projections(pkg, ctx, 4096, 3)),
+    "layer_projections_1": ("the projections of 4 attention layers' decode steps, 1 token: quantise then project "
+                            "per input, as two calls and as one",
+                            lambda pkg, ctx: layer_projections(pkg, ctx, 1, 20)),
     "ffn_projections_1": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 1 token",
                           lambda pkg, ctx: ffn_projections(pkg, ctx, 1, 20)),
     "ffn_projections_8": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 8 tokens",

@@ -370,6 +370,20 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
 int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
                         const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out);
 
+/* quantize_input followed by project on each matrix of one input
+ * (ops.rs:617-639, called so by full_attention ops.rs:954-958 and the FFN
+ * ops.rs:1600-1613): the same as q38_quantize_q8_k(ctx, n_tokens, width,
+ * d_x, d_q8k) and then q38_gemv_q8_k_multi(ctx, ggml_type, n_mats, rows,
+ * width, d_weights, d_q8k, n_tokens, d_out), bit for bit, d_q8k (16-byte
+ * aligned, q38_q8k_bytes) holding the quantised input afterwards; d_x
+ * [n_tokens][width] f32, 16-byte aligned.  Where every matrix stays on the
+ * GEMV (below 16 tokens, or matrices too small for the matrix unit) it is
+ * one launch instead of two: each GEMV workgroup quantises the input
+ * itself.  Fails with -1 as those two calls do. */
+int q38_quantize_project_q8_k(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
+                              const void *const *d_weights, const float *d_x, int n_tokens, void *d_q8k,
+                              float *const *d_out);
+
 /* tensor_gemv_f32 / tensor_gemm_f32 (src/kernel/tensor.rs:1095-1129,
  * :1175-1215): the projection path of weights project() does not quantise
  * for (ops.rs:632-637), with f32 activations d_x [n_tokens][width]:

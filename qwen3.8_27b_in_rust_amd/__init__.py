@@ -104,6 +104,8 @@ _SIGNATURES = {
     "q38_gemv_f32": (c_int, [_P, c_int, c_int, c_int, _P, _P, c_int, _P]),
     "q38_gemv_q8_k_multi": (c_int, [_P, c_int, c_int, _I32P, c_int, POINTER(c_void_p), _P, c_int,
                                     POINTER(c_void_p)]),
+    "q38_quantize_project_q8_k": (c_int, [_P, c_int, c_int, _I32P, c_int, POINTER(c_void_p), _P, c_int, _P,
+                                          POINTER(c_void_p)]),
     "q38_attn_prefill": (c_int, [_P, c_int, c_int, c_int, c_int, _P, _P, _P, _P, _P]),
     "q38_gdn_step": (c_int, [_P, c_int, _P, c_int64, _P, _P, _P, _P, _P, _P]),
     "q38_gdn_prefill": (c_int, [_P, _P, c_int, _P, _P, _P, _P, _P, _P]),
@@ -334,6 +336,13 @@ class Context:
         o = (c_void_p * n)(*[_ptr(x) for x in outs])
         _check(lib().q38_gemv_q8_k_multi(self.handle, ggml_type, n, _i32(rows), width, w, _ptr(q8k), n_tokens, o),
                "q38_gemv_q8_k_multi")
+
+    def quantize_project_q8_k(self, ggml_type, rows, width, weights, x, n_tokens, q8k, outs):
+        n = len(rows)
+        w = (c_void_p * n)(*[_ptr(v) for v in weights])
+        o = (c_void_p * n)(*[_ptr(v) for v in outs])
+        _check(lib().q38_quantize_project_q8_k(self.handle, ggml_type, n, _i32(rows), width, w, _ptr(x), n_tokens,
+                                               _ptr(q8k), o), "q38_quantize_project_q8_k")
 
     def attn_pre(self, n_tokens, pos0, q_norm, k_norm, q_and_gate, key, q_out, gate_out, k_out):
         _check(lib().q38_attn_pre(self.handle, n_tokens, pos0, _ptr(q_norm), _ptr(k_norm), _ptr(q_and_gate),

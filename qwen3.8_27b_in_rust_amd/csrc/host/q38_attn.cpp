@@ -1903,8 +1903,12 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
     return ctx->launch(ctx->f_quantize_q8k, width / Q38_Q8K_BLOCK, n_tokens, 1, 64, &a);
 }
 
-int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
-                        const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out) {
+/* The projections of one input; d_x non-NULL: the f32 input, quantised into
+ * d_q8k as q38_quantize_q8_k does (by the GEMV itself when every matrix
+ * stays on it, else by a q38_quantize_q8k launch first). */
+static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
+                          const void *const *d_weights, const float *d_x, const void *d_q8k, int n_tokens,
+                          float *const *d_out) {
     if (ctx == nullptr) return fail("ctx is NULL");
     int ti_occ = -1; /* kGemv index */
     for (int i = 0; i < kGemvTypes; ++i)
@@ -1938,8 +1942,9 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
         if ((uintptr_t)d_weights[i] % 16 != 0) return fail("d_weights[%d] must be 16-byte aligned", i);
         ++n_nonempty;
     }
-    if (n_nonempty == 0) return 0;
     if (d_q8k == nullptr || (uintptr_t)d_q8k % 16 != 0) return fail("d_q8k is NULL or not 16-byte aligned");
+    if (d_x != nullptr && (uintptr_t)d_x % 16 != 0) return fail("d_x must be 16-byte aligned");
+    if (n_nonempty == 0) return d_x != nullptr ? q38_quantize_q8_k(ctx, n_tokens, width, d_x, const_cast<void *>(d_q8k)) : 0;
     if (((long)n_tokens + Q38_GEMM_KS_TOKENS - 1) / Q38_GEMM_KS_TOKENS > 65535) return fail("too many tokens");
 
     /* Many tokens: the int8 matrix-unit forms, one launch per matrix.  The
@@ -1954,10 +1959,10 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     const int ti = ti_occ;
     const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
     const long ks_tok_tiles = ((long)n_tokens + Q38_GEMM_KS_TOKENS - 1) / Q38_GEMM_KS_TOKENS;
-    bool on_gemv[Q38_GEMV_MAX_MATS] = {};
+    bool on_gemv[Q38_GEMV_MAX_MATS] = {}, on_ks[Q38_GEMV_MAX_MATS] = {};
+    bool any_gemm = false;
     for (int i = 0; i < n_mats; ++i) {
         if (rows[i] == 0) continue;
-        const long row_tiles = ((long)rows[i] + Q38_GEMM_ROWS - 1) / Q38_GEMM_ROWS;
         const long ks_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS * ks_tok_tiles;
         bool ks = false, big = false;
         if (ctx->f_gemm_ks[ti] != nullptr) {
@@ -1969,10 +1974,20 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
             big = n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
                   (n_tokens >= Q38_GEMM_MIN_TOKENS && rows[i] >= 64L * Q38_GEMM_ROWS);
         }
-        if (!ks && !big) {
-            on_gemv[i] = true;
-            continue;
-        }
+        on_gemv[i] = !ks && !big;
+        on_ks[i] = ks;
+        any_gemm = any_gemm || ks || big;
+    }
+    /* the matrix-unit forms read the quantised input from memory */
+    if (d_x != nullptr && any_gemm) {
+        if (q38_quantize_q8_k(ctx, n_tokens, width, d_x, const_cast<void *>(d_q8k))) return -1;
+        d_x = nullptr;
+    }
+    for (int i = 0; i < n_mats; ++i) {
+        if (rows[i] == 0 || on_gemv[i]) continue;
+        const bool ks = on_ks[i];
+        const long row_tiles = ((long)rows[i] + Q38_GEMM_ROWS - 1) / Q38_GEMM_ROWS;
+        const long ks_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS * ks_tok_tiles;
         q38_gemv_args g;
         memset(&g, 0, sizeof(g));
         g.weights[0] = static_cast<const uint8_t *>(d_weights[i]);
@@ -2055,6 +2070,7 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     a.wg_begin[kept] = (int32_t)wgs;
     a.n_mats = kept;
     a.q8k = d_q8k;
+    a.x = d_x;
     a.width = width;
     a.n_tokens = n_tokens;
     a.tok_pass = tok_pass;
@@ -2062,6 +2078,18 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
     const unsigned lds =
         (unsigned)(grid_lds + tok_pass * blocks * Q38_GEMV_REC_BYTES + tok_pass * max_per_wg * blocks * 4 * nt);
     return ctx->launch(f, (unsigned)grid, 1, 1, 256, &a, lds);
+}
+
+int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
+                        const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out) {
+    return gemv_q8k_multi(ctx, ggml_type, n_mats, rows, width, d_weights, nullptr, d_q8k, n_tokens, d_out);
+}
+
+int q38_quantize_project_q8_k(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
+                              const void *const *d_weights, const float *d_x, int n_tokens, void *d_q8k,
+                              float *const *d_out) {
+    if (d_x == nullptr && n_tokens > 0) return fail("d_x is NULL");
+    return gemv_q8k_multi(ctx, ggml_type, n_mats, rows, width, d_weights, d_x, d_q8k, n_tokens, d_out);
 }
 
 int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const void *d_q8k,

@@ -681,6 +681,121 @@ Q38_DEV void unit_terms_iq4nl(const Unit<Q38_GGML_IQ4_NL> &u, const UnitScales<Q
     }
 }
 
+/* The (|x|, first index) maximum of a row of 16 lanes: each lane offers its
+ * candidate (best = |x|, val = x, idx = position in the block); a larger
+ * |x| wins, equal ones go to the lower index, so the order of the
+ * exchanges does not matter.  Four DPP steps (quad swaps, half-row and row
+ * mirrors) leave the row's winner in all 16 lanes. */
+Q38_DEV void row16_argmax(float &best, float &val, int &idx) {
+    auto step = [&](auto ctrl_tag) {
+        constexpr int ctrl = decltype(ctrl_tag)::value;
+        const float ob = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, best), ctrl,
+                                                                                0xF, 0xF, false));
+        const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, val), ctrl,
+                                                                                0xF, 0xF, false));
+        const int oi = __builtin_amdgcn_update_dpp(0, idx, ctrl, 0xF, 0xF, false);
+        if (ob > best || (ob == best && oi < idx)) {
+            best = ob;
+            val = ov;
+            idx = oi;
+        }
+    };
+    step(std::integral_constant<int, 0xB1>{});  /* quad_perm 1,0,3,2 */
+    step(std::integral_constant<int, 0x4E>{});  /* quad_perm 2,3,0,1 */
+    step(std::integral_constant<int, 0x141>{}); /* row_half_mirror */
+    step(std::integral_constant<int, 0x140>{}); /* row_mirror */
+}
+
+/* quantize_q8_k of one 256-value block (src/kernel/quant.rs:97-128) by a
+ * row of 16 lanes, lane g holding values 16 g .. 16 g + 15 in v: the same
+ * arithmetic as q8k_quantize_block (the first value of largest |x| sets
+ * inverse_scale = -127 / x, each value min(nearest(inverse_scale x), 127)).
+ * qw: the lane's 16 quants packed 4 per word; gsum: their sum (the block's
+ * group sum g); scale: 1 / inverse_scale.  An all-zero block gives zeros. */
+Q38_DEV void q8k_quantize_group16(const f32x4 (&v)[4], int g, uint32_t (&qw)[4], int &gsum, float &scale) {
+    float best = fabsf(v[0].x), val = v[0].x;
+    int idx = 16 * g;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (c == 0 && e == 0) continue;
+            if (fabsf(v[c][e]) > best) {
+                best = fabsf(v[c][e]);
+                val = v[c][e];
+                idx = 16 * g + 4 * c + e;
+            }
+        }
+    row16_argmax(best, val, idx);
+    if (best == 0.0f) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qw[c] = 0u;
+        gsum = 0;
+        scale = 0.0f;
+        return;
+    }
+    const float inverse_scale = -127.0f / val;
+    int sum = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        int q[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = min(q38_nearest_int(inverse_scale * v[c][e]), 127);
+        sum += q[0] + q[1] + q[2] + q[3];
+        qw[c] = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
+                ((uint32_t)(q[3] & 255) << 24);
+    }
+    gsum = sum;
+    scale = 1.0f / inverse_scale;
+}
+
+/* quantize_q8_k of one 256-value block (src/kernel/quant.rs:97-128) by
+ * one wave, lane l holding values 4l .. 4l+3 in v: the value of largest
+ * |x| (the first such, as the reference's scan keeps it) sets
+ * inverse_scale = -127 / x; each value becomes min(nearest(inverse_scale
+ * x), 127).  Returns the lane's 4 quants packed in a word; gsum (on lanes
+ * l % 4 == 0) is the sum of values 4l .. 4l+15's quants, scale the
+ * block's 1 / inverse_scale.  An all-zero block gives zeros. */
+Q38_DEV uint32_t q8k_quantize_block(const f32x4 v, int lane, int &gsum, float &scale) {
+    float best = fabsf(v.x), val = v.x;
+    int idx = 4 * lane;
+#pragma unroll
+    for (int c = 1; c < 4; ++c) {
+        if (fabsf(v[c]) > best) {
+            best = fabsf(v[c]);
+            val = v[c];
+            idx = 4 * lane + c;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ob = __shfl_xor(best, m, 64);
+        const float ov = __shfl_xor(val, m, 64);
+        const int oi = __shfl_xor(idx, m, 64);
+        if (ob > best || (ob == best && oi < idx)) {
+            best = ob;
+            val = ov;
+            idx = oi;
+        }
+    }
+    if (best == 0.0f) {
+        gsum = 0;
+        scale = 0.0f;
+        return 0u;
+    }
+    const float inverse_scale = -127.0f / val;
+    int q[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = min(q38_nearest_int(inverse_scale * v[c]), 127);
+    int sum = q[0] + q[1] + q[2] + q[3];
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    gsum = sum;
+    scale = 1.0f / inverse_scale;
+    return (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
+           ((uint32_t)(q[3] & 255) << 24);
+}
+
 /*
  * A workgroup owns rows [row0, row0 + R) of one of up to Q38_GEMV_MAX_MATS
  * matrices that read the same activations, and the tokens [tok0, tok0 + tp);
@@ -744,9 +859,6 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     float *terms = lscales + nrec;                                           /* [tp][units][NT] */
     const size_t g0 = (size_t)row0 * B;
 
-    Unit<TYPE> w[2];
-    load_unit<TYPE>(weights, g0 + min(tid, units - 1), w[0]);
-
     /* the tokens' blocks are contiguous from token tok0 in each of the three
      * planes: quants [T][W], sums [T][B][16], scales [T][B] */
     const int8_t *quants = static_cast<const int8_t *>(a.q8k) + (size_t)tok0 * width;
@@ -755,32 +867,89 @@ Q38_DEV void gemv_q8k(const q38_gemv_args &a) {
     sums += (size_t)tok0 * B * 16;
     const int nblk = tp * B;
     const int nq16 = nblk * 16, ns16 = nblk * 2; /* 16-byte pieces of quants and of sums */
-    {
-        /* the first 4 quant pieces, one sums piece and one scale of every
-         * thread loaded before any is written (one memory round trip; a
-         * copy loop would wait for each load in turn); indices past the end
-         * reload the last piece and are not written */
-        u32x4 qv[4], sv;
-        float sc;
+    const bool from_x = a.x != nullptr;
+    const int g = tid & 15;
+    const float *xs = a.x + (size_t)tok0 * width;
+    /* the activations' first loads go out before the weights' (loads return
+     * in order): with the f32 input, the first two rounds of 16 blocks (see
+     * below); else the first 4 quant pieces, one sums piece and one scale of
+     * every thread (indices past the end reload the last piece and are not
+     * written) */
+    f32x4 v0[2][4];
+    u32x4 qv[4], sv;
+    float sc;
+    if (from_x) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int i = min(16 * r + (tid >> 4), nblk - 1);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v0[r][c] = q38_ld4(xs + (size_t)i * 256 + 16 * g + 4 * c);
+        }
+    } else {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             qv[k] = *reinterpret_cast<const u32x4 *>(quants + (size_t)min(256 * k + tid, nq16 - 1) * 16);
         sv = *reinterpret_cast<const u32x4 *>(sums + (size_t)min(tid, ns16 - 1) * 8);
         sc = scales[min(tid, nblk - 1)];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int p = 256 * k + tid;
-            if (p < nq16) *reinterpret_cast<u32x4 *>(recs + (p >> 4) * kRec + (p & 15) * 16) = qv[k];
-        }
-        if (tid < ns16) *reinterpret_cast<u32x4 *>(lsums + tid * 8) = sv;
-        if (tid < nblk) lscales[tid] = sc;
     }
-    for (int p = 1024 + tid; p < nq16; p += 256)
-        *reinterpret_cast<u32x4 *>(recs + (p >> 4) * kRec + (p & 15) * 16) =
-            *reinterpret_cast<const u32x4 *>(quants + (size_t)p * 16);
-    for (int p = 256 + tid; p < ns16; p += 256)
-        *reinterpret_cast<u32x4 *>(lsums + p * 8) = *reinterpret_cast<const u32x4 *>(sums + (size_t)p * 8);
-    for (int p = 256 + tid; p < nblk; p += 256) lscales[p] = scales[p];
+    Unit<TYPE> w[2];
+    load_unit<TYPE>(weights, g0 + min(tid, units - 1), w[0]);
+
+    if (from_x) {
+        /* quantise the pass's tokens from the f32 input: block i (token
+         * tok0 + i / B, block i % B, values x[tok0 * W + 256 i ..]) by the
+         * 16 threads 16 (i % 16) .. + 15 of a round of 16 blocks, thread
+         * 16 b + g holding values 16 g .. 16 g + 15, two rounds' loads at a
+         * time.  The first row group of the pass also stores them to q8k. */
+        const bool store = grp == 0;
+        int8_t *gq = const_cast<int8_t *>(quants);
+        int16_t *gs = const_cast<int16_t *>(sums);
+        float *gsc = const_cast<float *>(scales);
+        for (int i0 = 0; i0 < nblk; i0 += 32) {
+            f32x4 v[2][4];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int i = min(i0 + 16 * r + (tid >> 4), nblk - 1);
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    v[r][c] = i0 == 0 ? v0[r][c] : q38_ld4(xs + (size_t)i * 256 + 16 * g + 4 * c);
+            }
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int i = i0 + 16 * r + (tid >> 4);
+                uint32_t qw[4];
+                int gsum;
+                float scale;
+                q8k_quantize_group16(v[r], g, qw, gsum, scale);
+                if (i < nblk) {
+                    *reinterpret_cast<u32x4 *>(recs + i * kRec + 16 * g) = u32x4{qw[0], qw[1], qw[2], qw[3]};
+                    lsums[i * 16 + g] = (int16_t)gsum;
+                    if (g == 0) lscales[i] = scale;
+                    if (store) {
+                        *reinterpret_cast<u32x4 *>(gq + (size_t)i * 256 + 16 * g) = u32x4{qw[0], qw[1], qw[2], qw[3]};
+                        gs[(size_t)i * 16 + g] = (int16_t)gsum;
+                        if (g == 0) gsc[i] = scale;
+                    }
+                }
+            }
+        }
+    } else {
+        {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int p = 256 * k + tid;
+                if (p < nq16) *reinterpret_cast<u32x4 *>(recs + (p >> 4) * kRec + (p & 15) * 16) = qv[k];
+            }
+            if (tid < ns16) *reinterpret_cast<u32x4 *>(lsums + tid * 8) = sv;
+            if (tid < nblk) lscales[tid] = sc;
+        }
+        for (int p = 1024 + tid; p < nq16; p += 256)
+            *reinterpret_cast<u32x4 *>(recs + (p >> 4) * kRec + (p & 15) * 16) =
+                *reinterpret_cast<const u32x4 *>(quants + (size_t)p * 16);
+        for (int p = 256 + tid; p < ns16; p += 256)
+            *reinterpret_cast<u32x4 *>(lsums + p * 8) = *reinterpret_cast<const u32x4 *>(sums + (size_t)p * 8);
+        for (int p = 256 + tid; p < nblk; p += 256) lscales[p] = scales[p];
+    }
     __syncthreads();
 
 #pragma unroll
@@ -1469,47 +1638,12 @@ extern "C" __global__ __launch_bounds__(64) void q38_quantize_q8k(q38_quantize_a
     float *scales = reinterpret_cast<float *>(sums + (size_t)a.n_tokens * blocks * 16);
     const size_t k = (size_t)tok * blocks + b;
     const f32x4 v = q38_ld4(a.x + (size_t)tok * width + (size_t)b * Q38_Q8K_BLOCK + 4 * lane);
-
-    /* the first element of the block with the largest |x| */
-    float best = fabsf(v.x), val = v.x;
-    int idx = 4 * lane;
-#pragma unroll
-    for (int c = 1; c < 4; ++c) {
-        if (fabsf(v[c]) > best) {
-            best = fabsf(v[c]);
-            val = v[c];
-            idx = 4 * lane + c;
-        }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ob = __shfl_xor(best, m, 64);
-        const float ov = __shfl_xor(val, m, 64);
-        const int oi = __shfl_xor(idx, m, 64);
-        if (ob > best || (ob == best && oi < idx)) {
-            best = ob;
-            val = ov;
-            idx = oi;
-        }
-    }
-    int8_t *qo = quants + k * Q38_Q8K_BLOCK;
-    if (best == 0.0f) {
-        reinterpret_cast<uint32_t *>(qo)[lane] = 0u;
-        if (lane < 16) sums[k * 16 + lane] = 0;
-        if (lane == 0) scales[k] = 0.0f;
-        return;
-    }
-    const float inverse_scale = -127.0f / val;
-    int q[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) q[c] = min(q38_nearest_int(inverse_scale * v[c]), 127);
-    reinterpret_cast<uint32_t *>(qo)[lane] = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) |
-                                             ((uint32_t)(q[2] & 255) << 16) | ((uint32_t)(q[3] & 255) << 24);
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if ((lane & 3) == 0) sums[k * 16 + lane / 4] = (int16_t)s;
-    if (lane == 0) scales[k] = 1.0f / inverse_scale;
+    int gsum;
+    float scale;
+    const uint32_t qw = q8k_quantize_block(v, lane, gsum, scale);
+    reinterpret_cast<uint32_t *>(quants + k * Q38_Q8K_BLOCK)[lane] = qw;
+    if ((lane & 3) == 0) sums[k * 16 + lane / 4] = (int16_t)gsum;
+    if (lane == 0) scales[k] = scale;
 }
 
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q4k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q4_K>(a); }

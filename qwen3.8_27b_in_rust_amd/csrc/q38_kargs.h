@@ -354,6 +354,10 @@ typedef struct {
     int32_t wg_begin[Q38_GEMV_MAX_MATS + 1];
     int32_t n_mats;
     const void *q8k; /* planar Q8_K of T tokens */
+    /* GEMV only: when set, the f32 input [T][width] -- each workgroup
+     * quantises the tokens of its pass itself, and the first row group of
+     * each pass also writes them to q8k */
+    const float *x;
     int32_t width;
     int32_t n_tokens;
     int32_t tok_pass;

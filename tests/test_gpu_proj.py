@@ -146,6 +146,43 @@ def test_gemv_multi_equals_single(ctx, ref, name, T):
 
 
 @pytest.mark.parametrize("name", sorted(TYPES))
+@pytest.mark.parametrize("rows,W,T", [([1500, 0, 96, 1], 1280, 1), ([257, 64], HIDDEN, 3),
+                                      ([300, 40], 17408, 9), ([1500, 96], 1280, 40)])
+def test_quantize_project_equals_separate_calls(ctx, ref, name, rows, W, T):
+    """quantize_input then project in one call (q38_quantize_project_q8_k):
+    every output and every byte of the quantised input as
+    q38_quantize_q8_k + q38_gemv_q8_k_multi, and the oracle.  Below 16
+    tokens the GEMV quantises the input itself (17408-wide rows: passes of
+    3, 3 and 3 tokens, each pass's first row group storing its tokens); at
+    40 tokens the 1500-row matrix takes the matrix unit, so the input is
+    quantised by its own launch first."""
+    ty = TYPES[name]
+    x = _activations(T, W, 0x51333900 + T + W)
+    d_x = ctx.array(x)
+    q8 = ref.quantize_q8_k(x)
+    wbs = [_random_kquant(ty, max(r, 1), W, 0x51333901 + ty + i)[:r] for i, r in enumerate(rows)]
+    d_ws = [ctx.array(wb, np.uint8) if r else None for wb, r in zip(wbs, rows)]
+    nq = ctx.q8k_bytes(T, W)
+    d_q_sep = ctx.empty((nq,), np.uint8)
+    d_q_fused = ctx.empty((nq,), np.uint8)
+    ctx.fill_normal(d_q_fused, nq // 4, 0x5133390F)  # stale bytes that the call must overwrite
+    outs_sep = [ctx.empty((T, max(r, 1))) for r in rows]
+    outs_fused = [ctx.empty((T, max(r, 1))) for r in rows]
+    ctx.quantize_q8_k(T, W, d_x, d_q_sep)
+    ctx.gemv_q8_k_multi(ty, rows, W, d_ws, d_q_sep, T, outs_sep)
+    ctx.quantize_project_q8_k(ty, rows, W, d_ws, d_x, T, d_q_fused, outs_fused)
+    assert np.array_equal(d_q_fused.download(), d_q_sep.download())
+    assert np.array_equal(d_q_fused.download(), q8)
+    for wb, r, a_, b_ in zip(wbs, rows, outs_sep, outs_fused):
+        if r == 0:
+            continue
+        got = b_.download()
+        assert np.array_equal(got.view(np.uint32), a_.download().view(np.uint32))
+        want = ref.gemv_q8_k(ty, wb, q8, T, W, threads=16)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", sorted(TYPES))
 @pytest.mark.parametrize("rows,W,T", [(130, 1280, 32), (2050, 256, 33), (1100, 1280, 65), (700, HIDDEN, 130),
                                       (2100, 2304, 64), (8200, 256, 16), (4200, 2304, 40), (4100, 768, 1000)])
 def test_gemm_many_tokens_bit_exact(ctx, ref, name, rows, W, T):
