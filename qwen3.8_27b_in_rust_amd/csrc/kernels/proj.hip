@@ -1670,9 +1670,13 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_iq4xs(q38_gemv_ar
 }
 /* Q6_K, IQ4_XS, IQ2_XS, IQ2_S and IQ3_XXS are held to 168 registers (three
  * workgroups per CU; a few dwords spill): 4096-token prompts through
- * 17408 x 5120 ran 3-10% faster than at 169-178 registers and two. */
+ * 17408 x 5120 ran 3-10% faster than at 169-178 registers and two.  Q5_K
+ * is held to 256 (two workgroups; 4 dwords spill): left free it takes 259
+ * and one, 2.20 against 1.83 ms. */
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q4k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q4_K>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q5k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q5_K>(a); }
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void q38_gemm_q8k_q5k(q38_gemv_args a) {
+    gemm_q8k<Q38_GGML_Q5_K>(a);
+}
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void q38_gemm_q8k_q6k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q6_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q2k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q2_K>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_q3k(q38_gemv_args a) { gemm_q8k<Q38_GGML_Q3_K>(a); }
