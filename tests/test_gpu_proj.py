@@ -270,6 +270,19 @@ def test_projection_argument_checks(pkg, ctx):
         ctx.gemv_q8_k_multi(12, [4, 4], 256, [q, None], q, 1, [o, o])
     with pytest.raises(pkg.Q38Error, match="multiple of 256"):
         pkg.Context.q8k_bytes(1, 100)
+    with pytest.raises(pkg.Q38Error, match="d_x is NULL"):
+        ctx.quantize_project_q8_k(12, [4], 256, [q], None, 1, q, [o])
+    with pytest.raises(pkg.Q38Error, match="d_x must be 16-byte aligned"):
+        ctx.quantize_project_q8_k(12, [4], 256, [q], x.offset(1), 1, q, [o])
+    with pytest.raises(pkg.Q38Error, match="unsupported quant type"):
+        ctx.quantize_project_q8_k(8, [4], 256, [q], x, 1, q, [o])
+    # every matrix empty: only the quantisation runs
+    xs = ctx.array(np.linspace(-2.0, 2.0, 256, dtype=np.float32))
+    q2 = ctx.empty((ctx.q8k_bytes(1, 256),), np.uint8)
+    ctx.quantize_project_q8_k(12, [0], 256, [None], xs, 1, q2, [None])
+    q3 = ctx.empty((ctx.q8k_bytes(1, 256),), np.uint8)
+    ctx.quantize_q8_k(1, 256, xs, q3)
+    assert np.array_equal(q2.download(), q3.download())
 
 
 def test_projections_feed_full_core(pkg, ctx, ref, margin, synth):
