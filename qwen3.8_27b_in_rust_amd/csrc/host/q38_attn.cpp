@@ -1900,7 +1900,7 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
     a.q8k = d_q8k;
     a.width = width;
     a.n_tokens = n_tokens;
-    return ctx->launch(ctx->f_quantize_q8k, width / Q38_Q8K_BLOCK, n_tokens, 1, 64, &a);
+    return ctx->launch(ctx->f_quantize_q8k, (width / Q38_Q8K_BLOCK + 15) / 16, n_tokens, 1, 256, &a);
 }
 
 /* The projections of one input; d_x non-NULL: the f32 input, quantised into

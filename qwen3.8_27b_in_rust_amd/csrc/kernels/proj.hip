@@ -707,9 +707,10 @@ Q38_DEV void row16_argmax(float &best, float &val, int &idx) {
 }
 
 /* quantize_q8_k of one 256-value block (src/kernel/quant.rs:97-128) by a
- * row of 16 lanes, lane g holding values 16 g .. 16 g + 15 in v: the same
- * arithmetic as q8k_quantize_block (the first value of largest |x| sets
- * inverse_scale = -127 / x, each value min(nearest(inverse_scale x), 127)).
+ * row of 16 lanes, lane g holding values 16 g .. 16 g + 15 in v: the value
+ * of largest |x| (the first such, as the reference's scan keeps it) sets
+ * inverse_scale = -127 / x; each value becomes min(nearest(inverse_scale
+ * x), 127).
  * qw: the lane's 16 quants packed 4 per word; gsum: their sum (the block's
  * group sum g); scale: 1 / inverse_scale.  An all-zero block gives zeros. */
 Q38_DEV void q8k_quantize_group16(const f32x4 (&v)[4], int g, uint32_t (&qw)[4], int &gsum, float &scale) {
@@ -747,53 +748,6 @@ Q38_DEV void q8k_quantize_group16(const f32x4 (&v)[4], int g, uint32_t (&qw)[4],
     }
     gsum = sum;
     scale = 1.0f / inverse_scale;
-}
-
-/* quantize_q8_k of one 256-value block (src/kernel/quant.rs:97-128) by
- * one wave, lane l holding values 4l .. 4l+3 in v: the value of largest
- * |x| (the first such, as the reference's scan keeps it) sets
- * inverse_scale = -127 / x; each value becomes min(nearest(inverse_scale
- * x), 127).  Returns the lane's 4 quants packed in a word; gsum (on lanes
- * l % 4 == 0) is the sum of values 4l .. 4l+15's quants, scale the
- * block's 1 / inverse_scale.  An all-zero block gives zeros. */
-Q38_DEV uint32_t q8k_quantize_block(const f32x4 v, int lane, int &gsum, float &scale) {
-    float best = fabsf(v.x), val = v.x;
-    int idx = 4 * lane;
-#pragma unroll
-    for (int c = 1; c < 4; ++c) {
-        if (fabsf(v[c]) > best) {
-            best = fabsf(v[c]);
-            val = v[c];
-            idx = 4 * lane + c;
-        }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ob = __shfl_xor(best, m, 64);
-        const float ov = __shfl_xor(val, m, 64);
-        const int oi = __shfl_xor(idx, m, 64);
-        if (ob > best || (ob == best && oi < idx)) {
-            best = ob;
-            val = ov;
-            idx = oi;
-        }
-    }
-    if (best == 0.0f) {
-        gsum = 0;
-        scale = 0.0f;
-        return 0u;
-    }
-    const float inverse_scale = -127.0f / val;
-    int q[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) q[c] = min(q38_nearest_int(inverse_scale * v[c]), 127);
-    int sum = q[0] + q[1] + q[2] + q[3];
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    gsum = sum;
-    scale = 1.0f / inverse_scale;
-    return (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
-           ((uint32_t)(q[3] & 255) << 24);
 }
 
 /*
@@ -1627,23 +1581,31 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq4nl(q38_gemv_ar
     }
 }
 
-extern "C" __global__ __launch_bounds__(64) void q38_quantize_q8k(q38_quantize_args a) {
-    const int b = blockIdx.x;
+extern "C" __global__ __launch_bounds__(256) void q38_quantize_q8k(q38_quantize_args a) {
+    /* block 16 x + t / 16 of token y by the 16 threads 16 (t / 16) .. + 15,
+     * thread g holding values 16 g .. 16 g + 15 (q8k_quantize_group16) */
+    const int b = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int g = threadIdx.x & 15;
     const int tok = blockIdx.y;
-    const int lane = threadIdx.x;
     const int width = a.width;
     const int blocks = width / Q38_Q8K_BLOCK;
+    const int bc = min(b, blocks - 1); /* rows past the last block work on it and store nothing */
     int8_t *quants = static_cast<int8_t *>(a.q8k);
     int16_t *sums = reinterpret_cast<int16_t *>(quants + (size_t)a.n_tokens * width);
     float *scales = reinterpret_cast<float *>(sums + (size_t)a.n_tokens * blocks * 16);
-    const size_t k = (size_t)tok * blocks + b;
-    const f32x4 v = q38_ld4(a.x + (size_t)tok * width + (size_t)b * Q38_Q8K_BLOCK + 4 * lane);
+    const size_t k = (size_t)tok * blocks + bc;
+    const float *x = a.x + (size_t)tok * width + (size_t)bc * Q38_Q8K_BLOCK + 16 * g;
+    f32x4 v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = q38_ld4(x + 4 * c);
+    uint32_t qw[4];
     int gsum;
     float scale;
-    const uint32_t qw = q8k_quantize_block(v, lane, gsum, scale);
-    reinterpret_cast<uint32_t *>(quants + k * Q38_Q8K_BLOCK)[lane] = qw;
-    if ((lane & 3) == 0) sums[k * 16 + lane / 4] = (int16_t)gsum;
-    if (lane == 0) scales[k] = scale;
+    q8k_quantize_group16(v, g, qw, gsum, scale);
+    if (b >= blocks) return;
+    *reinterpret_cast<u32x4 *>(quants + k * Q38_Q8K_BLOCK + 16 * g) = u32x4{qw[0], qw[1], qw[2], qw[3]};
+    sums[k * 16 + g] = (int16_t)gsum;
+    if (g == 0) scales[k] = scale;
 }
 
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_q8k_q4k(q38_gemv_args a) { gemv_q8k<Q38_GGML_Q4_K>(a); }

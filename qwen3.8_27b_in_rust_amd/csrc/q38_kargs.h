@@ -310,7 +310,7 @@ typedef struct {
 #define Q38_GEMV_REC_BYTES (272 + 32 + 4) /* LDS bytes of one staged Q8_K block: padded quants, sums, scale */
 #define Q38_GEMV_ACT_LDS (64 * 1024) /* LDS for staged activations when tokens > 1 */
 
-/* quantize_q8_k: grid (B, T), 64 threads (one wave per block). */
+/* quantize_q8_k: grid (ceil(B / 16), T), 256 threads (16 per block). */
 typedef struct {
     const float *x; /* [T][W] */
     void *q8k;      /* planar, Q38_Q8K_BYTES(T, W) */
