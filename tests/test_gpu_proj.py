@@ -208,6 +208,47 @@ def test_gemm_many_tokens_bit_exact(ctx, ref, name, rows, W, T):
     assert bad.size == 0, (bad.size, bad[:5], got.reshape(-1)[bad[:5]], want.reshape(-1)[bad[:5]])
 
 
+def _ran(ctx, kernel, call):
+    """Whether call() launched kernel (the library's per-dispatch timer)."""
+    ctx.kernel_timer_start(kernel, 8)
+    call()
+    _, n = ctx.kernel_timer_stop()
+    return n > 0
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "IQ2_S", "IQ4_NL"])
+def test_projection_path_boundaries(ctx, ref, name):
+    """The library's choice between the GEMV and the matrix-unit forms at
+    each of its boundaries (16 tokens; 64 split-block workgroups of 32 rows
+    x 32 tokens; one workgroup per CU for the 16-wave form; 5 per CU, past
+    which the 128 x 64 tiles run): the expected kernel runs on each side, and
+    every output is the oracle's bit for bit.  IQ4_NL has no split-block
+    form and takes the 128 x 64 tiles from 32 tokens (16 for 8192+ rows)."""
+    ty = TYPES[name]
+    sfx = {"Q4_K": "q4k", "Q6_K": "q6k", "IQ2_S": "iq2s", "IQ4_NL": "iq4nl"}[name]
+    cus = ctx.info()["cu_count"]
+    W = 256
+    cases = [  # rows, tokens, kernel expected
+        (2048, 15, "q38_gemv_q8k_"), (2048, 16, "q38_gemm_ks16_q8k_"), (2016, 16, "q38_gemv_q8k_"),
+        (32 * cus, 16, "q38_gemm_ks16_q8k_"), (32 * cus + 1, 16, "q38_gemm_ks_q8k_"),
+        (32 * 5 * cus, 16, "q38_gemm_ks_q8k_"), (32 * 5 * cus + 1, 16, "q38_gemm_q8k_"),
+    ]
+    if name == "IQ4_NL":
+        cases = [(2048, 31, "q38_gemv_q8k_"), (2048, 32, "q38_gemm_q8k_"), (8191, 16, "q38_gemv_q8k_"),
+                 (8192, 16, "q38_gemm_q8k_")]
+    for rows, T, kern in cases:
+        x = _activations(T, W, 0x51333A00 + T + rows)
+        d_q = _quantize_on_device(ctx, x)
+        wb = _random_kquant(ty, rows, W, 0x51333A01 + ty + rows)
+        d_w = ctx.array(wb, np.uint8)
+        d_o = ctx.empty((T, rows))
+        assert _ran(ctx, kern + sfx, lambda: ctx.gemv_q8_k(ty, rows, W, d_w, d_q, T, d_o)), (rows, T, kern)
+        want = ref.gemv_q8_k(ty, wb, ref.quantize_q8_k(x), T, W, threads=16)
+        assert np.array_equal(d_o.download().view(np.uint32), want.view(np.uint32)), (rows, T)
+        for arr in (d_q, d_w, d_o):
+            arr.free()
+
+
 @pytest.mark.parametrize("name", sorted(F32_TYPES))
 @pytest.mark.parametrize("rows,W,T", [(48, HIDDEN, 1), (48, HIDDEN, 3), (257, 1024, 9), (5, 6144, 17),
                                       (1031, 2048, 1)])
