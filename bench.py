@@ -914,12 +914,12 @@ INT8_PEAK_TOPS = 5000.0
 
 def _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps):
     """Kernel time per call of one projection and the kernel that ran it:
-    the split-block matrix-unit form (16 or 8 waves), the 128 x 64 one or
+    the split-block matrix-unit form (16, 8 or 4 waves), the 128 x 64 one or
     the GEMV, as the library chose for the shape."""
     gemv = GEMV_KERNELS[ty]
     kernels = (gemv.replace("q38_gemv_q8k_", "q38_gemm_ks16_q8k_"), gemv.replace("q38_gemv_q8k_", "q38_gemm_ks_q8k_"),
-               gemv.replace("gemv", "gemm"), gemv)
-    for kern in kernels if ty != 20 else kernels[2:]:  # IQ4_NL has no split-block form
+               gemv.replace("q38_gemv_q8k_", "q38_gemm_ks4_q8k_"), gemv.replace("gemv", "gemm"), gemv)
+    for kern in kernels if ty != 20 else kernels[3:]:  # IQ4_NL has no split-block form
         ctx.kernel_timer_start(kern, reps * 64)
         for _ in range(reps):
             ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)

@@ -90,8 +90,8 @@ bool is_full_attention(int layer) { return layer >= 0 && ((layer + 1) % 4 == 0 |
 
 /* The weight formats of the Q8_K GEMV (tensor_gemv_q8_k's types,
  * tensor.rs:70-75): the GEMV kernel, its many-token form on the int8
- * matrix unit and that form with a row's blocks split over 8 or 16 waves
- * (for small grids), f32 terms per block in a row's sum, and the bytes of the
+ * matrix unit and that form with a row's blocks split over 8, 16 or 4
+ * waves (for small grids), f32 terms per block in a row's sum, and the bytes of the
  * lattice grid an IQ kernel copies into LDS. */
 struct GemvType {
     int ggml_type;
@@ -99,24 +99,25 @@ struct GemvType {
     const char *gemm_kernel;
     const char *gemm_ks_kernel;
     const char *gemm_ks16_kernel;
+    const char *gemm_ks4_kernel;
     int terms;
     int grid_bytes;
 };
 constexpr GemvType kGemv[] = {
-    {Q38_GGML_Q4_K, "q38_gemv_q8k_q4k", "q38_gemm_q8k_q4k", "q38_gemm_ks_q8k_q4k", "q38_gemm_ks16_q8k_q4k", 1, 0},
-    {Q38_GGML_Q5_K, "q38_gemv_q8k_q5k", "q38_gemm_q8k_q5k", "q38_gemm_ks_q8k_q5k", "q38_gemm_ks16_q8k_q5k", 1, 0},
-    {Q38_GGML_Q6_K, "q38_gemv_q8k_q6k", "q38_gemm_q8k_q6k", "q38_gemm_ks_q8k_q6k", "q38_gemm_ks16_q8k_q6k", 1, 0},
-    {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", "q38_gemm_q8k_q3k", "q38_gemm_ks_q8k_q3k", "q38_gemm_ks16_q8k_q3k", 1, 0},
-    {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", "q38_gemm_q8k_iq4xs", "q38_gemm_ks_q8k_iq4xs", "q38_gemm_ks16_q8k_iq4xs", 1, 0},
-    {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", "q38_gemm_q8k_q2k", "q38_gemm_ks_q8k_q2k", "q38_gemm_ks16_q8k_q2k", 1, 0},
-    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", "q38_gemm_q8k_iq4nl", nullptr, nullptr, 8, 0},
-    {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", "q38_gemm_q8k_iq2xxs", "q38_gemm_ks_q8k_iq2xxs", "q38_gemm_ks16_q8k_iq2xxs", 1, 256 * 8},
-    {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", "q38_gemm_q8k_iq2xs", "q38_gemm_ks_q8k_iq2xs", "q38_gemm_ks16_q8k_iq2xs", 1, 512 * 8},
-    {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", "q38_gemm_q8k_iq2s", "q38_gemm_ks_q8k_iq2s", "q38_gemm_ks16_q8k_iq2s", 1, 1024 * 8},
-    {Q38_GGML_IQ3_XXS, "q38_gemv_q8k_iq3xxs", "q38_gemm_q8k_iq3xxs", "q38_gemm_ks_q8k_iq3xxs", "q38_gemm_ks16_q8k_iq3xxs", 1, 256 * 4},
-    {Q38_GGML_IQ3_S, "q38_gemv_q8k_iq3s", "q38_gemm_q8k_iq3s", "q38_gemm_ks_q8k_iq3s", "q38_gemm_ks16_q8k_iq3s", 1, 512 * 4},
-    {Q38_GGML_IQ1_S, "q38_gemv_q8k_iq1s", "q38_gemm_q8k_iq1s", "q38_gemm_ks_q8k_iq1s", "q38_gemm_ks16_q8k_iq1s", 1, 2048 * 8},
-    {Q38_GGML_IQ1_M, "q38_gemv_q8k_iq1m", "q38_gemm_q8k_iq1m", "q38_gemm_ks_q8k_iq1m", "q38_gemm_ks16_q8k_iq1m", 1, 2048 * 8},
+    {Q38_GGML_Q4_K, "q38_gemv_q8k_q4k", "q38_gemm_q8k_q4k", "q38_gemm_ks_q8k_q4k", "q38_gemm_ks16_q8k_q4k", "q38_gemm_ks4_q8k_q4k", 1, 0},
+    {Q38_GGML_Q5_K, "q38_gemv_q8k_q5k", "q38_gemm_q8k_q5k", "q38_gemm_ks_q8k_q5k", "q38_gemm_ks16_q8k_q5k", "q38_gemm_ks4_q8k_q5k", 1, 0},
+    {Q38_GGML_Q6_K, "q38_gemv_q8k_q6k", "q38_gemm_q8k_q6k", "q38_gemm_ks_q8k_q6k", "q38_gemm_ks16_q8k_q6k", "q38_gemm_ks4_q8k_q6k", 1, 0},
+    {Q38_GGML_Q3_K, "q38_gemv_q8k_q3k", "q38_gemm_q8k_q3k", "q38_gemm_ks_q8k_q3k", "q38_gemm_ks16_q8k_q3k", "q38_gemm_ks4_q8k_q3k", 1, 0},
+    {Q38_GGML_IQ4_XS, "q38_gemv_q8k_iq4xs", "q38_gemm_q8k_iq4xs", "q38_gemm_ks_q8k_iq4xs", "q38_gemm_ks16_q8k_iq4xs", "q38_gemm_ks4_q8k_iq4xs", 1, 0},
+    {Q38_GGML_Q2_K, "q38_gemv_q8k_q2k", "q38_gemm_q8k_q2k", "q38_gemm_ks_q8k_q2k", "q38_gemm_ks16_q8k_q2k", "q38_gemm_ks4_q8k_q2k", 1, 0},
+    {Q38_GGML_IQ4_NL, "q38_gemv_q8k_iq4nl", "q38_gemm_q8k_iq4nl", nullptr, nullptr, nullptr, 8, 0},
+    {Q38_GGML_IQ2_XXS, "q38_gemv_q8k_iq2xxs", "q38_gemm_q8k_iq2xxs", "q38_gemm_ks_q8k_iq2xxs", "q38_gemm_ks16_q8k_iq2xxs", "q38_gemm_ks4_q8k_iq2xxs", 1, 256 * 8},
+    {Q38_GGML_IQ2_XS, "q38_gemv_q8k_iq2xs", "q38_gemm_q8k_iq2xs", "q38_gemm_ks_q8k_iq2xs", "q38_gemm_ks16_q8k_iq2xs", "q38_gemm_ks4_q8k_iq2xs", 1, 512 * 8},
+    {Q38_GGML_IQ2_S, "q38_gemv_q8k_iq2s", "q38_gemm_q8k_iq2s", "q38_gemm_ks_q8k_iq2s", "q38_gemm_ks16_q8k_iq2s", "q38_gemm_ks4_q8k_iq2s", 1, 1024 * 8},
+    {Q38_GGML_IQ3_XXS, "q38_gemv_q8k_iq3xxs", "q38_gemm_q8k_iq3xxs", "q38_gemm_ks_q8k_iq3xxs", "q38_gemm_ks16_q8k_iq3xxs", "q38_gemm_ks4_q8k_iq3xxs", 1, 256 * 4},
+    {Q38_GGML_IQ3_S, "q38_gemv_q8k_iq3s", "q38_gemm_q8k_iq3s", "q38_gemm_ks_q8k_iq3s", "q38_gemm_ks16_q8k_iq3s", "q38_gemm_ks4_q8k_iq3s", 1, 512 * 4},
+    {Q38_GGML_IQ1_S, "q38_gemv_q8k_iq1s", "q38_gemm_q8k_iq1s", "q38_gemm_ks_q8k_iq1s", "q38_gemm_ks16_q8k_iq1s", "q38_gemm_ks4_q8k_iq1s", 1, 2048 * 8},
+    {Q38_GGML_IQ1_M, "q38_gemv_q8k_iq1m", "q38_gemm_q8k_iq1m", "q38_gemm_ks_q8k_iq1m", "q38_gemm_ks16_q8k_iq1m", "q38_gemm_ks4_q8k_iq1m", 1, 2048 * 8},
 };
 constexpr int kGemvTypes = (int)(sizeof(kGemv) / sizeof(kGemv[0]));
 /* The split-block GEMM's grid: at least this many workgroups (fewer: the
@@ -156,6 +157,7 @@ struct q38_ctx {
     hipFunction_t f_gemm[kGemvTypes] = {};    /* by kGemv index: the int8 matrix-unit form */
     hipFunction_t f_gemm_ks[kGemvTypes] = {};   /* and its split-block form */
     hipFunction_t f_gemm_ks16[kGemvTypes] = {}; /* ... on 16 waves */
+    hipFunction_t f_gemm_ks4[kGemvTypes] = {};  /* ... on 4 waves */
     hipFunction_t f_gemv_q8k[kGemvTypes] = {}; /* by kGemv index */
     hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
     hipModule_t mod_synth = nullptr;
@@ -445,6 +447,8 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
             Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_ks[i], ctx->mod_proj, kGemv[i].gemm_ks_kernel));
         if (kGemv[i].gemm_ks16_kernel != nullptr)
             Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_ks16[i], ctx->mod_proj, kGemv[i].gemm_ks16_kernel));
+        if (kGemv[i].gemm_ks4_kernel != nullptr)
+            Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_ks4[i], ctx->mod_proj, kGemv[i].gemm_ks4_kernel));
     }
     const std::string p_synth = dir + "/synth.hsaco";
     Q38_HIP(hipModuleLoad(&ctx->mod_synth, p_synth.c_str()));
@@ -637,6 +641,7 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
             if (kGemv[i].gemm_kernel != nullptr && name == kGemv[i].gemm_kernel) f = ctx->f_gemm[i];
             if (kGemv[i].gemm_ks_kernel != nullptr && name == kGemv[i].gemm_ks_kernel) f = ctx->f_gemm_ks[i];
             if (kGemv[i].gemm_ks16_kernel != nullptr && name == kGemv[i].gemm_ks16_kernel) f = ctx->f_gemm_ks16[i];
+            if (kGemv[i].gemm_ks4_kernel != nullptr && name == kGemv[i].gemm_ks4_kernel) f = ctx->f_gemm_ks4[i];
         }
         if (f == nullptr) return fail("unknown kernel %s", kernel_name);
     }
@@ -1952,8 +1957,8 @@ static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *ro
      * Q38_GEMM_MIN_TOKENS tokens on where its grid has at least
      * kGemmKsMinTiles workgroups (on fewer, e.g. 1024 x 5120 below 64
      * tokens, the GEMV is faster), while it has at most kGemmKsMaxPerCu
-     * workgroups per CU (16 waves each where it has at most one, else 8);
-     * beyond that the 128 x 64 tiles (measured on the FFN, q|gate and k
+     * workgroups per CU (16, 8 or 4 waves each, below); beyond that the
+     * 128 x 64 tiles (measured on the FFN, q|gate and k
      * matrices, 4-512 tokens).  IQ4_NL, which has only
      * the 128 x 64 form, takes it from 32 tokens (16 for 8192+ rows). */
     const int ti = ti_occ;
@@ -1999,11 +2004,19 @@ static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *ro
         g.n_tokens = n_tokens;
         if (ks) {
             const long ks_row_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS;
-            /* at most a workgroup per CU: 16 waves split the blocks */
-            const bool wide = ks_tiles <= (long)ctx->cu_count && ctx->f_gemm_ks16[ti] != nullptr;
-            if (ctx->launch(wide ? ctx->f_gemm_ks16[ti] : ctx->f_gemm_ks[ti], (unsigned)ks_row_tiles,
-                            (unsigned)ks_tok_tiles, 1, 64 * (wide ? Q38_GEMM_KS_WAVES_WIDE : Q38_GEMM_KS_WAVES), &g))
-                return -1;
+            /* waves per workgroup by workgroups per CU: up to one, 16 waves
+             * split the blocks; up to 1.5, 8; beyond, 4 (measured on the FFN,
+             * q|gate and k matrices at 16-256 tokens) */
+            hipFunction_t fk = ctx->f_gemm_ks[ti];
+            int waves = Q38_GEMM_KS_WAVES;
+            if (ks_tiles <= (long)ctx->cu_count && ctx->f_gemm_ks16[ti] != nullptr) {
+                fk = ctx->f_gemm_ks16[ti];
+                waves = Q38_GEMM_KS_WAVES_WIDE;
+            } else if (2 * ks_tiles > 3L * ctx->cu_count && ctx->f_gemm_ks4[ti] != nullptr) {
+                fk = ctx->f_gemm_ks4[ti];
+                waves = Q38_GEMM_KS_WAVES_NARROW;
+            }
+            if (ctx->launch(fk, (unsigned)ks_row_tiles, (unsigned)ks_tok_tiles, 1, 64 * waves, &g)) return -1;
         } else if (ctx->launch(ctx->f_gemm[ti], (unsigned)row_tiles, (unsigned)tok_tiles, 1, 256, &g)) {
             return -1;
         }

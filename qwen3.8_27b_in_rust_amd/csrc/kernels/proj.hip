@@ -1420,9 +1420,8 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
 
 /* The matrix-unit form with the blocks of a row split over the waves, for
  * grids that the 128-row x 64-token tiles would leave small (few rows or
- * few tokens): a workgroup of W waves (Q38_GEMM_KS_WAVES, or
- * Q38_GEMM_KS_WAVES_WIDE where the grid has at most a workgroup per CU)
- * owns 32 rows x 32 tokens, and wave w takes blocks w, w + W, w + 2W, ...  Each
+ * few tokens): a workgroup of W waves (16, 8 or 4 as the grid has at most
+ * one workgroup per CU, 1.5, or more) owns 32 rows x 32 tokens, and wave w takes blocks w, w + W, w + 2W, ...  Each
  * block's f32 terms are the ones gemm_q8k forms (gemm_tile_terms); a round
  * of W blocks leaves them in LDS, and the workgroup adds them to the row
  * totals in block order, so every output is the reference's sum bit for
@@ -1663,6 +1662,10 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemm_q8k_iq1m(q38_gemv_arg
     extern "C" __global__ __launch_bounds__(64 * Q38_GEMM_KS_WAVES_WIDE) void q38_gemm_ks16_q8k_##name(          \
         q38_gemv_args a) {                                                                                        \
         gemm_ks_q8k<T, Q38_GEMM_KS_WAVES_WIDE>(a);                                                                \
+    }                                                                                                             \
+    extern "C" __global__ __launch_bounds__(64 * Q38_GEMM_KS_WAVES_NARROW) void q38_gemm_ks4_q8k_##name(         \
+        q38_gemv_args a) {                                                                                        \
+        gemm_ks_q8k<T, Q38_GEMM_KS_WAVES_NARROW>(a);                                                              \
     }
 Q38_GEMM_KS(q4k, Q38_GGML_Q4_K)
 Q38_GEMM_KS(q5k, Q38_GGML_Q5_K)

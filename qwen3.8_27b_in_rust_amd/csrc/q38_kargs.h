@@ -343,9 +343,11 @@ typedef struct {
 #define Q38_GEMM_KS_ROWS 32
 #define Q38_GEMM_KS_TOKENS 32
 #define Q38_GEMM_KS_WAVES 8
-/* ... and 16 waves (q38_gemm_ks16_q8k_*, 1024 threads, one workgroup per CU)
- * where that grid has at most one workgroup per CU */
+/* ... 16 waves (q38_gemm_ks16_q8k_*, 1024 threads, one workgroup per CU)
+ * where that grid has at most one workgroup per CU, and 4 waves
+ * (q38_gemm_ks4_q8k_*, 256 threads) where it has more than 1.5 */
 #define Q38_GEMM_KS_WAVES_WIDE 16
+#define Q38_GEMM_KS_WAVES_NARROW 4
 typedef struct {
     const uint8_t *weights[Q38_GEMV_MAX_MATS]; /* [rows][B * block_bytes], 16-byte aligned */
     float *out[Q38_GEMV_MAX_MATS];             /* [T][rows] */

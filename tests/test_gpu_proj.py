@@ -220,8 +220,9 @@ def _ran(ctx, kernel, call):
 def test_projection_path_boundaries(ctx, ref, name):
     """The library's choice between the GEMV and the matrix-unit forms at
     each of its boundaries (16 tokens; 64 split-block workgroups of 32 rows
-    x 32 tokens; one workgroup per CU for the 16-wave form; 5 per CU, past
-    which the 128 x 64 tiles run): the expected kernel runs on each side, and
+    x 32 tokens; one workgroup per CU for the 16-wave form, 1.5 for the
+    8-wave one, 5 for the 4-wave one, past which the 128 x 64 tiles run):
+    the expected kernel runs on each side, and
     every output is the oracle's bit for bit.  IQ4_NL has no split-block
     form and takes the 128 x 64 tiles from 32 tokens (16 for 8192+ rows)."""
     ty = TYPES[name]
@@ -231,7 +232,8 @@ def test_projection_path_boundaries(ctx, ref, name):
     cases = [  # rows, tokens, kernel expected
         (2048, 15, "q38_gemv_q8k_"), (2048, 16, "q38_gemm_ks16_q8k_"), (2016, 16, "q38_gemv_q8k_"),
         (32 * cus, 16, "q38_gemm_ks16_q8k_"), (32 * cus + 1, 16, "q38_gemm_ks_q8k_"),
-        (32 * 5 * cus, 16, "q38_gemm_ks_q8k_"), (32 * 5 * cus + 1, 16, "q38_gemm_q8k_"),
+        (48 * cus, 16, "q38_gemm_ks_q8k_"), (48 * cus + 1, 16, "q38_gemm_ks4_q8k_"),
+        (32 * 5 * cus, 16, "q38_gemm_ks4_q8k_"), (32 * 5 * cus + 1, 16, "q38_gemm_q8k_"),
     ]
     if name == "IQ4_NL":
         cases = [(2048, 31, "q38_gemv_q8k_"), (2048, 32, "q38_gemm_q8k_"), (8191, 16, "q38_gemv_q8k_"),
