@@ -363,10 +363,13 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
  * full_attention, ops.rs:954-958; ffn gate and up, ops.rs:1600-1613): up
  * to 4 matrices of one type and width, matrix i with rows[i] rows at
  * d_weights[i], its output at d_out[i] [n_tokens][rows[i]], in one launch.
- * Each output equals q38_gemv_q8_k's for that matrix bit for bit; the
- * matrices that stay on the GEMV stream back to back in one launch, so the
- * start and end of a launch are paid once (those on the matrix unit take a
- * launch each). */
+ * Each output equals q38_gemv_q8_k's for that matrix bit for bit, and the
+ * matrices share launches: below 16 tokens every matrix streams through one
+ * GEMV launch; from 16 on, a matrix whose 32-row x 32-token grid exceeds 5
+ * workgroups per CU takes the 128 x 64 tiles, a launch of its own, and the
+ * others share one split-block launch where their grids add up to 64
+ * workgroups (the GEMV otherwise), so a matrix may take another form here
+ * than alone (IQ4_NL: each matrix as in q38_gemv_q8_k). */
 int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
                         const void *const *d_weights, const void *d_q8k, int n_tokens, float *const *d_out);
 

@@ -1952,47 +1952,45 @@ static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *ro
     if (n_nonempty == 0) return d_x != nullptr ? q38_quantize_q8_k(ctx, n_tokens, width, d_x, const_cast<void *>(d_q8k)) : 0;
     if (((long)n_tokens + Q38_GEMM_KS_TOKENS - 1) / Q38_GEMM_KS_TOKENS > 65535) return fail("too many tokens");
 
-    /* Many tokens: the int8 matrix-unit forms, one launch per matrix.  The
-     * split-block form (32 rows x 32 tokens per workgroup) from
-     * Q38_GEMM_MIN_TOKENS tokens on where its grid has at least
-     * kGemmKsMinTiles workgroups (on fewer, e.g. 1024 x 5120 below 64
-     * tokens, the GEMV is faster), while it has at most kGemmKsMaxPerCu
-     * workgroups per CU (16, 8 or 4 waves each, below); beyond that the
-     * 128 x 64 tiles (measured on the FFN, q|gate and k
-     * matrices, 4-512 tokens).  IQ4_NL, which has only
-     * the 128 x 64 form, takes it from 32 tokens (16 for 8192+ rows). */
+    /* Many tokens: the int8 matrix-unit forms.  A matrix whose split-block
+     * grid (32 rows x 32 tokens per workgroup) would exceed kGemmKsMaxPerCu
+     * workgroups per CU takes the 128 x 64 tiles, a launch of its own; from
+     * Q38_GEMM_MIN_TOKENS tokens on, the others share one split-block launch
+     * where their grids add up to at least kGemmKsMinTiles workgroups (on
+     * fewer, e.g. 1024 x 5120 alone below 64 tokens, the GEMV is faster)
+     * (measured on the FFN, q|gate and k matrices, 4-512 tokens).  IQ4_NL,
+     * which has only the 128 x 64 form, takes it from 32 tokens (16 for
+     * 8192+ rows). */
     const int ti = ti_occ;
     const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
     const long ks_tok_tiles = ((long)n_tokens + Q38_GEMM_KS_TOKENS - 1) / Q38_GEMM_KS_TOKENS;
-    bool on_gemv[Q38_GEMV_MAX_MATS] = {}, on_ks[Q38_GEMV_MAX_MATS] = {};
-    bool any_gemm = false;
+    bool on_gemv[Q38_GEMV_MAX_MATS] = {}, on_big[Q38_GEMV_MAX_MATS] = {};
+    bool any_gemm = false, ks_call = false;
+    long ks_total = 0; /* workgroups of the shared split-block launch */
     for (int i = 0; i < n_mats; ++i) {
         if (rows[i] == 0) continue;
-        const long ks_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS * ks_tok_tiles;
-        bool ks = false, big = false;
         if (ctx->f_gemm_ks[ti] != nullptr) {
-            if (n_tokens >= Q38_GEMM_MIN_TOKENS && ks_tiles >= kGemmKsMinTiles) {
-                ks = ks_tiles <= kGemmKsMaxPerCu * (long)ctx->cu_count;
-                big = !ks;
-            }
+            const long ks_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS * ks_tok_tiles;
+            on_big[i] = n_tokens >= Q38_GEMM_MIN_TOKENS && ks_tiles > kGemmKsMaxPerCu * (long)ctx->cu_count;
+            if (!on_big[i]) ks_total += ks_tiles;
         } else if (has_gemm) {
-            big = n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
-                  (n_tokens >= Q38_GEMM_MIN_TOKENS && rows[i] >= 64L * Q38_GEMM_ROWS);
+            on_big[i] = n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
+                        (n_tokens >= Q38_GEMM_MIN_TOKENS && rows[i] >= 64L * Q38_GEMM_ROWS);
         }
-        on_gemv[i] = !ks && !big;
-        on_ks[i] = ks;
-        any_gemm = any_gemm || ks || big;
+        any_gemm = any_gemm || on_big[i];
     }
+    if (ctx->f_gemm_ks[ti] != nullptr)
+        ks_call = n_tokens >= Q38_GEMM_MIN_TOKENS && ks_total >= kGemmKsMinTiles;
+    any_gemm = any_gemm || ks_call;
+    for (int i = 0; i < n_mats; ++i) on_gemv[i] = rows[i] > 0 && !on_big[i] && !ks_call;
     /* the matrix-unit forms read the quantised input from memory */
     if (d_x != nullptr && any_gemm) {
         if (q38_quantize_q8_k(ctx, n_tokens, width, d_x, const_cast<void *>(d_q8k))) return -1;
         d_x = nullptr;
     }
     for (int i = 0; i < n_mats; ++i) {
-        if (rows[i] == 0 || on_gemv[i]) continue;
-        const bool ks = on_ks[i];
+        if (!on_big[i]) continue;
         const long row_tiles = ((long)rows[i] + Q38_GEMM_ROWS - 1) / Q38_GEMM_ROWS;
-        const long ks_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS * ks_tok_tiles;
         q38_gemv_args g;
         memset(&g, 0, sizeof(g));
         g.weights[0] = static_cast<const uint8_t *>(d_weights[i]);
@@ -2002,24 +2000,41 @@ static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *ro
         g.q8k = d_q8k;
         g.width = width;
         g.n_tokens = n_tokens;
-        if (ks) {
-            const long ks_row_tiles = ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS;
-            /* waves per workgroup by workgroups per CU: up to one, 16 waves
-             * split the blocks; up to 1.5, 8; beyond, 4 (measured on the FFN,
-             * q|gate and k matrices at 16-256 tokens) */
-            hipFunction_t fk = ctx->f_gemm_ks[ti];
-            int waves = Q38_GEMM_KS_WAVES;
-            if (ks_tiles <= (long)ctx->cu_count && ctx->f_gemm_ks16[ti] != nullptr) {
-                fk = ctx->f_gemm_ks16[ti];
-                waves = Q38_GEMM_KS_WAVES_WIDE;
-            } else if (2 * ks_tiles > 3L * ctx->cu_count && ctx->f_gemm_ks4[ti] != nullptr) {
-                fk = ctx->f_gemm_ks4[ti];
-                waves = Q38_GEMM_KS_WAVES_NARROW;
-            }
-            if (ctx->launch(fk, (unsigned)ks_row_tiles, (unsigned)ks_tok_tiles, 1, 64 * waves, &g)) return -1;
-        } else if (ctx->launch(ctx->f_gemm[ti], (unsigned)row_tiles, (unsigned)tok_tiles, 1, 256, &g)) {
-            return -1;
+        if (ctx->launch(ctx->f_gemm[ti], (unsigned)row_tiles, (unsigned)tok_tiles, 1, 256, &g)) return -1;
+    }
+    if (ks_call) {
+        /* workgroup x serves 32-row tile x - wg_begin[m] of the launch's
+         * matrix m.  Waves per workgroup by workgroups per CU: up to one, 16
+         * waves split the blocks; up to 1.5, 8; beyond, 4 (measured on the
+         * FFN, q|gate and k matrices at 16-256 tokens) */
+        q38_gemv_args g;
+        memset(&g, 0, sizeof(g));
+        long row_tiles = 0;
+        int m = 0;
+        for (int i = 0; i < n_mats; ++i) {
+            if (rows[i] == 0 || on_big[i]) continue;
+            g.weights[m] = static_cast<const uint8_t *>(d_weights[i]);
+            g.out[m] = d_out[i];
+            g.rows[m] = rows[i];
+            g.wg_begin[m] = (int32_t)row_tiles;
+            row_tiles += ((long)rows[i] + Q38_GEMM_KS_ROWS - 1) / Q38_GEMM_KS_ROWS;
+            ++m;
         }
+        g.wg_begin[m] = (int32_t)row_tiles;
+        g.n_mats = m;
+        g.q8k = d_q8k;
+        g.width = width;
+        g.n_tokens = n_tokens;
+        hipFunction_t fk = ctx->f_gemm_ks[ti];
+        int waves = Q38_GEMM_KS_WAVES;
+        if (ks_total <= (long)ctx->cu_count && ctx->f_gemm_ks16[ti] != nullptr) {
+            fk = ctx->f_gemm_ks16[ti];
+            waves = Q38_GEMM_KS_WAVES_WIDE;
+        } else if (2 * ks_total > 3L * ctx->cu_count && ctx->f_gemm_ks4[ti] != nullptr) {
+            fk = ctx->f_gemm_ks4[ti];
+            waves = Q38_GEMM_KS_WAVES_NARROW;
+        }
+        if (ctx->launch(fk, (unsigned)row_tiles, (unsigned)ks_tok_tiles, 1, 64 * waves, &g)) return -1;
     }
 
     /* The GEMV over the other matrices, in one launch.  Tokens per pass: as

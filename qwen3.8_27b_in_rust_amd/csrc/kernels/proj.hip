@@ -1421,12 +1421,15 @@ Q38_DEV void gemm_q8k(const q38_gemv_args &a) {
 /* The matrix-unit form with the blocks of a row split over the waves, for
  * grids that the 128-row x 64-token tiles would leave small (few rows or
  * few tokens): a workgroup of W waves (16, 8 or 4 as the grid has at most
- * one workgroup per CU, 1.5, or more) owns 32 rows x 32 tokens, and wave w takes blocks w, w + W, w + 2W, ...  Each
- * block's f32 terms are the ones gemm_q8k forms (gemm_tile_terms); a round
- * of W blocks leaves them in LDS, and the workgroup adds them to the row
- * totals in block order, so every output is the reference's sum bit for
- * bit.  The activations are read straight from the Q8_K rows (tokens past
- * the prompt read the last one; their outputs are not stored). */
+ * one workgroup per CU, 1.5, or more) owns 32 rows x 32 tokens, and wave w
+ * takes blocks w, w + W, w + 2W, ...  Each block's f32 terms are the ones
+ * gemm_q8k forms (gemm_tile_terms); a round of W blocks leaves them in LDS,
+ * and the workgroup adds them to the row totals in block order, so every
+ * output is the reference's sum bit for bit.  The activations are read
+ * straight from the Q8_K rows (tokens past the prompt read the last one;
+ * their outputs are not stored).  Up to Q38_GEMV_MAX_MATS matrices of one
+ * input share a launch: matrix m takes the 32-row tiles wg_begin[m] ..
+ * wg_begin[m+1]-1 along x. */
 template <int TYPE, int W>
 Q38_DEV void gemm_ks_q8k(const q38_gemv_args &a) {
     constexpr int kThreads = 64 * W;
@@ -1446,8 +1449,14 @@ Q38_DEV void gemm_ks_q8k(const q38_gemv_args &a) {
     const uint32_t hm = lane_half_mask(h);
     const int width = a.width;
     const int B = width / Q38_Q8K_BLOCK;
-    const int rows = a.rows[0];
-    const int row0 = blockIdx.x * Q38_GEMM_KS_ROWS;
+    /* the matrix of this 32-row tile: matrices take consecutive tile ranges */
+    int mat = 0;
+#pragma unroll
+    for (int i = 1; i < Q38_GEMV_MAX_MATS; ++i) mat += (i < a.n_mats && (int)blockIdx.x >= a.wg_begin[i]) ? 1 : 0;
+    const uint8_t *weights = a.weights[mat];
+    float *out = a.out[mat];
+    const int rows = a.rows[mat];
+    const int row0 = ((int)blockIdx.x - a.wg_begin[mat]) * Q38_GEMM_KS_ROWS;
     const int rowc = min(row0 + (lane & 31), rows - 1);
     const int t0 = blockIdx.y * Q38_GEMM_KS_TOKENS;
     const int T = a.n_tokens;
@@ -1471,8 +1480,8 @@ Q38_DEV void gemm_ks_q8k(const q38_gemv_args &a) {
         const int b = r * W + wave;
         if (b < B) {
             Unit<TYPE> u;
-            if constexpr (kGemmHalfUnit<TYPE>) load_unit_half<TYPE>(a.weights[0], (size_t)rowc * B + b, h, u);
-            else load_unit<TYPE>(a.weights[0], (size_t)rowc * B + b, u);
+            if constexpr (kGemmHalfUnit<TYPE>) load_unit_half<TYPE>(weights, (size_t)rowc * B + b, h, u);
+            else load_unit<TYPE>(weights, (size_t)rowc * B + b, u);
             i32x4 A[8];
 #pragma unroll
             for (int st = 0; st < 8; ++st) A[st] = *reinterpret_cast<const i32x4 *>(arow + b * 256 + 32 * st);
@@ -1498,7 +1507,7 @@ Q38_DEV void gemm_ks_q8k(const q38_gemv_args &a) {
     for (int k = 0; k < kOwn; ++k) {
         const int idx = tid + kThreads * k, e = idx >> 6, l = idx & 63;
         const int tok = t0 + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3), row = row0 + (l & 31);
-        if (tok < T && row < rows) a.out[0][(size_t)tok * rows + row] = total[k];
+        if (tok < T && row < rows) out[(size_t)tok * rows + row] = total[k];
     }
 }
 

@@ -122,8 +122,7 @@ def test_gemv_multi_equals_single(ctx, ref, name, T):
     """Several matrices on one input in one launch (q|gate, k, v of a layer
     are 12288, 1024, 1024 rows; here smaller, with an empty matrix and a
     one-row one): every output bit for bit as the single-matrix launch and
-    the oracle.  At 40 tokens the 1500-row matrix takes the matrix unit and
-    the small ones the GEMV, in one call."""
+    the oracle.  At 40 tokens the three share one split-block launch."""
     ty = TYPES[name]
     W = 1280
     x = _activations(T, W, 0x513338E0 + T)
@@ -249,6 +248,40 @@ def test_projection_path_boundaries(ctx, ref, name):
         assert np.array_equal(d_o.download().view(np.uint32), want.view(np.uint32)), (rows, T)
         for arr in (d_q, d_w, d_o):
             arr.free()
+
+
+@pytest.mark.parametrize("name", ["Q4_K", "Q5_K", "IQ3_S"])
+def test_multi_matrices_share_the_split_block_launch(ctx, ref, name):
+    """The path of a multi-matrix call at 16 tokens: a matrix past 5
+    split-block workgroups per CU takes the 128 x 64 tiles on its own, and
+    the others share one split-block launch when their grids add up to 64
+    workgroups, though neither would take it alone (63 and 2); every output
+    is the single-matrix call's and the oracle's bit for bit."""
+    ty = TYPES[name]
+    sfx = {"Q4_K": "q4k", "Q5_K": "q5k", "IQ3_S": "iq3s"}[name]
+    cus = ctx.info()["cu_count"]
+    W, T = 256, 16
+    x = _activations(T, W, 0x51333B00)
+    d_q = _quantize_on_device(ctx, x)
+    q8 = ref.quantize_q8_k(x)
+    rows = [2016, 160 * cus + 1, 0, 33]
+    wbs = [_random_kquant(ty, max(r, 1), W, 0x51333B01 + ty + i)[:r] for i, r in enumerate(rows)]
+    d_ws = [ctx.array(wb, np.uint8) if r else None for wb, r in zip(wbs, rows)]
+    d_os = [ctx.empty((T, max(r, 1))) for r in rows]
+    call = lambda: ctx.gemv_q8_k_multi(ty, rows, W, d_ws, d_q, T, d_os)
+    assert _ran(ctx, "q38_gemm_q8k_" + sfx, call)
+    assert _ran(ctx, "q38_gemm_ks16_q8k_" + sfx, call)
+    assert not _ran(ctx, "q38_gemv_q8k_" + sfx, call)
+    for i, (wb, r, d_w, d_o) in enumerate(zip(wbs, rows, d_ws, d_os)):
+        if r == 0:
+            continue
+        got = d_o.download()
+        want = ref.gemv_q8_k(ty, wb, q8, T, W, threads=16)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), r
+        if i != 1:  # alone, the small matrices take the GEMV: the same bits
+            single = ctx.empty((T, r))
+            assert _ran(ctx, "q38_gemv_q8k_" + sfx, lambda: ctx.gemv_q8_k(ty, r, W, d_w, d_q, T, single))
+            assert np.array_equal(got.view(np.uint32), single.download().view(np.uint32)), r
 
 
 @pytest.mark.parametrize("name", sorted(F32_TYPES))
