@@ -910,6 +910,46 @@ def weight_formats_prompt(pkg, ctx, n_tokens: int, reps: int):
 
 
 INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+F32_PATH_TYPES = {0: ("F32", 4.0), 1: ("F16", 2.0), 30: ("BF16", 2.0), 8: ("Q8_0", 34.0 / 32.0)}
+
+
+def f32_path(pkg, ctx, reps: int):
+    """The projection path of weights project() does not quantise for
+    (q38_gemv_f32: F32, F16, BF16, Q8_0) through 17408 x 5120 at 1 and 4096
+    tokens and the 48-row beta / alpha shape (48 x 5120) at 4096: kernel
+    duration, the kernel the library chose (GEMV below 16 tokens, the bf16
+    matrix unit from 16 on), weight bytes per second and useful f32
+    operations per second (2 x rows x width x tokens; the matrix unit runs 3,
+    5 or 6 bf16 products per multiply for BF16/Q8_0, F16, F32 weights).
+    Weights are random bytes (timing only)."""
+    res = {}
+    for rows, width, n_tokens in ((17408, 5120, 1), (17408, 5120, 4096), (48, 5120, 4096)):
+        x = ctx.empty((n_tokens, width))
+        ctx.fill_normal(x, n_tokens * width, 0x51335600 + n_tokens)
+        out = ctx.empty((n_tokens, rows))
+        for ty, (name, bpw) in F32_PATH_TYPES.items():
+            nbytes = int(rows * width * bpw)
+            w = ctx.empty((nbytes + 16,), np.uint8)
+            ctx.fill_normal(w, (nbytes + 16) // 4, 0x51335610 + ty, sigma=0.05)
+            ctx.gemv_f32(ty, rows, width, w, x, n_tokens, out)
+            ctx.sync()
+            sfx = name.lower()
+            for kern in ("q38_gemm_f32_" + sfx, "q38_gemv_f32_" + sfx):
+                ctx.kernel_timer_start(kern, reps)
+                for _ in range(reps):
+                    ctx.gemv_f32(ty, rows, width, w, x, n_tokens, out)
+                k_ms, k_n = ctx.kernel_timer_stop()
+                if k_n > 0:
+                    break
+            ms = k_ms / reps
+            res[f"{name}_{rows}x{width}_T{n_tokens}"] = {
+                "kernel": kern, "ms": round(ms, 4), "weights_gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "tflop_s": round(2.0 * rows * width * n_tokens / (ms * 1e-3) / 1e12, 2)}
+            w.free()
+        x.free()
+        out.free()
+    return res
 
 
 def _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps):
@@ -1055,6 +1095,8 @@ EXTRAS = {
                          lambda pkg, ctx: weight_formats(pkg, ctx, 3)),
     "weight_formats_prompt_4096": ("a 4096-token prompt through a 17408x5120 matrix in each Q8_K weight format",
                                    lambda pkg, ctx: weight_formats_prompt(pkg, ctx, 4096, 2)),
+    "f32_path_projections": ("F32/F16/BF16/Q8_0 weights (the f32-input path) at 1 and 4096 tokens",
+                             lambda pkg, ctx: f32_path(pkg, ctx, 3)),
 }
 
 

@@ -160,6 +160,7 @@ struct q38_ctx {
     hipFunction_t f_gemm_ks4[kGemvTypes] = {};  /* ... on 4 waves */
     hipFunction_t f_gemv_q8k[kGemvTypes] = {}; /* by kGemv index */
     hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
+    hipFunction_t f_gemm_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* the same, on the matrix unit */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
     hipFunction_t f_copy = nullptr;
@@ -435,6 +436,10 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[1], ctx->mod_proj, "q38_gemv_f32_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[2], ctx->mod_proj, "q38_gemv_f32_bf16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[3], ctx->mod_proj, "q38_gemv_f32_q8_0"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[0], ctx->mod_proj, "q38_gemm_f32_f32"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[1], ctx->mod_proj, "q38_gemm_f32_f16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[2], ctx->mod_proj, "q38_gemm_f32_bf16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[3], ctx->mod_proj, "q38_gemm_f32_q8_0"));
     for (int i = 0; i < kGemvTypes; ++i) {
         int n = 0;
         Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, ctx->f_gemv_q8k[i], 256, 0));
@@ -629,6 +634,10 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemv_f32_f16") f = ctx->f_gemv_f32[1];
     else if (name == "q38_gemv_f32_bf16") f = ctx->f_gemv_f32[2];
     else if (name == "q38_gemv_f32_q8_0") f = ctx->f_gemv_f32[3];
+    else if (name == "q38_gemm_f32_f32") f = ctx->f_gemm_f32[0];
+    else if (name == "q38_gemm_f32_f16") f = ctx->f_gemm_f32[1];
+    else if (name == "q38_gemm_f32_bf16") f = ctx->f_gemm_f32[2];
+    else if (name == "q38_gemm_f32_q8_0") f = ctx->f_gemm_f32[3];
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
     else if (name == "q38_prefill_merge") f = ctx->f_prefill_merge;
@@ -2146,6 +2155,9 @@ int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d
     const long row_groups = ((long)rows + 3) / 4;
     const long tok_groups = ((long)n_tokens + Q38_GEMV_TOKENS - 1) / Q38_GEMV_TOKENS;
     if (row_groups > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
+    /* from Q38_GEMM_F32_MIN_TOKENS tokens on (widths a multiple of 64), the
+     * bf16 matrix unit: 128 rows x 64 tokens per workgroup */
+    const bool on_unit = n_tokens >= Q38_GEMM_F32_MIN_TOKENS && width % Q38_GEMM_F32_K == 0;
     q38_gemv_f32_args a;
     memset(&a, 0, sizeof(a));
     a.weights = static_cast<const uint8_t *>(d_weights);
@@ -2155,6 +2167,9 @@ int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d
     a.rows = rows;
     a.width = width;
     a.n_tokens = n_tokens;
+    if (on_unit)
+        return ctx->launch(ctx->f_gemm_f32[ti], (unsigned)((rows + Q38_GEMM_F32_ROWS - 1) / Q38_GEMM_F32_ROWS),
+                           (unsigned)((n_tokens + Q38_GEMM_F32_TOKENS - 1) / Q38_GEMM_F32_TOKENS), 1, 256, &a);
     return ctx->launch(ctx->f_gemv_f32[ti], (unsigned)row_groups, (unsigned)tok_groups, 1, 256, &a);
 }
 

@@ -1817,3 +1817,273 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_f32(q38_gemv_f32_
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_f16(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_F16>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_bf16(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_BF16>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_q8_0(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_Q8_0>(a); }
+
+/*
+ * The same projections for many tokens on the bf16 matrix unit
+ * (v_mfma_f32_32x32x16_bf16, f32 accumulation), exact products:
+ *  - every activation x splits by truncation into three bf16 parts,
+ *    x = x1 + x2 + x3 exactly (each part takes the next 8 of f32's 24
+ *    significant bits; the differences are exact in f32);
+ *  - BF16 weights are one part; F16 weights two (w = w1 + w2 exactly, 8 + 3
+ *    bits); F32 weights three, like x; Q8_0 weights are their int8 quants,
+ *    exact in bf16, the block's f16 scale d applied to the block's sum
+ *    (d * q is exact in f32, so d * sum(q x) is the reference's sum of
+ *    (d q) x up to the order of the additions);
+ *  - a product of two parts is exact in f32 (8 x 8 bits), and the parts'
+ *    products below 2^-21 of w x are left out (F16: w2 x3; F32: w2 x3,
+ *    w3 x2, w3 x3), so each output is the exact sum up to f32 rounding of
+ *    the additions, as for the GEMV above (the reference's own x86 build
+ *    reassociates these sums too).
+ * Tile: 128 weight rows x 64 tokens per workgroup of 4 waves, wave w
+ * computing rows 64 (w & 1) .. +63 of tokens 32 (w >> 1) .. +31 (two 32 x
+ * 32 accumulators, C column = weight row, so a token's 32 outputs are one
+ * 128-byte store).  The k loop runs in stages of 64: each thread loads 16
+ * activations of one token and 32 weights of one row (Q8_0: one block),
+ * splits them into bf16 parts in LDS in the operands' lane layout, and the
+ * next stage's loads go out before the matrix steps of this one.  Within a
+ * 32-k slice, lane half h of substep s takes k 16h + 8s .. +7 for A and B
+ * alike.  Tokens past T read the last token and rows past the matrix its
+ * last row; neither is stored.  grid (ceil(rows / 128), ceil(T / 64)), 256
+ * threads; width a multiple of 64.
+ */
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int TYPE> struct F32wParts { static constexpr int n = 1; };
+template <> struct F32wParts<Q38_GGML_F16> { static constexpr int n = 2; };
+template <> struct F32wParts<Q38_GGML_F32> { static constexpr int n = 3; };
+
+/* bf16 bits of the upper halves of two f32 bit patterns: a low, b high */
+Q38_DEV uint32_t pack_hi16(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+/* eight f32 values into bf16 parts by truncation: v = p0 + p1 (+ p2) */
+template <int NP>
+Q38_DEV void split_parts(const float (&v)[8], u32x4 (&p)[NP]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float r0 = v[2 * i], r1 = v[2 * i + 1];
+#pragma unroll
+        for (int k = 0; k < NP; ++k) {
+            const uint32_t u0 = __float_as_uint(r0), u1 = __float_as_uint(r1);
+            p[k][i] = pack_hi16(u0, u1);
+            if (k + 1 < NP) {
+                r0 -= __uint_as_float(u0 & 0xFFFF0000u);
+                r1 -= __uint_as_float(u1 & 0xFFFF0000u);
+            }
+        }
+    }
+}
+
+Q38_DEV f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+
+/* c + the products of x's parts with w's parts above 2^-21 of w x, the
+ * smallest first: x1 w1, x2 w1, x3 w1 (+ x1 w2, x2 w2; + x1 w3) */
+template <int PW>
+Q38_DEV f32x16 f32w_products(const u32x4 (&ax)[3], const u32x4 (&bw)[PW], f32x16 c) {
+    if constexpr (PW == 3) c = mfma_bf16(ax[0], bw[2], c);
+    if constexpr (PW >= 2) c = mfma_bf16(ax[1], bw[1], c);
+    c = mfma_bf16(ax[2], bw[0], c);
+    if constexpr (PW >= 2) c = mfma_bf16(ax[0], bw[1], c);
+    c = mfma_bf16(ax[1], bw[0], c);
+    return mfma_bf16(ax[0], bw[0], c);
+}
+
+/* raw weights of one row's 32-k slice (Q8_0: one 34-byte block) */
+template <int TYPE> struct F32wRaw { u32x4 v[TYPE == Q38_GGML_F32 ? 8 : 4]; uint32_t tail[2]; };
+
+template <int TYPE>
+Q38_DEV void f32w_load(const uint8_t *row, int slice, F32wRaw<TYPE> &r) {
+    if constexpr (TYPE == Q38_GGML_Q8_0) {
+        /* the block starts 2-byte aligned: 8 dwords from the dword boundary
+         * at or below it and the halfwords at 30 and 32 (as f32_unit) */
+        const size_t s = (size_t)slice * 34;
+        const uint32_t o = (uint32_t)((uintptr_t)(row + s) & 3);
+        const u32x4 *base = reinterpret_cast<const u32x4 *>(row + (s - o));
+        __builtin_memcpy(&r.v[0], base, 16);
+        __builtin_memcpy(&r.v[1], reinterpret_cast<const uint8_t *>(base) + 16, 16);
+        r.tail[0] = *reinterpret_cast<const uint16_t *>(row + s + 30);
+        r.tail[1] = *reinterpret_cast<const uint16_t *>(row + s + 32);
+    } else {
+        constexpr int n = TYPE == Q38_GGML_F32 ? 8 : 4;
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(row + (size_t)slice * (16 * n));
+#pragma unroll
+        for (int i = 0; i < n; ++i) r.v[i] = src[i];
+    }
+}
+
+constexpr int kF32wRows = Q38_GEMM_F32_ROWS, kF32wTok = Q38_GEMM_F32_TOKENS, kF32wK = Q38_GEMM_F32_K;
+static_assert(kF32wRows == 128 && kF32wTok == 64 && kF32wK == 64, "the tile the lane mapping below assumes");
+
+template <int TYPE>
+Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
+    constexpr int PW = F32wParts<TYPE>::n;
+    /* operand units (16 bytes: 8 bf16 of one lane) in the lane layout */
+    __shared__ __align__(16) u32x4 xs[3][2][2][2][64];  /* [part][token tile][slice][substep][lane] */
+    __shared__ __align__(16) u32x4 ws[PW][4][2][2][64]; /* [part][row tile][slice][substep][lane] */
+    __shared__ float ds[2][kF32wRows];                   /* Q8_0: [slice][row] block scale */
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int rows = a.rows, W = a.width, T = a.n_tokens;
+    const int row0 = blockIdx.x * kF32wRows;
+    const int t0 = blockIdx.y * kF32wTok;
+    /* this thread's loads: 16 activations of token xt (k 16 c .. +15 of a
+     * stage), and slice wj of weight row wr */
+    const int xl = tid >> 2, c = tid & 3;
+    const float *xp = a.x + (size_t)min(t0 + xl, T - 1) * W + 16 * c;
+    const int wl = tid >> 1, wj = tid & 1;
+    const uint8_t *wrow = a.weights + (size_t)min(row0 + wl, rows - 1) * a.row_bytes;
+    const int n_stages = W / kF32wK;
+
+    f32x4 xr[4];
+    F32wRaw<TYPE> wr;
+    auto load = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[i] = q38_ld4(xp + (size_t)st * kF32wK + 4 * i);
+        f32w_load<TYPE>(wrow, 2 * st + wj, wr);
+    };
+
+    f32x16 acc[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[r][e] = 0.0f;
+    const int tt = wave >> 1;
+    const int rt0 = 2 * (wave & 1);
+
+    load(0);
+    for (int st = 0; st < n_stages; ++st) {
+        /* activations: slice c >> 1, lane half c & 1, substeps 0 and 1 */
+        {
+            const int j = c >> 1, h = c & 1, ln = 32 * h + (xl & 31), xt = xl >> 5;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[i] = xr[2 * sb + (i >> 2)][i & 3];
+                u32x4 p[3];
+                split_parts<3>(v, p);
+#pragma unroll
+                for (int k = 0; k < 3; ++k) xs[k][xt][j][sb][ln] = p[k];
+            }
+        }
+        /* weights: row wl, slice wj, lane halves 0 and 1, substeps 0 and 1 */
+        {
+            const int rt = wl >> 5, rl = wl & 31;
+            if constexpr (TYPE == Q38_GGML_Q8_0) {
+                uint32_t b[9];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    b[i] = wr.v[0][i];
+                    b[4 + i] = wr.v[1][i];
+                }
+                const uint32_t o = (uint32_t)((uintptr_t)(wrow + (size_t)(2 * st + wj) * 34) & 3);
+                uint32_t q[9];
+#pragma unroll
+                for (int i = 0; i < 7; ++i) q[i] = __builtin_amdgcn_alignbyte(b[i + 1], b[i], o);
+                q[7] = __builtin_amdgcn_alignbyte(wr.tail[0], b[7], o);
+                q[8] = wr.tail[1];
+                /* q[0] bytes 0-1: the f16 scale; quant i is byte 2 + i */
+                ds[wj][wl] = q38_f16(q[0]);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) {
+                        u32x4 u;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int k0 = 16 * h + 8 * sb + 2 * i + 2; /* byte of the first quant */
+                            const int k1 = k0 + 1;
+                            const float f0 = (float)(int)(int8_t)(q[k0 >> 2] >> (8 * (k0 & 3)));
+                            const float f1 = (float)(int)(int8_t)(q[k1 >> 2] >> (8 * (k1 & 3)));
+                            u[i] = pack_hi16(__float_as_uint(f0), __float_as_uint(f1));
+                        }
+                        ws[0][rt][wj][sb][32 * h + rl] = u;
+                    }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) {
+                        if constexpr (TYPE == Q38_GGML_BF16) {
+                            ws[0][rt][wj][sb][32 * h + rl] = wr.v[2 * h + sb];
+                        } else {
+                            float v[8];
+                            if constexpr (TYPE == Q38_GGML_F16) {
+                                const u32x4 u = wr.v[2 * h + sb];
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) {
+                                    v[2 * i] = q38_f16(u[i]);
+                                    v[2 * i + 1] = q38_f16(u[i] >> 16);
+                                }
+                            } else {
+                                const u32x4 u0 = wr.v[4 * h + 2 * sb], u1 = wr.v[4 * h + 2 * sb + 1];
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) {
+                                    v[i] = __uint_as_float(u0[i]);
+                                    v[4 + i] = __uint_as_float(u1[i]);
+                                }
+                            }
+                            u32x4 p[PW];
+                            split_parts<PW>(v, p);
+#pragma unroll
+                            for (int k = 0; k < PW; ++k) ws[k][rt][wj][sb][32 * h + rl] = p[k];
+                        }
+                    }
+            }
+        }
+        __syncthreads();
+        if (st + 1 < n_stages) load(st + 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f32x16 blk[2];
+            if constexpr (TYPE == Q38_GGML_Q8_0) {
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) blk[r][e] = 0.0f;
+            }
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                u32x4 ax[3];
+#pragma unroll
+                for (int k = 0; k < 3; ++k) ax[k] = xs[k][tt][j][sb][lane];
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    u32x4 bw[PW];
+#pragma unroll
+                    for (int k = 0; k < PW; ++k) bw[k] = ws[k][rt0 + r][j][sb][lane];
+                    if constexpr (TYPE == Q38_GGML_Q8_0) blk[r] = f32w_products<PW>(ax, bw, blk[r]);
+                    else acc[r] = f32w_products<PW>(ax, bw, acc[r]);
+                }
+            }
+            if constexpr (TYPE == Q38_GGML_Q8_0) {
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const float d = ds[j][32 * (rt0 + r) + (lane & 31)];
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[r][e] = __builtin_fmaf(d, blk[r][e], acc[r][e]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int row = row0 + 32 * (rt0 + r) + (lane & 31);
+        if (row >= rows) continue;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int tok = t0 + 32 * tt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            if (tok < T) a.out[(size_t)tok * rows + row] = acc[r][e];
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_f32(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_F32>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_f16(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_F16>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_bf16(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_BF16>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_q8_0(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_Q8_0>(a); }

@@ -367,7 +367,14 @@ typedef struct {
 } q38_gemv_args;
 
 /* f32-input projections (F32, F16, BF16, Q8_0 weights): grid (ceil(rows /
- * 4), ceil(T / Q38_GEMV_TOKENS)), 256 threads, one wave per row. */
+ * 4), ceil(T / Q38_GEMV_TOKENS)), 256 threads, one wave per row; from
+ * Q38_GEMM_F32_MIN_TOKENS tokens on (width a multiple of Q38_GEMM_F32_K) the
+ * bf16 matrix-unit form, grid (ceil(rows / Q38_GEMM_F32_ROWS), ceil(T /
+ * Q38_GEMM_F32_TOKENS)), 256 threads. */
+#define Q38_GEMM_F32_MIN_TOKENS 16
+#define Q38_GEMM_F32_ROWS 128
+#define Q38_GEMM_F32_TOKENS 64
+#define Q38_GEMM_F32_K 64
 typedef struct {
     const uint8_t *weights; /* [rows][row_bytes], 4-byte aligned (16 for F32/F16/BF16) */
     const float *x;         /* [T][width], 16-byte aligned */

@@ -286,15 +286,22 @@ def test_multi_matrices_share_the_split_block_launch(ctx, ref, name):
 
 @pytest.mark.parametrize("name", sorted(F32_TYPES))
 @pytest.mark.parametrize("rows,W,T", [(48, HIDDEN, 1), (48, HIDDEN, 3), (257, 1024, 9), (5, 6144, 17),
-                                      (1031, 2048, 1)])
+                                      (1031, 2048, 1), (48, HIDDEN, 64), (300, 1024, 100), (129, 768, 33),
+                                      (64, 320, 16), (40, 1032, 20)])
 def test_gemv_f32_path(ctx, ref, name, rows, W, T):
     """tensor_gemv_f32 / tensor_gemm_f32 for the weight types project()
     does not quantise for (the 48-row beta / alpha projections of a DeltaNet
-    layer and other shapes; several token passes): every element within
-    1e-5 of the sum of |w x| of the oracle's sequential chain, and of the
-    float64 dot of the weights decoded in numpy; a one-hot input row gives
-    each weight exactly."""
+    layer and other shapes; several token passes; from 16 tokens on the
+    matrix-unit form, with partial row and token tiles, and the GEMV where
+    the width is not a multiple of 64): every element within 1e-5 of the
+    sum of |w x| of the oracle's sequential chain, and of the float64 dot of
+    the weights decoded in numpy; a one-hot input row gives each weight
+    exactly."""
     ty = F32_TYPES[name]
+    if ty == 8 and W % 64:
+        pytest.skip("Q8_0 rows are a multiple of 64 wide")
+    sfx = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0"}[ty]
+    kern = ("q38_gemm_f32_" if T >= 16 and W % 64 == 0 else "q38_gemv_f32_") + sfx
     rng = np.random.default_rng(0x51333940 + ty + rows)
     x = rng.standard_normal((T, W)).astype(np.float32)
     if T > 1:
@@ -303,7 +310,8 @@ def test_gemv_f32_path(ctx, ref, name, rows, W, T):
         x[T - 1, W - 3] = 1.0
     wb, wv = _random_f32_path(ty, rows, W, 0x51333941 + ty + W)
     d_o = ctx.empty((T, rows))
-    ctx.gemv_f32(ty, rows, W, ctx.array(wb, np.uint8), ctx.array(x), T, d_o)
+    d_w, d_x = ctx.array(wb, np.uint8), ctx.array(x)
+    assert _ran(ctx, kern, lambda: ctx.gemv_f32(ty, rows, W, d_w, d_x, T, d_o))
     got = d_o.download().astype(np.float64)
     want = ref.gemv_f32(ty, wb, x, threads=16).astype(np.float64)
     exact = x.astype(np.float64) @ wv.T
