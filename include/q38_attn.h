@@ -393,14 +393,16 @@ int q38_quantize_project_q8_k(q38_ctx *ctx, int ggml_type, int n_mats, const int
  * F32 (ggml type 0), F16 (1), BF16 (30) or Q8_0 (8) weights d_weights
  * [rows][row bytes] in the GGUF layout, d_out [n_tokens][rows].  width a
  * multiple of 8 (Q8_0: of 64), d_weights 16-byte aligned (Q8_0: 4), d_x
- * 16-byte aligned.  Every product w * x is the reference's (Q8_0: d * q,
- * exact in f32, then multiplied); the sums are reassociated (the reference's
- * own x86 build reassociates them too), so each element lies within the
- * rounding of an f32 sum of the reference's scalar dot_*_scalar
- * (tensor.rs:79-117).  Below 16 tokens a GEMV; from 16 on, where width is a
- * multiple of 64, the bf16 matrix unit with x split exactly into three bf16
- * parts (and F16 / F32 weights into two / three), every product exact, Q8_0
- * block scales applied to each block's sum. */
+ * 16-byte aligned.  Every product w * x enters the sum exactly (fused
+ * multiply-adds, or products of exact bf16 parts), Q8_0's block scale d
+ * applied to the block's sum of q * x (d * q is exact in f32, as the
+ * reference forms it); the sums are reassociated (the reference's own x86
+ * build reassociates them too), so each element lies within the rounding of
+ * an f32 sum of the reference's scalar dot_*_scalar (tensor.rs:79-117).
+ * Below 16 tokens a GEMV (Q8_0: the activations staged in LDS per 8 or 16
+ * rows); from 16 on, where width is a multiple of 64, the bf16 matrix unit
+ * with x split exactly into three bf16 parts (F16 / F32 weights into two /
+ * three). */
 int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const float *d_x,
                  int n_tokens, float *d_out);
 

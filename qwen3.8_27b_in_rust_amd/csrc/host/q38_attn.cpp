@@ -159,8 +159,9 @@ struct q38_ctx {
     hipFunction_t f_gemm_ks16[kGemvTypes] = {}; /* ... on 16 waves */
     hipFunction_t f_gemm_ks4[kGemvTypes] = {};  /* ... on 4 waves */
     hipFunction_t f_gemv_q8k[kGemvTypes] = {}; /* by kGemv index */
-    hipFunction_t f_gemv_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* F32, F16, BF16, Q8_0 weights */
+    hipFunction_t f_gemv_f32[3] = {nullptr, nullptr, nullptr}; /* F32, F16, BF16 weights */
     hipFunction_t f_gemm_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* the same, on the matrix unit */
+    hipFunction_t f_gemv_q80s[2][4] = {}; /* Q8_0, activations staged in LDS: [RW 2, 4][TP 1, 2, 4, 8] */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
     hipFunction_t f_copy = nullptr;
@@ -435,11 +436,16 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[0], ctx->mod_proj, "q38_gemv_f32_f32"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[1], ctx->mod_proj, "q38_gemv_f32_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[2], ctx->mod_proj, "q38_gemv_f32_bf16"));
-    Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_f32[3], ctx->mod_proj, "q38_gemv_f32_q8_0"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[0], ctx->mod_proj, "q38_gemm_f32_f32"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[1], ctx->mod_proj, "q38_gemm_f32_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[2], ctx->mod_proj, "q38_gemm_f32_bf16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[3], ctx->mod_proj, "q38_gemm_f32_q8_0"));
+    for (int r = 0; r < 2; ++r)
+        for (int t = 0; t < 4; ++t) {
+            char nm[64];
+            snprintf(nm, sizeof(nm), "q38_gemv_f32_q8_0s_r%d_t%d", 2 << r, 1 << t);
+            Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q80s[r][t], ctx->mod_proj, nm));
+        }
     for (int i = 0; i < kGemvTypes; ++i) {
         int n = 0;
         Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, ctx->f_gemv_q8k[i], 256, 0));
@@ -633,11 +639,13 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemv_f32_f32") f = ctx->f_gemv_f32[0];
     else if (name == "q38_gemv_f32_f16") f = ctx->f_gemv_f32[1];
     else if (name == "q38_gemv_f32_bf16") f = ctx->f_gemv_f32[2];
-    else if (name == "q38_gemv_f32_q8_0") f = ctx->f_gemv_f32[3];
     else if (name == "q38_gemm_f32_f32") f = ctx->f_gemm_f32[0];
     else if (name == "q38_gemm_f32_f16") f = ctx->f_gemm_f32[1];
     else if (name == "q38_gemm_f32_bf16") f = ctx->f_gemm_f32[2];
     else if (name == "q38_gemm_f32_q8_0") f = ctx->f_gemm_f32[3];
+    else if (name.rfind("q38_gemv_f32_q8_0s_r", 0) == 0 && name.size() == 24 && (name[20] == '2' || name[20] == '4') &&
+             name[21] == '_' && name[22] == 't' && (name[23] == '1' || name[23] == '2' || name[23] == '4' || name[23] == '8'))
+        f = ctx->f_gemv_q80s[name[20] == '4'][name[23] == '1' ? 0 : name[23] == '2' ? 1 : name[23] == '4' ? 2 : 3];
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
     else if (name == "q38_prefill_merge") f = ctx->f_prefill_merge;
@@ -2170,7 +2178,19 @@ int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d
     if (on_unit)
         return ctx->launch(ctx->f_gemm_f32[ti], (unsigned)((rows + Q38_GEMM_F32_ROWS - 1) / Q38_GEMM_F32_ROWS),
                            (unsigned)((n_tokens + Q38_GEMM_F32_TOKENS - 1) / Q38_GEMM_F32_TOKENS), 1, 256, &a);
-    return ctx->launch(ctx->f_gemv_f32[ti], (unsigned)row_groups, (unsigned)tok_groups, 1, 256, &a);
+    /* Q8_0: the activations staged in LDS once per 4 RW rows, TP tokens a
+     * pass (the smallest of 1, 2, 4, 8 that holds min(T, 8)); 4 rows a wave
+     * for 8-token passes, else 2 (measured on 1024-17408 rows x 5120 and
+     * 5120 x 17408: 2 rows 5-20% faster at 1-4 tokens, 4 rows 2-20% at 8) */
+    if (ti == 3) {
+        const int tpi = n_tokens <= 1 ? 0 : n_tokens <= 2 ? 1 : n_tokens <= 4 ? 2 : 3;
+        const int tp = 1 << tpi;
+        const bool wide = tp == 8;
+        const long wg_rows = wide ? 16 : 8;
+        return ctx->launch(ctx->f_gemv_q80s[wide][tpi], (unsigned)((rows + wg_rows - 1) / wg_rows),
+                           (unsigned)((n_tokens + tp - 1) / tp), 1, 256, &a);
+    }
+    return ctx->launch(ctx->f_gemv_f32[ti], (unsigned)row_groups, (unsigned)tok_groups, 1, 256, &a); /* ti < 3 */
 }
 
 }  /* extern "C" */

@@ -1692,15 +1692,15 @@ Q38_GEMM_KS(iq1m, Q38_GGML_IQ1_M)
 #undef Q38_GEMM_KS
 
 /*
- * Projections of f32 activations by F32, F16, BF16 or Q8_0 weights (the
- * path project() takes for weights it does not quantise for, ops.rs:632-637:
- * tensor_gemv_f32 / tensor_gemm_f32, tensor.rs:1095-1129, :1175-1215).
- * grid (ceil(rows / 4), ceil(T / tok_pass)), 256 threads: one wave per
- * weight row, the row read once per pass of up to 8 tokens.  A lane takes
- * units of E consecutive weights (E = 8; Q8_0: one 32-weight block), units
- * lane, lane + 64, ... of the row, decodes them to f32 exactly (f16 and bf16
- * widen exactly; Q8_0 is d * q rounded once, the reference's product) and
- * adds w * x into its partial sum with fused multiply-adds, unit after unit;
+ * Projections of f32 activations by F32, F16 or BF16 weights (the path
+ * project() takes for weights it does not quantise for, ops.rs:632-637:
+ * tensor_gemv_f32 / tensor_gemm_f32, tensor.rs:1095-1129, :1175-1215; Q8_0
+ * weights below) below 16 tokens.  grid (ceil(rows / 4), ceil(T / 8)), 256
+ * threads: one wave per weight row, the row read once per pass of up to 8
+ * tokens.  A lane takes units of 8 consecutive weights, units lane, lane +
+ * 64, ... of the row, decodes them to f32 exactly (f16 and bf16 widen
+ * exactly) and adds w * x into its partial sum with fused multiply-adds,
+ * unit after unit;
  * the 64 partial sums are then added by a butterfly.  Every product is the
  * reference's; the order of the additions is not (the reference runs one
  * chain over the row on its scalar path and 8-lane partial sums on x86), so
@@ -1710,9 +1710,8 @@ template <int TYPE> struct F32Unit;
 template <> struct F32Unit<Q38_GGML_F32> { static constexpr int E = 8, bytes = 32; };
 template <> struct F32Unit<Q38_GGML_F16> { static constexpr int E = 8, bytes = 16; };
 template <> struct F32Unit<Q38_GGML_BF16> { static constexpr int E = 8, bytes = 16; };
-template <> struct F32Unit<Q38_GGML_Q8_0> { static constexpr int E = 32, bytes = 34; };
 
-/* Unit u of a row starting at `row` (4-byte aligned): its E weights. */
+/* Unit u of a row starting at `row` (16-byte aligned): its E weights. */
 template <int TYPE>
 Q38_DEV void f32_unit(const uint8_t *row, int u, float (&w)[F32Unit<TYPE>::E]) {
     if (TYPE == Q38_GGML_F32) {
@@ -1724,7 +1723,7 @@ Q38_DEV void f32_unit(const uint8_t *row, int u, float (&w)[F32Unit<TYPE>::E]) {
             w[i] = __uint_as_float(v0[i]);
             w[4 + i] = __uint_as_float(v1[i]);
         }
-    } else if (TYPE == Q38_GGML_F16 || TYPE == Q38_GGML_BF16) {
+    } else {
         u32x4 v;
         __builtin_memcpy(&v, row + (size_t)u * 16, 16);
 #pragma unroll
@@ -1736,38 +1735,6 @@ Q38_DEV void f32_unit(const uint8_t *row, int u, float (&w)[F32Unit<TYPE>::E]) {
                 w[2 * i] = __uint_as_float(v[i] << 16);
                 w[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
             }
-        }
-    } else {
-        /* a 34-byte block starts 2-byte aligned: 8 dwords from the dword
-         * boundary at or below it and the halfwords at 30 and 32, shifted
-         * into 9 words from the start (bytes 0-1 the f16 scale, 2-33 the
-         * quants); every byte read lies in this block or the one before */
-        const size_t s = (size_t)u * 34;
-        const uint32_t o = (uint32_t)((uintptr_t)(row + s) & 3); /* 0 or 2 for a 4-byte aligned matrix */
-        const uint32_t *base = reinterpret_cast<const uint32_t *>(row + (s - o));
-        uint32_t win[9];
-        u32x4 v0, v1;
-        __builtin_memcpy(&v0, base, 16);
-        __builtin_memcpy(&v1, base + 4, 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            win[i] = v0[i];
-            win[4 + i] = v1[i];
-        }
-        win[8] = *reinterpret_cast<const uint16_t *>(row + s + 30);
-        const uint32_t h32 = *reinterpret_cast<const uint16_t *>(row + s + 32);
-        uint32_t b[9];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) b[j] = __builtin_amdgcn_alignbyte(win[j + 1], win[j], o);
-        /* word 7 (bytes 28..31): the window's word 7 when o == 0; with
-         * o == 2 its upper half and the halfword at 30 */
-        b[8] = h32;
-        const float d = q38_f16(b[0]);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            const int byte = 2 + i;
-            const int q = (int)(int8_t)((b[byte >> 2] >> (8 * (byte & 3))) & 255u);
-            w[i] = d * (float)q;
         }
     }
 }
@@ -1816,7 +1783,6 @@ Q38_DEV void gemv_f32(const q38_gemv_f32_args &a) {
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_f32(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_F32>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_f16(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_F16>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_bf16(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_BF16>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_q8_0(q38_gemv_f32_args a) { gemv_f32<Q38_GGML_Q8_0>(a); }
 
 /*
  * The same projections for many tokens on the bf16 matrix unit
@@ -2087,3 +2053,136 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_f32(q38_gemv_f32_
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_f16(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_F16>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_bf16(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_BF16>(a); }
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_q8_0(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_Q8_0>(a); }
+
+/*
+ * Q8_0 weights below 16 tokens: a workgroup of 4 waves takes 4 RW rows (RW
+ * per wave) and a pass of TP tokens, and walks the row in chunks of 32
+ * blocks (1024 values).  Each chunk's activations are staged in LDS once
+ * for all the workgroup's rows (a block at a 36-float stride, so 16 lanes
+ * reading consecutive blocks with 16-byte reads touch 64 distinct banks);
+ * lane l takes block l % 32 of the chunk in rows l / 32, l / 32 + 2, ...
+ * of its wave: the 32 quants are converted to f32 and multiplied into the
+ * staged activations (fused multiply-adds, the products exact), and the
+ * block's f16 scale d is applied to that sum (d * q is exact in f32, so
+ * this is the reference's sum of (d q) x up to the order of the additions).
+ * The next chunk's weights and activations are loaded while this one is
+ * computed; a row's 32 lanes add their sums at the end.  Tokens past T in
+ * the last pass repeat token T - 1 and rows past the matrix its last row;
+ * neither is stored.  grid (ceil(rows / (4 RW)), ceil(T / TP)), 256 threads.
+ */
+constexpr int kQ80Stride = 36; /* floats per staged block */
+
+template <int RW, int TP>
+Q38_DEV void gemv_q80s(const q38_gemv_f32_args &a) {
+    constexpr int U = RW / 2; /* units per lane and chunk */
+    __shared__ __align__(16) float xst[TP][32 * kQ80Stride];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int W = a.width, B = W / 32, T = a.n_tokens, rows = a.rows;
+    const int tok0 = blockIdx.y * TP;
+    const int n_chunks = (B + 31) / 32;
+    /* staging: thread -> block sb of the chunk, values sk .. sk + 3 */
+    const int sb = tid >> 3, sk = 4 * (tid & 7);
+    const float *xsrc[TP];
+#pragma unroll
+    for (int t = 0; t < TP; ++t) xsrc[t] = a.x + (size_t)min(tok0 + t, T - 1) * W + 32 * sb + sk;
+    /* units: block cb of the chunk in rows rw[j] */
+    const int cb = lane & 31;
+    const int r0 = blockIdx.x * 4 * RW + RW * wave + (lane >> 5);
+    const uint8_t *wrow[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) wrow[j] = a.weights + (size_t)min(r0 + 2 * j, rows - 1) * a.row_bytes;
+
+    f32x4 xr[TP];
+    F32wRaw<Q38_GGML_Q8_0> wc[U], wn[U];
+    auto load = [&](int ch, F32wRaw<Q38_GGML_Q8_0>(&w)[U]) {
+        const bool xin = 32 * ch + sb < B;
+#pragma unroll
+        for (int t = 0; t < TP; ++t) xr[t] = xin ? q38_ld4(xsrc[t] + (size_t)ch * 1024) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (32 * ch + cb < B) {
+#pragma unroll
+            for (int j = 0; j < U; ++j) f32w_load<Q38_GGML_Q8_0>(wrow[j], 32 * ch + cb, w[j]);
+        }
+    };
+    float acc[U][TP];
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+#pragma unroll
+        for (int t = 0; t < TP; ++t) acc[j][t] = 0.0f;
+
+    load(0, wc);
+    for (int ch = 0; ch < n_chunks; ++ch) {
+#pragma unroll
+        for (int t = 0; t < TP; ++t) q38_st4(&xst[t][sb * kQ80Stride + sk], xr[t]);
+        __syncthreads();
+        if (ch + 1 < n_chunks) load(ch + 1, wn);
+        const int blk = 32 * ch + cb;
+        if (blk < B) {
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                uint32_t b[9];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    b[i] = wc[j].v[0][i];
+                    b[4 + i] = wc[j].v[1][i];
+                }
+                const uint32_t o = (uint32_t)((uintptr_t)(wrow[j] + (size_t)blk * 34) & 3);
+                uint32_t q[9];
+#pragma unroll
+                for (int i = 0; i < 7; ++i) q[i] = __builtin_amdgcn_alignbyte(b[i + 1], b[i], o);
+                q[7] = __builtin_amdgcn_alignbyte(wc[j].tail[0], b[7], o);
+                q[8] = wc[j].tail[1];
+                float sum[TP];
+#pragma unroll
+                for (int t = 0; t < TP; ++t) sum[t] = 0.0f;
+#pragma unroll
+                for (int i4 = 0; i4 < 8; ++i4) {
+                    float wq[4];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const int byte = 2 + 4 * i4 + c;
+                        wq[c] = (float)(int)(int8_t)(q[byte >> 2] >> (8 * (byte & 3)));
+                    }
+#pragma unroll
+                    for (int t = 0; t < TP; ++t) {
+                        const f32x4 xv = q38_ld4(&xst[t][cb * kQ80Stride + 4 * i4]);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) sum[t] = __builtin_fmaf(wq[c], xv[c], sum[t]);
+                    }
+                }
+                const float d = q38_f16(q[0]);
+#pragma unroll
+                for (int t = 0; t < TP; ++t) acc[j][t] = __builtin_fmaf(d, sum[t], acc[j][t]);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < U; ++j) wc[j] = wn[j];
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+#pragma unroll
+        for (int t = 0; t < TP; ++t) {
+            float v = acc[j][t];
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+            const int row = r0 + 2 * j;
+            if (cb == 0 && row < rows && tok0 + t < T) a.out[(size_t)(tok0 + t) * rows + row] = v;
+        }
+    }
+}
+
+#define Q38_GEMV_Q80S(rw, tp)                                                                           \
+    extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_q8_0s_r##rw##_t##tp(q38_gemv_f32_args a) { \
+        gemv_q80s<rw, tp>(a);                                                                             \
+    }
+Q38_GEMV_Q80S(2, 1)
+Q38_GEMV_Q80S(2, 2)
+Q38_GEMV_Q80S(2, 4)
+Q38_GEMV_Q80S(2, 8)
+Q38_GEMV_Q80S(4, 1)
+Q38_GEMV_Q80S(4, 2)
+Q38_GEMV_Q80S(4, 4)
+Q38_GEMV_Q80S(4, 8)
+#undef Q38_GEMV_Q80S
