@@ -916,15 +916,15 @@ F32_PATH_TYPES = {0: ("F32", 4.0), 1: ("F16", 2.0), 30: ("BF16", 2.0), 8: ("Q8_0
 
 def f32_path(pkg, ctx, reps: int):
     """The projection path of weights project() does not quantise for
-    (q38_gemv_f32: F32, F16, BF16, Q8_0) through 17408 x 5120 at 1 and 4096
-    tokens and the 48-row beta / alpha shape (48 x 5120) at 4096: kernel
-    duration, the kernel the library chose (GEMV below 16 tokens, the bf16
-    matrix unit from 16 on), weight bytes per second and useful f32
+    (q38_gemv_f32: F32, F16, BF16, Q8_0) through 17408 x 5120 at 1, 16 and
+    4096 tokens and the 48-row beta / alpha shape (48 x 5120) at 4096: kernel
+    duration, the kernel the library chose (the GEMV for few tokens, the
+    bf16 matrix unit's split-k or 128 x 64 form), weight bytes per second and useful f32
     operations per second (2 x rows x width x tokens; the matrix unit runs 3,
     5 or 6 bf16 products per multiply for BF16/Q8_0, F16, F32 weights).
     Weights are random bytes (timing only)."""
     res = {}
-    for rows, width, n_tokens in ((17408, 5120, 1), (17408, 5120, 4096), (48, 5120, 4096)):
+    for rows, width, n_tokens in ((17408, 5120, 1), (17408, 5120, 16), (17408, 5120, 4096), (48, 5120, 4096)):
         x = ctx.empty((n_tokens, width))
         ctx.fill_normal(x, n_tokens * width, 0x51335600 + n_tokens)
         out = ctx.empty((n_tokens, rows))
@@ -935,7 +935,7 @@ def f32_path(pkg, ctx, reps: int):
             ctx.gemv_f32(ty, rows, width, w, x, n_tokens, out)
             ctx.sync()
             sfx = name.lower()
-            kerns = ["q38_gemm_f32_" + sfx]
+            kerns = ["q38_gemm_f32_" + sfx, "q38_gemm_f32s_" + sfx]
             kerns += ["q38_gemv_f32_q8_0s_r%d_t%d" % (r, t) for r in (2, 4) for t in (1, 2, 4, 8)] if ty == 8 else \
                 ["q38_gemv_f32_" + sfx]
             for kern in kerns:
@@ -1098,7 +1098,7 @@ EXTRAS = {
                          lambda pkg, ctx: weight_formats(pkg, ctx, 3)),
     "weight_formats_prompt_4096": ("a 4096-token prompt through a 17408x5120 matrix in each Q8_K weight format",
                                    lambda pkg, ctx: weight_formats_prompt(pkg, ctx, 4096, 2)),
-    "f32_path_projections": ("F32/F16/BF16/Q8_0 weights (the f32-input path) at 1 and 4096 tokens",
+    "f32_path_projections": ("F32/F16/BF16/Q8_0 weights (the f32-input path) at 1, 16 and 4096 tokens",
                              lambda pkg, ctx: f32_path(pkg, ctx, 3)),
 }
 

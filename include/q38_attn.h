@@ -399,10 +399,10 @@ int q38_quantize_project_q8_k(q38_ctx *ctx, int ggml_type, int n_mats, const int
  * reference forms it); the sums are reassociated (the reference's own x86
  * build reassociates them too), so each element lies within the rounding of
  * an f32 sum of the reference's scalar dot_*_scalar (tensor.rs:79-117).
- * Below 16 tokens a GEMV (Q8_0: the activations staged in LDS per 8 or 16
- * rows); from 16 on, where width is a multiple of 64, the bf16 matrix unit
- * with x split exactly into three bf16 parts (F16 / F32 weights into two /
- * three). */
+ * Few tokens take a GEMV (Q8_0: the activations staged in LDS per 8 or 16
+ * rows); from 4 tokens (Q8_0: 9) on, where width is a multiple of 64, the
+ * bf16 matrix unit with x split exactly into three bf16 parts (F16 / F32
+ * weights into two / three). */
 int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const float *d_x,
                  int n_tokens, float *d_out);
 

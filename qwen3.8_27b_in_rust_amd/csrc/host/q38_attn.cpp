@@ -161,6 +161,7 @@ struct q38_ctx {
     hipFunction_t f_gemv_q8k[kGemvTypes] = {}; /* by kGemv index */
     hipFunction_t f_gemv_f32[3] = {nullptr, nullptr, nullptr}; /* F32, F16, BF16 weights */
     hipFunction_t f_gemm_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* the same, on the matrix unit */
+    hipFunction_t f_gemm_f32s[4] = {nullptr, nullptr, nullptr, nullptr}; /* few tokens, k split over the waves */
     hipFunction_t f_gemv_q80s[2][4] = {}; /* Q8_0, activations staged in LDS: [RW 2, 4][TP 1, 2, 4, 8] */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
@@ -440,6 +441,10 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[1], ctx->mod_proj, "q38_gemm_f32_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[2], ctx->mod_proj, "q38_gemm_f32_bf16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32[3], ctx->mod_proj, "q38_gemm_f32_q8_0"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32s[0], ctx->mod_proj, "q38_gemm_f32s_f32"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32s[1], ctx->mod_proj, "q38_gemm_f32s_f16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32s[2], ctx->mod_proj, "q38_gemm_f32s_bf16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32s[3], ctx->mod_proj, "q38_gemm_f32s_q8_0"));
     for (int r = 0; r < 2; ++r)
         for (int t = 0; t < 4; ++t) {
             char nm[64];
@@ -643,6 +648,10 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemm_f32_f16") f = ctx->f_gemm_f32[1];
     else if (name == "q38_gemm_f32_bf16") f = ctx->f_gemm_f32[2];
     else if (name == "q38_gemm_f32_q8_0") f = ctx->f_gemm_f32[3];
+    else if (name == "q38_gemm_f32s_f32") f = ctx->f_gemm_f32s[0];
+    else if (name == "q38_gemm_f32s_f16") f = ctx->f_gemm_f32s[1];
+    else if (name == "q38_gemm_f32s_bf16") f = ctx->f_gemm_f32s[2];
+    else if (name == "q38_gemm_f32s_q8_0") f = ctx->f_gemm_f32s[3];
     else if (name.rfind("q38_gemv_f32_q8_0s_r", 0) == 0 && name.size() == 24 && (name[20] == '2' || name[20] == '4') &&
              name[21] == '_' && name[22] == 't' && (name[23] == '1' || name[23] == '2' || name[23] == '4' || name[23] == '8'))
         f = ctx->f_gemv_q80s[name[20] == '4'][name[23] == '1' ? 0 : name[23] == '2' ? 1 : name[23] == '4' ? 2 : 3];
@@ -2142,6 +2151,9 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
     return q38_gemv_q8_k_multi(ctx, ggml_type, 1, &rows, width, &d_weights, d_q8k, n_tokens, &d_out);
 }
 
+static const int kF32UnitMinTokens = 4;
+static const int kF32UnitMinTokensQ80 = 9;
+
 int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d_weights, const float *d_x,
                  int n_tokens, float *d_out) {
     if (ctx == nullptr) return fail("ctx is NULL");
@@ -2163,9 +2175,33 @@ int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d
     const long row_groups = ((long)rows + 3) / 4;
     const long tok_groups = ((long)n_tokens + Q38_GEMV_TOKENS - 1) / Q38_GEMV_TOKENS;
     if (row_groups > 0x7FFFFFFFL || tok_groups > 65535) return fail("too many rows or tokens");
-    /* from Q38_GEMM_F32_MIN_TOKENS tokens on (widths a multiple of 64), the
-     * bf16 matrix unit: 128 rows x 64 tokens per workgroup */
-    const bool on_unit = n_tokens >= Q38_GEMM_F32_MIN_TOKENS && width % Q38_GEMM_F32_K == 0;
+    /* Widths a multiple of 64 take the bf16 matrix unit from 4 tokens on
+     * (Q8_0: from 9, its staged GEMV being faster up to 8): up to 32 tokens,
+     * or where the 128 x 64 tiles would give fewer than half a workgroup per
+     * CU, 64 rows x 32 tokens per workgroup with k split over its waves;
+     * otherwise the 128 x 64 tiles (measured on 48-17408 rows x 5120 and
+     * 5120 x 17408, 2-4096 tokens: e.g. BF16 17408 x 5120 at 15 tokens 72
+     * against 188 us as the GEMV, at 48 tokens 105 against 123 us on the
+     * split-k form; 48 x 5120 at 4096 tokens 39 against 99 us) */
+    const bool unit_width = width % Q38_GEMM_F32_K == 0;
+    const long big_wgs = ((long)rows + Q38_GEMM_F32_ROWS - 1) / Q38_GEMM_F32_ROWS *
+                         (((long)n_tokens + Q38_GEMM_F32_TOKENS - 1) / Q38_GEMM_F32_TOKENS);
+    const bool on_unit_any = unit_width && n_tokens >= (ti == 3 ? kF32UnitMinTokensQ80 : kF32UnitMinTokens);
+    const bool skinny = on_unit_any && (n_tokens <= 32 || 2 * big_wgs < (long)ctx->cu_count);
+    const bool on_unit = on_unit_any && !skinny;
+    if (skinny) {
+        q38_gemv_f32_args s;
+        memset(&s, 0, sizeof(s));
+        s.weights = static_cast<const uint8_t *>(d_weights);
+        s.x = d_x;
+        s.out = d_out;
+        s.row_bytes = (int64_t)(width / block) * block_bytes;
+        s.rows = rows;
+        s.width = width;
+        s.n_tokens = n_tokens;
+        return ctx->launch(ctx->f_gemm_f32s[ti], (unsigned)((rows + 63) / 64), (unsigned)((n_tokens + 31) / 32), 1,
+                           256, &s);
+    }
     q38_gemv_f32_args a;
     memset(&a, 0, sizeof(a));
     a.weights = static_cast<const uint8_t *>(d_weights);

@@ -2055,6 +2055,179 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_bf16(q38_gemv_f32
 extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_q8_0(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_Q8_0>(a); }
 
 /*
+ * The matrix-unit form for few tokens: a workgroup of 4 waves owns 64 rows x
+ * 32 tokens (two 32 x 32 accumulators per wave) and the waves split the k
+ * range into 4 contiguous parts of 32-value slices, so the grid has a
+ * workgroup per 64 rows where the 128 x 64 tiles have one per 128 rows and
+ * 64 tokens.  No LDS in the k loop: lane l loads the 16 activations of token
+ * l % 32 and the 16 weights of rows l % 32 and 32 + l % 32 that its lane half
+ * l / 32 supplies to the slice's two k substeps, splits them into bf16 parts
+ * in registers (as the 128 x 64 form: exact parts, the same products), and
+ * the next slice's loads go out before this slice's matrix steps.  The four
+ * waves' accumulators are added through LDS in wave order, so the sums do
+ * not depend on timing.  grid (ceil(rows / 64), ceil(T / 32)), 256 threads;
+ * width a multiple of 64.
+ */
+template <int TYPE> struct F32sRaw { u32x4 v[TYPE == Q38_GGML_F32 ? 4 : 2]; };
+template <> struct F32sRaw<Q38_GGML_Q8_0> { u32x4 v[1]; uint32_t tail, d; };
+
+/* lane half h of slice `slice` of a row: its 16 weights (Q8_0: 16 quants of
+ * block `slice` and the block's scale) */
+template <int TYPE>
+Q38_DEV void f32s_load(const uint8_t *row, int slice, int h, F32sRaw<TYPE> &r) {
+    if constexpr (TYPE == Q38_GGML_Q8_0) {
+        /* quants 16h .. 16h + 15 start 2-byte aligned: 16 bytes from the
+         * dword boundary at or below them and the halfword at 14 */
+        const uint8_t *p = row + (size_t)slice * 34 + 2 + 16 * h;
+        const uint32_t o = (uint32_t)((uintptr_t)p & 3);
+        __builtin_memcpy(&r.v[0], p - o, 16);
+        r.tail = *reinterpret_cast<const uint16_t *>(p + 14);
+        r.d = *reinterpret_cast<const uint16_t *>(row + (size_t)slice * 34);
+    } else {
+        constexpr int n = TYPE == Q38_GGML_F32 ? 4 : 2;
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(row + (size_t)slice * (32 * n) + 16 * n * h);
+#pragma unroll
+        for (int i = 0; i < n; ++i) r.v[i] = src[i];
+    }
+}
+
+/* the weights of substep sb as PW bf16 parts */
+template <int TYPE>
+Q38_DEV void f32s_parts(const F32sRaw<TYPE> &r, int sb, const uint8_t *p, u32x4 (&out)[F32wParts<TYPE>::n]) {
+    if constexpr (TYPE == Q38_GGML_BF16) {
+        out[0] = r.v[sb];
+    } else if constexpr (TYPE == Q38_GGML_Q8_0) {
+        const uint32_t o = (uint32_t)((uintptr_t)p & 3);
+        uint32_t q[4];
+        q[0] = __builtin_amdgcn_alignbyte(r.v[0][1], r.v[0][0], o);
+        q[1] = __builtin_amdgcn_alignbyte(r.v[0][2], r.v[0][1], o);
+        q[2] = __builtin_amdgcn_alignbyte(r.v[0][3], r.v[0][2], o);
+        q[3] = __builtin_amdgcn_alignbyte(r.tail, r.v[0][3], o);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t w = q[2 * sb + (i >> 1)];
+            const int b0 = 2 * (i & 1);
+            const float f0 = (float)(int)(int8_t)(w >> (8 * b0));
+            const float f1 = (float)(int)(int8_t)(w >> (8 * b0 + 8));
+            out[0][i] = pack_hi16(__float_as_uint(f0), __float_as_uint(f1));
+        }
+    } else {
+        float v[8];
+        if constexpr (TYPE == Q38_GGML_F16) {
+            const u32x4 u = r.v[sb];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = q38_f16(u[i]);
+                v[2 * i + 1] = q38_f16(u[i] >> 16);
+            }
+        } else {
+            const u32x4 u0 = r.v[2 * sb], u1 = r.v[2 * sb + 1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = __uint_as_float(u0[i]);
+                v[4 + i] = __uint_as_float(u1[i]);
+            }
+        }
+        split_parts<F32wParts<TYPE>::n>(v, out);
+    }
+}
+
+template <int TYPE>
+Q38_DEV void gemm_f32s(const q38_gemv_f32_args &a) {
+    constexpr int PW = F32wParts<TYPE>::n;
+    __shared__ float red[3][2][16][64]; /* waves 1-3: [wave - 1][tile][element][lane] */
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int rows = a.rows, W = a.width, T = a.n_tokens;
+    const int row0 = blockIdx.x * 64;
+    const int t0 = blockIdx.y * 32;
+    const int n_slices = W / 32;
+    const int s_begin = n_slices * wave / 4, s_end = n_slices * (wave + 1) / 4;
+    const float *xp = a.x + (size_t)min(t0 + l32, T - 1) * W + 16 * h;
+    const uint8_t *wp[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) wp[r] = a.weights + (size_t)min(row0 + 32 * r + l32, rows - 1) * a.row_bytes;
+
+    f32x4 xc[4], xn[4];
+    F32sRaw<TYPE> wc[2], wn[2];
+    auto load = [&](int sl, f32x4(&xr)[4], F32sRaw<TYPE>(&wr)[2]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[i] = q38_ld4(xp + (size_t)sl * 32 + 4 * i);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) f32s_load<TYPE>(wp[r], sl, h, wr[r]);
+    };
+    f32x16 acc[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[r][e] = 0.0f;
+    if (s_begin < s_end) load(s_begin, xc, wc);
+    for (int sl = s_begin; sl < s_end; ++sl) {
+        if (sl + 1 < s_end) load(sl + 1, xn, wn);
+        f32x16 blk[2];
+        if constexpr (TYPE == Q38_GGML_Q8_0) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) blk[r][e] = 0.0f;
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = xc[2 * sb + (i >> 2)][i & 3];
+            u32x4 ax[3];
+            split_parts<3>(v, ax);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                u32x4 bw[PW];
+                f32s_parts<TYPE>(wc[r], sb, wp[r] + (size_t)sl * 34 + 2 + 16 * h, bw);
+                if constexpr (TYPE == Q38_GGML_Q8_0) blk[r] = f32w_products<PW>(ax, bw, blk[r]);
+                else acc[r] = f32w_products<PW>(ax, bw, acc[r]);
+            }
+        }
+        if constexpr (TYPE == Q38_GGML_Q8_0) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                /* this lane's output column is its own row l % 32 of tile r */
+                const float d = q38_f16(wc[r].d);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[r][e] = __builtin_fmaf(d, blk[r][e], acc[r][e]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xc[i] = xn[i];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) wc[r] = wn[r];
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) red[wave - 1][r][e][lane] = acc[r][e];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int row = row0 + 32 * r + l32;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float v = ((acc[r][e] + red[0][r][e][lane]) + red[1][r][e][lane]) + red[2][r][e][lane];
+            const int tok = t0 + 8 * (e >> 2) + 4 * h + (e & 3);
+            if (row < rows && tok < T) a.out[(size_t)tok * rows + row] = v;
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32s_f32(q38_gemv_f32_args a) { gemm_f32s<Q38_GGML_F32>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32s_f16(q38_gemv_f32_args a) { gemm_f32s<Q38_GGML_F16>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32s_bf16(q38_gemv_f32_args a) { gemm_f32s<Q38_GGML_BF16>(a); }
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32s_q8_0(q38_gemv_f32_args a) { gemm_f32s<Q38_GGML_Q8_0>(a); }
+
+/*
  * Q8_0 weights below 16 tokens: a workgroup of 4 waves takes 4 RW rows (RW
  * per wave) and a pass of TP tokens, and walks the row in chunks of 32
  * blocks (1024 values).  Each chunk's activations are staged in LDS once

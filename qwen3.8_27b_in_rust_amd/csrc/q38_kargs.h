@@ -366,18 +366,18 @@ typedef struct {
     int32_t tok_groups;
 } q38_gemv_args;
 
-/* f32-input projections (F32, F16, BF16, Q8_0 weights): grid (ceil(rows /
- * 4), ceil(T / Q38_GEMV_TOKENS)), 256 threads, one wave per row; from
- * Q38_GEMM_F32_MIN_TOKENS tokens on (width a multiple of Q38_GEMM_F32_K) the
- * bf16 matrix-unit form, grid (ceil(rows / Q38_GEMM_F32_ROWS), ceil(T /
- * Q38_GEMM_F32_TOKENS)), 256 threads. */
-#define Q38_GEMM_F32_MIN_TOKENS 16
+/* f32-input projections (F32, F16, BF16, Q8_0 weights): the GEMV, grid
+ * (ceil(rows / 4), ceil(T / Q38_GEMV_TOKENS)), 256 threads, one wave per
+ * row; the bf16 matrix-unit forms (width a multiple of Q38_GEMM_F32_K):
+ * q38_gemm_f32_*, grid (ceil(rows / Q38_GEMM_F32_ROWS), ceil(T /
+ * Q38_GEMM_F32_TOKENS)), and q38_gemm_f32s_*, grid (ceil(rows / 64),
+ * ceil(T / 32)), 256 threads. */
 #define Q38_GEMM_F32_ROWS 128
 #define Q38_GEMM_F32_TOKENS 64
 #define Q38_GEMM_F32_K 64
-/* q38_gemv_f32_q8_0s_r{RW}_t{TP} (Q8_0 weights below
- * Q38_GEMM_F32_MIN_TOKENS tokens): grid (ceil(rows / (4 RW)), ceil(T / TP)),
- * 256 threads, RW 2 or 4, TP 1, 2, 4 or 8 */
+/* q38_gemv_f32_q8_0s_r{RW}_t{TP} (Q8_0 weights, few tokens): grid
+ * (ceil(rows / (4 RW)), ceil(T / TP)), 256 threads, RW 2 or 4, TP 1, 2, 4
+ * or 8 */
 typedef struct {
     const uint8_t *weights; /* [rows][row_bytes], 4-byte aligned (16 for F32/F16/BF16) */
     const float *x;         /* [T][width], 16-byte aligned */

@@ -288,13 +288,14 @@ def test_multi_matrices_share_the_split_block_launch(ctx, ref, name):
 @pytest.mark.parametrize("rows,W,T", [(48, HIDDEN, 1), (48, HIDDEN, 3), (257, 1024, 9), (5, 6144, 17),
                                       (1031, 2048, 1), (48, HIDDEN, 64), (300, 1024, 100), (129, 768, 33),
                                       (64, 320, 16), (40, 1032, 20), (37, 64, 5), (19, 17408, 2), (70, 14528, 3),
-                                      (33, 6144, 15)])
+                                      (33, 6144, 15), (2048, 256, 512), (100, 1024, 9)])
 def test_gemv_f32_path(ctx, ref, name, rows, W, T):
     """tensor_gemv_f32 / tensor_gemm_f32 for the weight types project()
     does not quantise for (the 48-row beta / alpha projections of a DeltaNet
-    layer and other shapes; several token passes; from 16 tokens on the
-    matrix-unit form, with partial row and token tiles, and the GEMV where
-    the width is not a multiple of 64): every element within 1e-5 of the
+    layer and other shapes; several token passes; from 4 tokens on the
+    matrix-unit forms, with partial row and token tiles and k ranges that
+    leave a wave empty, and the GEMV where the width is not a multiple of
+    64): every element within 1e-5 of the
     sum of |w x| of the oracle's sequential chain, and of the float64 dot of
     the weights decoded in numpy; a one-hot input row gives each weight
     exactly."""
@@ -302,10 +303,13 @@ def test_gemv_f32_path(ctx, ref, name, rows, W, T):
     if ty == 8 and W % 64:
         pytest.skip("Q8_0 rows are a multiple of 64 wide")
     sfx = {0: "f32", 1: "f16", 30: "bf16", 8: "q8_0"}[ty]
-    kern = ("q38_gemm_f32_" if T >= 16 and W % 64 == 0 else "q38_gemv_f32_") + sfx
-    if ty == 8 and T < 16:  # the activations staged in LDS, 1-8 tokens a pass (8: 4 rows a wave)
+    if W % 64 or T < (9 if ty == 8 else 4):  # the GEMV; Q8_0: activations staged in LDS
         tp = min(t for t in (1, 2, 4, 8) if t >= min(T, 8))
-        kern += "s_r%d_t%d" % (4 if tp == 8 else 2, tp)
+        kern = "q38_gemv_f32_" + sfx + ("s_r%d_t%d" % (4 if tp == 8 else 2, tp) if ty == 8 else "")
+    else:  # the matrix unit: k split over the waves up to 32 tokens or on small grids
+        big_wgs = -(-rows // 128) * -(-T // 64)
+        skinny = T <= 32 or 2 * big_wgs < ctx.info()["cu_count"]
+        kern = ("q38_gemm_f32s_" if skinny else "q38_gemm_f32_") + sfx
     rng = np.random.default_rng(0x51333940 + ty + rows)
     x = rng.standard_normal((T, W)).astype(np.float32)
     if T > 1:
