@@ -288,7 +288,7 @@ def test_multi_matrices_share_the_split_block_launch(ctx, ref, name):
 @pytest.mark.parametrize("rows,W,T", [(48, HIDDEN, 1), (48, HIDDEN, 3), (257, 1024, 9), (5, 6144, 17),
                                       (1031, 2048, 1), (48, HIDDEN, 64), (300, 1024, 100), (129, 768, 33),
                                       (64, 320, 16), (40, 1032, 20), (37, 64, 5), (19, 17408, 2), (70, 14528, 3),
-                                      (33, 6144, 15), (2048, 256, 512), (100, 1024, 9)])
+                                      (33, 6144, 15), (2048, 256, 512), (100, 1024, 9), (70, 17408, 12)])
 def test_gemv_f32_path(ctx, ref, name, rows, W, T):
     """tensor_gemv_f32 / tensor_gemm_f32 for the weight types project()
     does not quantise for (the 48-row beta / alpha projections of a DeltaNet
