@@ -975,7 +975,7 @@ def _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps):
 def prompt_projections(pkg, ctx, n_tokens: int, reps: int):
     """The FFN projections of one layer for a prompt of n_tokens (gate
     17408 x 5120 Q4_K, down 5120 x 17408 Q6_K; the int8 matrix-unit form
-    from 16 tokens on): kernel time and int8 operations per second
+    from 8 tokens on): kernel time and int8 operations per second
     (2 x rows x width x tokens; the K-quant expansion and the block terms
     are not counted)."""
     res = {"tokens": n_tokens}

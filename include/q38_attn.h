@@ -349,7 +349,7 @@ int q38_quantize_q8_k(q38_ctx *ctx, int n_tokens, int width, const float *d_x, v
  * d_q8k from q38_quantize_q8_k, d_out [n_tokens][rows] (token-major, as the
  * reference's batched form writes it).  width is at most 49152.  Each
  * element equals the reference's scalar dot_q*_k_q8_k (tensor.rs:301-457)
- * or dot_iq*_q8_k (src/kernel/iq.rs:355-667) bit for bit.  From 16 tokens
+ * or dot_iq*_q8_k (src/kernel/iq.rs:355-667) bit for bit.  From 8 tokens
  * on, where the matrix has rows for 64+ tiles of 32 rows x 32 tokens, the
  * integer dots run on the int8 matrix unit (IQ4_NL: from 32 tokens, 16 for
  * 8192+ rows); the result is the same bit for bit.  Other weight types
@@ -364,8 +364,8 @@ int q38_gemv_q8_k(q38_ctx *ctx, int ggml_type, int rows, int width, const void *
  * to 4 matrices of one type and width, matrix i with rows[i] rows at
  * d_weights[i], its output at d_out[i] [n_tokens][rows[i]], in one launch.
  * Each output equals q38_gemv_q8_k's for that matrix bit for bit, and the
- * matrices share launches: below 16 tokens every matrix streams through one
- * GEMV launch; from 16 on, a matrix whose 32-row x 32-token grid exceeds 5
+ * matrices share launches: below 8 tokens every matrix streams through one
+ * GEMV launch; from 8 on, a matrix whose 32-row x 32-token grid exceeds 5
  * workgroups per CU takes the 128 x 64 tiles, a launch of its own, and the
  * others share one split-block launch where their grids add up to 64
  * workgroups (the GEMV otherwise), so a matrix may take another form here
@@ -380,7 +380,7 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
  * width, d_weights, d_q8k, n_tokens, d_out), bit for bit, d_q8k (16-byte
  * aligned, q38_q8k_bytes) holding the quantised input afterwards; d_x
  * [n_tokens][width] f32, 16-byte aligned.  Where every matrix stays on the
- * GEMV (below 16 tokens, or matrices too small for the matrix unit) it is
+ * GEMV (below 8 tokens, or matrices too small for the matrix unit) it is
  * one launch instead of two: each GEMV workgroup quantises the input
  * itself.  Fails with -1 as those two calls do. */
 int q38_quantize_project_q8_k(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,

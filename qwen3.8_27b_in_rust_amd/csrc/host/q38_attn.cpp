@@ -1984,9 +1984,11 @@ static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *ro
      * Q38_GEMM_MIN_TOKENS tokens on, the others share one split-block launch
      * where their grids add up to at least kGemmKsMinTiles workgroups (on
      * fewer, e.g. 1024 x 5120 alone below 64 tokens, the GEMV is faster)
-     * (measured on the FFN, q|gate and k matrices, 4-512 tokens).  IQ4_NL,
-     * which has only the 128 x 64 form, takes it from 32 tokens (16 for
-     * 8192+ rows). */
+     * (measured on the FFN, q|gate and k matrices, 4-512 tokens: at 8 tokens
+     * as fast as the GEMV for one matrix, at 9-15 tokens 1.2-1.6x faster,
+     * where the GEMV takes two passes; a layer's projections at 8-15 tokens
+     * 1.4-2x faster).  IQ4_NL, which has only the 128 x 64 form, takes it
+     * from Q38_GEMM_IQ4NL_MIN_TOKENS tokens (half as many for 8192+ rows). */
     const int ti = ti_occ;
     const long tok_tiles = ((long)n_tokens + Q38_GEMM_TOKENS - 1) / Q38_GEMM_TOKENS;
     const long ks_tok_tiles = ((long)n_tokens + Q38_GEMM_KS_TOKENS - 1) / Q38_GEMM_KS_TOKENS;
@@ -2000,8 +2002,8 @@ static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *ro
             on_big[i] = n_tokens >= Q38_GEMM_MIN_TOKENS && ks_tiles > kGemmKsMaxPerCu * (long)ctx->cu_count;
             if (!on_big[i]) ks_total += ks_tiles;
         } else if (has_gemm) {
-            on_big[i] = n_tokens >= 2 * Q38_GEMM_MIN_TOKENS ||
-                        (n_tokens >= Q38_GEMM_MIN_TOKENS && rows[i] >= 64L * Q38_GEMM_ROWS);
+            on_big[i] = n_tokens >= Q38_GEMM_IQ4NL_MIN_TOKENS ||
+                        (2 * n_tokens >= Q38_GEMM_IQ4NL_MIN_TOKENS && rows[i] >= 64L * Q38_GEMM_ROWS);
         }
         any_gemm = any_gemm || on_big[i];
     }

@@ -331,9 +331,10 @@ typedef struct {
 #define Q38_GEMV_MAX_MATS 4
 /* From this many tokens the projections may run on the int8 matrix unit
  * (q38_gemm_q8k_*: grid (ceil(rows / 128), ceil(T / 64)), 256 threads, the
- * same arguments with one matrix; IQ4_NL from twice as many for matrices
- * of under 8192 rows). */
-#define Q38_GEMM_MIN_TOKENS 16
+ * same arguments with one matrix); IQ4_NL, which has only that form, from
+ * Q38_GEMM_IQ4NL_MIN_TOKENS (half as many for matrices of 8192+ rows). */
+#define Q38_GEMM_MIN_TOKENS 8
+#define Q38_GEMM_IQ4NL_MIN_TOKENS 32
 #define Q38_GEMM_ROWS 128
 #define Q38_GEMM_TOKENS 64
 /* Where that grid holds few workgroups (few rows or tokens), the blocks of a

@@ -185,7 +185,7 @@ def test_quantize_project_equals_separate_calls(ctx, ref, name, rows, W, T):
 @pytest.mark.parametrize("rows,W,T", [(130, 1280, 32), (2050, 256, 33), (1100, 1280, 65), (700, HIDDEN, 130),
                                       (2100, 2304, 64), (8200, 256, 16), (4200, 2304, 40), (4100, 768, 1000)])
 def test_gemm_many_tokens_bit_exact(ctx, ref, name, rows, W, T):
-    """The matrix-unit forms from 16 tokens on, bit for bit against the
+    """The matrix-unit forms from 8 tokens on, bit for bit against the
     oracle, with partial row and token tiles.  The split-block form (32 rows
     x 32 tokens per workgroup, a row's blocks split over the waves) where
     its grid has 64 to 1280 workgroups: on 16 waves up to 256 workgroups
@@ -218,7 +218,7 @@ def _ran(ctx, kernel, call):
 @pytest.mark.parametrize("name", ["Q4_K", "Q6_K", "IQ2_S", "IQ4_NL"])
 def test_projection_path_boundaries(ctx, ref, name):
     """The library's choice between the GEMV and the matrix-unit forms at
-    each of its boundaries (16 tokens; 64 split-block workgroups of 32 rows
+    each of its boundaries (8 tokens; 64 split-block workgroups of 32 rows
     x 32 tokens; one workgroup per CU for the 16-wave form, 1.5 for the
     8-wave one, 5 for the 4-wave one, past which the 128 x 64 tiles run):
     the expected kernel runs on each side, and
@@ -229,10 +229,10 @@ def test_projection_path_boundaries(ctx, ref, name):
     cus = ctx.info()["cu_count"]
     W = 256
     cases = [  # rows, tokens, kernel expected
-        (2048, 15, "q38_gemv_q8k_"), (2048, 16, "q38_gemm_ks16_q8k_"), (2016, 16, "q38_gemv_q8k_"),
-        (32 * cus, 16, "q38_gemm_ks16_q8k_"), (32 * cus + 1, 16, "q38_gemm_ks_q8k_"),
-        (48 * cus, 16, "q38_gemm_ks_q8k_"), (48 * cus + 1, 16, "q38_gemm_ks4_q8k_"),
-        (32 * 5 * cus, 16, "q38_gemm_ks4_q8k_"), (32 * 5 * cus + 1, 16, "q38_gemm_q8k_"),
+        (2048, 7, "q38_gemv_q8k_"), (2048, 8, "q38_gemm_ks16_q8k_"), (2016, 8, "q38_gemv_q8k_"),
+        (32 * cus, 8, "q38_gemm_ks16_q8k_"), (32 * cus + 1, 8, "q38_gemm_ks_q8k_"),
+        (48 * cus, 8, "q38_gemm_ks_q8k_"), (48 * cus + 1, 8, "q38_gemm_ks4_q8k_"),
+        (32 * 5 * cus, 8, "q38_gemm_ks4_q8k_"), (32 * 5 * cus + 1, 8, "q38_gemm_q8k_"),
     ]
     if name == "IQ4_NL":
         cases = [(2048, 31, "q38_gemv_q8k_"), (2048, 32, "q38_gemm_q8k_"), (8191, 16, "q38_gemv_q8k_"),
@@ -252,7 +252,7 @@ def test_projection_path_boundaries(ctx, ref, name):
 
 @pytest.mark.parametrize("name", ["Q4_K", "Q5_K", "IQ3_S"])
 def test_multi_matrices_share_the_split_block_launch(ctx, ref, name):
-    """The path of a multi-matrix call at 16 tokens: a matrix past 5
+    """The path of a multi-matrix call at 8 tokens: a matrix past 5
     split-block workgroups per CU takes the 128 x 64 tiles on its own, and
     the others share one split-block launch when their grids add up to 64
     workgroups, though neither would take it alone (63 and 2); every output
@@ -260,7 +260,7 @@ def test_multi_matrices_share_the_split_block_launch(ctx, ref, name):
     ty = TYPES[name]
     sfx = {"Q4_K": "q4k", "Q5_K": "q5k", "IQ3_S": "iq3s"}[name]
     cus = ctx.info()["cu_count"]
-    W, T = 256, 16
+    W, T = 256, 8
     x = _activations(T, W, 0x51333B00)
     d_q = _quantize_on_device(ctx, x)
     q8 = ref.quantize_q8_k(x)
