@@ -935,7 +935,7 @@ def f32_path(pkg, ctx, reps: int):
             ctx.gemv_f32(ty, rows, width, w, x, n_tokens, out)
             ctx.sync()
             sfx = name.lower()
-            kerns = ["q38_gemm_f32_" + sfx, "q38_gemm_f32s_" + sfx]
+            kerns = ["q38_gemm_f32w_" + sfx, "q38_gemm_f32_" + sfx, "q38_gemm_f32s_" + sfx]
             kerns += ["q38_gemv_f32_q8_0s_r%d_t%d" % (r, t) for r in (2, 4) for t in (1, 2, 4, 8)] if ty == 8 else \
                 ["q38_gemv_f32_" + sfx]
             for kern in kerns:

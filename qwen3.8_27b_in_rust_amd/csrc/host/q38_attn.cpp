@@ -162,6 +162,7 @@ struct q38_ctx {
     hipFunction_t f_gemv_f32[3] = {nullptr, nullptr, nullptr}; /* F32, F16, BF16 weights */
     hipFunction_t f_gemm_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* the same, on the matrix unit */
     hipFunction_t f_gemm_f32s[4] = {nullptr, nullptr, nullptr, nullptr}; /* few tokens, k split over the waves */
+    hipFunction_t f_gemm_f32w[4] = {nullptr, nullptr, nullptr, nullptr}; /* 128-token tiles (not F32) */
     hipFunction_t f_gemv_q80s[2][4] = {}; /* Q8_0, activations staged in LDS: [RW 2, 4][TP 1, 2, 4, 8] */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
@@ -445,6 +446,9 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32s[1], ctx->mod_proj, "q38_gemm_f32s_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32s[2], ctx->mod_proj, "q38_gemm_f32s_bf16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32s[3], ctx->mod_proj, "q38_gemm_f32s_q8_0"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32w[1], ctx->mod_proj, "q38_gemm_f32w_f16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32w[2], ctx->mod_proj, "q38_gemm_f32w_bf16"));
+    Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32w[3], ctx->mod_proj, "q38_gemm_f32w_q8_0"));
     for (int r = 0; r < 2; ++r)
         for (int t = 0; t < 4; ++t) {
             char nm[64];
@@ -652,6 +656,9 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemm_f32s_f16") f = ctx->f_gemm_f32s[1];
     else if (name == "q38_gemm_f32s_bf16") f = ctx->f_gemm_f32s[2];
     else if (name == "q38_gemm_f32s_q8_0") f = ctx->f_gemm_f32s[3];
+    else if (name == "q38_gemm_f32w_f16") f = ctx->f_gemm_f32w[1];
+    else if (name == "q38_gemm_f32w_bf16") f = ctx->f_gemm_f32w[2];
+    else if (name == "q38_gemm_f32w_q8_0") f = ctx->f_gemm_f32w[3];
     else if (name.rfind("q38_gemv_f32_q8_0s_r", 0) == 0 && name.size() == 24 && (name[20] == '2' || name[20] == '4') &&
              name[21] == '_' && name[22] == 't' && (name[23] == '1' || name[23] == '2' || name[23] == '4' || name[23] == '8'))
         f = ctx->f_gemv_q80s[name[20] == '4'][name[23] == '1' ? 0 : name[23] == '2' ? 1 : name[23] == '4' ? 2 : 3];
@@ -2213,9 +2220,17 @@ int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d
     a.rows = rows;
     a.width = width;
     a.n_tokens = n_tokens;
-    if (on_unit)
-        return ctx->launch(ctx->f_gemm_f32[ti], (unsigned)((rows + Q38_GEMM_F32_ROWS - 1) / Q38_GEMM_F32_ROWS),
+    if (on_unit) {
+        /* 128-token tiles where they still give 4+ workgroups per CU
+         * (measured: 5-11% faster at 4096 tokens through 5120-17408 rows,
+         * 12-25% slower at 512-1024 tokens, where the grid shrinks) */
+        const long row_tiles = ((long)rows + Q38_GEMM_F32_ROWS - 1) / Q38_GEMM_F32_ROWS;
+        const long wide_tok = ((long)n_tokens + Q38_GEMM_F32_WIDE_TOKENS - 1) / Q38_GEMM_F32_WIDE_TOKENS;
+        if (ctx->f_gemm_f32w[ti] != nullptr && row_tiles * wide_tok >= 4L * ctx->cu_count)
+            return ctx->launch(ctx->f_gemm_f32w[ti], (unsigned)row_tiles, (unsigned)wide_tok, 1, 256, &a);
+        return ctx->launch(ctx->f_gemm_f32[ti], (unsigned)row_tiles,
                            (unsigned)((n_tokens + Q38_GEMM_F32_TOKENS - 1) / Q38_GEMM_F32_TOKENS), 1, 256, &a);
+    }
     /* Q8_0: the activations staged in LDS once per 4 RW rows, TP tokens a
      * pass (the smallest of 1, 2, 4, 8 that holds min(T, 8)); 4 rows a wave
      * for 8-token passes, else 2 (measured on 1024-17408 rows x 5120 and

@@ -1800,17 +1800,19 @@ extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_bf16(q38_gemv_f32
  *    w3 x2, w3 x3), so each output is the exact sum up to f32 rounding of
  *    the additions, as for the GEMV above (the reference's own x86 build
  *    reassociates these sums too).
- * Tile: 128 weight rows x 64 tokens per workgroup of 4 waves, wave w
- * computing rows 64 (w & 1) .. +63 of tokens 32 (w >> 1) .. +31 (two 32 x
- * 32 accumulators, C column = weight row, so a token's 32 outputs are one
- * 128-byte store).  The k loop runs in stages of 64: each thread loads 16
+ * Tile: 128 weight rows x 32 TT tokens per workgroup of 4 waves (TT 2 or
+ * 4): with TT = 2 wave w computes rows 64 (w & 1) .. +63 of tokens 32 (w >>
+ * 1) .. +31, with TT = 4 all 128 rows of tokens 32 w .. +31 (TT 32 x 32
+ * accumulators; C column = weight row, so a token's 32 outputs are one
+ * 128-byte store; the wider tile reads each activation part from LDS for
+ * 4 row tiles instead of 2 and converts each weight for 128 tokens).  The k loop runs in stages of 64: each thread loads 16
  * activations of one token and 32 weights of one row (Q8_0: one block),
  * splits them into bf16 parts in LDS in the operands' lane layout, and the
  * next stage's loads go out before the matrix steps of this one.  Within a
  * 32-k slice, lane half h of substep s takes k 16h + 8s .. +7 for A and B
  * alike.  Tokens past T read the last token and rows past the matrix its
- * last row; neither is stored.  grid (ceil(rows / 128), ceil(T / 64)), 256
- * threads; width a multiple of 64.
+ * last row; neither is stored.  grid (ceil(rows / 128), ceil(T / (32 TT))),
+ * 256 threads; width a multiple of 64.
  */
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -1880,14 +1882,16 @@ Q38_DEV void f32w_load(const uint8_t *row, int slice, F32wRaw<TYPE> &r) {
     }
 }
 
-constexpr int kF32wRows = Q38_GEMM_F32_ROWS, kF32wTok = Q38_GEMM_F32_TOKENS, kF32wK = Q38_GEMM_F32_K;
-static_assert(kF32wRows == 128 && kF32wTok == 64 && kF32wK == 64, "the tile the lane mapping below assumes");
+constexpr int kF32wRows = Q38_GEMM_F32_ROWS, kF32wK = Q38_GEMM_F32_K;
+static_assert(kF32wRows == 128 && kF32wK == 64, "the tile the lane mapping below assumes");
 
-template <int TYPE>
+template <int TYPE, int TT>
 Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
     constexpr int PW = F32wParts<TYPE>::n;
+    constexpr int RPW = TT; /* row tiles per wave: 4 row tiles x TT token tiles over 4 waves */
+    constexpr int XQ = TT / 2; /* 64-token groups a thread stages */
     /* operand units (16 bytes: 8 bf16 of one lane) in the lane layout */
-    __shared__ __align__(16) u32x4 xs[3][2][2][2][64];  /* [part][token tile][slice][substep][lane] */
+    __shared__ __align__(16) u32x4 xs[3][TT][2][2][64]; /* [part][token tile][slice][substep][lane] */
     __shared__ __align__(16) u32x4 ws[PW][4][2][2][64]; /* [part][row tile][slice][substep][lane] */
     __shared__ float ds[2][kF32wRows];                   /* Q8_0: [slice][row] block scale */
     const int tid = threadIdx.x;
@@ -1895,41 +1899,46 @@ Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
     const int wave = tid >> 6;
     const int rows = a.rows, W = a.width, T = a.n_tokens;
     const int row0 = blockIdx.x * kF32wRows;
-    const int t0 = blockIdx.y * kF32wTok;
+    const int t0 = blockIdx.y * 32 * TT;
     /* this thread's loads: 16 activations of token xt (k 16 c .. +15 of a
      * stage), and slice wj of weight row wr */
     const int xl = tid >> 2, c = tid & 3;
-    const float *xp = a.x + (size_t)min(t0 + xl, T - 1) * W + 16 * c;
+    const float *xp[XQ];
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) xp[q] = a.x + (size_t)min(t0 + xl + 64 * q, T - 1) * W + 16 * c;
     const int wl = tid >> 1, wj = tid & 1;
     const uint8_t *wrow = a.weights + (size_t)min(row0 + wl, rows - 1) * a.row_bytes;
     const int n_stages = W / kF32wK;
 
-    f32x4 xr[4];
+    f32x4 xr[XQ][4];
     F32wRaw<TYPE> wr;
     auto load = [&](int st) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[i] = q38_ld4(xp + (size_t)st * kF32wK + 4 * i);
+        for (int q = 0; q < XQ; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xr[q][i] = q38_ld4(xp[q] + (size_t)st * kF32wK + 4 * i);
         f32w_load<TYPE>(wrow, 2 * st + wj, wr);
     };
 
-    f32x16 acc[2];
+    f32x16 acc[RPW];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[r][e] = 0.0f;
-    const int tt = wave >> 1;
-    const int rt0 = 2 * (wave & 1);
+    const int tt = TT == 4 ? wave : wave >> 1;
+    const int rt0 = TT == 4 ? 0 : 2 * (wave & 1);
 
     load(0);
     for (int st = 0; st < n_stages; ++st) {
         /* activations: slice c >> 1, lane half c & 1, substeps 0 and 1 */
-        {
-            const int j = c >> 1, h = c & 1, ln = 32 * h + (xl & 31), xt = xl >> 5;
+#pragma unroll
+        for (int q = 0; q < XQ; ++q) {
+            const int j = c >> 1, h = c & 1, ln = 32 * h + (xl & 31), xt = (xl >> 5) + 2 * q;
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
                 float v[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = xr[2 * sb + (i >> 2)][i & 3];
+                for (int i = 0; i < 8; ++i) v[i] = xr[q][2 * sb + (i >> 2)][i & 3];
                 u32x4 p[3];
                 split_parts<3>(v, p);
 #pragma unroll
@@ -2005,10 +2014,10 @@ Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
         if (st + 1 < n_stages) load(st + 1);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            f32x16 blk[2];
+            f32x16 blk[RPW];
             if constexpr (TYPE == Q38_GGML_Q8_0) {
 #pragma unroll
-                for (int r = 0; r < 2; ++r)
+                for (int r = 0; r < RPW; ++r)
 #pragma unroll
                     for (int e = 0; e < 16; ++e) blk[r][e] = 0.0f;
             }
@@ -2018,7 +2027,7 @@ Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
 #pragma unroll
                 for (int k = 0; k < 3; ++k) ax[k] = xs[k][tt][j][sb][lane];
 #pragma unroll
-                for (int r = 0; r < 2; ++r) {
+                for (int r = 0; r < RPW; ++r) {
                     u32x4 bw[PW];
 #pragma unroll
                     for (int k = 0; k < PW; ++k) bw[k] = ws[k][rt0 + r][j][sb][lane];
@@ -2028,7 +2037,7 @@ Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
             }
             if constexpr (TYPE == Q38_GGML_Q8_0) {
 #pragma unroll
-                for (int r = 0; r < 2; ++r) {
+                for (int r = 0; r < RPW; ++r) {
                     const float d = ds[j][32 * (rt0 + r) + (lane & 31)];
 #pragma unroll
                     for (int e = 0; e < 16; ++e) acc[r][e] = __builtin_fmaf(d, blk[r][e], acc[r][e]);
@@ -2038,7 +2047,7 @@ Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
         __syncthreads();
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < RPW; ++r) {
         const int row = row0 + 32 * (rt0 + r) + (lane & 31);
         if (row >= rows) continue;
 #pragma unroll
@@ -2049,10 +2058,21 @@ Q38_DEV void gemm_f32w(const q38_gemv_f32_args &a) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_f32(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_F32>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_f16(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_F16>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_bf16(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_BF16>(a); }
-extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_q8_0(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_Q8_0>(a); }
+static_assert(Q38_GEMM_F32_TOKENS == 64 && Q38_GEMM_F32_WIDE_TOKENS == 128, "2 and 4 token tiles per workgroup");
+/* F32 weights only at 64 tokens: at 128 their three parts per weight take
+ * 257 registers (one wave per SIMD) and measured no faster */
+extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_f32(q38_gemv_f32_args a) { gemm_f32w<Q38_GGML_F32, 2>(a); }
+#define Q38_GEMM_F32(name, T)                                                                              \
+    extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32_##name(q38_gemv_f32_args a) {          \
+        gemm_f32w<T, 2>(a);                                                                               \
+    }                                                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void q38_gemm_f32w_##name(q38_gemv_f32_args a) {         \
+        gemm_f32w<T, 4>(a);                                                                               \
+    }
+Q38_GEMM_F32(f16, Q38_GGML_F16)
+Q38_GEMM_F32(bf16, Q38_GGML_BF16)
+Q38_GEMM_F32(q8_0, Q38_GGML_Q8_0)
+#undef Q38_GEMM_F32
 
 /*
  * The matrix-unit form for few tokens: a workgroup of 4 waves owns 64 rows x

@@ -371,10 +371,12 @@ typedef struct {
  * (ceil(rows / 4), ceil(T / Q38_GEMV_TOKENS)), 256 threads, one wave per
  * row; the bf16 matrix-unit forms (width a multiple of Q38_GEMM_F32_K):
  * q38_gemm_f32_*, grid (ceil(rows / Q38_GEMM_F32_ROWS), ceil(T /
- * Q38_GEMM_F32_TOKENS)), and q38_gemm_f32s_*, grid (ceil(rows / 64),
- * ceil(T / 32)), 256 threads. */
+ * Q38_GEMM_F32_TOKENS)), q38_gemm_f32w_*, the same with
+ * Q38_GEMM_F32_WIDE_TOKENS tokens per workgroup, and q38_gemm_f32s_*, grid
+ * (ceil(rows / 64), ceil(T / 32)), 256 threads. */
 #define Q38_GEMM_F32_ROWS 128
 #define Q38_GEMM_F32_TOKENS 64
+#define Q38_GEMM_F32_WIDE_TOKENS 128
 #define Q38_GEMM_F32_K 64
 /* q38_gemv_f32_q8_0s_r{RW}_t{TP} (Q8_0 weights, few tokens): grid
  * (ceil(rows / (4 RW)), ceil(T / TP)), 256 threads, RW 2 or 4, TP 1, 2, 4

@@ -288,7 +288,8 @@ def test_multi_matrices_share_the_split_block_launch(ctx, ref, name):
 @pytest.mark.parametrize("rows,W,T", [(48, HIDDEN, 1), (48, HIDDEN, 3), (257, 1024, 9), (5, 6144, 17),
                                       (1031, 2048, 1), (48, HIDDEN, 64), (300, 1024, 100), (129, 768, 33),
                                       (64, 320, 16), (40, 1032, 20), (37, 64, 5), (19, 17408, 2), (70, 14528, 3),
-                                      (33, 6144, 15), (2048, 256, 512), (100, 1024, 9), (70, 17408, 12)])
+                                      (33, 6144, 15), (2048, 256, 512), (100, 1024, 9), (70, 17408, 12),
+                                      (4100, 128, 4096)])
 def test_gemv_f32_path(ctx, ref, margin, name, rows, W, T):
     """tensor_gemv_f32 / tensor_gemm_f32 for the weight types project()
     does not quantise for (the 48-row beta / alpha projections of a DeltaNet
@@ -307,9 +308,11 @@ def test_gemv_f32_path(ctx, ref, margin, name, rows, W, T):
         tp = min(t for t in (1, 2, 4, 8) if t >= min(T, 8))
         kern = "q38_gemv_f32_" + sfx + ("s_r%d_t%d" % (4 if tp == 8 else 2, tp) if ty == 8 else "")
     else:  # the matrix unit: k split over the waves up to 32 tokens or on small grids
+        cus = ctx.info()["cu_count"]
         big_wgs = -(-rows // 128) * -(-T // 64)
-        skinny = T <= 32 or 2 * big_wgs < ctx.info()["cu_count"]
-        kern = ("q38_gemm_f32s_" if skinny else "q38_gemm_f32_") + sfx
+        skinny = T <= 32 or 2 * big_wgs < cus
+        wide = ty != 0 and -(-rows // 128) * -(-T // 128) >= 4 * cus  # 128-token tiles (not F32)
+        kern = ("q38_gemm_f32s_" if skinny else "q38_gemm_f32w_" if wide else "q38_gemm_f32_") + sfx
     rng = np.random.default_rng(0x51333940 + ty + rows)
     x = rng.standard_normal((T, W)).astype(np.float32)
     if T > 1:

@@ -75,7 +75,8 @@ def test_split_block_gemm_fits_its_workgroups(kernels):
 def test_f32_path_kernels_do_not_spill(kernels):
     """The f32-input path: the GEMV and the bf16 matrix-unit form (two
     workgroups per CU: at most 256 registers), no spills."""
-    f32 = {k: v for k, v in kernels.items() if k.startswith(("q38_gemv_f32_", "q38_gemm_f32_", "q38_gemm_f32s_"))}
-    assert len(f32) == 19
+    f32 = {k: v for k, v in kernels.items()
+           if k.startswith(("q38_gemv_f32_", "q38_gemm_f32_", "q38_gemm_f32s_", "q38_gemm_f32w_"))}
+    assert len(f32) == 22
     for name, (vgpr, scratch) in f32.items():
         assert scratch == 0 and vgpr <= 256, (name, vgpr, scratch)
