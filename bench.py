@@ -914,6 +914,15 @@ BF16_PEAK_TFLOPS = 2500.0
 F32_PATH_TYPES = {0: ("F32", 4.0), 1: ("F16", 2.0), 30: ("BF16", 2.0), 8: ("Q8_0", 34.0 / 32.0)}
 
 
+def _f32_path_kernels(ty: int) -> list:
+    """The kernels q38_gemv_f32 may launch for weight type ty."""
+    sfx = F32_PATH_TYPES[ty][0].lower()
+    kerns = ["q38_gemm_f32_" + sfx, "q38_gemm_f32s_" + sfx] + (["q38_gemm_f32w_" + sfx] if ty != 0 else [])
+    if ty == 8:
+        return kerns + ["q38_gemv_f32_q8_0s_r%d_t%d" % (r, t) for r in (2, 4) for t in (1, 2, 4, 8)]
+    return kerns + ["q38_gemv_f32_" + sfx]
+
+
 def f32_path(pkg, ctx, reps: int):
     """The projection path of weights project() does not quantise for
     (q38_gemv_f32: F32, F16, BF16, Q8_0) through 17408 x 5120 at 1, 16 and
@@ -934,11 +943,7 @@ def f32_path(pkg, ctx, reps: int):
             ctx.fill_normal(w, (nbytes + 16) // 4, 0x51335610 + ty, sigma=0.05)
             ctx.gemv_f32(ty, rows, width, w, x, n_tokens, out)
             ctx.sync()
-            sfx = name.lower()
-            kerns = ["q38_gemm_f32w_" + sfx, "q38_gemm_f32_" + sfx, "q38_gemm_f32s_" + sfx]
-            kerns += ["q38_gemv_f32_q8_0s_r%d_t%d" % (r, t) for r in (2, 4) for t in (1, 2, 4, 8)] if ty == 8 else \
-                ["q38_gemv_f32_" + sfx]
-            for kern in kerns:
+            for kern in _f32_path_kernels(ty):
                 ctx.kernel_timer_start(kern, reps)
                 for _ in range(reps):
                     ctx.gemv_f32(ty, rows, width, w, x, n_tokens, out)
@@ -1192,7 +1197,10 @@ def main():
         sys.exit(2)
     for name in wanted:
         log(f"{name}: {EXTRAS[name][0]}")
-        extra[name] = EXTRAS[name][1](pkg, ctx)
+        try:
+            extra[name] = EXTRAS[name][1](pkg, ctx)
+        except pkg.Q38Error as e:  # a library error in one extra is recorded; the headline line still prints
+            extra[name] = {"error": str(e)}
         log(f"{name}: {json.dumps(extra[name])}")
 
     line = {
