@@ -812,25 +812,19 @@ def ffn_projections(pkg, ctx, n_tokens: int, reps: int, layers: int = 4):
     if g_us is not None:
         res["fused_gate_up_sweep_graph_us"] = g_us
         res["fused_gate_up_sweep_graph_gb_s"] = total_bytes / (g_us * 1e-6) / 1e9
-    ctx.kernel_timer_start(GEMV_KERNELS[12], reps * layers)
-    for _ in range(reps):
-        sweep_fused()
-    k_ms, k_n = ctx.kernel_timer_stop()
-    us = k_ms * 1e3 / max(k_n, 1)
+    kern, k_ms, k_n = _timed_q8k_kernel(ctx, 12, sweep_fused, reps, reps * layers)
+    us = k_ms * 1e3 / k_n
     b = 2 * gemv_bytes(12, 17408, 5120, n_tokens)
-    res["q4k_gate_up_2x17408x5120"] = {"kernel_us": us, "launches": k_n, "algorithmic_bytes": b,
+    res["q4k_gate_up_2x17408x5120"] = {"kernel": kern, "kernel_us": us, "launches": k_n, "algorithmic_bytes": b,
                                        "gb_s": b / (us * 1e-6) / 1e9,
                                        "frac_hbm": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
     out2.free()
     for ty, label in ((12, "q4k_17408x5120"), (14, "q6k_5120x17408")):
-        ctx.kernel_timer_start(GEMV_KERNELS[ty], reps * 3 * layers)
-        for _ in range(reps):
-            sweep()
-        k_ms, k_n = ctx.kernel_timer_stop()
-        us = k_ms * 1e3 / max(k_n, 1)
+        kern, k_ms, k_n = _timed_q8k_kernel(ctx, ty, sweep, reps, reps * 3 * layers)
+        us = k_ms * 1e3 / k_n
         rows, width = (17408, 5120) if ty == 12 else (5120, 17408)
         b = gemv_bytes(ty, rows, width, n_tokens)
-        res[label] = {"kernel_us": us, "launches": k_n, "algorithmic_bytes": b,
+        res[label] = {"kernel": kern, "kernel_us": us, "launches": k_n, "algorithmic_bytes": b,
                       "gb_s": b / (us * 1e-6) / 1e9, "frac_hbm": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
     for *_, w in mats:
         w.free()
@@ -960,21 +954,37 @@ def f32_path(pkg, ctx, reps: int):
     return res
 
 
+def _q8k_kernels(ty: int) -> tuple:
+    """The kernels q38_gemv_q8_k may launch for weight type ty: the
+    split-block matrix-unit forms (16, 8, 4 waves), the 128 x 64 one, the
+    GEMV (IQ4_NL: the last two)."""
+    gemv = GEMV_KERNELS[ty]
+    kernels = (gemv.replace("q38_gemv_q8k_", "q38_gemm_ks16_q8k_"), gemv.replace("q38_gemv_q8k_", "q38_gemm_ks_q8k_"),
+               gemv.replace("q38_gemv_q8k_", "q38_gemm_ks4_q8k_"), gemv.replace("gemv", "gemm"), gemv)
+    return kernels if ty != 20 else kernels[3:]
+
+
+def _timed_q8k_kernel(ctx, ty, work, reps, max_launches):
+    """(kernel, total ms, launches) of the weight-type-ty projection kernel
+    that reps calls of work() launch (the first of _q8k_kernels(ty) that
+    runs)."""
+    for kern in _q8k_kernels(ty):
+        ctx.kernel_timer_start(kern, max_launches)
+        for _ in range(reps):
+            work()
+        k_ms, k_n = ctx.kernel_timer_stop()
+        if k_n > 0:
+            return kern, k_ms, k_n
+    raise RuntimeError(f"no projection kernel of type {ty} was launched")
+
+
 def _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps):
     """Kernel time per call of one projection and the kernel that ran it:
     the split-block matrix-unit form (16, 8 or 4 waves), the 128 x 64 one or
     the GEMV, as the library chose for the shape."""
-    gemv = GEMV_KERNELS[ty]
-    kernels = (gemv.replace("q38_gemv_q8k_", "q38_gemm_ks16_q8k_"), gemv.replace("q38_gemv_q8k_", "q38_gemm_ks_q8k_"),
-               gemv.replace("q38_gemv_q8k_", "q38_gemm_ks4_q8k_"), gemv.replace("gemv", "gemm"), gemv)
-    for kern in kernels if ty != 20 else kernels[3:]:  # IQ4_NL has no split-block form
-        ctx.kernel_timer_start(kern, reps * 64)
-        for _ in range(reps):
-            ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
-        k_ms, k_n = ctx.kernel_timer_stop()
-        if k_n > 0:
-            return kern, k_ms / reps
-    raise RuntimeError(f"no projection kernel of type {ty} was launched")
+    kern, k_ms, _ = _timed_q8k_kernel(ctx, ty, lambda: ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out), reps,
+                                      reps * 64)
+    return kern, k_ms / reps
 
 
 def prompt_projections(pkg, ctx, n_tokens: int, reps: int):
@@ -1199,8 +1209,8 @@ def main():
         log(f"{name}: {EXTRAS[name][0]}")
         try:
             extra[name] = EXTRAS[name][1](pkg, ctx)
-        except pkg.Q38Error as e:  # a library error in one extra is recorded; the headline line still prints
-            extra[name] = {"error": str(e)}
+        except Exception as e:  # a failure in one extra is recorded; the headline line still prints
+            extra[name] = {"error": f"{type(e).__name__}: {e}"}
         log(f"{name}: {json.dumps(extra[name])}")
 
     line = {

@@ -30,12 +30,8 @@ def test_bench_timer_names_are_known():
     used = {bench.DECODE_KERNEL, "q38_attn_decode_merge", "q38_gdn_step_rows", "q38_noop", "q38_gdn_decode",
             "q38_attn_prefill_mfma", "q38_prefill_merge", "q38_kv_split_mfma", "q38_attn_decode_split_many",
             "q38_gdn_pre", "q38_gdn_post", "q38_copy_f32"}
-    for ty, gemv in bench.GEMV_KERNELS.items():
-        used.add(gemv)
-        used.add(gemv.replace("gemv", "gemm"))
-        if ty != 20:  # IQ4_NL has no split-block form
-            for form in ("ks16", "ks", "ks4"):
-                used.add(gemv.replace("q38_gemv_q8k_", "q38_gemm_%s_q8k_" % form))
+    for ty in bench.GEMV_KERNELS:
+        used.update(bench._q8k_kernels(ty))
     for ty in bench.F32_PATH_TYPES:
         used.update(bench._f32_path_kernels(ty))
     unknown = sorted(n for n in used if not _accepts(names, n))
