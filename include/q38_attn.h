@@ -379,10 +379,9 @@ int q38_gemv_q8_k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows
  * d_x, d_q8k) and then q38_gemv_q8_k_multi(ctx, ggml_type, n_mats, rows,
  * width, d_weights, d_q8k, n_tokens, d_out), bit for bit, d_q8k (16-byte
  * aligned, q38_q8k_bytes) holding the quantised input afterwards; d_x
- * [n_tokens][width] f32, 16-byte aligned.  Where every matrix stays on the
- * GEMV (below 8 tokens, or matrices too small for the matrix unit) it is
- * one launch instead of two: each GEMV workgroup quantises the input
- * itself.  Fails with -1 as those two calls do. */
+ * [n_tokens][width] f32, 16-byte aligned.  For one token (every matrix
+ * then on the GEMV) it is one launch instead of two: each GEMV workgroup
+ * quantises the input itself.  Fails with -1 as those two calls do. */
 int q38_quantize_project_q8_k(q38_ctx *ctx, int ggml_type, int n_mats, const int *rows, int width,
                               const void *const *d_weights, const float *d_x, int n_tokens, void *d_q8k,
                               float *const *d_out);

@@ -123,6 +123,11 @@ constexpr int kGemvTypes = (int)(sizeof(kGemv) / sizeof(kGemv[0]));
 /* The split-block GEMM's grid: at least this many workgroups (fewer: the
  * GEMV), at most this many per CU (more: the 128 x 64 tiles) */
 constexpr long kGemmKsMinTiles = 64;
+/* q38_quantize_project_q8_k folds the quantisation into the GEMV up to this
+ * many tokens (a layer's four projections, measured at 1-7 tokens: one
+ * token 65.5 against 68.0 us folded; two 84.5 against 74.8 us, every
+ * workgroup quantising both tokens) */
+constexpr int kQuantizeFoldMaxTokens = 1;
 constexpr long kGemmKsMaxPerCu = 5;
 
 }  // namespace
@@ -2018,8 +2023,10 @@ static int gemv_q8k_multi(q38_ctx *ctx, int ggml_type, int n_mats, const int *ro
         ks_call = n_tokens >= Q38_GEMM_MIN_TOKENS && ks_total >= kGemmKsMinTiles;
     any_gemm = any_gemm || ks_call;
     for (int i = 0; i < n_mats; ++i) on_gemv[i] = rows[i] > 0 && !on_big[i] && !ks_call;
-    /* the matrix-unit forms read the quantised input from memory */
-    if (d_x != nullptr && any_gemm) {
+    /* the matrix-unit forms read the quantised input from memory; the GEMV
+     * quantises it itself, in every workgroup, up to kQuantizeFoldMaxTokens
+     * tokens (beyond, that repeated work costs more than the launch) */
+    if (d_x != nullptr && (any_gemm || n_tokens > kQuantizeFoldMaxTokens)) {
         if (q38_quantize_q8_k(ctx, n_tokens, width, d_x, const_cast<void *>(d_q8k))) return -1;
         d_x = nullptr;
     }

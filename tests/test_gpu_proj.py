@@ -150,10 +150,10 @@ def test_gemv_multi_equals_single(ctx, ref, name, T):
 def test_quantize_project_equals_separate_calls(ctx, ref, name, rows, W, T):
     """quantize_input then project in one call (q38_quantize_project_q8_k):
     every output and every byte of the quantised input as
-    q38_quantize_q8_k + q38_gemv_q8_k_multi, and the oracle.  Below 16
-    tokens the GEMV quantises the input itself (17408-wide rows: passes of
-    3, 3 and 3 tokens, each pass's first row group storing its tokens); at
-    40 tokens the 1500-row matrix takes the matrix unit, so the input is
+    q38_quantize_q8_k + q38_gemv_q8_k_multi, and the oracle.  For one token
+    the GEMV quantises the input itself (the first row group storing it);
+    from two tokens (3 and 9 here, the latter 17408 wide) and where a matrix
+    takes the matrix unit (the 1500-row one at 40 tokens) the input is
     quantised by its own launch first."""
     ty = TYPES[name]
     x = _activations(T, W, 0x51333900 + T + W)
