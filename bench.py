@@ -28,10 +28,12 @@ context, batched paged decode,
 the launch floor, one-token linear_core over 48 layers, the 64-layer full
 stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
 the Q4_K/Q6_K FFN projections for 1 and 8 tokens and for prompts, a decode
-layer's projection chain with the input quantised apart or inside the GEMV, one token
-and a 4096-token prompt through one matrix in every weight format, and the
-recurrent-state checkpoint, each rotating over enough buffers to defeat the
-cache where the weights are streamed.
+layer's projection chain (quantise then project per input, as two calls and
+as one) for 1, 8 and 32 tokens, one token and a 4096-token prompt through
+one matrix in every Q8_K weight format, the F32/F16/BF16/Q8_0 projection
+path at 1, 16 and 4096 tokens, and the recurrent-state checkpoint, each
+rotating over enough buffers to defeat the cache where the weights are
+streamed.
 """
 from __future__ import annotations
 
@@ -1105,6 +1107,10 @@ EXTRAS = {
     "layer_projections_1": ("the projections of 4 attention layers' decode steps, 1 token: quantise then project "
                             "per input, as two calls and as one",
                             lambda pkg, ctx: layer_projections(pkg, ctx, 1, 20)),
+    "layer_projections_8": ("the same projections for a batch of 8 tokens",
+                            lambda pkg, ctx: layer_projections(pkg, ctx, 8, 10)),
+    "layer_projections_32": ("the same projections for a batch of 32 tokens",
+                             lambda pkg, ctx: layer_projections(pkg, ctx, 32, 10)),
     "ffn_projections_1": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 1 token",
                           lambda pkg, ctx: ffn_projections(pkg, ctx, 1, 20)),
     "ffn_projections_8": ("FFN projections (Q4_K gate/up, Q6_K down) of 4 layers, 8 tokens",
