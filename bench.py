@@ -915,7 +915,8 @@ def _f32_path_kernels(ty: int) -> list:
     sfx = F32_PATH_TYPES[ty][0].lower()
     kerns = ["q38_gemm_f32_" + sfx, "q38_gemm_f32s_" + sfx] + (["q38_gemm_f32w_" + sfx] if ty != 0 else [])
     if ty == 8:
-        return kerns + ["q38_gemv_f32_q8_0s_r%d_t%d" % (r, t) for r in (2, 4) for t in (1, 2, 4, 8)]
+        return kerns + ["q38_gemv_f32_q8_0s_r2_t1", "q38_gemv_f32_q8_0s_r2_t2", "q38_gemv_f32_q8_0s_r2_t4",
+                        "q38_gemv_f32_q8_0s_r4_t8"]
     return kerns + ["q38_gemv_f32_" + sfx]
 
 

@@ -168,7 +168,7 @@ struct q38_ctx {
     hipFunction_t f_gemm_f32[4] = {nullptr, nullptr, nullptr, nullptr}; /* the same, on the matrix unit */
     hipFunction_t f_gemm_f32s[4] = {nullptr, nullptr, nullptr, nullptr}; /* few tokens, k split over the waves */
     hipFunction_t f_gemm_f32w[4] = {nullptr, nullptr, nullptr, nullptr}; /* 128-token tiles (not F32) */
-    hipFunction_t f_gemv_q80s[2][4] = {}; /* Q8_0, activations staged in LDS: [RW 2, 4][TP 1, 2, 4, 8] */
+    hipFunction_t f_gemv_q80s[4] = {}; /* Q8_0, activations staged in LDS: TP 1, 2, 4 (RW 2), 8 (RW 4) */
     hipModule_t mod_synth = nullptr;
     hipFunction_t f_fill_normal = nullptr;
     hipFunction_t f_copy = nullptr;
@@ -454,12 +454,11 @@ int q38_ctx_create(q38_ctx **out, int device, const char *module_dir) {
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32w[1], ctx->mod_proj, "q38_gemm_f32w_f16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32w[2], ctx->mod_proj, "q38_gemm_f32w_bf16"));
     Q38_HIP(hipModuleGetFunction(&ctx->f_gemm_f32w[3], ctx->mod_proj, "q38_gemm_f32w_q8_0"));
-    for (int r = 0; r < 2; ++r)
-        for (int t = 0; t < 4; ++t) {
-            char nm[64];
-            snprintf(nm, sizeof(nm), "q38_gemv_f32_q8_0s_r%d_t%d", 2 << r, 1 << t);
-            Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q80s[r][t], ctx->mod_proj, nm));
-        }
+    for (int t = 0; t < 4; ++t) {
+        char nm[64];
+        snprintf(nm, sizeof(nm), "q38_gemv_f32_q8_0s_r%d_t%d", t == 3 ? 4 : 2, 1 << t);
+        Q38_HIP(hipModuleGetFunction(&ctx->f_gemv_q80s[t], ctx->mod_proj, nm));
+    }
     for (int i = 0; i < kGemvTypes; ++i) {
         int n = 0;
         Q38_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, ctx->f_gemv_q8k[i], 256, 0));
@@ -664,9 +663,10 @@ int q38_kernel_timer_start(q38_ctx *ctx, const char *kernel_name, int max_launch
     else if (name == "q38_gemm_f32w_f16") f = ctx->f_gemm_f32w[1];
     else if (name == "q38_gemm_f32w_bf16") f = ctx->f_gemm_f32w[2];
     else if (name == "q38_gemm_f32w_q8_0") f = ctx->f_gemm_f32w[3];
-    else if (name.rfind("q38_gemv_f32_q8_0s_r", 0) == 0 && name.size() == 24 && (name[20] == '2' || name[20] == '4') &&
-             name[21] == '_' && name[22] == 't' && (name[23] == '1' || name[23] == '2' || name[23] == '4' || name[23] == '8'))
-        f = ctx->f_gemv_q80s[name[20] == '4'][name[23] == '1' ? 0 : name[23] == '2' ? 1 : name[23] == '4' ? 2 : 3];
+    else if (name == "q38_gemv_f32_q8_0s_r2_t1") f = ctx->f_gemv_q80s[0];
+    else if (name == "q38_gemv_f32_q8_0s_r2_t2") f = ctx->f_gemv_q80s[1];
+    else if (name == "q38_gemv_f32_q8_0s_r2_t4") f = ctx->f_gemv_q80s[2];
+    else if (name == "q38_gemv_f32_q8_0s_r4_t8") f = ctx->f_gemv_q80s[3];
     else if (name == "q38_attn_prefill_mfma") f = ctx->f_prefill;
     else if (name == "q38_kv_split_mfma") f = ctx->f_kv_split;
     else if (name == "q38_prefill_merge") f = ctx->f_prefill_merge;
@@ -2245,9 +2245,8 @@ int q38_gemv_f32(q38_ctx *ctx, int ggml_type, int rows, int width, const void *d
     if (ti == 3) {
         const int tpi = n_tokens <= 1 ? 0 : n_tokens <= 2 ? 1 : n_tokens <= 4 ? 2 : 3;
         const int tp = 1 << tpi;
-        const bool wide = tp == 8;
-        const long wg_rows = wide ? 16 : 8;
-        return ctx->launch(ctx->f_gemv_q80s[wide][tpi], (unsigned)((rows + wg_rows - 1) / wg_rows),
+        const long wg_rows = tp == 8 ? 16 : 8;
+        return ctx->launch(ctx->f_gemv_q80s[tpi], (unsigned)((rows + wg_rows - 1) / wg_rows),
                            (unsigned)((n_tokens + tp - 1) / tp), 1, 256, &a);
     }
     return ctx->launch(ctx->f_gemv_f32[ti], (unsigned)row_groups, (unsigned)tok_groups, 1, 256, &a); /* ti < 3 */

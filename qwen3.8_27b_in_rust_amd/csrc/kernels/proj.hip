@@ -2370,12 +2370,9 @@ Q38_DEV void gemv_q80s(const q38_gemv_f32_args &a) {
     extern "C" __global__ __launch_bounds__(256) void q38_gemv_f32_q8_0s_r##rw##_t##tp(q38_gemv_f32_args a) { \
         gemv_q80s<rw, tp>(a);                                                                             \
     }
+/* the pairs the host launches: 2 rows a wave for 1-4 tokens a pass, 4 for 8 */
 Q38_GEMV_Q80S(2, 1)
 Q38_GEMV_Q80S(2, 2)
 Q38_GEMV_Q80S(2, 4)
-Q38_GEMV_Q80S(2, 8)
-Q38_GEMV_Q80S(4, 1)
-Q38_GEMV_Q80S(4, 2)
-Q38_GEMV_Q80S(4, 4)
 Q38_GEMV_Q80S(4, 8)
 #undef Q38_GEMV_Q80S

@@ -379,8 +379,8 @@ typedef struct {
 #define Q38_GEMM_F32_WIDE_TOKENS 128
 #define Q38_GEMM_F32_K 64
 /* q38_gemv_f32_q8_0s_r{RW}_t{TP} (Q8_0 weights, few tokens): grid
- * (ceil(rows / (4 RW)), ceil(T / TP)), 256 threads, RW 2 or 4, TP 1, 2, 4
- * or 8 */
+ * (ceil(rows / (4 RW)), ceil(T / TP)), 256 threads; (RW, TP) one of (2, 1),
+ * (2, 2), (2, 4), (4, 8) */
 typedef struct {
     const uint8_t *weights; /* [rows][row_bytes], 4-byte aligned (16 for F32/F16/BF16) */
     const float *x;         /* [T][width], 16-byte aligned */
