@@ -30,7 +30,8 @@ stack at 128K, the bare DeltaNet step for one and for 32 states per launch,
 the Q4_K/Q6_K FFN projections for 1 and 8 tokens and for prompts, a decode
 layer's projection chain (quantise then project per input, as two calls and
 as one) for 1, 8 and 32 tokens, one token and a 4096-token prompt through
-one matrix in every Q8_K weight format, the F32/F16/BF16/Q8_0 projection
+one matrix in every Q8_K weight format, the FFN projections' kernel and time
+at 1-4096 tokens, the F32/F16/BF16/Q8_0 projection
 path at 1, 16 and 4096 tokens, and the recurrent-state checkpoint, each
 rotating over enough buffers to defeat the cache where the weights are
 streamed.
@@ -990,6 +991,37 @@ def _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps):
     return kern, k_ms / reps
 
 
+def projection_sweep(pkg, ctx, reps: int):
+    """The FFN gate (17408 x 5120 Q4_K) and down (5120 x 17408 Q6_K)
+    projections at 1 to 4096 tokens: the kernel q38_gemv_q8_k chose (GEMV,
+    split-block matrix-unit form of 16 / 8 / 4 waves, 128 x 64 tiles), its
+    duration and its rate in weight bytes and int8 operations.  One matrix,
+    reused (cache-resident below ~200 MB); random weights (timing only)."""
+    res = {}
+    for ty, rows, width, label in ((12, 17408, 5120, "q4k_17408x5120"), (14, 5120, 17408, "q6k_5120x17408")):
+        nbytes = rows * (width // 256) * QUANT_BLOCK_BYTES[ty]
+        w = ctx.empty((nbytes,), np.uint8)
+        ctx.fill_normal(w, nbytes // 4, 0x51335700 + ty)
+        per = {}
+        for n_tokens in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 4096):
+            x = ctx.empty((n_tokens, width))
+            ctx.fill_normal(x, n_tokens * width, 0x51335710 + n_tokens)
+            q = ctx.empty((ctx.q8k_bytes(n_tokens, width),), np.uint8)
+            ctx.quantize_q8_k(n_tokens, width, x, q)
+            out = ctx.empty((n_tokens, rows))
+            ctx.gemv_q8_k(ty, rows, width, w, q, n_tokens, out)
+            ctx.sync()
+            kern, ms = _timed_projection(ctx, ty, rows, width, w, q, n_tokens, out, reps)
+            per[n_tokens] = {"kernel": kern, "us": round(ms * 1e3, 2),
+                             "weights_gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                             "int8_tops": round(2.0 * rows * width * n_tokens / (ms * 1e-3) / 1e12, 1)}
+            for a in (x, q, out):
+                a.free()
+        res[label] = per
+        w.free()
+    return res
+
+
 def prompt_projections(pkg, ctx, n_tokens: int, reps: int):
     """The FFN projections of one layer for a prompt of n_tokens (gate
     17408 x 5120 Q4_K, down 5120 x 17408 Q6_K; the int8 matrix-unit form
@@ -1101,6 +1133,8 @@ EXTRAS = {
                               lambda pkg, ctx: gdn_steps(pkg, ctx, 1, 1, 384, 32)),
     "recurrent_checkpoint": ("recurrent-state checkpoint of one sequence (157 MB)",
                              lambda pkg, ctx: recurrent_checkpoint(pkg, ctx, 20)),
+    "projection_sweep": ("FFN gate and down projections at 1-4096 tokens: the kernel chosen and its time",
+                         lambda pkg, ctx: projection_sweep(pkg, ctx, 3)),
     "prompt_projections_64": ("FFN projections of one layer for 64 prompt tokens",
                               lambda pkg, ctx: prompt_projections(pkg, ctx, 64, 5)),
     "prompt_projections_4096": ("FFN projections of one layer for a 4096-token prompt",
