@@ -17,11 +17,16 @@ names.  Each failure message names its seed and case.
   truncates over two sequences and two full-attention layers, with the
   prefill images kept and converted whole every call (bit-identical outputs),
   rows held against the restatement of full_core's attention
-  (src/model/ops.rs:868-938, :1153-1172) within 1e-3."""
+  (src/model/ops.rs:868-938, :1153-1172) within 1e-3;
+- linear_core: 1-3 sequences fed random pieces (one token, a few, 37-700)
+  in consecutive calls, the conv and recurrent states carried between them,
+  against the restatement run token by token (ops.rs:1088-1099, :744-804):
+  outputs within 1e-3, the conv state bit-exact, the recurrent state within
+  1e-4 relative."""
 import numpy as np
 import pytest
 from oracle_checks import _random_f32_path, _random_kquant
-from parity import abs_rel
+from parity import TOL_ABS, abs_rel, state_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -232,3 +237,51 @@ def test_random_kv_call_sequences(pkg, ctx, ref, synth, margin, seed):
             d.free()
     margin("out max-abs (sampled rows, all runs)", worst[0], 1e-3)
     margin("out rel (sampled rows, all runs)", worst[1], 1e-3)
+
+
+GDN_STATE = 48 * 128 * 128
+
+
+@pytest.mark.parametrize("seed", [0x5133C000, 0x5133C001, 0x5133C002])
+def test_random_linear_core_pieces(ctx, ref, margin, seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 4))
+    f32 = lambda *shape, s=1.0: (rng.standard_normal(shape) * s).astype(np.float32)
+    conv_w, dt = f32(10240 * 4, s=0.5), f32(48)
+    a = -np.abs(f32(48))
+    norm = (1.0 + f32(128, s=0.1)).astype(np.float32)
+    conv = f32(n, 30720)
+    delta = f32(n, GDN_STATE, s=0.02)
+    d_w = [ctx.array(x) for x in (conv_w, dt, a, norm)]
+    d_conv, d_delta = ctx.array(conv), ctx.array(delta)
+    c_ref = [conv[s].copy() for s in range(n)]
+    s_ref = [delta[s].copy() for s in range(n)]
+    pieces = [int(rng.choice([1, 1, 1, 2, 3, 5, 8, 16, 37, 63, 64, 65, 129, 300, 700])) for _ in range(8)]
+    worst = 0.0
+    for call, T in enumerate(pieces):
+        qkv, z = f32(n, T, 10240), f32(n, T, 6144)
+        b, al = f32(n, T, 48), f32(n, T, 48)
+        d_in = [ctx.array(x) for x in (qkv, z, b, al)]
+        d_out = ctx.empty((n * T, 6144))
+        ctx.linear_core(n, T, *d_w, d_conv, d_delta, *d_in, d_out)
+        got = d_out.download().reshape(n, T, 6144)
+        for d in d_in + [d_out]:
+            d.free()
+        for s in range(n):
+            for t in range(T):
+                o = ref.linear_core(conv_w, dt, a, norm, c_ref[s], s_ref[s], qkv[s, t], z[s, t], b[s, t], al[s, t],
+                                    threads=16)
+                e = float(np.max(np.abs(got[s, t] - o)))
+                assert e <= TOL_ABS, (seed, n, pieces, call, s, t, e)
+                worst = max(worst, e)
+        got_conv = d_conv.download().reshape(n, 30720)
+        got_delta = d_delta.download().reshape(n, GDN_STATE)
+        for s in range(n):
+            assert np.array_equal(got_conv[s], c_ref[s]), (seed, pieces, call, s)
+            rel = state_rel(got_delta[s], s_ref[s])
+            assert max(rel) <= 1e-4, (seed, n, pieces, call, s, rel)
+    for d in d_w + [d_conv, d_delta]:
+        d.free()
+    margin("out max-abs (every row, every call)", worst, TOL_ABS)
+    rel = max(max(state_rel(got_delta[s], s_ref[s])) for s in range(n))
+    margin("final state rel (max and Frobenius)", rel, 1e-4)
