@@ -22,7 +22,11 @@ names.  Each failure message names its seed and case.
   in consecutive calls, the conv and recurrent states carried between them,
   against the restatement run token by token (ops.rs:1088-1099, :744-804):
   outputs within 1e-3, the conv state bit-exact, the recurrent state within
-  1e-4 relative."""
+  1e-4 relative;
+- the replayed decode graph (q38_decode_graph_*): 1-3 sequences, positions
+  drawn per replay anywhere in the cached range (split counts and page
+  boundaries change between replays), every replay bit-identical to the
+  plain q38_attn_decode calls at the same positions."""
 import numpy as np
 import pytest
 from oracle_checks import _random_f32_path, _random_kquant
@@ -285,3 +289,42 @@ def test_random_linear_core_pieces(ctx, ref, margin, seed):
     margin("out max-abs (every row, every call)", worst, TOL_ABS)
     rel = max(max(state_rel(got_delta[s], s_ref[s])) for s in range(n))
     margin("final state rel (max and Frobenius)", rel, 1e-4)
+
+
+@pytest.mark.parametrize("seed", [0x5133D000, 0x5133D001, 0x5133D002])
+def test_random_graph_replays(pkg, ctx, seed):
+    rng = np.random.default_rng(seed)
+    n_seq, n_tok, layers = int(rng.integers(1, 4)), 6000, (3, 7)
+    gate = bool(rng.random() < 0.7)
+    kv = pkg.KVCache(ctx, n_slots=2, max_pages=n_seq * (n_tok // 16 + 8), max_seqs=n_seq,
+                     max_tokens_per_seq=n_tok + 64)
+    try:
+        seqs = [kv.seq_create() for _ in range(n_seq)]
+        d_k, d_v = ctx.empty((n_tok, 1024)), ctx.empty((n_tok, 1024))
+        for li, layer in enumerate(layers):
+            for b, sq in enumerate(seqs):
+                ctx.fill_normal(d_k, n_tok * 1024, seed + 16 * li + 2 * b)
+                ctx.fill_normal(d_v, n_tok * 1024, seed + 16 * li + 2 * b + 1)
+                kv.write(layer, sq, 0, n_tok, d_k, d_v)
+        f32 = lambda *shape: ctx.array(rng.standard_normal(shape).astype(np.float32))
+        q = {L: f32(n_seq, 6144) for L in layers}
+        g = {L: f32(n_seq, 6144) if gate else None for L in layers}
+        kn = {L: f32(n_seq, 1024) for L in layers}
+        vn = {L: f32(n_seq, 1024) for L in layers}
+        out_g = {L: ctx.empty((n_seq, 24, 256)) for L in layers}
+        out_p = {L: ctx.empty((n_seq, 24, 256)) for L in layers}
+        calls = [{"layer": L, "q": q[L], "k_new": kn[L], "v_new": vn[L], "out": out_g[L],
+                  **({"gate": g[L]} if gate else {})} for L in layers]
+        draw = lambda: [int(rng.choice([rng.integers(0, 64), rng.integers(0, n_tok + 1)])) for _ in range(n_seq)]
+        with kv.decode_graph(seqs, draw(), calls) as graph:
+            for rep in range(8):
+                pos = draw()
+                graph.set_positions(pos)
+                graph.launch()
+                for L in layers:
+                    kv.attn_decode(L, seqs, pos, q[L], out_p[L], k_new=kn[L], v_new=vn[L], gate=g[L])
+                for L in layers:
+                    got, want = out_g[L].download(), out_p[L].download()
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seed, n_seq, rep, pos, L)
+    finally:
+        kv.close()
