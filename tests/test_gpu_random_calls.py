@@ -23,6 +23,10 @@ names.  Each failure message names its seed and case.
   against the restatement run token by token (ops.rs:1088-1099, :744-804):
   outputs within 1e-3, the conv state bit-exact, the recurrent state within
   1e-4 relative;
+- full_core (q38_full_core: the q/k norms, RoPE at each sequence's position,
+  the append, attention and the gate; ops.rs:813-940): 1-4 sequences of
+  random lengths advanced token by token, each step against the restatement
+  on its own caches (appended rows included) within 1e-3;
 - the replayed decode graph (q38_decode_graph_*): 1-3 sequences, positions
   drawn per replay anywhere in the cached range (split counts and page
   boundaries change between replays), every replay bit-identical to the
@@ -30,7 +34,7 @@ names.  Each failure message names its seed and case.
 import numpy as np
 import pytest
 from oracle_checks import _random_f32_path, _random_kquant
-from parity import TOL_ABS, abs_rel, state_rel
+from parity import TOL_ABS, TOL_REL, abs_rel, state_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -328,3 +332,49 @@ def test_random_graph_replays(pkg, ctx, seed):
                     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seed, n_seq, rep, pos, L)
     finally:
         kv.close()
+
+
+@pytest.mark.parametrize("seed", [0x5133E000, 0x5133E007, 0x5133E009, 0x5133E00E])  # 2-4 sequences, position 0 to 1949
+def test_random_full_core_steps(pkg, ctx, ref, margin, seed):
+    rng = np.random.default_rng(seed)
+    n_seq, ctx_len, layer = int(rng.integers(1, 5)), 2048, 3  # the first full-attention layer: the
+    # restatement indexes its caches by full-attention layer ([layer / 4][ctx_len][1024])
+    f32 = lambda *shape, s=1.0, m=0.0: (m + rng.standard_normal(shape) * s).astype(np.float32)
+    qn, kn = f32(256, s=0.2, m=1.0), f32(256, s=0.2, m=1.0)
+    pos = [int(rng.choice([rng.integers(0, 40), rng.integers(0, ctx_len - 8)])) for _ in range(n_seq)]
+    kv = pkg.KVCache(ctx, n_slots=17, max_pages=n_seq * ctx_len // 16 + 8, max_seqs=n_seq, max_tokens_per_seq=ctx_len)
+    worst = (0.0, 0.0)
+    try:
+        seqs = [kv.seq_create() for _ in range(n_seq)]
+        caches = []
+        for sq, p in zip(seqs, pos):
+            kc, vc = np.zeros((ctx_len, 1024), np.float32), np.zeros((ctx_len, 1024), np.float32)
+            if p:
+                kc[:p], vc[:p] = f32(p, 1024), f32(p, 1024)
+                d_k0, d_v0 = ctx.array(kc[:p]), ctx.array(vc[:p])
+                kv.write(layer, sq, 0, p, d_k0, d_v0)
+                d_k0.free()
+                d_v0.free()
+            caches.append((kc, vc))
+        d_qn, d_kn = ctx.array(qn), ctx.array(kn)
+        for step in range(4):
+            qg, key, val = f32(n_seq, 12288), f32(n_seq, 1024), f32(n_seq, 1024)
+            d_in = [ctx.array(x) for x in (qg, key, val)]
+            d_o = ctx.empty((n_seq, 24, 256))
+            kv.full_core(layer, seqs, pos, d_qn, d_kn, *d_in, d_o)
+            got = d_o.download().reshape(n_seq, 6144)
+            for d in d_in + [d_o]:
+                d.free()
+            for b in range(n_seq):
+                kc, vc = caches[b]
+                want, _ = ref.full_core(qn, kn, qg[b], key[b], val[b], kc, vc, ctx_len, pos[b], layer, threads=16)
+                e = abs_rel(got[b], np.asarray(want).reshape(-1))
+                assert e[0] <= TOL_ABS and e[1] <= TOL_REL, (seed, n_seq, step, b, pos[b], e)
+                worst = tuple(max(x, y) for x, y in zip(worst, e))
+            pos = [p + 1 for p in pos]
+        d_qn.free()
+        d_kn.free()
+    finally:
+        kv.close()
+    margin("out max-abs (every sequence and step)", worst[0], TOL_ABS)
+    margin("out rel (every sequence and step)", worst[1], TOL_REL)
